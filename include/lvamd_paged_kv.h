@@ -1,0 +1,175 @@
+/*
+ * lvamd_paged_kv.h — C ABI of the MI355X (gfx950) paged-KV attention backend.
+ *
+ * Every entry point takes raw device pointers, element strides and sizes,
+ * enqueues its kernels on the given HIP stream, performs no host
+ * synchronisation and no device allocation, and returns an lvamd_status
+ * (0 = success, negative = error; lvamd_status_string names it).
+ *
+ * Physical KV layout (unchanged from light-vllm): per layer two tensors,
+ * keys and values, each [num_blocks, block_size, num_kv_heads, head_size],
+ * contiguous, of the cache dtype.  A physical "slot" is
+ * block_id * block_size + offset, so slot s addresses the row
+ * pool + s * num_kv_heads * head_size.
+ *
+ * Reference interfaces each entry point replaces are cited per function
+ * (paths relative to the light-vllm source tree).
+ */
+#ifndef LVAMD_PAGED_KV_H
+#define LVAMD_PAGED_KV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* lvamd_stream_t; /* a hipStream_t; NULL = the legacy default stream */
+
+enum lvamd_status {
+  LVAMD_OK = 0,
+  LVAMD_ERR_INVALID_ARGUMENT = -1,  /* null pointer, negative size, misaligned row  */
+  LVAMD_ERR_UNSUPPORTED = -2,       /* dtype / head_size / group size not built     */
+  LVAMD_ERR_WORKSPACE = -3,         /* workspace smaller than the *_workspace_size  */
+  LVAMD_ERR_LAUNCH = -4             /* hipLaunchKernel / hipGetLastError failed     */
+};
+
+enum lvamd_dtype { LVAMD_F32 = 0, LVAMD_F16 = 1, LVAMD_BF16 = 2 };
+
+/* Number of int32 fields per request in the attention metadata
+ * (table_off, num_table_blocks, computed, q_len, q_start, vis_off, vis_words, 0). */
+#define LVAMD_REQ_FIELDS 8
+/* Number of int32 fields per split-K work unit (req, partition, column_tile, partial_slot). */
+#define LVAMD_UNIT_FIELDS 4
+/* Number of int32 fields per merge job (req, column_tile, first_partial_slot, num_partitions). */
+#define LVAMD_MERGE_FIELDS 4
+/* Number of int32 fields per prefill work unit (req, first query of the block, num queries, 0). */
+#define LVAMD_PREFILL_FIELDS 4
+
+const char* lvamd_status_string(int status);
+
+/* Library version, for the Python loader's compatibility check. */
+int lvamd_abi_version(void);
+
+/*
+ * Slot-mapped KV append:  key_pool[slots[t]] = key[t], value_pool[slots[t]] = value[t]
+ * for every token t with slots[t] >= 0 (a negative slot marks an inactive token
+ * and is skipped, as in the validated write path).  Slots must be unique and
+ * < num_blocks * block_size (the caller proves this on the host, as
+ * PagedAttentionMetadata.validate_block_tables does).  Bit-exact row copy.
+ *
+ * key/value: [num_tokens, num_kv_heads, head_size] with the given token and
+ * head strides (elements); the head_size dimension must be contiguous.
+ *
+ * Replaces: PagedKVCache.write_prepared / write
+ *   (src/light_vllm/runtime/execution/paged_cache.py:209-254) and the Triton
+ *   _write_paged_kv_kernel (src/light_vllm/runtime/execution/triton_paged_attention.py:31-104).
+ */
+int lvamd_kv_append(const void* key, int64_t key_token_stride, int64_t key_head_stride,
+                    const void* value, int64_t value_token_stride, int64_t value_head_stride,
+                    void* key_pool, void* value_pool, const int64_t* slots, int64_t num_tokens,
+                    int32_t num_kv_heads, int32_t head_size, int32_t dtype,
+                    lvamd_stream_t stream);
+
+/*
+ * Split-K paged attention for short query runs (decode, speculative tree
+ * verification): one wave per (work unit, kv head, ...), bf16/fp16 QK^T and
+ * PV on MFMA 16x16x32 (fp32 on MFMA 16x16x4), fp32 online softmax, partial
+ * (m, l, acc) per partition merged by lvamd_paged_attention_merge.
+ *
+ * q:   [T, num_kv_heads*group, head_size] (token/head strides in elements)
+ * out: same shape, written for every query token that a unit covers.
+ * req_meta [num_requests][LVAMD_REQ_FIELDS], tables (flat int32 block ids),
+ * vis (uint32 ancestor bit rows, only for requests with vis_off >= 0),
+ * units [num_units][LVAMD_UNIT_FIELDS].  A unit whose partial_slot is -1
+ * covers the whole sequence and writes out directly; otherwise it writes
+ * its partial to part_acc [slots][num_kv_heads][16][head_size] and part_ml
+ * [slots][num_kv_heads][16][2] (fp32).
+ * scale is the caller's softmax scale (1/sqrt(head_size) for Qwen2).
+ *
+ * Together with lvamd_paged_attention_merge and lvamd_paged_prefill this
+ * replaces TorchPagedAttention.forward/_attend_query_token
+ *   (src/light_vllm/runtime/execution/paged_attention.py:268-380) and the Triton
+ *   _grouped_paged_attention_kernel / _paged_attention_kernel
+ *   (src/light_vllm/runtime/execution/triton_paged_attention.py:107-391, launch :519-559).
+ */
+int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                       const void* key_pool, const void* value_pool,
+                       void* out, int64_t out_token_stride, int64_t out_head_stride,
+                       const int32_t* req_meta, const int32_t* tables, const uint32_t* vis,
+                       const int32_t* units, int32_t num_units,
+                       float* part_acc, float* part_ml, int64_t num_partial_slots,
+                       int32_t num_kv_heads, int32_t group, int32_t head_size,
+                       int32_t block_size, int32_t partition_tokens, float scale,
+                       int32_t dtype, lvamd_stream_t stream);
+
+/*
+ * Log-sum-exp merge of split-K partials into out, one job per
+ * (request, column tile): jobs [num_jobs][LVAMD_MERGE_FIELDS].
+ * Replaces the same reference functions as lvamd_paged_decode (the reference
+ * has no split-K; this is the cross-partition half of that computation).
+ */
+int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
+                                void* out, int64_t out_token_stride, int64_t out_head_stride,
+                                const int32_t* req_meta, const int32_t* jobs, int32_t num_jobs,
+                                int32_t num_kv_heads, int32_t group, int32_t head_size,
+                                int32_t dtype, lvamd_stream_t stream);
+
+/*
+ * Chunked-prefill paged attention for long query runs: one workgroup per
+ * (prefill unit, kv head); the unit's queries x the kv head's group of query
+ * heads are MFMA columns, K/V tiles are gathered through the block table into
+ * LDS and shared by the workgroup's waves.  units [num_units][LVAMD_PREFILL_FIELDS].
+ * Replaces the prefill half of the same reference functions as lvamd_paged_decode.
+ */
+int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                        const void* key_pool, const void* value_pool,
+                        void* out, int64_t out_token_stride, int64_t out_head_stride,
+                        const int32_t* req_meta, const int32_t* tables, const uint32_t* vis,
+                        const int32_t* units, int32_t num_units,
+                        int32_t num_kv_heads, int32_t group, int32_t head_size,
+                        int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream);
+
+/*
+ * Tree-KV compact across all layers: for every layer l and pair i,
+ * row dst_slots[i] of keys[l] and values[l] receives the bytes row
+ * src_slots[i] held before the call (every source is read before any
+ * destination is written, so overlapping paths are safe).  Pairs with
+ * src == dst may be passed or omitted.  Destinations must be unique.
+ * layer_key_ptrs / layer_value_ptrs: device arrays of num_layers pool base
+ * addresses (uint64).  row_bytes = num_kv_heads * head_size * element size,
+ * equal for all layers of one call.  When num_pairs exceeds
+ * lvamd_kv_compact_inline_pairs(), workspace must hold
+ * lvamd_kv_compact_workspace_size(...) bytes; otherwise it may be NULL.
+ *
+ * Replaces: PagedKVCache.compact's gather / clone / scatter loop
+ *   (src/light_vllm/runtime/execution/paged_cache.py:315-326); host-side
+ *   validation and the moved-token count stay in Python (:269-314, :326).
+ */
+int lvamd_kv_compact(const uint64_t* layer_key_ptrs, const uint64_t* layer_value_ptrs,
+                     int32_t num_layers, int64_t row_bytes,
+                     const int64_t* src_slots, const int64_t* dst_slots, int64_t num_pairs,
+                     void* workspace, int64_t workspace_bytes, lvamd_stream_t stream);
+int64_t lvamd_kv_compact_inline_pairs(void);
+int64_t lvamd_kv_compact_workspace_size(int64_t num_pairs, int32_t num_layers, int64_t row_bytes);
+
+/*
+ * Copy-on-write block copy across all layers: block dst_blocks[i] of keys[l]
+ * and values[l] becomes a byte copy of block src_blocks[i].  Sources and
+ * destinations must be disjoint sets and destinations unique (checked by the
+ * Python caller).  block_bytes = block_size * row_bytes.
+ *
+ * No reference counterpart: light-vllm's prefix cache shares only complete
+ * read-only pages (src/light_vllm/runtime/kv_cache.py:661-723).  This is the
+ * primitive a partial-page prefix share needs.
+ */
+int lvamd_kv_block_copy(const uint64_t* layer_key_ptrs, const uint64_t* layer_value_ptrs,
+                        int32_t num_layers, int64_t block_bytes,
+                        const int64_t* src_blocks, const int64_t* dst_blocks, int64_t num_pairs,
+                        lvamd_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LVAMD_PAGED_KV_H */

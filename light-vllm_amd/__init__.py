@@ -1,0 +1,66 @@
+"""MI355X-native (gfx950) paged-KV attention backend for light-vllm.
+
+The directory name is not a Python identifier, so the package registers itself
+as ``light_vllm_amd`` on import and all of its modules use that name.  Import
+it with ``importlib.import_module("light-vllm_amd")`` (the repository root on
+``sys.path``), then use ``light_vllm_amd``.
+"""
+
+import sys as _sys
+
+_sys.modules.setdefault("light_vllm_amd", _sys.modules[__name__])
+
+from light_vllm_amd.backend import HipPagedAttention, HipPagedAttentionBackend  # noqa: E402
+from light_vllm_amd.errors import (  # noqa: E402
+    ExecutionError,
+    ExecutionNotReadyError,
+    KVCacheCapacityError,
+    KVCacheError,
+)
+from light_vllm_amd.interfaces import (  # noqa: E402
+    AttentionLayerSpec,
+    DraftTree,
+    ModelKVCacheSpec,
+    QueryLayout,
+)
+from light_vllm_amd.layout import (  # noqa: E402
+    append_draft_layout,
+    linear_query_layout,
+    query_visibility,
+    semantic_positions,
+)
+from light_vllm_amd.metadata import PagedAttentionMetadata  # noqa: E402
+from light_vllm_amd.paged_cache import (  # noqa: E402
+    PagedKVCache,
+    PagedKVCacheConfig,
+    PagedKVWriteMapping,
+    PagedLayerCache,
+    hip_block_copy,
+    hip_compact,
+    kv_cache_bytes_per_block,
+)
+
+__all__ = [
+    "AttentionLayerSpec",
+    "DraftTree",
+    "ExecutionError",
+    "ExecutionNotReadyError",
+    "HipPagedAttention",
+    "HipPagedAttentionBackend",
+    "KVCacheCapacityError",
+    "KVCacheError",
+    "ModelKVCacheSpec",
+    "PagedAttentionMetadata",
+    "PagedKVCache",
+    "PagedKVCacheConfig",
+    "PagedKVWriteMapping",
+    "PagedLayerCache",
+    "QueryLayout",
+    "append_draft_layout",
+    "hip_block_copy",
+    "hip_compact",
+    "kv_cache_bytes_per_block",
+    "linear_query_layout",
+    "query_visibility",
+    "semantic_positions",
+]

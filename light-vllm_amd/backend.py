@@ -1,0 +1,225 @@
+"""The HIP paged-attention backend: ``create(cache, metadata) -> context``.
+
+Drop-in for light-vllm's ``PagedAttentionBackend`` protocol
+(src/light_vllm/runtime/execution/paged_attention.py:209-223).  A context is
+created once per model step by ``PagedStepHandler.forward``
+(src/light_vllm/runtime/execution/worker.py:286) and its ``forward`` is called
+once per layer by the model (src/light_vllm/modeling/models/qwen2.py:417-423):
+
+1. validate shapes exactly as ``_validate_paged_attention_tensors``
+   (paged_attention.py:226-247) plus the dtype/device rule of the Triton
+   backend (triton_paged_attention.py:475-478);
+2. append this step's K/V into the pool (HIP ``lvamd_kv_append``), stream-
+   ordered before attention, so a query sees its own K/V;
+3. attend: split-K decode kernel for short query runs, MFMA prefill kernel for
+   long ones, merge kernel for split partials, all on the current stream with
+   no host synchronisation.
+
+The backend reads the cache and metadata only through light-vllm's public
+surface, so the reference's ``PagedKVCache`` and ``PagedAttentionMetadata``
+work unchanged.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from light_vllm_amd import native
+from light_vllm_amd.errors import KVCacheError
+from light_vllm_amd.paged_cache import current_stream, dtype_code, hip_append
+from light_vllm_amd.plan import StepPlan
+
+SUPPORTED_HEAD_SIZES = (32, 64, 80, 96, 128, 256)
+
+
+def validate_paged_attention_tensors(cache, metadata, layer_id: str, query: Tensor, key: Tensor, value: Tensor):
+    """Shape checks shared by every backend (paged_attention.py:226-247)."""
+
+    layer_spec = cache.layer_spec(layer_id)
+    if query.ndim != 3:
+        raise KVCacheError("paged attention query must have three dimensions")
+    if query.shape[0] != key.shape[0] or value.shape != key.shape:
+        raise KVCacheError("paged attention Q/K/V token dimensions must match")
+    if query.shape[0] != metadata.num_query_tokens:
+        raise KVCacheError("paged attention metadata token count does not match query")
+    if tuple(query.shape[1:]) != (layer_spec.num_query_heads, layer_spec.head_size):
+        raise KVCacheError("paged attention query shape does not match the layer spec")
+    if tuple(key.shape[1:]) != (layer_spec.num_kv_heads, layer_spec.head_size):
+        raise KVCacheError("paged attention K/V shape does not match the layer spec")
+    return layer_spec
+
+
+class _Workspace:
+    """Split-K partials, grown on demand and reused by every layer and step.
+
+    Layers run in stream order on one stream, so one buffer serves them all.
+    """
+
+    def __init__(self) -> None:
+        self._buffer: Tensor | None = None
+
+    def get(self, num_floats: int, device: torch.device) -> Tensor:
+        if self._buffer is None or self._buffer.numel() < num_floats or self._buffer.device != device:
+            self._buffer = torch.empty(max(num_floats, 1), dtype=torch.float32, device=device)
+        return self._buffer
+
+
+class HipPagedAttention:
+    """Per-step context: writes each layer's K/V, then runs paged attention."""
+
+    def __init__(self, cache, metadata, workspace: _Workspace, plan: StepPlan) -> None:
+        self._cache = cache
+        self._metadata = metadata
+        self._layer_ids: set[str] = set()
+        self._workspace = workspace
+        self._plan = plan
+        self._lib = native.load()
+
+    @property
+    def layer_ids(self) -> frozenset[str]:
+        return frozenset(self._layer_ids)
+
+    @property
+    def plan(self) -> StepPlan:
+        return self._plan
+
+    def forward(self, layer_id: str, query: Tensor, key: Tensor, value: Tensor, *, scale: float) -> Tensor:
+        if layer_id in self._layer_ids:
+            raise KVCacheError(f"paged attention layer {layer_id!r} ran more than once")
+        self._layer_ids.add(layer_id)
+        spec = validate_paged_attention_tensors(self._cache, self._metadata, layer_id, query, key, value)
+        config = self._cache.config
+        if query.device != config.device or query.dtype != config.dtype:
+            raise KVCacheError("HIP paged attention query dtype and device must match the KV cache")
+        if key.dtype != config.dtype or value.dtype != config.dtype:
+            raise KVCacheError("paged KV update dtype and device must match the cache")
+        if spec.head_size not in SUPPORTED_HEAD_SIZES:
+            raise KVCacheError(
+                f"HIP paged attention supports head sizes {SUPPORTED_HEAD_SIZES}, not {spec.head_size}"
+            )
+
+        # 1. append (write before attend).
+        hip_append(self._cache, layer_id, key, value, self._plan.slots)
+
+        # 2. attend.
+        if query.stride(2) != 1 or (query.stride(0) * query.element_size()) % 16 or (
+            query.stride(1) * query.element_size()
+        ) % 16 or query.data_ptr() % 16:
+            query = query.contiguous()
+        out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+        self.attend(layer_id, query, out, scale=scale)
+        return out
+
+    def attend(self, layer_id: str, query: Tensor, out: Tensor, *, scale: float) -> None:
+        """Paged attention of ``query`` against the pool into ``out`` (no append)."""
+
+        launch = self.decode_launch(layer_id, query, out, scale=scale)
+        if launch is not None:
+            launch.decode()
+            launch.merge()
+        self.prefill(layer_id, query, out, scale=scale)
+
+    def decode_launch(self, layer_id: str, query: Tensor, out: Tensor, *, scale: float) -> "_DecodeLaunch | None":
+        """Bound split-K decode + merge launches for this layer, or None if no decode rows."""
+
+        spec = self._cache.layer_spec(layer_id)
+        group = spec.num_query_heads // spec.num_kv_heads
+        work = self._plan.work(group, spec.num_kv_heads)
+        if not work.num_units:
+            return None
+        part_acc = part_ml = None
+        if work.num_partial_slots:
+            per_slot = spec.num_kv_heads * 16
+            buf = self._workspace.get(work.num_partial_slots * per_slot * (spec.head_size + 2), query.device)
+            part_acc = buf.data_ptr()
+            part_ml = part_acc + work.num_partial_slots * per_slot * spec.head_size * 4
+        return _DecodeLaunch(self._lib, self._cache, self._plan, work, spec, group, self._cache.layer(layer_id),
+                             query, out, float(scale), part_acc, part_ml)
+
+    def prefill(self, layer_id: str, query: Tensor, out: Tensor, *, scale: float) -> None:
+        spec = self._cache.layer_spec(layer_id)
+        group = spec.num_query_heads // spec.num_kv_heads
+        work = self._plan.work(group, spec.num_kv_heads)
+        if not work.num_prefill_units:
+            return
+        layer = self._cache.layer(layer_id)
+        plan = self._plan
+        status = self._lib.lvamd_paged_prefill(
+            query.data_ptr(), query.stride(0), query.stride(1),
+            layer.keys.data_ptr(), layer.values.data_ptr(),
+            out.data_ptr(), out.stride(0), out.stride(1),
+            plan.req_meta.data_ptr(), plan.tables.data_ptr(), plan.vis.data_ptr(),
+            work.prefill_units.data_ptr(), work.num_prefill_units,
+            spec.num_kv_heads, group, spec.head_size,
+            self._cache.config.block_size, float(scale), dtype_code(query.dtype), current_stream(query.device),
+        )
+        native.check(status, "lvamd_paged_prefill")
+
+
+class _DecodeLaunch:
+    """The decode and merge kernel launches of one layer, with bound arguments."""
+
+    def __init__(self, lib, cache, plan, work, spec, group, layer, query, out, scale, part_acc, part_ml) -> None:
+        self.work = work
+        stream = current_stream(query.device)
+        dt = dtype_code(query.dtype)
+        self._lib = lib
+        self._decode_args = (
+            query.data_ptr(), query.stride(0), query.stride(1),
+            layer.keys.data_ptr(), layer.values.data_ptr(),
+            out.data_ptr(), out.stride(0), out.stride(1),
+            plan.req_meta.data_ptr(), plan.tables.data_ptr(), plan.vis.data_ptr(),
+            work.units.data_ptr(), work.num_units,
+            part_acc, part_ml, work.num_partial_slots,
+            spec.num_kv_heads, group, spec.head_size,
+            cache.config.block_size, work.partition_tokens, scale, dt, stream,
+        )
+        self._merge_args = None
+        if work.num_jobs:
+            self._merge_args = (
+                part_acc, part_ml,
+                out.data_ptr(), out.stride(0), out.stride(1),
+                plan.req_meta.data_ptr(), work.jobs.data_ptr(), work.num_jobs,
+                spec.num_kv_heads, group, spec.head_size, dt, stream,
+            )
+
+    def decode(self) -> None:
+        native.check(self._lib.lvamd_paged_decode(*self._decode_args), "lvamd_paged_decode")
+
+    def merge(self) -> None:
+        if self._merge_args is not None:
+            native.check(self._lib.lvamd_paged_attention_merge(*self._merge_args), "lvamd_paged_attention_merge")
+
+
+class HipPagedAttentionBackend:
+    """Creates one ``HipPagedAttention`` per model step.
+
+    Construction fails with ``ExecutionNotReadyError`` when the HIP library is
+    missing, like the Triton backend without Triton
+    (triton_paged_attention.py:566-570).  The step plan of the most recent
+    metadata object is kept: metadata objects are immutable, so a second
+    ``create`` with the same object (and a cache of the same geometry) reuses
+    the validated, staged plan.
+    """
+
+    def __init__(self, *, use_prefill_kernel: bool = False) -> None:
+        native.load()
+        self._workspace = _Workspace()
+        self._use_prefill = use_prefill_kernel
+        self._last: tuple[object, object, StepPlan] | None = None
+
+    def create(self, cache, metadata) -> HipPagedAttention:
+        config = cache.config
+        key = (config.num_blocks, config.block_size, config.device)
+        last = self._last
+        if last is not None and last[0] == key and last[1] is metadata:
+            plan = last[2]
+        else:
+            if config.device.type != "cuda":
+                raise KVCacheError("HIP paged attention requires a GPU KV cache")
+            metadata.validate_block_tables(num_blocks=config.num_blocks, block_size=config.block_size)
+            plan = StepPlan(metadata, block_size=config.block_size, device=config.device,
+                            use_prefill=self._use_prefill)
+            self._last = (key, metadata, plan)
+        return HipPagedAttention(cache, metadata, self._workspace, plan)

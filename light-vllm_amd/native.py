@@ -1,0 +1,102 @@
+"""ctypes binding of the gfx950 HIP library (``liblvamd_hip.so``).
+
+The library is the product: there is no CPU or PyTorch fallback.  ``load()``
+raises ``ExecutionNotReadyError`` when the library has not been built, and
+every call that returns a non-zero status raises ``ExecutionError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+import re
+from pathlib import Path
+
+from light_vllm_amd.errors import ExecutionError, ExecutionNotReadyError
+
+LIB_NAME = "liblvamd_hip.so"
+ABI_VERSION = 1
+PACKAGE_DIR = Path(__file__).resolve().parent
+REPO_ROOT = PACKAGE_DIR.parent
+HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
+
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+REQ_FIELDS = 8
+UNIT_FIELDS = 4
+MERGE_FIELDS = 4
+PREFILL_FIELDS = 4
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+
+# name -> (restype, argtypes); must match include/lvamd_paged_kv.h.
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "lvamd_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "lvamd_abi_version": (ctypes.c_int, []),
+    "lvamd_kv_append": (
+        ctypes.c_int,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i32, _i32, _i32, _p],
+    ),
+    "lvamd_paged_decode": (
+        ctypes.c_int,
+        [_p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i32, _p, _p, _i64,
+         _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p],
+    ),
+    "lvamd_paged_attention_merge": (
+        ctypes.c_int,
+        [_p, _p, _p, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p],
+    ),
+    "lvamd_paged_prefill": (
+        ctypes.c_int,
+        [_p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i32,
+         _i32, _i32, _i32, _i32, _f32, _i32, _p],
+    ),
+    "lvamd_kv_compact": (
+        ctypes.c_int,
+        [_p, _p, _i32, _i64, _p, _p, _i64, _p, _i64, _p],
+    ),
+    "lvamd_kv_compact_inline_pairs": (_i64, []),
+    "lvamd_kv_compact_workspace_size": (_i64, [_i64, _i32, _i64]),
+    "lvamd_kv_block_copy": (
+        ctypes.c_int,
+        [_p, _p, _i32, _i64, _p, _p, _i64, _p],
+    ),
+}
+
+
+def library_path() -> Path:
+    return PACKAGE_DIR / LIB_NAME
+
+
+def header_functions() -> list[str]:
+    """Names of every function the C header declares."""
+
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lvamd_[a-z0-9_]+)\s*\(", text)))
+
+
+@functools.lru_cache(maxsize=1)
+def load() -> ctypes.CDLL:
+    path = library_path()
+    if not path.exists():
+        raise ExecutionNotReadyError(
+            f"the HIP library {path} is not built; run __graft_entry__.build() first"
+        )
+    lib = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    version = lib.lvamd_abi_version()
+    if version != ABI_VERSION:
+        raise ExecutionNotReadyError(f"{path} has ABI version {version}, expected {ABI_VERSION}")
+    return lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        message = load().lvamd_status_string(status).decode()
+        raise ExecutionError(f"{what} failed: {message} (status {status})")

@@ -1,0 +1,195 @@
+"""GPU parity of the KV movement kernels: append, compact, block copy.
+
+All three must be bit-exact against the CPU oracle: full pools are compared
+byte for byte (as integer views), so every untouched byte must be unchanged.
+"""
+
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import light_vllm_amd as lv
+from oracle import paged_kv_oracle as O
+
+pytestmark = pytest.mark.gpu
+if not torch.cuda.is_available():
+    pytest.skip("needs an MI355X GPU", allow_module_level=True)
+
+DEV = torch.device("cuda:0")
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())
+INT_VIEW = {torch.float32: torch.int32, torch.float16: torch.int16, torch.bfloat16: torch.int16}
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.view(INT_VIEW[t.dtype]).cpu().numpy()
+
+
+def _announce(name: str) -> None:
+    print(f"[gpu] {name}", file=sys.stderr, flush=True)
+
+
+def _cache(*, hkv, d, bs, nb, dtype, layers=1, hq=None):
+    spec = lv.ModelKVCacheSpec(tuple(lv.AttentionLayerSpec(f"l{i}", hq or hkv, hkv, d) for i in range(layers)))
+    cache = lv.PagedKVCache(spec, lv.PagedKVCacheConfig(num_blocks=nb, block_size=bs, dtype=dtype, device=DEV))
+    gen = torch.Generator(device=DEV).manual_seed(nb * 7 + d)
+    for i in range(layers):
+        layer = cache.layer(f"l{i}")
+        for pool in (layer.keys, layer.values):
+            pool.copy_(torch.randn(pool.shape, generator=gen, device=DEV).to(dtype))
+    return cache
+
+
+@pytest.mark.parametrize(
+    "name,hkv,d,bs,nb,dtype,tokens",
+    [
+        ("c1_fp32", 2, 64, 16, 256, torch.float32, 4),
+        ("c2_bf16", 4, 128, 16, 32768, torch.bfloat16, 64),
+        ("c3_bf16_4152", 4, 128, 16, 4096, torch.bfloat16, 4152),
+        ("fp16_d80_bs3", 2, 80, 3, 64, torch.float16, 29),
+    ],
+)
+def test_append_is_bit_exact(name, hkv, d, bs, nb, dtype, tokens) -> None:
+    _announce(f"append {name}")
+    cache = _cache(hkv=hkv, d=d, bs=bs, nb=nb, dtype=dtype)
+    layer = cache.layer("l0")
+    rng = np.random.default_rng(tokens)
+    slots = rng.choice(nb * bs, size=tokens, replace=False)
+    key = torch.randn((tokens, hkv, d)).to(dtype).to(DEV)
+    value = torch.randn((tokens, hkv, d)).to(dtype).to(DEV)
+    kb, vb = _bits(layer.keys), _bits(layer.values)
+    O.append(kb, vb, _bits(key), _bits(value), slots)
+    cache.write("l0", key, value, torch.tensor(slots, device=DEV))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_bits(layer.keys), kb)
+    np.testing.assert_array_equal(_bits(layer.values), vb)
+
+
+def test_append_reads_strided_views_and_skips_inactive_tokens() -> None:
+    _announce("append strided")
+    hq, hkv, d = 28, 4, 128
+    cache = _cache(hkv=hkv, d=d, bs=16, nb=64, dtype=torch.bfloat16, hq=hq)
+    layer = cache.layer("l0")
+    qkv = torch.randn((10, hq + 2 * hkv, d)).to(torch.bfloat16).to(DEV)  # fused QKV output
+    key, value = qkv[:, hq : hq + hkv], qkv[:, hq + hkv :]
+    assert not key.is_contiguous()
+    slots = np.array([5, -1, 17, 900, -1, 0, 31, 640, 1023, 2])
+    kb, vb = _bits(layer.keys), _bits(layer.values)
+    O.append(kb, vb, _bits(key.contiguous()), _bits(value.contiguous()), slots)
+    cache.write("l0", key, value, torch.tensor(slots, device=DEV))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_bits(layer.keys), kb)
+    np.testing.assert_array_equal(_bits(layer.values), vb)
+
+
+def test_append_validation_matches_reference_errors() -> None:
+    cache = _cache(hkv=2, d=64, bs=16, nb=8, dtype=torch.float32)
+    k = torch.randn((2, 2, 64), device=DEV)
+    with pytest.raises(lv.KVCacheError, match="out-of-range physical slot"):
+        cache.write("l0", k, k, torch.tensor([0, 128], device=DEV))
+    with pytest.raises(lv.KVCacheError, match="same physical slot twice"):
+        cache.write("l0", k, k, torch.tensor([3, 3], device=DEV))
+    with pytest.raises(lv.KVCacheError, match="dtype and device must match"):
+        cache.write("l0", k.half(), k.half(), torch.tensor([0, 1], device=DEV))
+
+
+def test_compact_known_answer_on_gpu() -> None:
+    _announce("compact known answer")
+    c = GOLDEN["compact"]
+    spec = lv.ModelKVCacheSpec((lv.AttentionLayerSpec("attention", 2, c["num_kv_heads"], c["head_size"]),))
+    cache = lv.PagedKVCache(spec, lv.PagedKVCacheConfig(num_blocks=c["num_blocks"], block_size=c["block_size"],
+                                                        dtype=torch.float32, device=DEV))
+    prefix = torch.tensor(c["prefix_keys"], dtype=torch.float32, device=DEV)
+    cache.write("attention", prefix, prefix + c["prefix_value_offset"], torch.tensor(c["prefix_slots"], device=DEV))
+    layout = lv.QueryLayout(tuple(c["parents"]))
+    md = lv.PagedAttentionMetadata(block_tables=(tuple(c["block_table"]),), num_computed_tokens=(c["num_computed_tokens"],),
+                                   query_layouts=(layout,), num_readonly_prefix_blocks=(c["num_readonly_prefix_blocks"],))
+    qk = torch.tensor(c["query_keys"], dtype=torch.float32, device=DEV)
+    cache.write("attention", qk, qk + c["query_value_offset"], md.slot_mapping(block_size=c["block_size"], device=DEV))
+    moved = cache.compact(tuple(c["block_table"]), num_computed_tokens=c["num_computed_tokens"],
+                          num_query_tokens=len(layout), num_reserved_query_tokens=len(layout),
+                          retained_query_indices=tuple(c["retained"]),
+                          num_readonly_prefix_blocks=c["num_readonly_prefix_blocks"])
+    torch.cuda.synchronize()
+    layer = cache.layer("attention")
+    flat_k = layer.keys.view(-1, c["num_kv_heads"], c["head_size"])
+    flat_v = layer.values.view(-1, c["num_kv_heads"], c["head_size"])
+    assert torch.equal(layer.keys[1], prefix)
+    assert torch.equal(flat_k[c["destination_slots"]], qk[c["retained"]])
+    assert torch.equal(flat_v[c["destination_slots"]], qk[c["retained"]] + c["query_value_offset"])
+    assert moved == c["expected_moved"]
+
+
+@pytest.mark.parametrize("n_retained", [1, 5, 9, 16, 17, 40])
+def test_compact_matches_oracle_across_layers(n_retained) -> None:
+    _announce(f"compact n={n_retained}")
+    rng = np.random.default_rng(n_retained)
+    bs, nb, layers, computed = 16, 96, 3, 37
+    q = max(n_retained + 3, 9)
+    cache = _cache(hkv=2, d=128, bs=bs, nb=nb, dtype=torch.bfloat16, layers=layers, hq=12)
+    table = tuple(int(b) for b in rng.permutation(nb)[: (computed + q + bs - 1) // bs])
+    retained = tuple(int(i) for i in rng.permutation(q)[:n_retained])
+    pools = [(_bits(cache.layer(f"l{i}").keys), _bits(cache.layer(f"l{i}").values)) for i in range(layers)]
+    expect_moved = O.compact(pools, table, num_computed_tokens=computed, num_query_tokens=q,
+                             num_reserved_query_tokens=q, retained_query_indices=retained, num_blocks=nb, block_size=bs)
+    moved = cache.compact(table, num_computed_tokens=computed, num_query_tokens=q, num_reserved_query_tokens=q,
+                          retained_query_indices=retained)
+    torch.cuda.synchronize()
+    assert moved == expect_moved
+    for i, (kb, vb) in enumerate(pools):
+        np.testing.assert_array_equal(_bits(cache.layer(f"l{i}").keys), kb)
+        np.testing.assert_array_equal(_bits(cache.layer(f"l{i}").values), vb)
+
+
+def test_compact_identity_path_writes_nothing_and_returns_zero() -> None:
+    cache = _cache(hkv=2, d=64, bs=4, nb=8, dtype=torch.float32)
+    before = _bits(cache.layer("l0").keys)
+    assert cache.compact((3, 1), num_computed_tokens=2, num_query_tokens=3, num_reserved_query_tokens=3,
+                         retained_query_indices=(0, 1, 2)) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_bits(cache.layer("l0").keys), before)
+
+
+def test_compact_validation_errors() -> None:
+    cache = _cache(hkv=2, d=64, bs=2, nb=8, dtype=torch.float32)
+    with pytest.raises(lv.KVCacheError, match="exceeds the paged KV tail"):
+        cache.compact((0, 1), num_computed_tokens=1, num_query_tokens=2, num_reserved_query_tokens=2,
+                      retained_query_indices=(2,))
+    with pytest.raises(ValueError, match="unique"):
+        cache.compact((0, 1), num_computed_tokens=1, num_query_tokens=2, num_reserved_query_tokens=2,
+                      retained_query_indices=(1, 1))
+    with pytest.raises(lv.KVCacheError, match="exactly cover"):
+        cache.compact((0,), num_computed_tokens=1, num_query_tokens=2, num_reserved_query_tokens=2,
+                      retained_query_indices=(1,))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_block_copy_matches_closed_form(dtype) -> None:
+    _announce(f"block copy {dtype}")
+    rng = np.random.default_rng(5)
+    nb, layers = 200, 4
+    cache = _cache(hkv=2, d=128, bs=16, nb=nb, dtype=dtype, layers=layers, hq=12)
+    perm = [int(x) for x in rng.permutation(nb)]
+    src, dst = perm[:32], perm[32:64]
+    pools = [(_bits(cache.layer(f"l{i}").keys), _bits(cache.layer(f"l{i}").values)) for i in range(layers)]
+    O.block_copy(pools, src, dst)
+    cache.copy_blocks(src, dst)
+    torch.cuda.synchronize()
+    for i, (kb, vb) in enumerate(pools):
+        np.testing.assert_array_equal(_bits(cache.layer(f"l{i}").keys), kb)
+        np.testing.assert_array_equal(_bits(cache.layer(f"l{i}").values), vb)
+
+
+def test_block_copy_rejects_overlap_and_duplicates() -> None:
+    cache = _cache(hkv=2, d=64, bs=4, nb=8, dtype=torch.float32)
+    with pytest.raises(lv.KVCacheError, match="disjoint"):
+        cache.copy_blocks([1, 2], [2, 3])
+    with pytest.raises(lv.KVCacheError, match="twice"):
+        cache.copy_blocks([1, 2], [4, 4])
+    with pytest.raises(lv.KVCacheError, match="invalid physical block"):
+        cache.copy_blocks([1], [8])

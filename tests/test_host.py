@@ -1,0 +1,225 @@
+"""CPU tests of the host side: the restated metadata/layout/validation against
+the reference's known answers and the oracle, the step planner's device
+metadata, and the C-ABI library's exports (loaded, no kernel launched)."""
+
+from __future__ import annotations
+
+import ctypes
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import light_vllm_amd as lv
+from light_vllm_amd import native
+from light_vllm_amd.plan import StepPlan
+from oracle import paged_kv_oracle as O
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())
+CPU = torch.device("cpu")
+
+
+def _layouts(*lengths):
+    return tuple(lv.linear_query_layout(n) for n in lengths)
+
+
+def _metadata(case):
+    n = len(case["block_tables"])
+    return lv.PagedAttentionMetadata(
+        block_tables=tuple(tuple(t) for t in case["block_tables"]),
+        num_computed_tokens=tuple(case["num_computed_tokens"]),
+        query_layouts=_layouts(*case["query_lengths"]),
+        num_reserved_query_tokens=tuple(case.get("reserved", case["query_lengths"])),
+        num_readonly_prefix_blocks=tuple(case.get("readonly", [0] * n)),
+    )
+
+
+@pytest.mark.parametrize("case", GOLDEN["slot_mapping"], ids=lambda c: c["source"][:40])
+def test_metadata_slot_mapping_known_answers(case) -> None:
+    assert _metadata(case).slot_mapping(block_size=case["block_size"], device=CPU).tolist() == case["expected"]
+
+
+@pytest.mark.parametrize("case", GOLDEN["validation_errors"], ids=lambda c: c["source"][-30:])
+def test_metadata_validation_known_errors(case) -> None:
+    with pytest.raises(lv.KVCacheError, match=case["match"]):
+        _metadata(case).validate_block_tables(num_blocks=case["num_blocks"], block_size=case["block_size"])
+
+
+def test_metadata_visibility_and_request_indices_known_answer() -> None:
+    c = GOLDEN["visibility_packing"]
+    md = lv.PagedAttentionMetadata(
+        block_tables=tuple(tuple(t) for t in c["block_tables"]),
+        num_computed_tokens=tuple(c["num_computed_tokens"]),
+        query_layouts=tuple(lv.QueryLayout(tuple(p)) for p in c["layouts"]),
+    )
+    vis, starts = md.visibility_tensor(device=CPU)
+    assert vis.tolist() == c["visibility"]
+    assert starts.tolist() == c["visibility_start"]
+    assert md.query_start_loc == tuple(c["query_start_loc"])
+    assert md.request_indices_tensor(device=CPU).tolist() == c["request_indices"]
+    assert not md.has_only_linear_queries
+
+
+def test_layout_known_answers() -> None:
+    c = GOLDEN["query_layout"]
+    layout = lv.QueryLayout(tuple(c["parents"]))
+    assert list(lv.semantic_positions(layout, prefix_length=c["prefix_length"])) == c["positions"]
+    assert [list(r) for r in lv.query_visibility(layout)] == c["visibility"]
+    d = c["append_draft"]
+    draft = lv.DraftTree((7, 9, 8), tuple(d["draft_parents"]))
+    assert list(lv.append_draft_layout(d["num_inputs"], draft).parent_indices) == d["expected"]
+    with pytest.raises(ValueError, match="precede"):
+        lv.DraftTree((4, 5), (-1, 1))
+    with pytest.raises(ValueError, match="siblings"):
+        lv.DraftTree((4, 4), (-1, -1))
+
+
+def test_visible_logical_positions_known_answer() -> None:
+    c = GOLDEN["visible_positions"]
+    md = lv.PagedAttentionMetadata(
+        block_tables=((2, 0),), num_computed_tokens=(c["num_computed_tokens"],),
+        query_layouts=(lv.QueryLayout(tuple(c["parents"])),),
+    )
+    assert [list(p) for p in md.visible_logical_positions(0)] == c["expected"]
+
+
+def _random_metadata(rng, *, batch, bs, tree=False):
+    computed = [int(x) for x in rng.integers(0, 60, size=batch)]
+    layouts = []
+    for _ in range(batch):
+        q = int(rng.integers(1, 40))
+        if tree:
+            parents = tuple([-1] + [int(rng.integers(0, i)) for i in range(1, q)])
+        else:
+            parents = tuple(range(-1, q - 1))
+        layouts.append(lv.QueryLayout(parents))
+    reserved = [len(l) + int(rng.integers(0, 3)) for l in layouts]
+    need = [(c + r + bs - 1) // bs for c, r in zip(computed, reserved)]
+    perm = [int(x) for x in rng.permutation(sum(need) + 5)]
+    tables, off = [], 0
+    for n in need:
+        tables.append(tuple(perm[off : off + n]))
+        off += n
+    return lv.PagedAttentionMetadata(
+        block_tables=tuple(tables), num_computed_tokens=tuple(computed), query_layouts=tuple(layouts),
+        num_reserved_query_tokens=tuple(reserved),
+    )
+
+
+@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("bs", (1, 3, 16))
+def test_plan_slots_match_oracle_slot_mapping(seed, bs) -> None:
+    rng = np.random.default_rng(seed)
+    md = _random_metadata(rng, batch=7, bs=bs, tree=seed % 2 == 1)
+    plan = StepPlan(md, block_size=bs, device=CPU)
+    expect = O.slot_mapping(md.block_tables, md.num_computed_tokens, md.query_lengths,
+                            md.num_reserved_query_tokens, bs)
+    assert plan.slots.tolist() == expect.tolist()
+    assert plan.slots.tolist() == md.slot_mapping(block_size=bs, device=CPU).tolist()
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_plan_visibility_bits_match_oracle(seed) -> None:
+    rng = np.random.default_rng(100 + seed)
+    md = _random_metadata(rng, batch=5, bs=4, tree=True)
+    plan = StepPlan(md, block_size=4, device=CPU)
+    meta = plan.req_meta.view(-1, native.REQ_FIELDS).numpy()
+    words = plan.vis.numpy().view(np.uint32)
+    for r, layout in enumerate(md.query_layouts):
+        vis = O.query_visibility(layout.parent_indices)
+        if O.is_linear(layout.parent_indices):
+            assert meta[r, 5] == -1
+            continue
+        off, w = meta[r, 5], meta[r, 6]
+        q = len(layout)
+        for i in range(q):
+            for j in range(q):
+                bit = (int(words[off + i * w + j // 32]) >> (j % 32)) & 1
+                assert bit == int(vis[i, j])
+
+
+def test_plan_request_table_and_work_units_cover_every_query_once() -> None:
+    rng = np.random.default_rng(9)
+    md = _random_metadata(rng, batch=9, bs=16)
+    plan = StepPlan(md, block_size=16, device=CPU, use_prefill=False)
+    meta = plan.req_meta.view(-1, native.REQ_FIELDS).numpy()
+    assert meta[:, 2].tolist() == list(md.num_computed_tokens)
+    assert meta[:, 3].tolist() == list(md.query_lengths)
+    assert meta[:, 4].tolist() == list(md.query_start_loc[:-1])
+    flat = plan.tables.numpy()
+    for r, table in enumerate(md.block_tables):
+        assert flat[meta[r, 0] : meta[r, 0] + meta[r, 1]].tolist() == list(table)
+    group = 7
+    work = plan.work(group, 4)
+    units = work.units.numpy()
+    pt = work.partition_tokens
+    covered = {}
+    for req, part, ctile, pslot in units:
+        seq = md.num_computed_tokens[req] + md.query_lengths[req]
+        assert 0 <= part * pt < seq
+        assert 0 <= ctile * 16 < md.query_lengths[req] * group
+        covered.setdefault((req, ctile), []).append(part)
+    for r in range(md.batch_size):
+        seq = md.num_computed_tokens[r] + md.query_lengths[r]
+        nparts = -(-seq // pt)
+        for ct in range(-(-(md.query_lengths[r] * group) // 16)):
+            assert sorted(covered[(r, ct)]) == list(range(nparts))
+    # partial slots are dense and each merge job owns a consecutive run
+    slots = sorted(int(s) for s in units[:, 3] if s >= 0)
+    assert slots == list(range(work.num_partial_slots))
+    for req, ctile, ps0, np_ in (work.jobs.numpy() if work.num_jobs else []):
+        run = [int(u[3]) for u in units if u[0] == req and u[2] == ctile]
+        assert sorted(run) == list(range(ps0, ps0 + np_))
+
+
+def test_prefill_units_tile_every_long_request() -> None:
+    rng = np.random.default_rng(12)
+    md = _random_metadata(rng, batch=6, bs=16)
+    plan = StepPlan(md, block_size=16, device=CPU, use_prefill=True)
+    work = plan.work(7, 4)
+    seen = {}
+    if work.num_prefill_units:
+        for req, q0, nq, _ in work.prefill_units.numpy():
+            seen.setdefault(int(req), []).extend(range(q0, q0 + nq))
+    for r, q in enumerate(md.query_lengths):
+        if q > 16:
+            assert sorted(seen[r]) == list(range(q))
+        else:
+            assert r not in seen
+
+
+def test_library_loads_and_exports_every_header_function() -> None:
+    lib = native.load()
+    declared = native.header_functions()
+    assert declared, "no functions parsed from the header"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+        assert name in native.SIGNATURES, f"{name} has no ctypes signature"
+    assert lib.lvamd_abi_version() == native.ABI_VERSION
+    assert lib.lvamd_status_string(-3).decode() == "workspace too small"
+    assert lib.lvamd_kv_compact_inline_pairs() == 16
+    assert lib.lvamd_kv_compact_workspace_size(17, 28, 1024) == 17 * 28 * 2 * 1024
+    # Argument checks run before any HIP call, so they are safe without a GPU.
+    assert lib.lvamd_kv_append(None, 0, 0, None, 0, 0, None, None, None, 1, 2, 64, 2, None) == -1
+    assert lib.lvamd_paged_decode(None, 0, 0, None, None, None, 0, 0, None, None, None, None, 1,
+                                  None, None, 0, 4, 7, 72, 16, 256, ctypes.c_float(0.1), 2, None) == -2
+
+
+def test_backend_refuses_a_cpu_cache() -> None:
+    spec = lv.ModelKVCacheSpec((lv.AttentionLayerSpec("attention", 4, 2, 64),))
+    with pytest.raises(lv.KVCacheError, match="requires a GPU"):
+        lv.PagedKVCache(spec, lv.PagedKVCacheConfig(num_blocks=4, block_size=2))
+
+    class _CpuCache:
+        config = lv.PagedKVCacheConfig(num_blocks=4, block_size=2)
+
+    md = lv.PagedAttentionMetadata(block_tables=((0,),), num_computed_tokens=(0,), query_layouts=_layouts(1))
+    with pytest.raises(lv.KVCacheError, match="requires a GPU"):
+        lv.HipPagedAttentionBackend().create(_CpuCache(), md)
+
+
+def test_kv_cache_bytes_per_block() -> None:
+    spec = lv.ModelKVCacheSpec((lv.AttentionLayerSpec("attention", 2, 2, 4),))
+    assert lv.kv_cache_bytes_per_block(spec, block_size=2, dtype=torch.float32) == 128
