@@ -131,6 +131,43 @@ def cpu_baseline(metadata, cache, q, k, v, ctx, budget_s: float) -> dict:
     }
 
 
+def copy_calibration(args, device: torch.device) -> int:
+    """A plain device-to-device copy of 1 GiB: counter calibration and practical ceiling."""
+
+    nbytes = 1 << 30
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device=device) for _ in range(4)]
+    for b in bufs:
+        b.fill_(1)
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for i in range(args.warmup):
+        bufs[(2 * i + 1) % 4].copy_(bufs[(2 * i) % 4])
+    stream = torch.cuda.current_stream(device)
+    for i, (a, b) in enumerate(events):
+        a.record(stream)
+        bufs[(2 * i + 1) % 4].copy_(bufs[(2 * i) % 4])
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms = float(np.mean([a.elapsed_time(b) for a, b in events]))
+    gbs = 2 * nbytes / (ms * 1e-3) / 1e9
+    # Read-only ceiling: a float32 sum over 1 GiB (reduction writes ~nothing).
+    sums = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    views = [b.view(torch.float32) for b in bufs]
+    for i in range(args.warmup):
+        views[i % 4].sum()
+    for i, (a, b) in enumerate(sums):
+        a.record(stream)
+        views[i % 4].sum()
+        b.record(stream)
+    torch.cuda.synchronize()
+    read_ms = float(np.mean([a.elapsed_time(b) for a, b in sums]))
+    read_gbs = nbytes / (read_ms * 1e-3) / 1e9
+    print(json.dumps({"mode": "copy", "bytes_read": nbytes, "bytes_written": nbytes, "ms_per_copy": round(ms, 4),
+                      "read_plus_write_GBps": round(gbs, 1), "frac_of_8TBps": round(gbs / HBM_PEAK_GBS, 4),
+                      "read_only_ms": round(read_ms, 4), "read_only_GBps": round(read_gbs, 1)}),
+          flush=True)
+    return 0
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -139,8 +176,11 @@ def main() -> int:
     parser.add_argument("--sets", type=int, default=4, help="rotating pool sets (1 GiB each)")
     parser.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline work")
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--mode", choices=("full", "decode"), default="full",
-                        help="decode: only launch the decode kernel (for counter runs)")
+    parser.add_argument("--mode", choices=("full", "decode", "copy"), default="full",
+                        help="decode: only the decode kernel (counter runs); copy: a plain 1 GiB device "
+                             "copy of known size (counter calibration and the practical HBM ceiling)")
+    parser.add_argument("--partition", type=int, default=None,
+                        help="cap on the tokens one decode wave handles (default: spread over all resident waves)")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -150,10 +190,12 @@ def main() -> int:
         print("bench.py needs an MI355X GPU", file=sys.stderr)
         return 1
     device = torch.device("cuda:0")
+    if args.mode == "copy":
+        return copy_calibration(args, device)
     print(f"[bench] building C2 workload, {args.sets} pool sets", file=sys.stderr, flush=True)
     metadata, caches, q, k, v, ctx = build_workload(args.sets, device)
     nbytes = algorithmic_bytes(ctx)
-    backend = lv.HipPagedAttentionBackend()
+    backend = lv.HipPagedAttentionBackend(partition_tokens=args.partition)
     out = torch.empty_like(q)
 
     def step(i: int) -> torch.Tensor:
@@ -221,6 +263,8 @@ def main() -> int:
             "batch": C2.batch, "q_heads": C2.hq, "kv_heads": C2.hkv, "head_size": C2.d, "block_size": C2.bs,
             "pool_blocks": C2.num_blocks, "context": f"U[{C2.ctx_lo},{C2.ctx_hi}] seed {C2.seed}",
             "mean_context": float(ctx.mean()), "rotating_pool_sets": len(caches),
+            "decode_waves": launches[0].work.waves_per_head * C2.hkv if launches[0] else None,
+            "tiles_per_wave": launches[0].work.tiles_per_wave if launches[0] else None,
         },
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "tokens_per_s": round(C2.batch / (NUM_LAYERS * ms_per_step * 1e-3), 1),

@@ -39,8 +39,9 @@ enum lvamd_dtype { LVAMD_F32 = 0, LVAMD_F16 = 1, LVAMD_BF16 = 2 };
 /* Number of int32 fields per request in the attention metadata
  * (table_off, num_table_blocks, computed, q_len, q_start, vis_off, vis_words, 0). */
 #define LVAMD_REQ_FIELDS 8
-/* Number of int32 fields per split-K work unit (req, partition, column_tile, partial_slot). */
-#define LVAMD_UNIT_FIELDS 4
+/* Number of int32 fields per decode piece: (req, column_tile, token_begin, token_end,
+ * partial_slot, table_off, computed, q_len, q_start, vis_off, vis_words, 0, 0, 0, 0, 0). */
+#define LVAMD_PIECE_FIELDS 16
 /* Number of int32 fields per merge job (req, column_tile, first_partial_slot, num_partitions). */
 #define LVAMD_MERGE_FIELDS 4
 /* Number of int32 fields per prefill work unit (req, first query of the block, num queries, 0). */
@@ -73,19 +74,19 @@ int lvamd_kv_append(const void* key, int64_t key_token_stride, int64_t key_head_
 
 /*
  * Split-K paged attention for short query runs (decode, speculative tree
- * verification): one wave per (work unit, kv head, ...), bf16/fp16 QK^T and
- * PV on MFMA 16x16x32 (fp32 on MFMA 16x16x4), fp32 online softmax, partial
- * (m, l, acc) per partition merged by lvamd_paged_attention_merge.
- *
- * q:   [T, num_kv_heads*group, head_size] (token/head strides in elements)
- * out: same shape, written for every query token that a unit covers.
- * req_meta [num_requests][LVAMD_REQ_FIELDS], tables (flat int32 block ids),
- * vis (uint32 ancestor bit rows, only for requests with vis_off >= 0),
- * units [num_units][LVAMD_UNIT_FIELDS].  A unit whose partial_slot is -1
- * covers the whole sequence and writes out directly; otherwise it writes
- * its partial to part_acc [slots][num_kv_heads][16][head_size] and part_ml
- * [slots][num_kv_heads][16][2] (fp32).
- * scale is the caller's softmax scale (1/sqrt(head_size) for Qwen2).
+ * verification), stream-K scheduled: the decode rows' (request, column tile)
+ * segments are laid end to end in 32-token tiles and cut into waves_per_head
+ * equal contiguous shares; wave w of kv head h (workgroup h * waves_per_head
+ * + w, one wave64 each) processes pieces [wave_first[w], wave_first[w + 1]).
+ * A piece with partial_slot -1 covers its whole segment and writes out
+ * directly; others write (max, sum, acc) partials to part_acc
+ * [slots][num_kv_heads][16][head_size] and part_ml [slots][num_kv_heads][16][2]
+ * (fp32), combined by lvamd_paged_attention_merge.  MFMA columns are
+ * (query, head-in-group) pairs of one kv head, 16 per column tile.
+ * bf16/fp16 QK^T and PV on MFMA 16x16x32 (fp32 on 16x16x4), fp32 online
+ * softmax; K/V gathered through the block table (tables: flat int32 block
+ * ids), V staged by LDS DMA; vis holds uint32 ancestor bit rows for requests
+ * with vis_off >= 0.  scale is the caller's softmax scale.
  *
  * Together with lvamd_paged_attention_merge and lvamd_paged_prefill this
  * replaces TorchPagedAttention.forward/_attend_query_token
@@ -96,12 +97,15 @@ int lvamd_kv_append(const void* key, int64_t key_token_stride, int64_t key_head_
 int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_stride,
                        const void* key_pool, const void* value_pool,
                        void* out, int64_t out_token_stride, int64_t out_head_stride,
-                       const int32_t* req_meta, const int32_t* tables, const uint32_t* vis,
-                       const int32_t* units, int32_t num_units,
+                       const int32_t* pieces, const int32_t* wave_first, int32_t waves_per_head,
+                       const int32_t* tables, const uint32_t* vis,
                        float* part_acc, float* part_ml, int64_t num_partial_slots,
                        int32_t num_kv_heads, int32_t group, int32_t head_size,
-                       int32_t block_size, int32_t partition_tokens, float scale,
-                       int32_t dtype, lvamd_stream_t stream);
+                       int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream);
+
+/* How many decode waves (workgroups) the current device holds at once for this
+ * dtype and head size: the planner's stream-K width.  Needs a GPU. */
+int lvamd_paged_decode_resident_waves(int32_t dtype, int32_t head_size);
 
 /*
  * Log-sum-exp merge of split-K partials into out, one job per

@@ -121,12 +121,12 @@ class HipPagedAttention:
         self.prefill(layer_id, query, out, scale=scale)
 
     def decode_launch(self, layer_id: str, query: Tensor, out: Tensor, *, scale: float) -> "_DecodeLaunch | None":
-        """Bound split-K decode + merge launches for this layer, or None if no decode rows."""
+        """Bound stream-K decode + merge launches for this layer, or None if no decode rows."""
 
         spec = self._cache.layer_spec(layer_id)
         group = spec.num_query_heads // spec.num_kv_heads
-        work = self._plan.work(group, spec.num_kv_heads)
-        if not work.num_units:
+        work = self._work(spec, query.dtype)
+        if not work.waves_per_head:
             return None
         part_acc = part_ml = None
         if work.num_partial_slots:
@@ -137,10 +137,15 @@ class HipPagedAttention:
         return _DecodeLaunch(self._lib, self._cache, self._plan, work, spec, group, self._cache.layer(layer_id),
                              query, out, float(scale), part_acc, part_ml)
 
+    def _work(self, spec, dtype):
+        group = spec.num_query_heads // spec.num_kv_heads
+        resident = native.resident_decode_waves(dtype_code(dtype), spec.head_size)
+        return self._plan.work(group, spec.num_kv_heads, resident)
+
     def prefill(self, layer_id: str, query: Tensor, out: Tensor, *, scale: float) -> None:
         spec = self._cache.layer_spec(layer_id)
         group = spec.num_query_heads // spec.num_kv_heads
-        work = self._plan.work(group, spec.num_kv_heads)
+        work = self._work(spec, query.dtype)
         if not work.num_prefill_units:
             return
         layer = self._cache.layer(layer_id)
@@ -169,11 +174,11 @@ class _DecodeLaunch:
             query.data_ptr(), query.stride(0), query.stride(1),
             layer.keys.data_ptr(), layer.values.data_ptr(),
             out.data_ptr(), out.stride(0), out.stride(1),
-            plan.req_meta.data_ptr(), plan.tables.data_ptr(), plan.vis.data_ptr(),
-            work.units.data_ptr(), work.num_units,
+            work.pieces.data_ptr(), work.wave_first.data_ptr(), work.waves_per_head,
+            plan.tables.data_ptr(), plan.vis.data_ptr(),
             part_acc, part_ml, work.num_partial_slots,
             spec.num_kv_heads, group, spec.head_size,
-            cache.config.block_size, work.partition_tokens, scale, dt, stream,
+            cache.config.block_size, scale, dt, stream,
         )
         self._merge_args = None
         if work.num_jobs:
@@ -203,10 +208,16 @@ class HipPagedAttentionBackend:
     the validated, staged plan.
     """
 
-    def __init__(self, *, use_prefill_kernel: bool = False) -> None:
+    def __init__(self, *, use_prefill_kernel: bool = False, partition_tokens: int | None = None) -> None:
+        """``partition_tokens`` caps the tokens one decode wave handles (a tuning
+        knob; by default the planner spreads the work over every resident wave)."""
+
         native.load()
+        if partition_tokens is not None and (partition_tokens <= 0 or partition_tokens % 32):
+            raise ValueError("partition_tokens must be a positive multiple of 32")
         self._workspace = _Workspace()
         self._use_prefill = use_prefill_kernel
+        self._partition_tokens = partition_tokens
         self._last: tuple[object, object, StepPlan] | None = None
 
     def create(self, cache, metadata) -> HipPagedAttention:
@@ -220,6 +231,6 @@ class HipPagedAttentionBackend:
                 raise KVCacheError("HIP paged attention requires a GPU KV cache")
             metadata.validate_block_tables(num_blocks=config.num_blocks, block_size=config.block_size)
             plan = StepPlan(metadata, block_size=config.block_size, device=config.device,
-                            use_prefill=self._use_prefill)
+                            use_prefill=self._use_prefill, partition_tokens=self._partition_tokens)
             self._last = (key, metadata, plan)
         return HipPagedAttention(cache, metadata, self._workspace, plan)

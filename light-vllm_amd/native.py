@@ -15,14 +15,14 @@ from pathlib import Path
 from light_vllm_amd.errors import ExecutionError, ExecutionNotReadyError
 
 LIB_NAME = "liblvamd_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 REQ_FIELDS = 8
-UNIT_FIELDS = 4
+PIECE_FIELDS = 16
 MERGE_FIELDS = 4
 PREFILL_FIELDS = 4
 
@@ -41,9 +41,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "lvamd_paged_decode": (
         ctypes.c_int,
-        [_p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i32, _p, _p, _i64,
-         _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p],
+        [_p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _i32, _p, _p, _p, _p, _i64,
+         _i32, _i32, _i32, _i32, _f32, _i32, _p],
     ),
+    "lvamd_paged_decode_resident_waves": (ctypes.c_int, [_i32, _i32]),
     "lvamd_paged_attention_merge": (
         ctypes.c_int,
         [_p, _p, _p, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p],
@@ -94,6 +95,21 @@ def load() -> ctypes.CDLL:
     if version != ABI_VERSION:
         raise ExecutionNotReadyError(f"{path} has ABI version {version}, expected {ABI_VERSION}")
     return lib
+
+
+_RESIDENT: dict[tuple[int, int], int] = {}
+
+
+def resident_decode_waves(dtype_code: int, head_size: int) -> int:
+    """Decode waves the current GPU holds at once (cached per dtype and head size)."""
+
+    key = (dtype_code, head_size)
+    found = _RESIDENT.get(key)
+    if found is None:
+        found = load().lvamd_paged_decode_resident_waves(dtype_code, head_size)
+        check(min(found, 0), "lvamd_paged_decode_resident_waves")
+        _RESIDENT[key] = found
+    return found
 
 
 def check(status: int, what: str) -> None:

@@ -15,8 +15,8 @@ the same facts in a ragged layout the gfx950 kernels read directly:
 * ``vis``      uint32 ancestor bitmask rows for non-linear (tree) requests,
   bit j of row q set iff query q sees query j (``visibility_tensor``,
   paged_attention.py:174-186, packed 32 to a word);
-* per (group size, kv heads): split-K work units and merge jobs for requests
-  on the decode path, and query blocks for requests on the prefill path.
+* per (group size, kv heads): the stream-K split of the decode rows (pieces,
+  each wave's first piece, merge jobs) and query blocks for the prefill rows.
 
 All int32 facts of a step share one pinned buffer and one non-blocking H2D
 copy on the current stream; the work lists of each group size add one more.
@@ -40,8 +40,79 @@ DECODE_MAX_QUERIES = 16
 PREFILL_QUERY_BLOCK = 64
 # Compute units of an MI355X; the planner aims for several waves per CU.
 NUM_CUS = 256
+# Block-table entries a decode partition may span (the kernel's LDS slice).
+TABLE_SLICE = 256
+
+
+PIECE_FIELDS = 16
+TILE_TOKENS = 32
 
 _BIT_WEIGHTS = (np.uint64(1) << np.arange(32, dtype=np.uint64)).astype(np.uint64)
+
+
+def stream_k_pieces(
+    *,
+    seq: np.ndarray,
+    nct: np.ndarray,
+    rows: np.ndarray,
+    req_meta: np.ndarray,
+    num_kv_heads: int,
+    resident_waves: int,
+    block_size: int,
+    min_tiles_per_wave: int = 4,
+    max_tiles_per_wave: int | None = None,
+):
+    """Split the decode work evenly over the waves the GPU holds at once.
+
+    A segment is one (request, column tile); it has ceil(seq / 32) tiles of 32
+    tokens.  The segments of all decode rows are laid end to end and the
+    flattened tile range is cut into ``waves_per_head`` equal, contiguous
+    shares (the same cut for every kv head).  A wave's share is a list of
+    pieces: the part of each segment it covers.  A piece that covers a whole
+    segment writes the output directly; otherwise it writes a partial
+    (max, sum, acc) to its slot and a merge job combines the segment's
+    partials.  Returns (pieces [n, 16] int64, wave_first [W + 1], W, jobs
+    [m, 4], num_slots).
+    """
+
+    seg_req = np.repeat(np.flatnonzero(rows), nct[rows])
+    seg_ctile = np.concatenate([np.arange(n) for n in nct[rows]]) if rows.any() else np.zeros(0, np.int64)
+    seg_tiles = -(-seq[seg_req] // TILE_TOKENS)
+    total = int(seg_tiles.sum())
+    seg_start = np.zeros(len(seg_req) + 1, dtype=np.int64)
+    np.cumsum(seg_tiles, out=seg_start[1:])
+    # The block-table slice of a piece must fit the kernel's LDS copy.
+    cap = max(1, ((TABLE_SLICE - 2) * block_size) // TILE_TOKENS)
+    if max_tiles_per_wave is not None:
+        cap = max(1, min(cap, max_tiles_per_wave))
+    waves = max(1, min(max(1, resident_waves // num_kv_heads), -(-total // min_tiles_per_wave)))
+    waves = max(waves, -(-total // cap))
+    per_wave = -(-total // waves)  # equal shares; never above cap
+    waves = -(-total // per_wave)
+    cuts = np.unique(np.concatenate((seg_start, np.arange(0, total, per_wave), [total])))
+    lo, hi = cuts[:-1], cuts[1:]
+    seg = np.searchsorted(seg_start, lo, side="right") - 1
+    wave = lo // per_wave
+    npieces = np.bincount(seg, minlength=len(seg_req))
+    multi = npieces[seg] > 1
+    slot = np.where(multi, np.cumsum(multi) - 1, -1)
+    req = seg_req[seg]
+    pieces = np.zeros((len(lo), PIECE_FIELDS), dtype=np.int64)
+    pieces[:, 0] = req
+    pieces[:, 1] = seg_ctile[seg]
+    pieces[:, 2] = (lo - seg_start[seg]) * TILE_TOKENS
+    pieces[:, 3] = np.minimum((hi - seg_start[seg]) * TILE_TOKENS, seq[req])
+    pieces[:, 4] = slot
+    pieces[:, 5] = req_meta[req, 0]  # table_off
+    pieces[:, 6] = req_meta[req, 2]  # computed
+    pieces[:, 7] = req_meta[req, 3]  # q_len
+    pieces[:, 8] = req_meta[req, 4]  # q_start
+    pieces[:, 9] = req_meta[req, 5]  # vis_off
+    pieces[:, 10] = req_meta[req, 6]  # vis_words
+    wave_first = np.searchsorted(wave, np.arange(waves + 1), side="left")
+    first = multi & (lo == seg_start[seg])
+    jobs = np.stack([req[first], seg_ctile[seg[first]], slot[first], npieces[seg[first]]], axis=1)
+    return pieces, wave_first, waves, per_wave, jobs, int(multi.sum())
 
 
 def _stage_int32(array: np.ndarray, device: torch.device) -> Tensor:
@@ -55,12 +126,13 @@ def _stage_int32(array: np.ndarray, device: torch.device) -> Tensor:
 
 @dataclass(frozen=True, slots=True)
 class DecodeWork:
-    units: Tensor | None  # int32 [n_units, 4]
-    num_units: int
+    pieces: Tensor | None  # int32 [n_pieces, 16]
+    wave_first: Tensor | None  # int32 [waves_per_head + 1]
+    waves_per_head: int
     jobs: Tensor | None  # int32 [n_jobs, 4]
     num_jobs: int
     num_partial_slots: int
-    partition_tokens: int
+    tiles_per_wave: int
     prefill_units: Tensor | None  # int32 [n_prefill_units, 4]
     num_prefill_units: int
 
@@ -68,7 +140,15 @@ class DecodeWork:
 class StepPlan:
     """Device-resident metadata of one model step (valid for all of its layers)."""
 
-    def __init__(self, metadata, *, block_size: int, device: torch.device, use_prefill: bool = True) -> None:
+    def __init__(
+        self,
+        metadata,
+        *,
+        block_size: int,
+        device: torch.device,
+        use_prefill: bool = True,
+        partition_tokens: int | None = None,
+    ) -> None:
         self.block_size = block_size
         self.device = device
         layouts = tuple(metadata.query_layouts)
@@ -138,31 +218,29 @@ class StepPlan:
         self.batch_size = batch
         self.has_tree = bool(vis_parts)
         self.use_prefill = use_prefill
+        self.partition_tokens = partition_tokens
 
         self._computed = computed
         self._q_lens = q_lens
+        self._req_meta = req_meta
         self._work: dict[tuple[int, int], DecodeWork] = {}
 
     # -- work lists ---------------------------------------------------------
-    def work(self, group: int, num_kv_heads: int) -> DecodeWork:
-        key = (group, num_kv_heads)
+    def work(self, group: int, num_kv_heads: int, resident_waves: int = 8 * NUM_CUS) -> DecodeWork:
+        """Work lists for layers of this (group, kv heads) shape.
+
+        ``resident_waves`` is how many decode waves the GPU holds at once (the
+        library reports it per dtype and head size).
+        """
+
+        key = (group, num_kv_heads, resident_waves)
         found = self._work.get(key)
         if found is None:
-            found = self._build_work(group, num_kv_heads)
+            found = self._build_work(group, num_kv_heads, resident_waves)
             self._work[key] = found
         return found
 
-    def _choose_partition(self, seq: np.ndarray, decode_rows: np.ndarray, nct: np.ndarray, num_kv_heads: int) -> int:
-        """Partition length (tokens): long enough to amortise the merge, short
-        enough that the decode grid fills every CU several times."""
-
-        for tokens in (512, 256, 128, 64, 32):
-            waves = int((np.ceil(seq[decode_rows] / tokens) * nct[decode_rows]).sum()) * num_kv_heads
-            if waves >= 8 * NUM_CUS:
-                return tokens
-        return 32
-
-    def _build_work(self, group: int, num_kv_heads: int) -> DecodeWork:
+    def _build_work(self, group: int, num_kv_heads: int, resident_waves: int) -> DecodeWork:
         computed, q_lens = self._computed, self._q_lens
         batch = self.batch_size
         seq = computed + q_lens
@@ -171,32 +249,22 @@ class StepPlan:
         else:
             decode_rows = np.ones(batch, dtype=bool)
         nct = -(-(q_lens * group) // 16)
-        units = jobs = prefill_units = None
-        num_units = num_jobs = num_partial = num_prefill = 0
-        part_tokens = 256
+        pieces = wave_first = jobs = prefill_units = None
+        waves = num_jobs = num_partial = num_prefill = per_wave = 0
+        blocks = []
         if decode_rows.any():
-            part_tokens = self._choose_partition(seq, decode_rows, nct, num_kv_heads)
-            nparts = np.where(decode_rows, -(-seq // part_tokens), 0)
-            per_req = nparts * np.where(decode_rows, nct, 0)
-            num_units = int(per_req.sum())
-            req = np.repeat(np.arange(batch), per_req)
-            starts = np.zeros(batch, dtype=np.int64)
-            np.cumsum(per_req[:-1], out=starts[1:])
-            local = np.arange(num_units) - starts[req]
-            part = local % nparts[req]
-            ctile = local // nparts[req]
-            multi = nparts[req] > 1
-            pslot = np.where(multi, np.cumsum(multi) - 1, -1)
-            num_partial = int(multi.sum())
-            table = np.stack([req, part, ctile, pslot], axis=1)
-            first = multi & (part == 0)
-            job_tab = np.stack([req[first], ctile[first], pslot[first], nparts[req[first]]], axis=1)
+            max_tiles = None
+            if self.partition_tokens:
+                max_tiles = max(1, self.partition_tokens // TILE_TOKENS)
+            piece_tab, first_tab, waves, per_wave, job_tab, num_partial = stream_k_pieces(
+                seq=seq, nct=nct, rows=decode_rows, req_meta=self._req_meta, num_kv_heads=num_kv_heads,
+                resident_waves=resident_waves, block_size=self.block_size, max_tiles_per_wave=max_tiles,
+            )
+            num_pieces = int(piece_tab.shape[0])
             num_jobs = int(job_tab.shape[0])
-            blocks = [table.reshape(-1)]
+            blocks += [piece_tab.reshape(-1), first_tab.reshape(-1)]
             if num_jobs:
                 blocks.append(job_tab.reshape(-1))
-        else:
-            blocks = []
         prefill_rows = ~decode_rows
         if prefill_rows.any():
             nblk = np.where(prefill_rows, -(-q_lens // PREFILL_QUERY_BLOCK), 0)
@@ -216,12 +284,14 @@ class StepPlan:
         else:
             blob = None
         off = 0
-        if num_units:
-            units = blob[off : off + 4 * num_units].view(num_units, 4)
-            off += 4 * num_units
+        if waves:
+            pieces = blob[off : off + PIECE_FIELDS * num_pieces].view(num_pieces, PIECE_FIELDS)
+            off += PIECE_FIELDS * num_pieces
+            wave_first = blob[off : off + waves + 1]
+            off += waves + 1
         if num_jobs:
             jobs = blob[off : off + 4 * num_jobs].view(num_jobs, 4)
             off += 4 * num_jobs
         if num_prefill:
             prefill_units = blob[off : off + 4 * num_prefill].view(num_prefill, 4)
-        return DecodeWork(units, num_units, jobs, num_jobs, num_partial, part_tokens, prefill_units, num_prefill)
+        return DecodeWork(pieces, wave_first, waves, jobs, num_jobs, num_partial, per_wave, prefill_units, num_prefill)

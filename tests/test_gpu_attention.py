@@ -205,3 +205,14 @@ def test_shape_and_dtype_validation() -> None:
     ctx = lv.HipPagedAttentionBackend().create(step.cache, step.metadata)
     with pytest.raises(lv.KVCacheError, match="dtype and device must match"):
         ctx.forward("layer0", step.query.float(), step.key, step.value, scale=step.scale)
+
+
+@pytest.mark.parametrize("partition", (32, 512, 2048))
+@pytest.mark.parametrize("bs", (1, 16))
+def test_partition_sizes_including_global_table_fallback(partition, bs) -> None:
+    # bs=1 with 512/2048-token partitions needs more table entries than the LDS
+    # slice holds, so the kernel reads the table from global memory.
+    _announce(f"partition {partition} bs {bs}")
+    step = make_step(hq=28, hkv=4, d=128, bs=bs, dtype=torch.bfloat16, computed=[1200, 37, 2600],
+                     layouts=_lin(1, 2, 1), seed=partition + bs)
+    _run_and_check(step, backend=lv.HipPagedAttentionBackend(partition_tokens=partition))

@@ -140,7 +140,7 @@ def test_plan_visibility_bits_match_oracle(seed) -> None:
                 assert bit == int(vis[i, j])
 
 
-def test_plan_request_table_and_work_units_cover_every_query_once() -> None:
+def test_plan_request_table_matches_metadata() -> None:
     rng = np.random.default_rng(9)
     md = _random_metadata(rng, batch=9, bs=16)
     plan = StepPlan(md, block_size=16, device=CPU, use_prefill=False)
@@ -151,27 +151,54 @@ def test_plan_request_table_and_work_units_cover_every_query_once() -> None:
     flat = plan.tables.numpy()
     for r, table in enumerate(md.block_tables):
         assert flat[meta[r, 0] : meta[r, 0] + meta[r, 1]].tolist() == list(table)
-    group = 7
-    work = plan.work(group, 4)
-    units = work.units.numpy()
-    pt = work.partition_tokens
+
+
+@pytest.mark.parametrize("resident", (7, 64, 2048))
+@pytest.mark.parametrize("bs", (1, 16))
+@pytest.mark.parametrize("group", (1, 7))
+def test_stream_k_pieces_cover_every_segment_once(resident, bs, group) -> None:
+    rng = np.random.default_rng(resident + bs + group)
+    md = _random_metadata(rng, batch=11, bs=bs)
+    plan = StepPlan(md, block_size=bs, device=CPU, use_prefill=False)
+    work = plan.work(group, 4, resident)
+    pieces = work.pieces.numpy()
+    first = work.wave_first.numpy()
+    waves = work.waves_per_head
+    assert first[0] == 0 and first[-1] == len(pieces) and np.all(np.diff(first) >= 1)
+    cap = (254 * bs) // 32  # tiles whose block-table slice fits the kernel's LDS copy
+    assert work.tiles_per_wave <= max(cap, 1)
+    seqs = np.asarray(md.num_computed_tokens) + np.asarray(md.query_lengths)
+    nct = -(-(np.asarray(md.query_lengths) * group) // 16)
+    total_tiles = int((-(-seqs // 32) * nct).sum())
+    assert waves <= max(resident // 4, 1, -(-total_tiles // cap))
+    assert work.tiles_per_wave == -(-total_tiles // waves)
     covered = {}
-    for req, part, ctile, pslot in units:
-        seq = md.num_computed_tokens[req] + md.query_lengths[req]
-        assert 0 <= part * pt < seq
-        assert 0 <= ctile * 16 < md.query_lengths[req] * group
-        covered.setdefault((req, ctile), []).append(part)
-    for r in range(md.batch_size):
-        seq = md.num_computed_tokens[r] + md.query_lengths[r]
-        nparts = -(-seq // pt)
-        for ct in range(-(-(md.query_lengths[r] * group) // 16)):
-            assert sorted(covered[(r, ct)]) == list(range(nparts))
-    # partial slots are dense and each merge job owns a consecutive run
-    slots = sorted(int(s) for s in units[:, 3] if s >= 0)
-    assert slots == list(range(work.num_partial_slots))
-    for req, ctile, ps0, np_ in (work.jobs.numpy() if work.num_jobs else []):
-        run = [int(u[3]) for u in units if u[0] == req and u[2] == ctile]
-        assert sorted(run) == list(range(ps0, ps0 + np_))
+    for w in range(waves):
+        tiles = 0
+        for rec in pieces[first[w] : first[w + 1]]:
+            req, ctile, tb, te, slot = rec[:5]
+            assert 0 <= tb < te <= seqs[req] and tb % 32 == 0
+            assert rec[6] == md.num_computed_tokens[req] and rec[7] == md.query_lengths[req]
+            assert rec[8] == md.query_start_loc[req]
+            n_tab = (te - 1) // bs - tb // bs + 1
+            assert n_tab <= 254, "piece exceeds the kernel's LDS table slice"
+            covered.setdefault((req, ctile), []).append((tb, te, slot))
+            tiles += -(-(te - tb) // 32)
+        assert tiles <= work.tiles_per_wave
+    jobs = {(int(j[0]), int(j[1])): (int(j[2]), int(j[3])) for j in (work.jobs.numpy() if work.num_jobs else [])}
+    slots_seen = []
+    for r, q in enumerate(md.query_lengths):
+        for ct in range(-(-(q * group) // 16)):
+            spans = sorted(covered[(r, ct)])
+            assert spans[0][0] == 0 and spans[-1][1] == seqs[r]
+            assert all(a[1] == b[0] for a, b in zip(spans, spans[1:]))
+            if len(spans) == 1:
+                assert spans[0][2] == -1 and (r, ct) not in jobs
+            else:
+                s0, n = jobs[(r, ct)]
+                assert [sp[2] for sp in spans] == list(range(s0, s0 + n)) and n == len(spans)
+                slots_seen += list(range(s0, s0 + n))
+    assert sorted(slots_seen) == list(range(work.num_partial_slots))
 
 
 def test_prefill_units_tile_every_long_request() -> None:
@@ -203,8 +230,10 @@ def test_library_loads_and_exports_every_header_function() -> None:
     assert lib.lvamd_kv_compact_workspace_size(17, 28, 1024) == 17 * 28 * 2 * 1024
     # Argument checks run before any HIP call, so they are safe without a GPU.
     assert lib.lvamd_kv_append(None, 0, 0, None, 0, 0, None, None, None, 1, 2, 64, 2, None) == -1
-    assert lib.lvamd_paged_decode(None, 0, 0, None, None, None, 0, 0, None, None, None, None, 1,
-                                  None, None, 0, 4, 7, 72, 16, 256, ctypes.c_float(0.1), 2, None) == -2
+    assert lib.lvamd_paged_decode(None, 0, 0, None, None, None, 0, 0, None, None, 1, None, None,
+                                  None, None, 0, 4, 7, 72, 16, ctypes.c_float(0.1), 2, None) == -2
+    assert lib.lvamd_paged_decode(None, 0, 0, None, None, None, 0, 0, None, None, 1, None, None,
+                                  None, None, 0, 4, 7, 128, 16, ctypes.c_float(0.1), 2, None) == -1
 
 
 def test_backend_refuses_a_cpu_cache() -> None:
