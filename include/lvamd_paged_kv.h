@@ -30,7 +30,7 @@ enum lvamd_status {
   LVAMD_OK = 0,
   LVAMD_ERR_INVALID_ARGUMENT = -1,  /* null pointer, negative size, misaligned row  */
   LVAMD_ERR_UNSUPPORTED = -2,       /* dtype / head_size / group size not built     */
-  LVAMD_ERR_WORKSPACE = -3,         /* workspace smaller than the *_workspace_size  */
+  LVAMD_ERR_WORKSPACE = -3,         /* missing or undersized workspace              */
   LVAMD_ERR_LAUNCH = -4             /* hipLaunchKernel / hipGetLastError failed     */
 };
 
@@ -40,10 +40,12 @@ enum lvamd_dtype { LVAMD_F32 = 0, LVAMD_F16 = 1, LVAMD_BF16 = 2 };
  * (table_off, num_table_blocks, computed, q_len, q_start, vis_off, vis_words, 0). */
 #define LVAMD_REQ_FIELDS 8
 /* Number of int32 fields per decode piece: (req, column_tile, token_begin, token_end,
- * partial_slot, table_off, computed, q_len, q_start, vis_off, vis_words, 0, 0, 0, 0, 0). */
+ * partial_slot, table_off, computed, q_len, q_start, vis_off, vis_words, 0, 0, 0, 0, 0).
+ * A piece with partial_slot -1 covers its whole segment. */
 #define LVAMD_PIECE_FIELDS 16
-/* Number of int32 fields per merge job (req, column_tile, first_partial_slot, num_partitions). */
-#define LVAMD_MERGE_FIELDS 4
+/* Number of int32 fields per merge job:
+ * (req, column_tile, first_partial_slot, num_partials, q_start, q_len, 0, 0). */
+#define LVAMD_MERGE_FIELDS 8
 /* Number of int32 fields per prefill work unit (req, first query of the block, num queries, 0). */
 #define LVAMD_PREFILL_FIELDS 4
 
@@ -74,28 +76,42 @@ int lvamd_kv_append(const void* key, int64_t key_token_stride, int64_t key_head_
 
 /*
  * Split-K paged attention for short query runs (decode, speculative tree
- * verification), stream-K scheduled: the decode rows' (request, column tile)
- * segments are laid end to end in 32-token tiles and cut into waves_per_head
- * equal contiguous shares; wave w of kv head h (workgroup h * waves_per_head
- * + w, one wave64 each) processes pieces [wave_first[w], wave_first[w + 1]).
- * A piece with partial_slot -1 covers its whole segment and writes out
- * directly; others write (max, sum, acc) partials to part_acc
+ * verification), stream-K scheduled, with this step's KV append fused in.
+ *
+ * Work: the decode rows' (request, column tile) segments are laid end to end
+ * in 32-token units and cut into waves_per_head contiguous shares; wave w of
+ * kv head h (workgroup h * waves_per_head + w, one wave64 each) processes
+ * pieces [wave_first[w], wave_first[w + 1]) (LVAMD_PIECE_FIELDS int32 each).
+ * A piece with partial_slot -1 covers its whole segment and writes out; the
+ * others write fp32 (max, sum, acc) partials to part_acc
  * [slots][num_kv_heads][16][head_size] and part_ml [slots][num_kv_heads][16][2]
- * (fp32), combined by lvamd_paged_attention_merge.  MFMA columns are
- * (query, head-in-group) pairs of one kv head, 16 per column tile.
- * bf16/fp16 QK^T and PV on MFMA 16x16x32 (fp32 on 16x16x4), fp32 online
- * softmax; K/V gathered through the block table (tables: flat int32 block
- * ids), V staged by LDS DMA; vis holds uint32 ancestor bit rows for requests
- * with vis_off >= 0.  scale is the caller's softmax scale.
+ * for lvamd_paged_attention_merge.
+ *
+ * Append: when new_key / new_value are given ([tokens][num_kv_heads][D] with
+ * the given strides), keys and values at positions >= computed are read from
+ * them, and each such token's row is written to its pool slot (bit-exact copy;
+ * the slot comes from the block table, exactly PagedAttentionMetadata.slot_mapping).
+ * When they are NULL the pool must already hold this step's K/V.
+ *
+ * MFMA columns are (query, head-in-group) pairs of one kv head, 16 per column
+ * tile.  bf16/fp16 QK^T and PV on MFMA (fp32 on 16x16x4), fp32 online softmax;
+ * K/V gathered through the block table (tables: flat int32 block ids); vis
+ * holds uint32 ancestor bit rows for requests with vis_off >= 0.  scale is the
+ * caller's softmax scale.
  *
  * Together with lvamd_paged_attention_merge and lvamd_paged_prefill this
- * replaces TorchPagedAttention.forward/_attend_query_token
- *   (src/light_vllm/runtime/execution/paged_attention.py:268-380) and the Triton
- *   _grouped_paged_attention_kernel / _paged_attention_kernel
- *   (src/light_vllm/runtime/execution/triton_paged_attention.py:107-391, launch :519-559).
+ * replaces TorchPagedAttention.forward / _attend_query_token
+ * (src/light_vllm/runtime/execution/paged_attention.py:268-380), the
+ * write-before-attend of PagedKVCache.write_prepared (paged_cache.py:209-254,
+ * called at paged_attention.py:294-301) and the Triton _write_paged_kv_kernel /
+ * _grouped_paged_attention_kernel / _paged_attention_kernel
+ *   (src/light_vllm/runtime/execution/triton_paged_attention.py:31-104, 107-391,
+ *   launch :498-559).
  */
 int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_stride,
-                       const void* key_pool, const void* value_pool,
+                       const void* new_key, int64_t new_key_token_stride, int64_t new_key_head_stride,
+                       const void* new_value, int64_t new_value_token_stride, int64_t new_value_head_stride,
+                       void* key_pool, void* value_pool,
                        void* out, int64_t out_token_stride, int64_t out_head_stride,
                        const int32_t* pieces, const int32_t* wave_first, int32_t waves_per_head,
                        const int32_t* tables, const uint32_t* vis,
@@ -108,14 +124,14 @@ int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_str
 int lvamd_paged_decode_resident_waves(int32_t dtype, int32_t head_size);
 
 /*
- * Log-sum-exp merge of split-K partials into out, one job per
- * (request, column tile): jobs [num_jobs][LVAMD_MERGE_FIELDS].
- * Replaces the same reference functions as lvamd_paged_decode (the reference
- * has no split-K; this is the cross-partition half of that computation).
+ * Log-sum-exp merge of split-K partials into out, one wave per (job, kv head);
+ * jobs [num_jobs][LVAMD_MERGE_FIELDS].  Same reference functions as
+ * lvamd_paged_decode: the reference has no split-K, and this is the
+ * cross-partition half of that computation.
  */
 int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
                                 void* out, int64_t out_token_stride, int64_t out_head_stride,
-                                const int32_t* req_meta, const int32_t* jobs, int32_t num_jobs,
+                                const int32_t* jobs, int32_t num_jobs,
                                 int32_t num_kv_heads, int32_t group, int32_t head_size,
                                 int32_t dtype, lvamd_stream_t stream);
 

@@ -9,15 +9,13 @@ once per layer by the model (src/light_vllm/modeling/models/qwen2.py:417-423):
 1. validate shapes exactly as ``_validate_paged_attention_tensors``
    (paged_attention.py:226-247) plus the dtype/device rule of the Triton
    backend (triton_paged_attention.py:475-478);
-2. append this step's K/V into the pool (HIP ``lvamd_kv_append``), stream-
-   ordered before attention, so a query sees its own K/V;
-3. attend: split-K decode kernel for short query runs, MFMA prefill kernel for
-   long ones, merge kernel for split partials, all on the current stream with
-   no host synchronisation.
+2. attend with write-before-attend semantics: the stream-K decode kernel
+   reads this step's K/V from the inputs and appends them to their pool slots
+   itself, and a merge kernel combines its split partials; a step with
+   prefill rows appends first (HIP ``lvamd_kv_append``) and runs the MFMA
+   prefill kernel for them.  Everything is on the current stream with no host
+   synchronisation.
 
-The backend reads the cache and metadata only through light-vllm's public
-surface, so the reference's ``PagedKVCache`` and ``PagedAttentionMetadata``
-work unchanged.
 """
 
 from __future__ import annotations
@@ -65,6 +63,15 @@ class _Workspace:
         return self._buffer
 
 
+def _rows_aligned(t: Tensor) -> bool:
+    """Rows of 16-byte chunks: contiguous last dim, 16-byte aligned base and strides."""
+
+    es = t.element_size()
+    return t.stride(2) == 1 and t.data_ptr() % 16 == 0 and (t.stride(0) * es) % 16 == 0 and (
+        t.stride(1) * es
+    ) % 16 == 0
+
+
 class HipPagedAttention:
     """Per-step context: writes each layer's K/V, then runs paged attention."""
 
@@ -92,36 +99,44 @@ class HipPagedAttention:
         config = self._cache.config
         if query.device != config.device or query.dtype != config.dtype:
             raise KVCacheError("HIP paged attention query dtype and device must match the KV cache")
-        if key.dtype != config.dtype or value.dtype != config.dtype:
+        if key.dtype != config.dtype or value.dtype != config.dtype or key.device != config.device or (
+            value.device != config.device
+        ):
             raise KVCacheError("paged KV update dtype and device must match the cache")
         if spec.head_size not in SUPPORTED_HEAD_SIZES:
             raise KVCacheError(
                 f"HIP paged attention supports head sizes {SUPPORTED_HEAD_SIZES}, not {spec.head_size}"
             )
 
-        # 1. append (write before attend).
-        hip_append(self._cache, layer_id, key, value, self._plan.slots)
-
-        # 2. attend.
-        if query.stride(2) != 1 or (query.stride(0) * query.element_size()) % 16 or (
-            query.stride(1) * query.element_size()
-        ) % 16 or query.data_ptr() % 16:
+        if not _rows_aligned(query):
             query = query.contiguous()
         out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
-        self.attend(layer_id, query, out, scale=scale)
-        return out
-
-    def attend(self, layer_id: str, query: Tensor, out: Tensor, *, scale: float) -> None:
-        """Paged attention of ``query`` against the pool into ``out`` (no append)."""
-
-        launch = self.decode_launch(layer_id, query, out, scale=scale)
+        work = self._work(spec, query.dtype)
+        if work.num_prefill_units:
+            # Prefill rows read the pool, so the whole step is appended first.
+            hip_append(self._cache, layer_id, key, value, self._plan.slots)
+            launch = self.decode_launch(layer_id, query, out, scale=scale)
+        else:
+            if not _rows_aligned(key):
+                key = key.contiguous()
+            if not _rows_aligned(value):
+                value = value.contiguous()
+            launch = self.decode_launch(layer_id, query, out, scale=scale, key=key, value=value)
         if launch is not None:
             launch.decode()
             launch.merge()
         self.prefill(layer_id, query, out, scale=scale)
+        return out
 
-    def decode_launch(self, layer_id: str, query: Tensor, out: Tensor, *, scale: float) -> "_DecodeLaunch | None":
-        """Bound stream-K decode + merge launches for this layer, or None if no decode rows."""
+    def decode_launch(
+        self, layer_id: str, query: Tensor, out: Tensor, *, scale: float, key: Tensor | None = None,
+        value: Tensor | None = None,
+    ) -> "_DecodeLaunch | None":
+        """The bound decode and merge launches of this layer (None if it has no decode rows).
+
+        With ``key``/``value`` the launch also appends them (fused append);
+        without, the pool must already hold this step's K/V.
+        """
 
         spec = self._cache.layer_spec(layer_id)
         group = spec.num_query_heads // spec.num_kv_heads
@@ -135,7 +150,7 @@ class HipPagedAttention:
             part_acc = buf.data_ptr()
             part_ml = part_acc + work.num_partial_slots * per_slot * spec.head_size * 4
         return _DecodeLaunch(self._lib, self._cache, self._plan, work, spec, group, self._cache.layer(layer_id),
-                             query, out, float(scale), part_acc, part_ml)
+                             query, key, value, out, float(scale), part_acc, part_ml)
 
     def _work(self, spec, dtype):
         group = spec.num_query_heads // spec.num_kv_heads
@@ -165,13 +180,20 @@ class HipPagedAttention:
 class _DecodeLaunch:
     """The decode and merge kernel launches of one layer, with bound arguments."""
 
-    def __init__(self, lib, cache, plan, work, spec, group, layer, query, out, scale, part_acc, part_ml) -> None:
+    def __init__(self, lib, cache, plan, work, spec, group, layer, query, key, value, out, scale,
+                 part_acc, part_ml) -> None:
         self.work = work
         stream = current_stream(query.device)
         dt = dtype_code(query.dtype)
         self._lib = lib
+        if key is None:
+            new_k, new_v, ks, vs = None, None, (0, 0), (0, 0)
+        else:
+            new_k, new_v = key.data_ptr(), value.data_ptr()
+            ks, vs = (key.stride(0), key.stride(1)), (value.stride(0), value.stride(1))
         self._decode_args = (
             query.data_ptr(), query.stride(0), query.stride(1),
+            new_k, ks[0], ks[1], new_v, vs[0], vs[1],
             layer.keys.data_ptr(), layer.values.data_ptr(),
             out.data_ptr(), out.stride(0), out.stride(1),
             work.pieces.data_ptr(), work.wave_first.data_ptr(), work.waves_per_head,
@@ -183,9 +205,8 @@ class _DecodeLaunch:
         self._merge_args = None
         if work.num_jobs:
             self._merge_args = (
-                part_acc, part_ml,
-                out.data_ptr(), out.stride(0), out.stride(1),
-                plan.req_meta.data_ptr(), work.jobs.data_ptr(), work.num_jobs,
+                part_acc, part_ml, out.data_ptr(), out.stride(0), out.stride(1),
+                work.jobs.data_ptr(), work.num_jobs,
                 spec.num_kv_heads, group, spec.head_size, dt, stream,
             )
 

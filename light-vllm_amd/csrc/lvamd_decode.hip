@@ -1,5 +1,6 @@
 // Split-K paged attention for short query runs on gfx950 (decode and
-// speculative tree verification), plus the cross-partition merge.
+// speculative tree verification) with the step's KV append fused in, plus the
+// cross-partition merge.
 //
 // Semantics (light-vllm TorchPagedAttention, src/light_vllm/runtime/execution/
 // paged_attention.py:323-380): query token j of request r with c = computed
@@ -9,24 +10,35 @@
 // query dtype.  There is no split-K in the reference; this kernel splits each
 // sequence into partitions and merges their (max, sum, acc) partials.
 //
-// Mapping onto CDNA4 (one wave64 per workgroup):
-//   * A work unit is (request, partition, column tile); the grid is
-//     units x num_kv_heads, consecutive workgroups are the kv heads of the same
-//     unit so a physical block's rows are streamed together.
+// Mapping onto CDNA4 (one wave64 per workgroup, one workgroup per SIMD):
+//   * Stream-K: the (request, column tile) segments of all decode rows are
+//     laid end to end in 32-token units and cut into equal contiguous shares,
+//     one per wave; wave w of kv head h is workgroup h * waves_per_head + w and
+//     walks its pieces (the parts of segments inside its share).  A piece
+//     covering a whole segment writes the output; the others write partials
+//     that the merge kernel combines by log-sum-exp, one wave per (segment,
+//     kv head).  (Merging in the decode kernel, by the wave that completes a
+//     segment, put ~1000 instructions of cold code in the kernel's tail: the
+//     instruction-cache misses cost more than a separate launch.)
+//   * Fused append: this step's tokens are read from the input K/V and
+//     written to their pool slots by the piece that covers them.
 //   * MFMA columns are (query, head-in-group) pairs of one kv head: 16 per
 //     column tile, so a GQA group of 7 heads shares every K/V byte.
-//   * Per 32-token tile, lane (g = l/16, l%16) reads 16-byte chunks 4kk+g of
-//     token rows l%16 and 16+l%16: the K chunks land in VGPRs already in the
-//     A-operand layout of S^T = K Q^T (MFMA 16x16x32 bf16/fp16, 16x16x4 fp32);
-//     the V chunks of the same addresses go HBM -> LDS by 16-byte LDS DMA
-//     (global_load_lds), never through VGPRs.
+//   * Per tile (64 tokens, or fewer for wide rows), lane (g = l/16, l%16)
+//     loads 16-byte chunks 4kk+g of token rows 16s + l%16 of K and V: the K
+//     chunks land in VGPRs already in the A-operand layout of S^T = K Q^T
+//     (MFMA 16x16x32 bf16/fp16, 16x16x4 fp32); the V chunks are written to
+//     LDS after the current tile's PV.  (No LDS DMA: LLVM cannot tell an
+//     in-flight DMA into one buffer from reads of the other and would make
+//     every LDS read wait for the next tile's loads.)
 //   * The S^T accumulator layout (lane l: column l%16, tokens 4*(l/16)+r) is
 //     the B-operand layout of O^T = V^T P^T, so P never leaves its lane; the
 //     V^T A operand comes out of LDS with ds_read_b64_tr_b16 transpose reads
 //     (two per 16-row output tile).
-//   * The block-table slice of a partition sits in LDS, so tile addresses
-//     never wait on a table load; V is double-buffered in LDS and the next
-//     tile's K/V are in flight while the current tile computes.
+//   * The block-table slice of a piece sits in LDS, so tile addresses
+//     never wait on a table load; K is double-buffered in VGPRs and V in
+//     LDS, and the next tile's K/V are in flight while the current tile
+//     computes.
 //   * Online softmax in the log2 domain (scale*log2(e) folded in) with lazy
 //     rescaling: the running base only moves when a tile's max exceeds it by
 //     more than 2^8, decided by a wave vote, so most tiles skip the O^T rescale.
@@ -44,12 +56,14 @@ namespace lvamd {
 constexpr int kTableSlice = 256;
 // Lazy-rescale threshold in log2 units: probabilities stay below 2^8.
 constexpr float kRescaleSlack = 8.0f;
-
 struct DecodeArgs {
   const void* q;
   int64_t q_tok_stride, q_head_stride;
-  const void* k_pool;
-  const void* v_pool;
+  const void* k_new;  // this step's K/V [tokens][kv heads][D], or null
+  const void* v_new;
+  int64_t kn_tok_stride, kn_head_stride, vn_tok_stride, vn_head_stride;
+  void* k_pool;
+  void* v_pool;
   void* out;
   int64_t out_tok_stride, out_head_stride;
   const int32_t* __restrict__ pieces;      // [n_pieces][LVAMD_PIECE_FIELDS]
@@ -66,13 +80,9 @@ struct DecodeArgs {
   float scale_log2;
 };
 
-// s_waitcnt vmcnt(0) in the gfx9 encoding (expcnt and lgkmcnt left at their
-// maxima), through the builtin so LLVM's wait-insertion pass sees the wait.
-constexpr int kWaitVmcnt0 = 0x0F70;
-
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
-typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Max across the four 16-lane rows of a wave64 (xor 16 then xor 32) in VALU.
 __device__ __forceinline__ float row_max4(float v) {
@@ -88,13 +98,30 @@ __device__ __forceinline__ float row_sum4(float v) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// LDS slot (16-byte units) of V row r (0..31) chunk c of a 32-token tile:
-// the DMA of instruction (s = r/16, kk = c/4) writes 64 consecutive slots,
+// LDS slot (16-byte units) of V row r chunk c of a tile: the DMA of
+// instruction (s = r/16, kk = c/4) writes 64 consecutive slots,
 // lane 16*(c%4) + r%16 at slot 16*(c%4) + r%16.
 template <int NCH>
 __device__ __forceinline__ int vslot(int r, int c) {
   return ((r >> 4) * NCH + (c >> 2)) * 64 + (c & 3) * 16 + (r & 15);
 }
+
+// Decode tile shape: a tile is TT tokens of one kv head: TT = 64 when a
+// head's row slice is at most 256 bytes (bf16/fp16 up to D = 128, fp32 up to
+// D = 64), else 16, so one tile's K (and V) take at most 64 VGPRs per lane.
+template <typename T, int D>
+struct DecodeTile {
+  static constexpr int ROW = (int)sizeof(T) * D;
+  static constexpr int TT = ROW <= 256 ? 64 : 16;
+  static constexpr int SUB = TT / 16;                                // 16-row groups per tile
+  static constexpr int VSLOTS = SUB * TileShape<T, D>::NCH * 64;     // 16-byte LDS slots per V tile
+  // Each workgroup reserves more than 32 KiB of LDS (two V buffers of at
+  // least 1024 slots plus the table slice), so a CU holds at most four decode
+  // waves: one per SIMD.  Two waves sharing a SIMD stream at unequal rates
+  // (the older one wins arbitration), which left the younger waves of a
+  // static split finishing last.
+  static constexpr int VALLOC = VSLOTS < 1024 ? 1024 : VSLOTS;
+};
 
 // One piece of a wave's share: a contiguous token range of one
 // (request, column tile), with the request fields the kernel needs.
@@ -130,9 +157,12 @@ struct LaneCol {
 template <typename T, int D>
 __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   using S = TileShape<T, D>;
+  using DT = DecodeTile<T, D>;
   constexpr int E16 = S::E16, NCH = S::NCH, NT = S::NT, CPR = S::CPR;
-  constexpr int VSLOTS = 2 * NCH * 64;  // 16-byte LDS slots per V tile
-  __shared__ __attribute__((aligned(16))) uint4 vlds[2][VSLOTS];
+  constexpr int TT = DT::TT, SUB = DT::SUB;
+  constexpr int TAB_PER_LANE = kTableSlice / 64;
+  __shared__ __attribute__((aligned(16))) uint4 vlds_a[DT::VALLOC];
+  __shared__ __attribute__((aligned(16))) uint4 vlds_b[DT::VALLOC];
   __shared__ int32_t tab[2][kTableSlice];
 
   const int lane = threadIdx.x;
@@ -140,8 +170,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   const int g = lane >> 4;
   const int Hkv = a.num_kv_heads;
   const int G = a.group;
-  // Head-major grid: the waves of one kv head are consecutive workgroups, so
-  // the heads' slices of a row are not all requested at the same moment.
+  // Head-major grid: the waves of one kv head are consecutive workgroups.
   const int kvh = blockIdx.x / a.waves_per_head;
   const int w = blockIdx.x - kvh * a.waves_per_head;
   int p = a.wave_first[w];
@@ -149,24 +178,33 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   if (p >= p_end) return;
 
   const int64_t row_elems = (int64_t)Hkv * D;
-  const T* kbase = static_cast<const T*>(a.k_pool) + (int64_t)kvh * D;
-  const T* vbase = static_cast<const T*>(a.v_pool) + (int64_t)kvh * D;
+  T* const kbase = static_cast<T*>(a.k_pool) + (int64_t)kvh * D;
+  T* const vbase = static_cast<T*>(a.v_pool) + (int64_t)kvh * D;
+  // Fused append: this step's tokens are read from the input K/V (so no
+  // wave waits for another's pool write) and written to their pool slots by
+  // the column-tile-0 piece that covers them.
+  const T* const knew = a.k_new ? static_cast<const T*>(a.k_new) + (int64_t)kvh * a.kn_head_stride : nullptr;
+  const T* const vnew = a.v_new ? static_cast<const T*>(a.v_new) + (int64_t)kvh * a.vn_head_stride : nullptr;
 
   auto logical_block = [&](int pos) -> int {
     return a.bs_shift >= 0 ? (pos >> a.bs_shift) : (pos / a.block_size);
   };
 
-  // Block-table slice of a piece into tab[b] by 4-byte LDS DMA (the host keeps
-  // a piece within kTableSlice - 2 blocks).
-  auto issue_table = [&](const Piece& x, int b) {
+  // Block-table slice of a piece: loaded into registers (lane i holds entries
+  // i + 64j), stored to LDS when the piece's first tile is issued.  The host
+  // keeps a piece within kTableSlice - 2 blocks.
+  auto load_table = [&](const Piece& x, int (&t)[TAB_PER_LANE]) {
     const int lb0 = logical_block(x.tok_begin);
     const int n = logical_block(x.tok_end - 1) - lb0 + 1;
-    for (int i = 0; i < n; i += 64) {
-      if (i + lane < n) {
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.tables + x.table_off + lb0 + i + lane),
-                                         (lds_void_t*)(&tab[b][i]), 4, 0, 0);
-      }
+#pragma unroll
+    for (int j = 0; j < TAB_PER_LANE; ++j) {
+      const int i = j * 64 + lane;
+      t[j] = i < n ? a.tables[x.table_off + lb0 + i] : 0;
     }
+  };
+  auto store_table = [&](int b, const int (&t)[TAB_PER_LANE]) {
+#pragma unroll
+    for (int j = 0; j < TAB_PER_LANE; ++j) tab[b][j * 64 + lane] = t[j];
   };
 
   auto lane_col = [&](const Piece& x) -> LaneCol {
@@ -183,7 +221,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   };
 
   // B operand: Q^T chunks of this lane's column.
-  auto issue_q = [&](const Piece& x, uint4 (&qdst)[NCH]) {
+  auto load_q = [&](const Piece& x, uint4 (&qdst)[NCH]) {
     const LaneCol c = lane_col(x);
     const T* qrow = static_cast<const T*>(a.q) + (int64_t)(x.q_start + c.qi) * a.q_tok_stride +
                     (int64_t)c.qhead * a.q_head_stride;
@@ -194,34 +232,68 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
     }
   };
 
-  auto row_of = [&](const Piece& x, int b, int pos) -> int64_t {
-    const int seq_len = x.computed + x.q_len;
-    const int pc = pos < seq_len ? pos : seq_len - 1;
-    const int lb = logical_block(pc);
-    return (int64_t)tab[b][lb - logical_block(x.tok_begin)] * a.block_size + (pc - lb * a.block_size);
-  };
-
-  // Issue one 32-token tile of piece x: K chunks into registers, V chunks by
-  // 16-byte LDS DMA into V buffer vb.  Rows past the sequence end read the
-  // last real row (finite data whose probability is exactly 0).
-  auto issue_tile = [&](const Piece& x, int tb, int t0, int vb, uint4 (&kdst)[2][NCH]) {
-    const int64_t row0 = row_of(x, tb, t0 + l16);
-    const int64_t row1 = row_of(x, tb, t0 + 16 + l16);
+  // Issue one TT-token tile of piece x (table slice in tab[tb]): K chunks and
+  // V chunks into registers.  Positions past the piece read its last row
+  // (finite data, masked to probability 0, already in cache).  All row
+  // offsets are read from LDS before any load is issued.  fresh[s] is the
+  // pool offset of row group s's row when this tile must append it, else -1.
+  auto issue_tile = [&](const Piece& x, int tb, int t0, uint4 (&kdst)[SUB][NCH], uint4 (&vdst)[SUB][NCH],
+                        int64_t (&fresh)[SUB]) {
+    const int lb0 = logical_block(x.tok_begin);
+    const T* kp[SUB];
+    const T* vp[SUB];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int64_t off = (s == 0 ? row0 : row1) * row_elems;
+    for (int s = 0; s < SUB; ++s) {
+      const int pos = t0 + 16 * s + l16;
+      const int pc = pos < x.tok_end ? pos : x.tok_end - 1;
+      const int lb = logical_block(pc);
+      const int64_t off = ((int64_t)tab[tb][lb - lb0] * a.block_size + (pc - lb * a.block_size)) * row_elems;
+      kp[s] = kbase + off;
+      vp[s] = vbase + off;
+      fresh[s] = -1;
+      if (knew != nullptr && pc >= x.computed) {
+        const int64_t t = x.q_start + (pc - x.computed);
+        kp[s] = knew + t * a.kn_tok_stride;
+        vp[s] = vnew + t * a.vn_tok_stride;
+        if (x.ctile == 0 && pc == pos) fresh[s] = off;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < SUB; ++s)
 #pragma unroll
       for (int kk = 0; kk < NCH; ++kk) {
         const int c = kk * 4 + g;
         if (c < CPR) {
-          kdst[s][kk] = load16(kbase + off + c * E16);
-          __builtin_amdgcn_global_load_lds(static_cast<const void*>(vbase + off + c * E16),
-                                           (lds_void_t*)(&vlds[vb][(s * NCH + kk) * 64]), 16, 0, 0);
+          kdst[s][kk] = load16(kp[s] + c * E16);
+          vdst[s][kk] = load16(vp[s] + c * E16);
         } else {
           kdst[s][kk] = zero_u4();
+          vdst[s][kk] = zero_u4();
+        }
+      }
+  };
+  // Append the tile's fresh rows to the pool (bit-exact row copies).
+  auto store_fresh = [&](const uint4 (&kr)[SUB][NCH], const uint4 (&vr)[SUB][NCH], const int64_t (&fresh)[SUB]) {
+#pragma unroll
+    for (int s = 0; s < SUB; ++s) {
+      if (fresh[s] >= 0) {
+#pragma unroll
+        for (int kk = 0; kk < NCH; ++kk) {
+          const int c = kk * 4 + g;
+          if (c < CPR) {
+            *reinterpret_cast<uint4*>(kbase + fresh[s] + c * E16) = kr[s][kk];
+            *reinterpret_cast<uint4*>(vbase + fresh[s] + c * E16) = vr[s][kk];
+          }
         }
       }
     }
+  };
+  // V tile into LDS: chunk (s, kk) of lane l at slot (s * NCH + kk) * 64 + l.
+  auto stage_v = [&](uint4* vdst, const uint4 (&vr)[SUB][NCH]) {
+#pragma unroll
+    for (int s = 0; s < SUB; ++s)
+#pragma unroll
+      for (int kk = 0; kk < NCH; ++kk) vdst[(s * NCH + kk) * 64 + lane] = vr[s][kk];
   };
 
   // Prologue: this piece's table and Q, the next piece's table and Q, then
@@ -229,21 +301,29 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   Piece cur = read_piece(a.pieces, p);
   int tb = 0;
   uint4 qf[NCH], qn[NCH];
-  issue_table(cur, tb);
-  issue_q(cur, qf);
+  int tn[TAB_PER_LANE];
+  {
+    int tc[TAB_PER_LANE];
+    load_table(cur, tc);
+    store_table(tb, tc);
+  }
+  load_q(cur, qf);
   bool have_nxt = p + 1 < p_end;
+  bool nxt_stored = false;  // the next piece's table slice is in tab[tb ^ 1]
   Piece nxt = cur;
   if (have_nxt) {
     nxt = read_piece(a.pieces, p + 1);
-    issue_table(nxt, tb ^ 1);
-    issue_q(nxt, qn);
+    load_table(nxt, tn);
+    load_q(nxt, qn);
   }
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  uint4 kf[2][NCH];
-  int vb = 0;
-  issue_tile(cur, tb, cur.tok_begin, vb, kf);
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  bool nxt_pending = false;  // the next piece's table DMA is not known to have landed
+  uint4 ka[SUB][NCH], kb[SUB][NCH];
+  {
+    uint4 vr[SUB][NCH];
+    int64_t fresh[SUB];
+    issue_tile(cur, tb, cur.tok_begin, ka, vr, fresh);
+    stage_v(vlds_a, vr);
+    store_fresh(ka, vr, fresh);
+  }
 
   LaneCol lc = lane_col(cur);
   float m_run = -INFINITY;  // per-column base (log2 domain), uniform across the column's lanes
@@ -253,49 +333,69 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
   int t0 = cur.tok_begin;
 
-  while (true) {
-    // Keep the next tile in flight: the rest of this piece, else the first
-    // tile of the next piece.
-    const int nt0 = t0 + 32;
-    const bool next_in_cur = nt0 < cur.tok_end;
-    uint4 kn[2][NCH];
-    if (next_in_cur) {
-      issue_tile(cur, tb, nt0, vb ^ 1, kn);
-    } else if (have_nxt) {
-      if (nxt_pending) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-      issue_tile(nxt, tb ^ 1, nxt.tok_begin, vb ^ 1, kn);
+  // One tile: start loading the next tile into (kx, registers for vx), then
+  // compute the current one from (kc, vc), then stage the next V into vx.
+  // Returns true when the current piece has ended.
+  auto step = [&](uint4 (&kc)[SUB][NCH], uint4 (&kx)[SUB][NCH], uint4* vc, uint4* vx) -> bool {
+    // Masks: only tiles that reach the piece end or the query region need
+    // them.  A tree request's visibility words for this tile's query
+    // positions (j = pos - computed spans at most three words) are loaded
+    // before the next tile is issued.
+    const int computed = cur.computed;
+    const int tok_end = cur.tok_end;
+    const bool need_mask = t0 + TT > (computed < tok_end ? computed : tok_end);
+    uint32_t vw[3] = {0u, 0u, 0u};
+    const int jw0 = (t0 > computed ? t0 - computed : 0) >> 5;
+    if (need_mask && lc.vrow != nullptr) {
+      const int last_word = (cur.q_len - 1) >> 5;
+#pragma unroll
+      for (int i = 0; i < 3; ++i) vw[i] = lc.vrow[jw0 + i <= last_word ? jw0 + i : last_word];
     }
 
-    // S^T tile: rows = 32 tokens (two 16-row halves), columns = this lane's col.
-    f32x4 st[2];
+    const int nt0 = t0 + TT;
+    const bool next_in_cur = nt0 < cur.tok_end;
+    uint4 vr[SUB][NCH];
+    int64_t fresh[SUB];
+    const bool issued = next_in_cur || have_nxt;
+    if (next_in_cur) {
+      issue_tile(cur, tb, nt0, kx, vr, fresh);
+    } else if (have_nxt) {
+      if (!nxt_stored) {
+        store_table(tb ^ 1, tn);
+        nxt_stored = true;
+      }
+      issue_tile(nxt, tb ^ 1, nxt.tok_begin, kx, vr, fresh);
+    }
+
+    // S^T tile: rows = TT tokens (16-row groups), columns = this lane's col.
+    f32x4 st[SUB];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
+    for (int s = 0; s < SUB; ++s) {
       st[s] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < NCH; ++kk) st[s] = Mma<T>::qk(kf[s][kk], qf[kk], st[s]);
+      for (int kk = 0; kk < NCH; ++kk) st[s] = Mma<T>::qk(kc[s][kk], qf[kk], st[s]);
     }
 
-    // Scale and mask (only the tiles that reach the query region need masks).
-    const int computed = cur.computed;
-    const int seq_len = computed + cur.q_len;
-    const bool need_mask = t0 + 32 > computed;
-    float sv[2][4];
+    // Scale and mask.
+    float sv[SUB][4];
     float mt = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int s = 0; s < SUB; ++s)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int pos = t0 + 16 * s + 4 * g + r;
         bool vis = true;
         if (need_mask) {
-          if (pos >= seq_len) {
+          if (pos >= tok_end) {
             vis = false;
           } else if (pos >= computed) {
+            const int j = pos - computed;
             if (lc.vrow == nullptr) {
               vis = pos <= lc.lin_last;
             } else {
-              const int j = pos - computed;
-              vis = (lc.vrow[j >> 5] >> (j & 31)) & 1u;
+              const int wi = (j >> 5) - jw0;
+              const uint32_t word = wi == 0 ? vw[0] : (wi == 1 ? vw[1] : vw[2]);
+              vis = (word >> (j & 31)) & 1u;
             }
           }
         }
@@ -314,40 +414,65 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
       m_run = m_new;
     }
     const float base = (m_run == -INFINITY) ? 0.f : m_run;
-    float p4[2][4];
+    float p4[SUB][4];
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int s = 0; s < SUB; ++s)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         p4[s][r] = fast_exp2(sv[s][r] - base);
         l_run += p4[s][r];
       }
 
-    // O^T += V^T P^T with V^T from the LDS tile.
-    char* vbytes = reinterpret_cast<char*>(&vlds[vb][0]);
-    if constexpr (sizeof(T) == 2) {
-      using V8 = typename std::conditional<std::is_same<T, __bf16>::value, bf16x8, f16x8>::type;
-      V8 pb;
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) pb[s * 4 + r] = from_f32<T>(p4[s][r]);
+    // O^T += V^T P^T with V^T from the LDS tile: 32 tokens per MFMA k-step
+    // (16x16x32), or 16 (16x16x16) for a single 16-row group.
+    char* vbytes = reinterpret_cast<char*>(vc);
+    if constexpr (sizeof(T) == 2 && SUB == 1) {
+      using V4 = typename std::conditional<std::is_same<T, __bf16>::value, s16x4, f16x4>::type;
       const int q4 = l16 & 3;
+      T pt[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pt[r] = from_f32<T>(p4[0][r]);
+      const V4 pb = bitcast<V4>(pt);
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
-        // Lane (g, l16) addresses row 16j + 4g + l16/4, dims 16n + 4*(l16%4)..+3;
-        // the transpose hands it dims 16n + l16 of rows 16j + 4g + 0..3.
+        // The transpose hands lane (g, l16) dims 16n + l16 of rows 4g + 0..3:
+        // the A operand of a 16x16x16 step whose k index is 4g + e.
         const int c = 2 * n + (q4 >> 1);
         const int lo = vslot<NCH>(4 * g + (l16 >> 2), c) * 16 + (q4 & 1) * 8;
-        const int hi = vslot<NCH>(16 + 4 * g + (l16 >> 2), c) * 16 + (q4 & 1) * 8;
         const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vbytes + lo));
-        const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vbytes + hi));
-        const s16x4 both[2] = {v0, v1};
-        const V8 av = bitcast<V8>(both);
         if constexpr (std::is_same<T, __bf16>::value) {
-          acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb, acc[n], 0, 0, 0);
+          acc[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v0, pb, acc[n], 0, 0, 0);
         } else {
-          acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb, acc[n], 0, 0, 0);
+          acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(bitcast<f16x4>(v0), pb, acc[n], 0, 0, 0);
+        }
+      }
+    } else if constexpr (sizeof(T) == 2) {
+      using V8 = typename std::conditional<std::is_same<T, __bf16>::value, bf16x8, f16x8>::type;
+      const int q4 = l16 & 3;
+#pragma unroll
+      for (int h = 0; h < SUB / 2; ++h) {
+        V8 pb;
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pb[s * 4 + r] = from_f32<T>(p4[2 * h + s][r]);
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+          // Lane (g, l16) addresses row 32h + 16j + 4g + l16/4, dims
+          // 16n + 4*(l16%4)..+3; the transpose hands it dims 16n + l16 of rows
+          // 32h + 16j + 4g + 0..3.
+          const int c = 2 * n + (q4 >> 1);
+          const int lo = vslot<NCH>(32 * h + 4 * g + (l16 >> 2), c) * 16 + (q4 & 1) * 8;
+          const int hi = vslot<NCH>(32 * h + 16 + 4 * g + (l16 >> 2), c) * 16 + (q4 & 1) * 8;
+          const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vbytes + lo));
+          const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vbytes + hi));
+          const s16x4 both[2] = {v0, v1};
+          const V8 av = bitcast<V8>(both);
+          if constexpr (std::is_same<T, __bf16>::value) {
+            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb, acc[n], 0, 0, 0);
+          } else {
+            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb, acc[n], 0, 0, 0);
+          }
         }
       }
     } else {
@@ -356,7 +481,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
       for (int n = 0; n < NT; ++n) {
         const int d = 16 * n + l16;
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
+        for (int s = 0; s < SUB; ++s)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float av = vfl[vslot<NCH>(16 * s + 4 * g + r, d >> 2) * 4 + (d & 3)];
@@ -365,127 +490,141 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
       }
     }
 
-    // The next tile (K registers and V DMA) and any table/Q prefetch have
-    // landed once this wait returns.
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    nxt_pending = false;
-
-    if (!next_in_cur) {
-      // Piece finished: write the output (whole segment) or its partial.
-      const float l_tot = row_sum4(l_run);
-      if (cur.slot < 0) {
-        if (lc.ok) {
-          const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-          T* orow = static_cast<T*>(a.out) + (int64_t)(cur.q_start + lc.qi) * a.out_tok_stride +
-                    (int64_t)lc.qhead * a.out_head_stride;
-#pragma unroll
-          for (int n = 0; n < NT; ++n)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) orow[16 * n + 4 * g + r] = from_f32<T>(acc[n][r] * inv);
-        }
-      } else if (lc.ok) {
-        const int64_t cslot = ((int64_t)cur.slot * Hkv + kvh) * 16 + l16;
-        float* pacc = a.part_acc + cslot * D;
-#pragma unroll
-        for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(pacc + 16 * n + 4 * g) = acc[n];
-        if (g == 0) {
-          a.part_ml[cslot * 2 + 0] = m_run;
-          a.part_ml[cslot * 2 + 1] = l_tot;
-        }
-      }
-      if (!have_nxt) break;
-      // Switch to the next piece (its first tile is already in flight) and
-      // start fetching the one after.
-      cur = nxt;
-      tb ^= 1;
-#pragma unroll
-      for (int kk = 0; kk < NCH; ++kk) qf[kk] = qn[kk];
-      lc = lane_col(cur);
-      m_run = -INFINITY;
-      l_run = 0.f;
-#pragma unroll
-      for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-      t0 = cur.tok_begin;
-      ++p;
-      have_nxt = p + 1 < p_end;
-      if (have_nxt) {
-        nxt = read_piece(a.pieces, p + 1);
-        issue_table(nxt, tb ^ 1);
-        issue_q(nxt, qn);
-        nxt_pending = true;
-      }
-    } else {
-      t0 = nt0;
+    // Next tile's V into the other LDS buffer (this waits for its loads),
+    // and its fresh rows into the pool.
+    if (issued) {
+      stage_v(vx, vr);
+      store_fresh(kx, vr, fresh);
     }
+    if (next_in_cur) t0 = nt0;
+    return !next_in_cur;
+  };
+
+  // Piece finished: write the output (whole segment) or its partial, then
+  // switch to the next piece (its first tile is already staged) and start
+  // fetching the one after.  Returns false after the wave's last piece.
+  auto end_piece = [&]() -> bool {
+    const float l_tot = row_sum4(l_run);
+    if (cur.slot < 0) {
+      if (lc.ok) {
+        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+        T* orow = static_cast<T*>(a.out) + (int64_t)(cur.q_start + lc.qi) * a.out_tok_stride +
+                  (int64_t)lc.qhead * a.out_head_stride;
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+        for (int n = 0; n < NT; ++n)
 #pragma unroll
-      for (int kk = 0; kk < NCH; ++kk) kf[s][kk] = kn[s][kk];
-    vb ^= 1;
+          for (int r = 0; r < 4; ++r) orow[16 * n + 4 * g + r] = from_f32<T>(acc[n][r] * inv);
+      }
+    } else if (lc.ok) {
+      const int64_t cs = ((int64_t)cur.slot * Hkv + kvh) * 16 + l16;
+      float* pacc = a.part_acc + cs * D;
+#pragma unroll
+      for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(pacc + 16 * n + 4 * g) = acc[n];
+      if (g == 0) *reinterpret_cast<float2*>(a.part_ml + cs * 2) = make_float2(m_run, l_tot);
+    }
+    if (!have_nxt) return false;
+    cur = nxt;
+    tb ^= 1;
+#pragma unroll
+    for (int kk = 0; kk < NCH; ++kk) qf[kk] = qn[kk];
+    lc = lane_col(cur);
+    m_run = -INFINITY;
+    l_run = 0.f;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    t0 = cur.tok_begin;
+    ++p;
+    have_nxt = p + 1 < p_end;
+    nxt_stored = false;
+    if (have_nxt) {
+      nxt = read_piece(a.pieces, p + 1);
+      load_table(nxt, tn);
+      load_q(nxt, qn);
+    }
+    return true;
+  };
+
+  // The K registers and V buffers swap roles every tile; two step copies keep
+  // those roles static (a run-time choice would keep both K sets live).
+  while (true) {
+    if (step(ka, kb, vlds_a, vlds_b) && !end_piece()) break;
+    if (step(kb, ka, vlds_b, vlds_a) && !end_piece()) break;
   }
 }
 
 // ---------------------------------------------------------------------------
-// Merge: one thread per (job, kv head, column, 4-float chunk of the row);
-// partials are combined in one pass with a running log-sum-exp base.
+// Merge: one wave per (job, kv head); lane (g, l16) combines dims 16n + 4g..+3
+// of column l16 over the job's partials, four partials per round trip, by
+// log-sum-exp in the log2 domain.
 // ---------------------------------------------------------------------------
 struct MergeArgs {
   const float* part_acc;
   const float* part_ml;
   void* out;
   int64_t out_tok_stride, out_head_stride;
-  const int32_t* __restrict__ req_meta;
-  const int32_t* __restrict__ jobs;
-  int32_t num_jobs;
+  const int32_t* __restrict__ jobs;  // [num_jobs][LVAMD_MERGE_FIELDS]
   int32_t num_kv_heads;
   int32_t group;
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(256) void paged_merge_kernel(const MergeArgs a) {
-  constexpr int DC = D / 4;  // 16-byte chunks of one partial row
+__global__ __launch_bounds__(64) void paged_merge_kernel(const MergeArgs a) {
+  constexpr int NT = D / 16;
   const int Hkv = a.num_kv_heads;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int dc = (int)(gid % DC);
-  int64_t r = gid / DC;
-  const int cl = (int)(r % 16);
-  r /= 16;
-  const int kvh = (int)(r % Hkv);
-  const int64_t job = r / Hkv;
-  if (job >= a.num_jobs) return;
-  const int32_t* jb = a.jobs + job * LVAMD_MERGE_FIELDS;
-  const int req = jb[0], ctile = jb[1], ps0 = jb[2], np = jb[3];
-  const int32_t* rm = a.req_meta + req * LVAMD_REQ_FIELDS;
-  const int q_len = rm[3], q_start = rm[4];
   const int G = a.group;
-  const int col = ctile * 16 + cl;
+  const int job = blockIdx.x / Hkv;
+  const int kvh = blockIdx.x - job * Hkv;
+  const int lane = threadIdx.x;
+  const int l16 = lane & 15;
+  const int g = lane >> 4;
+  const int32_t* jb = a.jobs + (int64_t)job * LVAMD_MERGE_FIELDS;
+  const int ctile = jb[1], slot0 = jb[2], np = jb[3], q_start = jb[4], q_len = jb[5];
+  const int col = ctile * 16 + l16;
   if (col >= q_len * G) return;
   const int qi = col / G;
-  const int h = col - qi * G;
+  const int qhead = kvh * G + (col - qi * G);
 
-  const int64_t pstride = (int64_t)Hkv * 16;  // column slots per partial slot
-  const int64_t c0 = ((int64_t)ps0 * Hkv + kvh) * 16 + cl;
   float mrun = -INFINITY;
   float lsum = 0.f;
-  f32x4 o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-  for (int p = 0; p < np; ++p) {
-    const int64_t cs = c0 + p * pstride;
-    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + cs * 2);
-    const f32x4 pa = *reinterpret_cast<const f32x4*>(a.part_acc + cs * D + 4 * dc);
-    const float mnew = fmaxf(mrun, ml.x);
-    if (mnew == -INFINITY) continue;  // nothing visible so far
-    const float sc = fast_exp2(mrun - mnew);  // 0 while mrun is -inf
-    const float w = fast_exp2(ml.x - mnew);   // 0 for an empty partial
-    lsum = lsum * sc + w * ml.y;
-    o = o * sc + w * pa;
+  f32x4 o[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < np; j0 += 4) {
+    float2 ml[4];
+    f32x4 pa[4][NT];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t cs = ((int64_t)(slot0 + (j0 + i < np ? j0 + i : np - 1)) * Hkv + kvh) * 16 + l16;
+      ml[i] = *reinterpret_cast<const float2*>(a.part_ml + cs * 2);
+#pragma unroll
+      for (int n = 0; n < NT; ++n) pa[i][n] = *reinterpret_cast<const f32x4*>(a.part_acc + cs * D + 16 * n + 4 * g);
+    }
+    // One rescale per chunk, branch-free so the chunk's loads are issued
+    // together; entries past the job and empty partials weigh 0.
+    float mc = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mc = fmaxf(mc, j0 + i < np ? ml[i].x : -INFINITY);
+    const float mnew = fmaxf(mrun, mc);
+    const bool any = mnew != -INFINITY;
+    const float sc = (any && mrun != -INFINITY) ? fast_exp2(mrun - mnew) : (any ? 0.f : 1.f);
+    lsum *= sc;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) o[n] *= sc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float wt = (j0 + i < np && ml[i].x != -INFINITY) ? fast_exp2(ml[i].x - mnew) : 0.f;
+      lsum += wt * ml[i].y;
+#pragma unroll
+      for (int n = 0; n < NT; ++n) o[n] += wt * pa[i][n];
+    }
     mrun = mnew;
   }
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  T* orow = static_cast<T*>(a.out) + (int64_t)(q_start + qi) * a.out_tok_stride +
-            (int64_t)(kvh * G + h) * a.out_head_stride + 4 * dc;
+  T* orow = static_cast<T*>(a.out) + (int64_t)(q_start + qi) * a.out_tok_stride + (int64_t)qhead * a.out_head_stride;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) orow[i] = from_f32<T>(o[i] * inv);
+  for (int n = 0; n < NT; ++n)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) orow[16 * n + 4 * g + r] = from_f32<T>(o[n][r] * inv);
 }
 
 template <typename T>
@@ -505,12 +644,12 @@ static int launch_decode_t(int head_size, dim3 grid, hipStream_t s, const Decode
 template <typename T>
 static int launch_merge_t(int head_size, dim3 grid, hipStream_t s, const MergeArgs& a) {
   switch (head_size) {
-    case 32: hipLaunchKernelGGL((paged_merge_kernel<T, 32>), grid, dim3(256), 0, s, a); break;
-    case 64: hipLaunchKernelGGL((paged_merge_kernel<T, 64>), grid, dim3(256), 0, s, a); break;
-    case 80: hipLaunchKernelGGL((paged_merge_kernel<T, 80>), grid, dim3(256), 0, s, a); break;
-    case 96: hipLaunchKernelGGL((paged_merge_kernel<T, 96>), grid, dim3(256), 0, s, a); break;
-    case 128: hipLaunchKernelGGL((paged_merge_kernel<T, 128>), grid, dim3(256), 0, s, a); break;
-    case 256: hipLaunchKernelGGL((paged_merge_kernel<T, 256>), grid, dim3(256), 0, s, a); break;
+    case 32: hipLaunchKernelGGL((paged_merge_kernel<T, 32>), grid, dim3(64), 0, s, a); break;
+    case 64: hipLaunchKernelGGL((paged_merge_kernel<T, 64>), grid, dim3(64), 0, s, a); break;
+    case 80: hipLaunchKernelGGL((paged_merge_kernel<T, 80>), grid, dim3(64), 0, s, a); break;
+    case 96: hipLaunchKernelGGL((paged_merge_kernel<T, 96>), grid, dim3(64), 0, s, a); break;
+    case 128: hipLaunchKernelGGL((paged_merge_kernel<T, 128>), grid, dim3(64), 0, s, a); break;
+    case 256: hipLaunchKernelGGL((paged_merge_kernel<T, 256>), grid, dim3(64), 0, s, a); break;
     default: return LVAMD_ERR_UNSUPPORTED;
   }
   return launch_status();
@@ -527,7 +666,10 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 using namespace lvamd;
 
 extern "C" int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_stride,
-                                  const void* key_pool, const void* value_pool,
+                                  const void* new_key, int64_t new_key_token_stride, int64_t new_key_head_stride,
+                                  const void* new_value, int64_t new_value_token_stride,
+                                  int64_t new_value_head_stride,
+                                  void* key_pool, void* value_pool,
                                   void* out, int64_t out_token_stride, int64_t out_head_stride,
                                   const int32_t* pieces, const int32_t* wave_first, int32_t waves_per_head,
                                   const int32_t* tables, const uint32_t* vis,
@@ -536,20 +678,32 @@ extern "C" int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t
                                   int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream) {
   const int es = dtype_size(dtype);
   if (es == 0 || !head_size_supported(head_size)) return LVAMD_ERR_UNSUPPORTED;
-  if (waves_per_head < 0 || num_kv_heads <= 0 || group <= 0 || block_size <= 0) return LVAMD_ERR_INVALID_ARGUMENT;
+  if (waves_per_head < 0 || num_kv_heads <= 0 || group <= 0 || block_size <= 0 || num_partial_slots < 0)
+    return LVAMD_ERR_INVALID_ARGUMENT;
   if (waves_per_head == 0) return LVAMD_OK;
   if (!q || !key_pool || !value_pool || !out || !pieces || !wave_first || !tables)
     return LVAMD_ERR_INVALID_ARGUMENT;
   if (num_partial_slots > 0 && (!part_acc || !part_ml)) return LVAMD_ERR_WORKSPACE;
+  if ((new_key == nullptr) != (new_value == nullptr)) return LVAMD_ERR_INVALID_ARGUMENT;
   // 16-byte row chunks: base pointers and token/head strides must keep rows aligned.
   if (!aligned16(q) || !aligned16(key_pool) || !aligned16(value_pool) ||
       (q_token_stride * es) % 16 != 0 || (q_head_stride * es) % 16 != 0)
+    return LVAMD_ERR_INVALID_ARGUMENT;
+  if (new_key && (!aligned16(new_key) || !aligned16(new_value) || (new_key_token_stride * es) % 16 != 0 ||
+                  (new_key_head_stride * es) % 16 != 0 || (new_value_token_stride * es) % 16 != 0 ||
+                  (new_value_head_stride * es) % 16 != 0))
     return LVAMD_ERR_INVALID_ARGUMENT;
   if ((int64_t)waves_per_head * num_kv_heads > 0x7fffffffLL) return LVAMD_ERR_INVALID_ARGUMENT;
   DecodeArgs a;
   a.q = q;
   a.q_tok_stride = q_token_stride;
   a.q_head_stride = q_head_stride;
+  a.k_new = new_key;
+  a.v_new = new_value;
+  a.kn_tok_stride = new_key_token_stride;
+  a.kn_head_stride = new_key_head_stride;
+  a.vn_tok_stride = new_value_token_stride;
+  a.vn_head_stride = new_value_head_stride;
   a.k_pool = key_pool;
   a.v_pool = value_pool;
   a.out = out;
@@ -603,28 +757,24 @@ extern "C" int lvamd_paged_decode_resident_waves(int32_t dtype, int32_t head_siz
 
 extern "C" int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
                                            void* out, int64_t out_token_stride, int64_t out_head_stride,
-                                           const int32_t* req_meta, const int32_t* jobs, int32_t num_jobs,
+                                           const int32_t* jobs, int32_t num_jobs,
                                            int32_t num_kv_heads, int32_t group, int32_t head_size,
                                            int32_t dtype, lvamd_stream_t stream) {
-  const int es = dtype_size(dtype);
-  if (es == 0 || !head_size_supported(head_size)) return LVAMD_ERR_UNSUPPORTED;
+  if (dtype_size(dtype) == 0 || !head_size_supported(head_size)) return LVAMD_ERR_UNSUPPORTED;
   if (num_jobs < 0 || num_kv_heads <= 0 || group <= 0) return LVAMD_ERR_INVALID_ARGUMENT;
   if (num_jobs == 0) return LVAMD_OK;
-  if (!part_acc || !part_ml || !out || !req_meta || !jobs) return LVAMD_ERR_INVALID_ARGUMENT;
-  if ((int64_t)num_jobs * num_kv_heads * 16 * (head_size / 4) / 256 > 0x7fffffffLL) return LVAMD_ERR_INVALID_ARGUMENT;
+  if (!part_acc || !part_ml || !out || !jobs) return LVAMD_ERR_INVALID_ARGUMENT;
+  if ((int64_t)num_jobs * num_kv_heads > 0x7fffffffLL) return LVAMD_ERR_INVALID_ARGUMENT;
   MergeArgs a;
   a.part_acc = part_acc;
   a.part_ml = part_ml;
   a.out = out;
   a.out_tok_stride = out_token_stride;
   a.out_head_stride = out_head_stride;
-  a.req_meta = req_meta;
   a.jobs = jobs;
-  a.num_jobs = num_jobs;
   a.num_kv_heads = num_kv_heads;
   a.group = group;
-  const int64_t threads = (int64_t)num_jobs * num_kv_heads * 16 * (head_size / 4);
-  const dim3 grid((unsigned)((threads + 255) / 256));
+  const dim3 grid((unsigned)(num_jobs * num_kv_heads));
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case LVAMD_BF16: return launch_merge_t<__bf16>(head_size, grid, s, a);

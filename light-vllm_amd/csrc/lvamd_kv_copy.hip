@@ -178,13 +178,13 @@ const char* lvamd_status_string(int status) {
     case LVAMD_OK: return "ok";
     case LVAMD_ERR_INVALID_ARGUMENT: return "invalid argument";
     case LVAMD_ERR_UNSUPPORTED: return "unsupported dtype, head size or group size";
-    case LVAMD_ERR_WORKSPACE: return "workspace too small";
+    case LVAMD_ERR_WORKSPACE: return "workspace missing or too small";
     case LVAMD_ERR_LAUNCH: return "kernel launch failed";
     default: return "unknown status";
   }
 }
 
-int lvamd_abi_version(void) { return 2; }
+int lvamd_abi_version(void) { return 4; }
 
 int lvamd_kv_append(const void* key, int64_t key_token_stride, int64_t key_head_stride,
                     const void* value, int64_t value_token_stride, int64_t value_head_stride,

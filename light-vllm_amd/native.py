@@ -15,7 +15,7 @@ from pathlib import Path
 from light_vllm_amd.errors import ExecutionError, ExecutionNotReadyError
 
 LIB_NAME = "liblvamd_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 4
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
@@ -23,7 +23,7 @@ HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 REQ_FIELDS = 8
 PIECE_FIELDS = 16
-MERGE_FIELDS = 4
+MERGE_FIELDS = 8
 PREFILL_FIELDS = 4
 
 _p = ctypes.c_void_p
@@ -41,13 +41,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "lvamd_paged_decode": (
         ctypes.c_int,
-        [_p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _i32, _p, _p, _p, _p, _i64,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i64,
+         _p, _p, _i32, _p, _p, _p, _p, _i64,
          _i32, _i32, _i32, _i32, _f32, _i32, _p],
     ),
     "lvamd_paged_decode_resident_waves": (ctypes.c_int, [_i32, _i32]),
     "lvamd_paged_attention_merge": (
         ctypes.c_int,
-        [_p, _p, _p, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p],
+        [_p, _p, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p],
     ),
     "lvamd_paged_prefill": (
         ctypes.c_int,

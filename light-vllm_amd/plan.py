@@ -45,6 +45,7 @@ TABLE_SLICE = 256
 
 
 PIECE_FIELDS = 16
+MERGE_FIELDS = 8
 TILE_TOKENS = 32
 
 _BIT_WEIGHTS = (np.uint64(1) << np.arange(32, dtype=np.uint64)).astype(np.uint64)
@@ -66,13 +67,14 @@ def stream_k_pieces(
 
     A segment is one (request, column tile); it has ceil(seq / 32) tiles of 32
     tokens.  The segments of all decode rows are laid end to end and the
-    flattened tile range is cut into ``waves_per_head`` equal, contiguous
-    shares (the same cut for every kv head).  A wave's share is a list of
+    flattened tile range is cut into ``waves_per_head`` contiguous shares
+    that differ by at most one tile (the same cut for every kv head).  A wave's share is a list of
     pieces: the part of each segment it covers.  A piece that covers a whole
     segment writes the output directly; otherwise it writes a partial
     (max, sum, acc) to its slot and a merge job combines the segment's
-    partials.  Returns (pieces [n, 16] int64, wave_first [W + 1], W, jobs
-    [m, 4], num_slots).
+    partials, which a merge job per segment combines.  Returns (pieces
+    [n, 16] int64, wave_first [W + 1], W, largest share, jobs [m, 8] =
+    (req, column tile, first slot, partials, q_start, q_len, 0, 0), num_slots).
     """
 
     seg_req = np.repeat(np.flatnonzero(rows), nct[rows])
@@ -87,12 +89,14 @@ def stream_k_pieces(
         cap = max(1, min(cap, max_tiles_per_wave))
     waves = max(1, min(max(1, resident_waves // num_kv_heads), -(-total // min_tiles_per_wave)))
     waves = max(waves, -(-total // cap))
-    per_wave = -(-total // waves)  # equal shares; never above cap
-    waves = -(-total // per_wave)
-    cuts = np.unique(np.concatenate((seg_start, np.arange(0, total, per_wave), [total])))
+    per_wave = -(-total // waves)  # the largest share; never above cap
+    # Balanced shares: wave w covers units [w * total // W, (w + 1) * total // W),
+    # so shares differ by at most one unit and every wave has work.
+    bounds = (np.arange(waves + 1, dtype=np.int64) * total) // waves
+    cuts = np.unique(np.concatenate((seg_start, bounds)))
     lo, hi = cuts[:-1], cuts[1:]
     seg = np.searchsorted(seg_start, lo, side="right") - 1
-    wave = lo // per_wave
+    wave = np.searchsorted(bounds, lo, side="right") - 1
     npieces = np.bincount(seg, minlength=len(seg_req))
     multi = npieces[seg] > 1
     slot = np.where(multi, np.cumsum(multi) - 1, -1)
@@ -111,7 +115,14 @@ def stream_k_pieces(
     pieces[:, 10] = req_meta[req, 6]  # vis_words
     wave_first = np.searchsorted(wave, np.arange(waves + 1), side="left")
     first = multi & (lo == seg_start[seg])
-    jobs = np.stack([req[first], seg_ctile[seg[first]], slot[first], npieces[seg[first]]], axis=1)
+    jreq = req[first]
+    jobs = np.zeros((int(first.sum()), MERGE_FIELDS), dtype=np.int64)
+    jobs[:, 0] = jreq
+    jobs[:, 1] = seg_ctile[seg[first]]
+    jobs[:, 2] = slot[first]
+    jobs[:, 3] = npieces[seg[first]]
+    jobs[:, 4] = req_meta[jreq, 4]  # q_start
+    jobs[:, 5] = req_meta[jreq, 3]  # q_len
     return pieces, wave_first, waves, per_wave, jobs, int(multi.sum())
 
 
@@ -129,7 +140,7 @@ class DecodeWork:
     pieces: Tensor | None  # int32 [n_pieces, 16]
     wave_first: Tensor | None  # int32 [waves_per_head + 1]
     waves_per_head: int
-    jobs: Tensor | None  # int32 [n_jobs, 4]
+    jobs: Tensor | None  # int32 [n_jobs, 8]
     num_jobs: int
     num_partial_slots: int
     tiles_per_wave: int
@@ -290,8 +301,8 @@ class StepPlan:
             wave_first = blob[off : off + waves + 1]
             off += waves + 1
         if num_jobs:
-            jobs = blob[off : off + 4 * num_jobs].view(num_jobs, 4)
-            off += 4 * num_jobs
+            jobs = blob[off : off + MERGE_FIELDS * num_jobs].view(num_jobs, MERGE_FIELDS)
+            off += MERGE_FIELDS * num_jobs
         if num_prefill:
             prefill_units = blob[off : off + 4 * num_prefill].view(num_prefill, 4)
         return DecodeWork(pieces, wave_first, waves, jobs, num_jobs, num_partial, per_wave, prefill_units, num_prefill)

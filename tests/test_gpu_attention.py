@@ -216,3 +216,20 @@ def test_partition_sizes_including_global_table_fallback(partition, bs) -> None:
     step = make_step(hq=28, hkv=4, d=128, bs=bs, dtype=torch.bfloat16, computed=[1200, 37, 2600],
                      layouts=_lin(1, 2, 1), seed=partition + bs)
     _run_and_check(step, backend=lv.HipPagedAttentionBackend(partition_tokens=partition))
+
+
+
+def test_two_split_k_layers_share_the_workspace() -> None:
+    _announce("two split-K layers")
+    backend = lv.HipPagedAttentionBackend()
+    step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[3000, 1700, 40],
+                     layouts=_lin(1, 1, 1), num_layers=2, seed=21)
+    ctx = backend.create(step.cache, step.metadata)
+    assert ctx.plan.work(7, 4, lv.native.resident_decode_waves(2, 128)).num_jobs > 0
+    max_tol, mean_tol = tolerances(step.query.dtype)
+    for layer_index in range(2):
+        lid = step.layer_ids[layer_index]
+        out = ctx.forward(lid, step.query, step.key, step.value, scale=step.scale)
+        torch.cuda.synchronize()
+        err = np.abs(out.float().cpu().numpy() - oracle_attention(step, lid))
+        assert err.max() <= max_tol and err.mean() <= mean_tol

@@ -172,6 +172,7 @@ def test_stream_k_pieces_cover_every_segment_once(resident, bs, group) -> None:
     total_tiles = int((-(-seqs // 32) * nct).sum())
     assert waves <= max(resident // 4, 1, -(-total_tiles // cap))
     assert work.tiles_per_wave == -(-total_tiles // waves)
+    share_sizes = []
     covered = {}
     for w in range(waves):
         tiles = 0
@@ -185,7 +186,15 @@ def test_stream_k_pieces_cover_every_segment_once(resident, bs, group) -> None:
             covered.setdefault((req, ctile), []).append((tb, te, slot))
             tiles += -(-(te - tb) // 32)
         assert tiles <= work.tiles_per_wave
-    jobs = {(int(j[0]), int(j[1])): (int(j[2]), int(j[3])) for j in (work.jobs.numpy() if work.num_jobs else [])}
+        share_sizes.append(tiles)
+        # Only a share's first and last pieces can be partial.
+        wave_slots = pieces[first[w] : first[w + 1], 4]
+        assert all(sl < 0 for sl in wave_slots[1:-1])
+    assert max(share_sizes) - min(share_sizes) <= 1 and sum(share_sizes) == total_tiles
+    job_rows = work.jobs.numpy() if work.num_jobs else []
+    jobs = {(int(j[0]), int(j[1])): (int(j[2]), int(j[3])) for j in job_rows}
+    for j in job_rows:  # the merge kernel reads q_start and q_len from the job
+        assert j[4] == md.query_start_loc[j[0]] and j[5] == md.query_lengths[j[0]]
     slots_seen = []
     for r, q in enumerate(md.query_lengths):
         for ct in range(-(-(q * group) // 16)):
@@ -225,16 +234,17 @@ def test_library_loads_and_exports_every_header_function() -> None:
         assert hasattr(lib, name), f"{name} declared in the header but not exported"
         assert name in native.SIGNATURES, f"{name} has no ctypes signature"
     assert lib.lvamd_abi_version() == native.ABI_VERSION
-    assert lib.lvamd_status_string(-3).decode() == "workspace too small"
+    assert lib.lvamd_status_string(-3).decode() == "workspace missing or too small"
     assert lib.lvamd_kv_compact_inline_pairs() == 16
     assert lib.lvamd_kv_compact_workspace_size(17, 28, 1024) == 17 * 28 * 2 * 1024
     # Argument checks run before any HIP call, so they are safe without a GPU.
     assert lib.lvamd_kv_append(None, 0, 0, None, 0, 0, None, None, None, 1, 2, 64, 2, None) == -1
-    assert lib.lvamd_paged_decode(None, 0, 0, None, None, None, 0, 0, None, None, 1, None, None,
+    no_append = (None, 0, 0, None, 0, 0)
+    assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 1, None, None,
                                   None, None, 0, 4, 7, 72, 16, ctypes.c_float(0.1), 2, None) == -2
-    assert lib.lvamd_paged_decode(None, 0, 0, None, None, None, 0, 0, None, None, 1, None, None,
+    assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 1, None, None,
                                   None, None, 0, 4, 7, 128, 16, ctypes.c_float(0.1), 2, None) == -1
-
+    assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 2, None) == -1
 
 def test_backend_refuses_a_cpu_cache() -> None:
     spec = lv.ModelKVCacheSpec((lv.AttentionLayerSpec("attention", 4, 2, 64),))
