@@ -2,7 +2,8 @@
 """Headline benchmark: Qwen2.5-7B-shape paged decode on one MI355X.
 
 One step = one layer's hot path over the batch: the slot-mapped append of one
-new K/V token per sequence, then split-K paged decode attention (+ merge), on
+new K/V token per sequence (fused into the decode kernel), split-K paged decode
+attention and the merge of its partials, through the backend API, on
 seeded synthetic bf16 pools (64 sequences, contexts U[512, 4096], random
 non-overlapping block tables from a 32768-block pool, 28 Q / 4 KV heads,
 head_size 128, block_size 16).
@@ -12,7 +13,9 @@ head_size 128, block_size 16).
   resident in HBM.  Several independent pool sets rotate step by step so the
   256 MB Infinity Cache cannot serve a step from the previous one.
 * ``roofline``   the decode kernel alone: algorithmic bytes per launch / its
-  mean launch time from HIP events on the launch stream, against 8 TB/s.
+  mean launch time from HIP events on the launch stream (batches of
+  back-to-back launches), against 8 TB/s; ``traffic`` is the HBM bytes per
+  launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs.
 * ``cpu_baseline`` the CPU oracle (numpy restatement of light-vllm's Torch
   paged attention + index_copy append) on the same step, on this host.
 
@@ -168,6 +171,23 @@ def copy_calibration(args, device: torch.device) -> int:
     return 0
 
 
+TRAFFIC_SUMMARY = Path(__file__).resolve().parent / "profiles" / "paged_decode_c2_traffic.json"
+
+
+def measured_traffic() -> dict | None:
+    """HBM bytes per decode launch from the committed rocprofv3 counter runs.
+
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the decode kernel, each
+    scaled by what the same counter reads for a plain copy of known size
+    (the summary file records both runs and the factors).
+    """
+
+    if not TRAFFIC_SUMMARY.exists():
+        return None
+    summary = json.loads(TRAFFIC_SUMMARY.read_text())
+    return {"bytes_per_launch": summary["hbm_bytes_per_launch"], "source": TRAFFIC_SUMMARY.name}
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -222,27 +242,34 @@ def main() -> int:
     t0 = time.perf_counter()
     for i in range(args.steps):
         result = step(i)
+    submitted = time.perf_counter() - t0
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed / args.steps * 1e3
     assert torch.isfinite(result.float()).all()
-    print(f"[bench] timed {args.steps} steps: {ms_per_step:.4f} ms/step", file=sys.stderr, flush=True)
+    print(f"[bench] timed {args.steps} steps: {ms_per_step:.4f} ms/step "
+          f"(host submit {submitted / args.steps * 1e3:.4f} ms/step)", file=sys.stderr, flush=True)
 
-    # Decode kernel alone, HIP events on the launch stream (torch's current stream).
+    # Decode kernel alone: HIP events on the launch stream (torch's current
+    # stream) around batches of back-to-back launches, rotating pool sets.
     stream = torch.cuda.current_stream(device)
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    batch = 10
+    rounds = max(1, args.steps // batch)
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(rounds)]
     for i in range(args.warmup):
         launches[i % len(launches)].decode()
-    for i, (a, b) in enumerate(events):
+    for r, (a, b) in enumerate(events):
         a.record(stream)
-        launches[i % len(launches)].decode()
+        for i in range(batch):
+            launches[(r * batch + i) % len(launches)].decode()
         b.record(stream)
     torch.cuda.synchronize()
-    durations = np.array([a.elapsed_time(b) for a, b in events])  # ms
+    durations = np.array([a.elapsed_time(b) for a, b in events]) / batch  # ms per launch
     decode_ms = float(durations.mean())
     achieved = nbytes["decode"] / (decode_ms * 1e-3) / 1e9
-    print(f"[bench] decode kernel: mean {decode_ms * 1e3:.2f} us, p10 {np.percentile(durations, 10) * 1e3:.2f}, "
-          f"p90 {np.percentile(durations, 90) * 1e3:.2f}", file=sys.stderr, flush=True)
+    print(f"[bench] decode kernel: mean {decode_ms * 1e3:.2f} us over {rounds} x {batch} launches, "
+          f"p10 {np.percentile(durations, 10) * 1e3:.2f}, p90 {np.percentile(durations, 90) * 1e3:.2f}",
+          file=sys.stderr, flush=True)
 
     value = nbytes["step"] / (ms_per_step * 1e-3) / 1e9
     record = {
@@ -282,6 +309,10 @@ def main() -> int:
             "algorithmic_bytes_per_launch": nbytes["decode"],
         },
     }
+    traffic = measured_traffic()
+    if traffic is not None:
+        record["roofline"]["traffic"] = traffic["bytes_per_launch"]
+        record["roofline"]["traffic_source"] = traffic["source"]
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
         record["cpu_baseline"] = cpu_baseline(metadata, caches[0], q, k, v, ctx, args.cpu_budget)
