@@ -46,7 +46,7 @@ enum lvamd_dtype { LVAMD_F32 = 0, LVAMD_F16 = 1, LVAMD_BF16 = 2 };
 /* Number of int32 fields per merge job:
  * (req, column_tile, first_partial_slot, num_partials, q_start, q_len, 0, 0). */
 #define LVAMD_MERGE_FIELDS 8
-/* Number of int32 fields per prefill work unit (req, first query of the block, num queries, 0). */
+/* Number of int32 fields per prefill work unit (req, first column, columns, 0). */
 #define LVAMD_PREFILL_FIELDS 4
 
 const char* lvamd_status_string(int status);
@@ -136,11 +136,16 @@ int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
                                 int32_t dtype, lvamd_stream_t stream);
 
 /*
- * Chunked-prefill paged attention for long query runs: one workgroup per
- * (prefill unit, kv head); the unit's queries x the kv head's group of query
- * heads are MFMA columns, K/V tiles are gathered through the block table into
- * LDS and shared by the workgroup's waves.  units [num_units][LVAMD_PREFILL_FIELDS].
- * Replaces the prefill half of the same reference functions as lvamd_paged_decode.
+ * Chunked-prefill paged attention for long query runs (bf16 / fp16, head sizes
+ * 64, 80, 96, 128, 256): one 256-thread workgroup per (unit, kv head); a unit
+ * (units [num_units][LVAMD_PREFILL_FIELDS] = (req, first column, columns, 0))
+ * is a run of MFMA columns of one request, a column being a (query,
+ * head-in-group) pair, column c = query (c / group), head (c % group).  K/V
+ * tiles of 32 tokens are gathered through the block table into LDS and shared
+ * by the workgroup's waves; QK^T and PV on MFMA 16x16x32, fp32 online softmax.
+ * The pool must already hold this step's K/V (lvamd_kv_append).  req_meta is
+ * [batch][LVAMD_REQ_FIELDS].  Replaces the prefill half of the same reference
+ * functions as lvamd_paged_decode.
  */
 int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stride,
                         const void* key_pool, const void* value_pool,
@@ -149,6 +154,10 @@ int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_st
                         const int32_t* units, int32_t num_units,
                         int32_t num_kv_heads, int32_t group, int32_t head_size,
                         int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream);
+
+/* Columns per prefill unit for this dtype and head size (the planner's unit
+ * width), or 0 when the prefill kernel does not support them. */
+int lvamd_paged_prefill_unit_columns(int32_t dtype, int32_t head_size);
 
 /*
  * Tree-KV compact across all layers: for every layer l and pair i,

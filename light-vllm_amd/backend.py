@@ -75,8 +75,9 @@ def _rows_aligned(t: Tensor) -> bool:
 class HipPagedAttention:
     """Per-step context: writes each layer's K/V, then runs paged attention."""
 
-    def __init__(self, cache, metadata, workspace: _Workspace, plan: StepPlan) -> None:
+    def __init__(self, cache, metadata, workspace: _Workspace, plan: StepPlan, use_prefill: bool = True) -> None:
         self._cache = cache
+        self._use_prefill = use_prefill
         self._metadata = metadata
         self._layer_ids: set[str] = set()
         self._workspace = workspace
@@ -154,8 +155,10 @@ class HipPagedAttention:
 
     def _work(self, spec, dtype):
         group = spec.num_query_heads // spec.num_kv_heads
-        resident = native.resident_decode_waves(dtype_code(dtype), spec.head_size)
-        return self._plan.work(group, spec.num_kv_heads, resident)
+        code = dtype_code(dtype)
+        resident = native.resident_decode_waves(code, spec.head_size)
+        columns = native.prefill_unit_columns(code, spec.head_size) if self._use_prefill else 0
+        return self._plan.work(group, spec.num_kv_heads, resident, columns)
 
     def prefill(self, layer_id: str, query: Tensor, out: Tensor, *, scale: float) -> None:
         spec = self._cache.layer_spec(layer_id)
@@ -229,9 +232,11 @@ class HipPagedAttentionBackend:
     the validated, staged plan.
     """
 
-    def __init__(self, *, use_prefill_kernel: bool = False, partition_tokens: int | None = None) -> None:
-        """``partition_tokens`` caps the tokens one decode wave handles (a tuning
-        knob; by default the planner spreads the work over every resident wave)."""
+    def __init__(self, *, use_prefill_kernel: bool = True, partition_tokens: int | None = None) -> None:
+        """``use_prefill_kernel=False`` sends every request through the decode
+        kernel; ``partition_tokens`` caps the tokens one decode wave handles (a
+        tuning knob; by default the planner spreads the work over every
+        resident wave)."""
 
         native.load()
         if partition_tokens is not None and (partition_tokens <= 0 or partition_tokens % 32):
@@ -252,6 +257,6 @@ class HipPagedAttentionBackend:
                 raise KVCacheError("HIP paged attention requires a GPU KV cache")
             metadata.validate_block_tables(num_blocks=config.num_blocks, block_size=config.block_size)
             plan = StepPlan(metadata, block_size=config.block_size, device=config.device,
-                            use_prefill=self._use_prefill, partition_tokens=self._partition_tokens)
+                            partition_tokens=self._partition_tokens)
             self._last = (key, metadata, plan)
-        return HipPagedAttention(cache, metadata, self._workspace, plan)
+        return HipPagedAttention(cache, metadata, self._workspace, plan, self._use_prefill)

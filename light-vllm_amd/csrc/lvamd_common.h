@@ -36,19 +36,26 @@ template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float x) { return
 
 template <typename T> __device__ __forceinline__ float to_f32(T x) { return (float)x; }
 
-// Wave64 butterfly across the four 16-lane rows (xor 16, xor 32).
-__device__ __forceinline__ float wave_max_across_rows(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return v;
-}
-__device__ __forceinline__ float wave_sum_across_rows(float v) {
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
-}
-
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
+
+// Max / sum across the four 16-lane rows of a wave64 (xor 16 then xor 32),
+// with permlane swaps in VALU (no LDS traffic).
+__device__ __forceinline__ float row_max4(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float row_sum4(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
 // MFMA building blocks per storage type.
 template <typename T> struct Mma;
@@ -74,38 +81,6 @@ template <> struct Mma<float> {
     return c;
   }
 };
-
-// O^T[16n + l%16][col] += sum_t V[t][16n + l%16] * P[col][t] over a 32-token tile held
-// in LDS as natural rows (stride RSE elements), with P in the S^T accumulator
-// layout: p[s][r] is token 16s + 4*(l/16) + r of this lane's column.
-template <typename T, int RSE>
-__device__ __forceinline__ f32x4 pv_tile(const T* vt, int n, int l16, int g, const float (&p)[2][4], f32x4 acc) {
-  if constexpr (sizeof(T) == 2) {
-    using V8 = typename std::conditional<std::is_same<T, __bf16>::value, bf16x8, f16x8>::type;
-    V8 av, b;
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        av[s * 4 + r] = vt[(16 * s + 4 * g + r) * RSE + 16 * n + l16];
-        b[s * 4 + r] = from_f32<T>(p[s][r]);
-      }
-    if constexpr (std::is_same<T, __bf16>::value) {
-      return __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b, acc, 0, 0, 0);
-    } else {
-      return __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc, 0, 0, 0);
-    }
-  } else {
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float av = vt[(16 * s + 4 * g + r) * RSE + 16 * n + l16];
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, p[s][r], acc, 0, 0, 0);
-      }
-    return acc;
-  }
-}
 
 template <typename T, int D>
 struct TileShape {

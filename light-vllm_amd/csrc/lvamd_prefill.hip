@@ -1,5 +1,350 @@
-// Chunked-prefill paged attention (MFMA) — entry point.
+// Chunked-prefill paged attention on gfx950: long query runs (prompt chunks,
+// long tree verifications) of bf16/fp16 requests.
+//
+// Semantics are those of the decode kernel (light-vllm TorchPagedAttention,
+// src/light_vllm/runtime/execution/paged_attention.py:323-380): query j of a
+// request with c computed tokens sees logical positions [0, c) and
+// {c + i : i <= j} (linear) or {c + i : i an ancestor of j, or j} (tree);
+// q head h reads kv head h / group; fp32 scores and softmax.
+//
+// Mapping onto CDNA4:
+//   * A work unit is up to 16 * kColTilesPerWave(D) * 4 MFMA columns of one
+//     request, a column being a (query, head-in-group) pair of one kv head, so
+//     the GQA group shares every K/V byte.  One 256-thread workgroup per
+//     (unit, kv head); each of its four waves owns kColTilesPerWave column
+//     tiles of 16.
+//   * Keys go in 32-token tiles: the workgroup gathers a tile's K and V rows
+//     through the block table (16-byte coalesced loads, table entries
+//     prefetched two tiles ahead) into registers, then into a double-buffered
+//     LDS tile, one barrier per tile; the loads of tile t+1 are in flight
+//     while tile t computes.
+//   * S^T = K Q^T on MFMA 16x16x32: the K A operand is read from LDS once per
+//     wave and used for all its column tiles; the accumulator layout (lane l:
+//     column l%16, keys 4*(l/16)+r) is the B operand of O^T = V^T P^T, whose
+//     V^T A operand comes from LDS by ds_read_b64_tr_b16 transpose reads, also
+//     shared by the column tiles.
+//   * Online softmax in the log2 domain with lazy rescaling (wave vote), max
+//     and sum across the four 16-lane rows with permlane swaps.
+
+#include <cmath>
+#include <type_traits>
+
 #include "lvamd_common.h"
+
+namespace lvamd {
+
+namespace {
+
+constexpr float kRescaleSlack = 8.0f;  // log2 units: probabilities stay below 2^8
+constexpr int kKeyTile = 32;
+constexpr int kThreads = 256;
+
+}  // namespace
+
+// Column tiles of 16 per wave: 4 (64 columns) up to D = 128, 2 for D = 256,
+// which keeps the O^T accumulators within the accumulation registers.
+constexpr int prefill_col_tiles_per_wave(int d) { return d <= 128 ? 4 : 2; }
+constexpr int prefill_unit_columns(int d) { return 16 * prefill_col_tiles_per_wave(d) * (kThreads / 64); }
+
+template <typename T, int D>
+struct PrefillShape {
+  static constexpr int CPR = D * (int)sizeof(T) / 16;          // 16-byte chunks per row
+  static constexpr int RS = D * (int)sizeof(T) + 16;           // LDS row stride in bytes (bank spread)
+  static constexpr int LPT = (kKeyTile * CPR + kThreads - 1) / kThreads;  // chunks per thread per tile
+  static constexpr int CT = prefill_col_tiles_per_wave(D);
+  static constexpr int NCH = (D + 31) / 32;                    // 16x16x32 k-steps of QK^T
+  static constexpr int NT = D / 16;                            // 16-row tiles of O^T
+  static constexpr int TILE_BYTES = kKeyTile * RS;
+  static_assert(sizeof(T) == 2, "the prefill kernel is built for 16-bit types");
+};
+
+struct PrefillArgs {
+  const void* q;
+  int64_t q_tok_stride, q_head_stride;
+  const void* k_pool;
+  const void* v_pool;
+  void* out;
+  int64_t out_tok_stride, out_head_stride;
+  const int32_t* __restrict__ req_meta;  // [B][LVAMD_REQ_FIELDS]
+  const int32_t* __restrict__ tables;
+  const uint32_t* __restrict__ vis;
+  const int32_t* __restrict__ units;     // [n][LVAMD_PREFILL_FIELDS]
+  int32_t num_kv_heads;
+  int32_t group;
+  int32_t block_size;
+  int32_t bs_shift;
+  float scale_log2;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a) {
+  using P = PrefillShape<T, D>;
+  constexpr int CPR = P::CPR, RS = P::RS, LPT = P::LPT, CT = P::CT, NCH = P::NCH, NT = P::NT;
+  using V8 = typename std::conditional<std::is_same<T, __bf16>::value, bf16x8, f16x8>::type;
+  __shared__ __attribute__((aligned(16))) char klds[2][P::TILE_BYTES];
+  __shared__ __attribute__((aligned(16))) char vlds[2][P::TILE_BYTES];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int l16 = lane & 15;
+  const int g = lane >> 4;
+  const int Hkv = a.num_kv_heads;
+  const int G = a.group;
+  const int unit = blockIdx.x / Hkv;
+  const int kvh = blockIdx.x - unit * Hkv;
+  const int32_t* u = a.units + (int64_t)unit * LVAMD_PREFILL_FIELDS;
+  const int req = u[0], col0 = u[1], ncols = u[2];
+  const int32_t* rm = a.req_meta + (int64_t)req * LVAMD_REQ_FIELDS;
+  const int table_off = rm[0], computed = rm[2], q_len = rm[3], q_start = rm[4], vis_off = rm[5],
+            vis_words = rm[6];
+  const int col_end = col0 + ncols;  // exclusive, <= q_len * G
+  // Keys the unit needs: up to its last query's position.
+  const int kmax = computed + (col_end - 1) / G + 1;
+  const int ntiles = (kmax + kKeyTile - 1) / kKeyTile;
+
+  const int64_t row_elems = (int64_t)Hkv * D;
+  const T* kbase = static_cast<const T*>(a.k_pool) + (int64_t)kvh * D;
+  const T* vbase = static_cast<const T*>(a.v_pool) + (int64_t)kvh * D;
+
+  auto logical_block = [&](int pos) -> int {
+    return a.bs_shift >= 0 ? (pos >> a.bs_shift) : (pos / a.block_size);
+  };
+
+  // ---- tile gather: chunk i of this thread is (row, chunk) = divmod(tid + 256 i, CPR)
+  auto chunk_pos = [&](int t, int i) -> int {
+    const int idx = tid + kThreads * i;
+    const int pos = t * kKeyTile + (idx < kKeyTile * CPR ? idx / CPR : 0);
+    return pos < kmax ? pos : kmax - 1;  // rows past the unit read its last key (masked)
+  };
+  auto load_entries = [&](int t, int (&te)[LPT]) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) te[i] = a.tables[table_off + logical_block(chunk_pos(t, i))];
+  };
+  auto load_tile = [&](int t, const int (&te)[LPT], uint4 (&kr)[LPT], uint4 (&vr)[LPT]) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int idx = tid + kThreads * i;
+      const int pos = chunk_pos(t, i);
+      const int lb = logical_block(pos);
+      const int64_t off = ((int64_t)te[i] * a.block_size + (pos - lb * a.block_size)) * row_elems +
+                          (idx % CPR) * 8;
+      if (idx < kKeyTile * CPR) {
+        kr[i] = load16(kbase + off);
+        vr[i] = load16(vbase + off);
+      }
+    }
+  };
+  auto store_tile = [&](int b, const uint4 (&kr)[LPT], const uint4 (&vr)[LPT]) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int idx = tid + kThreads * i;
+      if (idx < kKeyTile * CPR) {
+        const int off = (idx / CPR) * RS + (idx % CPR) * 16;
+        *reinterpret_cast<uint4*>(klds[b] + off) = kr[i];
+        *reinterpret_cast<uint4*>(vlds[b] + off) = vr[i];
+      }
+    }
+  };
+
+  // ---- this wave's columns: (query qi, head) per column tile, and Q^T chunks
+  int qi[CT], lin_last[CT];
+  bool cok[CT];
+  const uint32_t* vrow[CT];
+  uint4 qf[CT][NCH];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const int col = col0 + 16 * (CT * wave + ct) + l16;
+    cok[ct] = col < col_end;
+    const int colc = cok[ct] ? col : col_end - 1;
+    qi[ct] = colc / G;
+    const int qhead = kvh * G + (colc - qi[ct] * G);
+    lin_last[ct] = computed + qi[ct];
+    vrow[ct] = vis_off >= 0 ? a.vis + vis_off + (int64_t)qi[ct] * vis_words : nullptr;
+    const T* qrow = static_cast<const T*>(a.q) + (int64_t)(q_start + qi[ct]) * a.q_tok_stride +
+                    (int64_t)qhead * a.q_head_stride;
+#pragma unroll
+    for (int kk = 0; kk < NCH; ++kk) {
+      const int ch = kk * 4 + g;
+      qf[ct][kk] = (cok[ct] && ch < CPR) ? load16(qrow + ch * 8) : zero_u4();
+    }
+  }
+  // Keys this wave's columns can see at most (its last valid query).
+  const int wave_col_last = col0 + 16 * CT * (wave + 1) - 1;
+  const int wave_kmax = computed + ((wave_col_last < col_end ? wave_col_last : col_end - 1) / G) + 1;
+  const bool wave_active = col0 + 16 * CT * wave < col_end;
+  // Tiles below this bound are visible to every column of the unit (for a
+  // tree request only the computed prefix is).
+  const int full_tiles = (vis_off >= 0 ? computed : computed + col0 / G + 1) / kKeyTile;
+
+  float m_run[CT], l_run[CT];
+  f32x4 acc[CT][NT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    m_run[ct] = -INFINITY;
+    l_run[ct] = 0.f;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) acc[ct][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // ---- prologue: tile 0 staged, entries of tiles 1 and 2 in flight
+  int te_next[LPT], te_after[LPT];
+  {
+    int te0[LPT];
+    uint4 kr[LPT], vr[LPT];
+    load_entries(0, te0);
+    load_tile(0, te0, kr, vr);
+    store_tile(0, kr, vr);
+  }
+  if (ntiles > 1) load_entries(1, te_next);
+  if (ntiles > 2) load_entries(2, te_after);
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int b = t & 1;
+    uint4 kr[LPT], vr[LPT];
+    const bool more = t + 1 < ntiles;
+    if (more) load_tile(t + 1, te_next, kr, vr);
+
+    if (wave_active && t * kKeyTile < wave_kmax) {
+      const char* kt = klds[b];
+      const char* vt = vlds[b];
+      // S^T for each column tile, K chunks shared.
+      f32x4 st[CT][2];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) st[ct][0] = st[ct][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int kk = 0; kk < NCH; ++kk) {
+          const int ch = kk * 4 + g;
+          const uint4 kc = ch < CPR ? *reinterpret_cast<const uint4*>(kt + (16 * s + l16) * RS + ch * 16)
+                                    : zero_u4();
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) st[ct][s] = Mma<T>::qk(kc, qf[ct][kk], st[ct][s]);
+        }
+      // Mask, online softmax, P^T operands.
+      const bool need_mask = t >= full_tiles;
+      V8 pb[CT];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        float sv[2][4];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int pos = t * kKeyTile + 16 * s + 4 * g + r;
+            bool vis = true;
+            if (need_mask) {
+              if (pos >= computed) {
+                if (vrow[ct] == nullptr) {
+                  vis = pos <= lin_last[ct];
+                } else {
+                  const int j = pos - computed;
+                  vis = j < q_len && ((vrow[ct][j >> 5] >> (j & 31)) & 1u);
+                }
+              }
+            }
+            const float x = vis ? st[ct][s][r] * a.scale_log2 : -INFINITY;
+            sv[s][r] = x;
+            mt = fmaxf(mt, x);
+          }
+        mt = row_max4(mt);
+        if (__any(mt > m_run[ct] + kRescaleSlack)) {
+          const float m_new = fmaxf(m_run[ct], mt);
+          const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run[ct] - m_new);
+          l_run[ct] *= alpha;
+#pragma unroll
+          for (int n = 0; n < NT; ++n) acc[ct][n] *= alpha;
+          m_run[ct] = m_new;
+        }
+        const float base = (m_run[ct] == -INFINITY) ? 0.f : m_run[ct];
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float p = fast_exp2(sv[s][r] - base);
+            l_run[ct] += p;
+            pb[ct][s * 4 + r] = from_f32<T>(p);
+          }
+      }
+      // O^T += V^T P^T: transpose reads shared by the column tiles.
+      const int q4 = l16 & 3;
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        const int lo = (4 * g + (l16 >> 2)) * RS + (16 * n + 4 * q4) * 2;
+        const int hi = lo + 16 * RS;
+        const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vt + lo));
+        const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vt + hi));
+        const s16x4 both[2] = {v0, v1};
+        const V8 av = bitcast<V8>(both);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          if constexpr (std::is_same<T, __bf16>::value) {
+            acc[ct][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[ct], acc[ct][n], 0, 0, 0);
+          } else {
+            acc[ct][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb[ct], acc[ct][n], 0, 0, 0);
+          }
+        }
+      }
+    }
+
+    if (more) {
+      // Entries two tiles ahead, then the next tile into the other buffer
+      // (read by every wave two barriers ago).
+#pragma unroll
+      for (int i = 0; i < LPT; ++i) te_next[i] = te_after[i];
+      if (t + 3 < ntiles) load_entries(t + 3, te_after);
+      store_tile(b ^ 1, kr, vr);
+    }
+    __syncthreads();
+  }
+
+  // ---- normalised output rows
+  if (!wave_active) return;
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const float l_tot = row_sum4(l_run[ct]);
+    if (!cok[ct]) continue;
+    const int col = col0 + 16 * (CT * wave + ct) + l16;
+    const int qhead = kvh * G + (col - qi[ct] * G);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    T* orow = static_cast<T*>(a.out) + (int64_t)(q_start + qi[ct]) * a.out_tok_stride +
+              (int64_t)qhead * a.out_head_stride;
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) orow[16 * n + 4 * g + r] = from_f32<T>(acc[ct][n][r] * inv);
+  }
+}
+
+template <typename T>
+static int launch_prefill_t(int head_size, dim3 grid, hipStream_t s, const PrefillArgs& a) {
+  switch (head_size) {
+    case 64: hipLaunchKernelGGL((paged_prefill_kernel<T, 64>), grid, dim3(kThreads), 0, s, a); break;
+    case 80: hipLaunchKernelGGL((paged_prefill_kernel<T, 80>), grid, dim3(kThreads), 0, s, a); break;
+    case 96: hipLaunchKernelGGL((paged_prefill_kernel<T, 96>), grid, dim3(kThreads), 0, s, a); break;
+    case 128: hipLaunchKernelGGL((paged_prefill_kernel<T, 128>), grid, dim3(kThreads), 0, s, a); break;
+    case 256: hipLaunchKernelGGL((paged_prefill_kernel<T, 256>), grid, dim3(kThreads), 0, s, a); break;
+    default: return LVAMD_ERR_UNSUPPORTED;
+  }
+  return launch_status();
+}
+
+static bool prefill_supported(int dtype, int head_size) {
+  return (dtype == LVAMD_BF16 || dtype == LVAMD_F16) &&
+         (head_size == 64 || head_size == 80 || head_size == 96 || head_size == 128 || head_size == 256);
+}
+
+}  // namespace lvamd
+
+using namespace lvamd;
+
+extern "C" int lvamd_paged_prefill_unit_columns(int32_t dtype, int32_t head_size) {
+  if (!prefill_supported(dtype, head_size)) return 0;
+  return prefill_unit_columns(head_size);
+}
 
 extern "C" int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stride,
                                    const void* key_pool, const void* value_pool,
@@ -8,8 +353,36 @@ extern "C" int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_
                                    const int32_t* units, int32_t num_units,
                                    int32_t num_kv_heads, int32_t group, int32_t head_size,
                                    int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream) {
-  (void)q; (void)q_token_stride; (void)q_head_stride; (void)key_pool; (void)value_pool; (void)out;
-  (void)out_token_stride; (void)out_head_stride; (void)req_meta; (void)tables; (void)vis; (void)units;
-  (void)num_kv_heads; (void)group; (void)head_size; (void)block_size; (void)scale; (void)dtype; (void)stream;
-  return num_units == 0 ? LVAMD_OK : LVAMD_ERR_UNSUPPORTED;
+  if (num_units < 0 || num_kv_heads <= 0 || group <= 0 || block_size <= 0) return LVAMD_ERR_INVALID_ARGUMENT;
+  if (num_units == 0) return LVAMD_OK;
+  if (!prefill_supported(dtype, head_size)) return LVAMD_ERR_UNSUPPORTED;
+  if (!q || !key_pool || !value_pool || !out || !req_meta || !tables || !vis || !units)
+    return LVAMD_ERR_INVALID_ARGUMENT;
+  const int es = dtype_size(dtype);
+  if (((uintptr_t)q & 15u) || ((uintptr_t)key_pool & 15u) || ((uintptr_t)value_pool & 15u) ||
+      (q_token_stride * es) % 16 != 0 || (q_head_stride * es) % 16 != 0)
+    return LVAMD_ERR_INVALID_ARGUMENT;
+  if ((int64_t)num_units * num_kv_heads > 0x7fffffffLL) return LVAMD_ERR_INVALID_ARGUMENT;
+  PrefillArgs a;
+  a.q = q;
+  a.q_tok_stride = q_token_stride;
+  a.q_head_stride = q_head_stride;
+  a.k_pool = key_pool;
+  a.v_pool = value_pool;
+  a.out = out;
+  a.out_tok_stride = out_token_stride;
+  a.out_head_stride = out_head_stride;
+  a.req_meta = req_meta;
+  a.tables = tables;
+  a.vis = vis;
+  a.units = units;
+  a.num_kv_heads = num_kv_heads;
+  a.group = group;
+  a.block_size = block_size;
+  a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  const dim3 grid((unsigned)(num_units * num_kv_heads));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dtype == LVAMD_BF16 ? launch_prefill_t<__bf16>(head_size, grid, s, a)
+                             : launch_prefill_t<_Float16>(head_size, grid, s, a);
 }

@@ -15,7 +15,7 @@ from pathlib import Path
 from light_vllm_amd.errors import ExecutionError, ExecutionNotReadyError
 
 LIB_NAME = "liblvamd_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
@@ -55,6 +55,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i32,
          _i32, _i32, _i32, _i32, _f32, _i32, _p],
     ),
+    "lvamd_paged_prefill_unit_columns": (ctypes.c_int, [_i32, _i32]),
     "lvamd_kv_compact": (
         ctypes.c_int,
         [_p, _p, _i32, _i64, _p, _p, _i64, _p, _i64, _p],
@@ -111,6 +112,12 @@ def resident_decode_waves(dtype_code: int, head_size: int) -> int:
         check(min(found, 0), "lvamd_paged_decode_resident_waves")
         _RESIDENT[key] = found
     return found
+
+
+def prefill_unit_columns(dtype_code: int, head_size: int) -> int:
+    """Columns per prefill work unit, 0 when the prefill kernel does not cover the shape."""
+
+    return int(load().lvamd_paged_prefill_unit_columns(dtype_code, head_size))
 
 
 def check(status: int, what: str) -> None:

@@ -34,10 +34,8 @@ from torch import Tensor
 from light_vllm_amd.layout import is_linear, query_visibility
 
 # Requests with at most this many queries use the split-K decode kernel;
-# longer runs use the MFMA prefill kernel.
+# longer runs use the MFMA prefill kernel when it covers the layer's shape.
 DECODE_MAX_QUERIES = 16
-# Query tokens per prefill work unit.
-PREFILL_QUERY_BLOCK = 64
 # Compute units of an MI355X; the planner aims for several waves per CU.
 NUM_CUS = 256
 # Block-table entries a decode partition may span (the kernel's LDS slice).
@@ -157,7 +155,6 @@ class StepPlan:
         *,
         block_size: int,
         device: torch.device,
-        use_prefill: bool = True,
         partition_tokens: int | None = None,
     ) -> None:
         self.block_size = block_size
@@ -228,7 +225,6 @@ class StepPlan:
         self.num_tokens = num_tokens
         self.batch_size = batch
         self.has_tree = bool(vis_parts)
-        self.use_prefill = use_prefill
         self.partition_tokens = partition_tokens
 
         self._computed = computed
@@ -237,25 +233,29 @@ class StepPlan:
         self._work: dict[tuple[int, int], DecodeWork] = {}
 
     # -- work lists ---------------------------------------------------------
-    def work(self, group: int, num_kv_heads: int, resident_waves: int = 8 * NUM_CUS) -> DecodeWork:
+    def work(
+        self, group: int, num_kv_heads: int, resident_waves: int = 8 * NUM_CUS, prefill_columns: int = 0
+    ) -> DecodeWork:
         """Work lists for layers of this (group, kv heads) shape.
 
-        ``resident_waves`` is how many decode waves the GPU holds at once (the
-        library reports it per dtype and head size).
+        ``resident_waves`` is how many decode waves the GPU holds at once and
+        ``prefill_columns`` the prefill kernel's unit width (0: every request
+        goes through the decode kernel); the library reports both per dtype and
+        head size.
         """
 
-        key = (group, num_kv_heads, resident_waves)
+        key = (group, num_kv_heads, resident_waves, prefill_columns)
         found = self._work.get(key)
         if found is None:
-            found = self._build_work(group, num_kv_heads, resident_waves)
+            found = self._build_work(group, num_kv_heads, resident_waves, prefill_columns)
             self._work[key] = found
         return found
 
-    def _build_work(self, group: int, num_kv_heads: int, resident_waves: int) -> DecodeWork:
+    def _build_work(self, group: int, num_kv_heads: int, resident_waves: int, prefill_columns: int) -> DecodeWork:
         computed, q_lens = self._computed, self._q_lens
         batch = self.batch_size
         seq = computed + q_lens
-        if self.use_prefill:
+        if prefill_columns > 0:
             decode_rows = q_lens <= DECODE_MAX_QUERIES
         else:
             decode_rows = np.ones(batch, dtype=bool)
@@ -278,17 +278,19 @@ class StepPlan:
                 blocks.append(job_tab.reshape(-1))
         prefill_rows = ~decode_rows
         if prefill_rows.any():
-            nblk = np.where(prefill_rows, -(-q_lens // PREFILL_QUERY_BLOCK), 0)
-            num_prefill = int(nblk.sum())
-            req = np.repeat(np.arange(batch), nblk)
+            # Units of prefill_columns (query, head-in-group) columns.
+            ncols = q_lens * group
+            nunit = np.where(prefill_rows, -(-ncols // prefill_columns), 0)
+            num_prefill = int(nunit.sum())
+            req = np.repeat(np.arange(batch), nunit)
             starts = np.zeros(batch, dtype=np.int64)
-            np.cumsum(nblk[:-1], out=starts[1:])
-            qb = (np.arange(num_prefill) - starts[req]) * PREFILL_QUERY_BLOCK
-            nq = np.minimum(PREFILL_QUERY_BLOCK, q_lens[req] - qb)
-            # Heaviest blocks (most visible keys) first: better tail balance.
-            work = computed[req] + qb + nq
+            np.cumsum(nunit[:-1], out=starts[1:])
+            col0 = (np.arange(num_prefill) - starts[req]) * prefill_columns
+            cols = np.minimum(prefill_columns, ncols[req] - col0)
+            # Heaviest units (keys x columns) first: better tail balance.
+            work = (computed[req] + (col0 + cols - 1) // group + 1) * cols
             order = np.argsort(-work, kind="stable")
-            ptab = np.stack([req[order], qb[order], nq[order], np.zeros(num_prefill, dtype=np.int64)], axis=1)
+            ptab = np.stack([req[order], col0[order], cols[order], np.zeros(num_prefill, dtype=np.int64)], axis=1)
             blocks.append(ptab.reshape(-1))
         if blocks:
             blob = _stage_int32(np.concatenate(blocks), self.device)

@@ -116,6 +116,16 @@ def oracle_attention(step: Step, layer_id: str, query: torch.Tensor | None = Non
     return O.paged_attention(q, k, v, tables, step.metadata.num_computed_tokens, parents, scale=step.scale)
 
 
+def dense_oracle_attention(step: Step, layer_id: str) -> np.ndarray:
+    """Independent fp64 masked-softmax oracle (vectorised per request), for
+    steps too large for the per-query online-softmax restatement."""
+
+    k, v, tables = referenced_pool(step.cache, layer_id, step.metadata)
+    q = step.query.float().cpu().numpy()
+    parents = [l.parent_indices for l in step.metadata.query_layouts]
+    return O.dense_attention(q, k, v, tables, step.metadata.num_computed_tokens, parents, scale=step.scale)
+
+
 def tolerances(dtype: torch.dtype) -> tuple[float, float]:
     """(max-abs, mean-abs) bounds: bf16 2e-2 / 2e-3 and fp32 1e-5 (the target's),
     fp16 3e-3 (the reference Triton test's fp16 atol) / 3e-4."""

@@ -1,0 +1,136 @@
+"""GPU parity of the MFMA chunked-prefill kernel against the CPU oracle.
+
+Requests with more than 16 queries of a bf16/fp16 layer take the prefill
+kernel; shorter ones take the decode kernel in the same step.  Tolerances as in
+paged_cases.tolerances (bf16 max-abs 2e-2 / mean-abs 2e-3, fp16 3e-3 / 3e-4).
+Large steps are checked against the independent fp64 dense oracle.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import light_vllm_amd as lv
+from paged_cases import DTYPES, dense_oracle_attention, make_step, oracle_attention, tolerances
+
+pytestmark = pytest.mark.gpu
+if not torch.cuda.is_available():
+    pytest.skip("needs an MI355X GPU", allow_module_level=True)
+
+DEV = torch.device("cuda:0")
+
+
+def _announce(name: str) -> None:
+    print(f"[gpu] {name}", file=sys.stderr, flush=True)
+
+
+def _lin(*lengths):
+    return [tuple(range(-1, n - 1)) for n in lengths]
+
+
+def _check(step, *, backend=None, dense=False, expect_prefill=True):
+    backend = backend or lv.HipPagedAttentionBackend()
+    ctx = backend.create(step.cache, step.metadata)
+    lid = step.layer_ids[0]
+    out = ctx.forward(lid, step.query, step.key, step.value, scale=step.scale)
+    torch.cuda.synchronize()
+    spec = step.cache.layer_spec(lid)
+    work = ctx._work(spec, step.query.dtype)
+    assert (work.num_prefill_units > 0) == expect_prefill
+    slots = step.metadata.slot_mapping(block_size=step.cache.config.block_size, device=DEV)
+    layer = step.cache.layer(lid)
+    nslots = step.cache.config.num_blocks * step.cache.config.block_size
+    hkv, d = step.key.shape[1:]
+    assert torch.equal(layer.keys.view(nslots, hkv, d).index_select(0, slots), step.key)
+    assert torch.equal(layer.values.view(nslots, hkv, d).index_select(0, slots), step.value)
+    expect = dense_oracle_attention(step, lid) if dense else oracle_attention(step, lid)
+    got = out.float().cpu().numpy()
+    err = np.abs(got - expect)
+    max_tol, mean_tol = tolerances(step.query.dtype)
+    assert np.isfinite(got).all()
+    assert err.max() <= max_tol, f"max-abs {err.max():.3e} > {max_tol}"
+    assert err.mean() <= mean_tol, f"mean-abs {err.mean():.3e} > {mean_tol}"
+    return out
+
+
+@pytest.mark.parametrize("dtype", ("bf16", "fp16"))
+@pytest.mark.parametrize("head_size", (64, 80, 96, 128, 256))
+def test_prefill_head_sizes_and_dtypes(dtype, head_size) -> None:
+    _announce(f"prefill d={head_size} {dtype}")
+    step = make_step(hq=8, hkv=2, d=head_size, bs=16, dtype=DTYPES[dtype], computed=[0, 37, 300, 90],
+                     layouts=_lin(40, 100, 17, 1), seed=head_size + 7)
+    _check(step)
+
+
+@pytest.mark.parametrize("bs", (1, 3, 16, 32))
+def test_prefill_block_sizes(bs) -> None:
+    _announce(f"prefill block size {bs}")
+    step = make_step(hq=28, hkv=4, d=128, bs=bs, dtype=torch.bfloat16, computed=[5, 140, 0],
+                     layouts=_lin(70, 33, 1), seed=100 + bs)
+    _check(step)
+
+
+def test_prefill_unit_boundaries_and_group_sizes() -> None:
+    # 37 queries x 7 heads = 259 columns: two units, the second with 3 columns;
+    # the group of 7 splits queries across column tiles and units.
+    _announce("prefill unit boundaries")
+    step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[64, 0],
+                     layouts=_lin(37, 73), seed=7)
+    _check(step)
+
+
+def test_prefill_tree_visibility() -> None:
+    _announce("prefill tree")
+    rng = np.random.default_rng(11)
+    parents = tuple([-1] + [int(rng.integers(0, i)) for i in range(1, 40)])
+    step = make_step(hq=12, hkv=2, d=128, bs=16, dtype=torch.bfloat16, computed=[100, 33],
+                     layouts=[parents, tuple(range(-1, 20))], seed=11)
+    _check(step)
+
+
+def test_prefill_lookahead_slots_are_not_read() -> None:
+    _announce("prefill lookahead poison")
+    step = make_step(hq=8, hkv=2, d=128, bs=4, dtype=torch.bfloat16, computed=[10, 3],
+                     layouts=_lin(30, 20), reserved=[37, 26], num_blocks=40, seed=3)
+    layer = step.cache.layer(step.layer_ids[0])
+    slots = set(step.metadata.slot_mapping(block_size=4, device=DEV).tolist())
+    flat_k = layer.keys.view(-1, 2, 128)
+    flat_v = layer.values.view(-1, 2, 128)
+    written = set()
+    for table, c in zip(step.metadata.block_tables, step.metadata.num_computed_tokens):
+        for pos in range(c):
+            written.add(table[pos // 4] * 4 + pos % 4)
+    poison = torch.tensor([s for s in range(flat_k.shape[0]) if s not in slots and s not in written], device=DEV)
+    flat_k[poison] = float("nan")
+    flat_v[poison] = float("nan")
+    _check(step)
+
+
+def test_c3_shape_mixed_batch() -> None:
+    # BASELINE C3 at reduced batch: 2 prefill chunks of 512 queries with prior
+    # context, plus 6 decode tokens, Qwen2.5-7B attention shape.
+    _announce("C3-shape mixed batch")
+    rng = np.random.default_rng(3)
+    computed = [int(c) for c in rng.integers(0, 3073, size=2)] + [int(c) for c in rng.integers(256, 4097, size=6)]
+    step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=computed,
+                     layouts=_lin(512, 512, *([1] * 6)), seed=3)
+    _check(step, dense=True)
+
+
+def test_prefill_kernel_agrees_with_the_decode_path() -> None:
+    _announce("prefill vs decode path")
+    step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[200, 0],
+                     layouts=_lin(64, 48), seed=8)
+    a = _check(step)
+    b = _check(step, backend=lv.HipPagedAttentionBackend(use_prefill_kernel=False), expect_prefill=False)
+    assert (a.float() - b.float()).abs().max().item() <= 2e-2
+
+
+def test_fp32_layers_use_the_decode_kernel() -> None:
+    _announce("fp32 long queries")
+    step = make_step(hq=4, hkv=2, d=64, bs=16, dtype=torch.float32, computed=[20], layouts=_lin(40), seed=5)
+    _check(step, expect_prefill=False)

@@ -143,7 +143,7 @@ def test_plan_visibility_bits_match_oracle(seed) -> None:
 def test_plan_request_table_matches_metadata() -> None:
     rng = np.random.default_rng(9)
     md = _random_metadata(rng, batch=9, bs=16)
-    plan = StepPlan(md, block_size=16, device=CPU, use_prefill=False)
+    plan = StepPlan(md, block_size=16, device=CPU)
     meta = plan.req_meta.view(-1, native.REQ_FIELDS).numpy()
     assert meta[:, 2].tolist() == list(md.num_computed_tokens)
     assert meta[:, 3].tolist() == list(md.query_lengths)
@@ -159,7 +159,7 @@ def test_plan_request_table_matches_metadata() -> None:
 def test_stream_k_pieces_cover_every_segment_once(resident, bs, group) -> None:
     rng = np.random.default_rng(resident + bs + group)
     md = _random_metadata(rng, batch=11, bs=bs)
-    plan = StepPlan(md, block_size=bs, device=CPU, use_prefill=False)
+    plan = StepPlan(md, block_size=bs, device=CPU)
     work = plan.work(group, 4, resident)
     pieces = work.pieces.numpy()
     first = work.wave_first.numpy()
@@ -210,20 +210,31 @@ def test_stream_k_pieces_cover_every_segment_once(resident, bs, group) -> None:
     assert sorted(slots_seen) == list(range(work.num_partial_slots))
 
 
-def test_prefill_units_tile_every_long_request() -> None:
-    rng = np.random.default_rng(12)
+@pytest.mark.parametrize("group,columns", ((7, 256), (1, 256), (4, 128)))
+def test_prefill_units_tile_every_long_request(group, columns) -> None:
+    rng = np.random.default_rng(12 + group)
     md = _random_metadata(rng, batch=6, bs=16)
-    plan = StepPlan(md, block_size=16, device=CPU, use_prefill=True)
-    work = plan.work(7, 4)
+    plan = StepPlan(md, block_size=16, device=CPU)
+    work = plan.work(group, 4, 2048, columns)
     seen = {}
-    if work.num_prefill_units:
-        for req, q0, nq, _ in work.prefill_units.numpy():
-            seen.setdefault(int(req), []).extend(range(q0, q0 + nq))
+    keys_prev = None
+    computed = np.asarray(md.num_computed_tokens)
+    for req, c0, n, _ in (work.prefill_units.numpy() if work.num_prefill_units else []):
+        assert 0 < n <= columns
+        seen.setdefault(int(req), []).extend(range(c0, c0 + n))
+        keys = (computed[req] + (c0 + n - 1) // group + 1) * n
+        assert keys_prev is None or keys <= keys_prev  # heaviest first
+        keys_prev = keys
+    decode_reqs = set()
+    if work.waves_per_head:
+        decode_reqs = {int(r) for r in work.pieces.numpy()[:, 0]}
     for r, q in enumerate(md.query_lengths):
         if q > 16:
-            assert sorted(seen[r]) == list(range(q))
+            assert sorted(seen[r]) == list(range(q * group)) and r not in decode_reqs
         else:
-            assert r not in seen
+            assert r not in seen and r in decode_reqs
+    # Without the prefill kernel every request is a decode row.
+    assert plan.work(group, 4, 2048, 0).num_prefill_units == 0
 
 
 def test_library_loads_and_exports_every_header_function() -> None:
