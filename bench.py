@@ -35,6 +35,7 @@ from pathlib import Path
 
 import numpy as np
 import torch
+from threadpoolctl import threadpool_limits
 
 ROOT = Path(__file__).resolve().parent
 if str(ROOT) not in sys.path:
@@ -116,13 +117,14 @@ def cpu_baseline(metadata, cache, q, k, v, ctx, budget_s: float) -> dict:
     scale = 1.0 / math.sqrt(C2.d)
     times = []
     start = time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        O.append(kpool, vpool, kn, vn, slots)
-        O.paged_attention(qn, kpool, vpool, tables, list(metadata.num_computed_tokens), parents, scale=scale)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - start >= budget_s or len(times) >= 50:
-            break
+    with threadpool_limits(1):
+        while True:
+            t0 = time.perf_counter()
+            O.append(kpool, vpool, kn, vn, slots)
+            O.paged_attention(qn, kpool, vpool, tables, list(metadata.num_computed_tokens), parents, scale=scale)
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() - start >= budget_s or len(times) >= 50:
+                break
     step_s = float(np.mean(times))
     return {
         "value": round(algorithmic_bytes(ctx)["step"] / step_s / 1e9, 4),
@@ -188,6 +190,399 @@ def measured_traffic() -> dict | None:
     return {"bytes_per_launch": summary["hbm_bytes_per_launch"], "source": TRAFFIC_SUMMARY.name}
 
 
+# ---------------------------------------------------------------------------
+# The other BASELINE configs (``--config c1|c3|c4|c5``): same backend API, each
+# with its own metric; C2 above is the headline line.
+# ---------------------------------------------------------------------------
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def _linear(n: int):
+    return lv.linear_query_layout(n)
+
+
+def _fill_pools(cache, layer_ids, gen, dtype) -> None:
+    for lid in layer_ids:
+        layer = cache.layer(lid)
+        for pool in (layer.keys, layer.values):
+            pool.copy_(torch.randn(pool.shape, generator=gen, device=pool.device, dtype=torch.float32).to(dtype))
+
+
+def _time_steps(fn, steps: int, warmup: int) -> tuple[float, float]:
+    """(ms per step, host submit ms per step) around ``steps`` calls of fn(i)."""
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fn(i)
+    submitted = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    return elapsed / steps * 1e3, submitted / steps * 1e3
+
+
+def _time_launches(fn, calls: int, warmup: int, device, batch: int = 10) -> float:
+    """Mean ms per fn(i) from HIP events on the current stream around batches of calls."""
+
+    stream = torch.cuda.current_stream(device)
+    for i in range(warmup):
+        fn(i)
+    rounds = max(1, calls // batch)
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(rounds)]
+    for r, (a, b) in enumerate(events):
+        a.record(stream)
+        for i in range(batch):
+            fn(r * batch + i)
+        b.record(stream)
+    torch.cuda.synchronize()
+    return float(np.mean([a.elapsed_time(b) for a, b in events])) / batch
+
+
+def _tables(rng, need, num_blocks, prefix=()):
+    free = [int(b) for b in rng.permutation(num_blocks) if int(b) not in set(prefix)]
+    tables, off = [], 0
+    for n in need:
+        n_private = n - len(prefix)
+        tables.append(tuple(prefix) + tuple(free[off : off + n_private]))
+        off += n_private
+    return tables
+
+
+def _record(*, metric, value, unit, higher, args, ms, dtype, workload, extra) -> dict:
+    rec = {
+        "metric": metric, "value": round(value, 4), "unit": unit, "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": higher, "scaling": "weak",
+        "vs_baseline": None, "dtype": dtype, "data": "synthetic: seeded N(0,1) pools, random block tables",
+        "config": {"workload": workload},
+    }
+    rec.update(extra)
+    return rec
+
+
+def _oracle_pools(cache, layer_id, tables):
+    used = sorted({b for t in tables for b in t})
+    remap = {b: i for i, b in enumerate(used)}
+    idx = torch.tensor(used, dtype=torch.long, device=cache.config.device)
+    layer = cache.layer(layer_id)
+    k = layer.keys.index_select(0, idx).float().cpu().numpy()
+    v = layer.values.index_select(0, idx).float().cpu().numpy()
+    return k, v, [tuple(remap[b] for b in t) for t in tables]
+
+
+def _time_oracle(fn, budget_s: float) -> tuple[float, int]:
+    times = []
+    start = time.perf_counter()
+    with threadpool_limits(1):
+        while True:
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() - start >= budget_s or len(times) >= 20:
+                break
+    return float(np.mean(times)), len(times)
+
+
+class C1:
+    hq, hkv, d, bs, num_blocks = 14, 2, 64, 16, 256
+    ctx = (37, 128, 200, 511)
+    dtype = torch.float32
+    seed = 1
+
+
+def run_c1(args, device) -> int:
+    cfg = C1
+    rng = np.random.default_rng(cfg.seed)
+    need = [(c + 1 + cfg.bs - 1) // cfg.bs for c in cfg.ctx]
+    tables = _tables(rng, need, cfg.num_blocks)
+    md = lv.PagedAttentionMetadata(block_tables=tuple(tables), num_computed_tokens=cfg.ctx,
+                                   query_layouts=tuple(_linear(1) for _ in cfg.ctx))
+    spec = lv.ModelKVCacheSpec((lv.AttentionLayerSpec("layer0", cfg.hq, cfg.hkv, cfg.d),))
+    cache = lv.PagedKVCache(spec, lv.PagedKVCacheConfig(num_blocks=cfg.num_blocks, block_size=cfg.bs,
+                                                        dtype=cfg.dtype, device=device))
+    gen = torch.Generator(device=device).manual_seed(cfg.seed)
+    _fill_pools(cache, ["layer0"], gen, cfg.dtype)
+    b = len(cfg.ctx)
+    q = torch.randn((b, cfg.hq, cfg.d), generator=gen, device=device)
+    k = torch.randn((b, cfg.hkv, cfg.d), generator=gen, device=device)
+    v = torch.randn((b, cfg.hkv, cfg.d), generator=gen, device=device)
+    scale = 1.0 / math.sqrt(cfg.d)
+    backend = lv.HipPagedAttentionBackend()
+    ms, host_ms = _time_steps(lambda i: backend.create(cache, md).forward("layer0", q, k, v, scale=scale),
+                              args.steps, args.warmup)
+    L = np.asarray(cfg.ctx) + 1
+    nbytes = int(L.sum()) * 2 * cfg.hkv * cfg.d * 4 + 2 * b * cfg.hq * cfg.d * 4 + 4 * b * cfg.hkv * cfg.d * 4
+    rec = _record(metric="paged decode step latency, Qwen2.5-0.5B shape fp32 bs4 (C1)", value=ms * 1e3, unit="us",
+                  higher=False, args=args, ms=ms, dtype="f32",
+                  workload="C1: 1 layer, 14 Q / 2 KV heads, D 64, fp32, block 16, pool 256, ctx {37,128,200,511}",
+                  extra={"gbps": round(nbytes / (ms * 1e-3) / 1e9, 2), "host_submit_ms": round(host_ms, 5)})
+    if not args.no_cpu_baseline:
+        from oracle import paged_kv_oracle as O  # checker/baseline only
+
+        kp, vp, otables = _oracle_pools(cache, "layer0", tables)
+        qn, kn, vn = q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy()
+        slots = O.slot_mapping(otables, list(cfg.ctx), [1] * b, [1] * b, cfg.bs)
+
+        def cpu_step():
+            O.append(kp, vp, kn, vn, slots)
+            O.paged_attention(qn, kp, vp, otables, list(cfg.ctx), [(-1,)] * b, scale=scale)
+
+        sec, n = _time_oracle(cpu_step, args.cpu_budget)
+        rec["cpu_baseline"] = {"value": round(sec * 1e6, 1), "unit": "us", "cores": 1, "kind": "port",
+                               "sample": f"full C1 step x{n}, numpy oracle, single thread"}
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+class C3:
+    hq, hkv, d, bs, num_blocks = 28, 4, 128, 16, 32768
+    n_prefill, chunk, prior = 8, 512, (0, 3072)
+    n_decode, ctx = 56, (256, 4096)
+    dtype = torch.bfloat16
+    seed = 3003
+    sets = 3
+
+
+def run_c3(args, device) -> int:
+    cfg = C3
+    rng = np.random.default_rng(cfg.seed)
+    computed = [int(c) for c in rng.integers(cfg.prior[0], cfg.prior[1] + 1, size=cfg.n_prefill)]
+    computed += [int(c) for c in rng.integers(cfg.ctx[0], cfg.ctx[1] + 1, size=cfg.n_decode)]
+    q_lens = [cfg.chunk] * cfg.n_prefill + [1] * cfg.n_decode
+    need = [(c + n + cfg.bs - 1) // cfg.bs for c, n in zip(computed, q_lens)]
+    tables = _tables(rng, need, cfg.num_blocks)
+    md = lv.PagedAttentionMetadata(block_tables=tuple(tables), num_computed_tokens=tuple(computed),
+                                   query_layouts=tuple(_linear(n) for n in q_lens))
+    spec = lv.ModelKVCacheSpec((lv.AttentionLayerSpec("layer0", cfg.hq, cfg.hkv, cfg.d),))
+    config = lv.PagedKVCacheConfig(num_blocks=cfg.num_blocks, block_size=cfg.bs, dtype=cfg.dtype, device=device)
+    gen = torch.Generator(device=device).manual_seed(cfg.seed)
+    caches = []
+    for _ in range(cfg.sets):
+        cache = lv.PagedKVCache(spec, config)
+        _fill_pools(cache, ["layer0"], gen, cfg.dtype)
+        caches.append(cache)
+    t = sum(q_lens)
+    q = torch.randn((t, cfg.hq, cfg.d), generator=gen, device=device).to(cfg.dtype)
+    k = torch.randn((t, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
+    v = torch.randn((t, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
+    scale = 1.0 / math.sqrt(cfg.d)
+    backend = lv.HipPagedAttentionBackend()
+    print(f"[bench] C3: {cfg.n_prefill} x {cfg.chunk} prefill + {cfg.n_decode} decode, T={t}", file=sys.stderr, flush=True)
+    ms, host_ms = _time_steps(
+        lambda i: backend.create(caches[i % len(caches)], md).forward("layer0", q, k, v, scale=scale),
+        args.steps, args.warmup)
+    ctxs = [backend.create(c, md) for c in caches]
+    out = torch.empty_like(q)
+    prefill_ms = _time_launches(lambda i: ctxs[i % len(ctxs)].prefill("layer0", q, out, scale=scale),
+                                args.steps, args.warmup, device)
+    launches = [c.decode_launch("layer0", q, out, scale=scale) for c in ctxs]
+
+    def decode(i):
+        launches[i % len(launches)].decode()
+        launches[i % len(launches)].merge()
+
+    decode_ms = _time_launches(decode, args.steps, args.warmup, device)
+    comp = np.asarray(computed, dtype=np.int64)
+    pre = comp[: cfg.n_prefill]
+    flops = 4 * cfg.hq * cfg.d * int(sum(cfg.chunk * (c + 1) + cfg.chunk * (cfg.chunk - 1) // 2 for c in pre))
+    dec_L = comp[cfg.n_prefill:] + 1
+    dec_bytes = int(dec_L.sum()) * 2 * cfg.hkv * cfg.d * 2 + 2 * cfg.n_decode * cfg.hq * cfg.d * 2
+    tflops = flops / (prefill_ms * 1e-3) / 1e12
+    rec = _record(
+        metric="chunked-prefill mixed step (C3): prefill kernel TFLOP/s vs bf16 MFMA peak, Qwen2.5-7B shape",
+        value=tflops, unit="TFLOP/s", higher=True, args=args, ms=ms, dtype="bf16",
+        workload="C3: 1 layer, 8 prefill chunks of 512 (prior U[0,3072], causal) + 56 decode tokens "
+                 "(ctx U[256,4096]), 28 Q / 4 KV heads, D 128, block 16, T=4152",
+        extra={
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                         "kernel": "paged_prefill_kernel<bf16,128>", "algorithmic_flops_per_launch": flops},
+            "prefill_kernel_us": round(prefill_ms * 1e3, 2),
+            "decode_rows_us": round(decode_ms * 1e3, 2),
+            "decode_rows_gbps": round(dec_bytes / (decode_ms * 1e-3) / 1e9, 1),
+            "step_ms": round(ms, 4), "host_submit_ms": round(host_ms, 5),
+        })
+    if not args.no_cpu_baseline:
+        from oracle import paged_kv_oracle as O  # checker/baseline only
+
+        # Sample: the first 16 queries of the first prefill chunk, all of their keys.
+        nq = 16
+        c0 = computed[0]
+        sample_table = tables[0][: (c0 + nq + cfg.bs - 1) // cfg.bs]
+        kp, vp, otables = _oracle_pools(caches[0], "layer0", [sample_table])
+        qn = q[:nq].float().cpu().numpy()
+        sec, n = _time_oracle(
+            lambda: O.paged_attention(qn, kp, vp, otables, [c0], [tuple(range(-1, nq - 1))], scale=scale),
+            args.cpu_budget)
+        sflops = 4 * cfg.hq * cfg.d * sum(c0 + j + 1 for j in range(nq))
+        rec["cpu_baseline"] = {"value": round(sflops / sec / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+                               "sample": f"16 queries of the first prefill chunk (context {c0}) x{n}, numpy oracle"}
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+class C4:
+    layers, hq, hkv, d, bs, batch, ctx = 28, 28, 4, 128, 16, 16, 32768
+    dtype = torch.bfloat16
+    seed = 4004
+
+
+def run_c4(args, device) -> int:
+    cfg = C4
+    rng = np.random.default_rng(cfg.seed)
+    per_seq = (cfg.ctx + 1 + cfg.bs - 1) // cfg.bs
+    num_blocks = cfg.batch * per_seq + 16
+    tables = _tables(rng, [per_seq] * cfg.batch, num_blocks)
+    md = lv.PagedAttentionMetadata(block_tables=tuple(tables), num_computed_tokens=(cfg.ctx,) * cfg.batch,
+                                   query_layouts=tuple(_linear(1) for _ in range(cfg.batch)))
+    layer_ids = [f"layer{i}" for i in range(cfg.layers)]
+    spec = lv.ModelKVCacheSpec(tuple(lv.AttentionLayerSpec(lid, cfg.hq, cfg.hkv, cfg.d) for lid in layer_ids))
+    cache = lv.PagedKVCache(spec, lv.PagedKVCacheConfig(num_blocks=num_blocks, block_size=cfg.bs,
+                                                        dtype=cfg.dtype, device=device))
+    gen = torch.Generator(device=device).manual_seed(cfg.seed)
+    print(f"[bench] C4: filling {cfg.layers} pools of {num_blocks} blocks", file=sys.stderr, flush=True)
+    _fill_pools(cache, layer_ids, gen, cfg.dtype)
+    q = torch.randn((cfg.batch, cfg.hq, cfg.d), generator=gen, device=device).to(cfg.dtype)
+    k = torch.randn((cfg.batch, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
+    v = torch.randn((cfg.batch, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
+    scale = 1.0 / math.sqrt(cfg.d)
+    backend = lv.HipPagedAttentionBackend()
+
+    def step(i):
+        ctx = backend.create(cache, md)
+        for lid in layer_ids:
+            ctx.forward(lid, q, k, v, scale=scale)
+
+    steps = max(1, min(args.steps, 40))
+    ms, host_ms = _time_steps(step, steps, min(args.warmup, 5))
+    L = cfg.ctx + 1
+    per_layer = cfg.batch * L * 2 * cfg.hkv * cfg.d * 2 + 2 * cfg.batch * cfg.hq * cfg.d * 2 + \
+        cfg.batch * per_seq * 4 + 4 * cfg.batch * cfg.hkv * cfg.d * 2
+    gbps = cfg.layers * per_layer / (ms * 1e-3) / 1e9
+    work = backend.create(cache, md)._work(spec.layers[0], cfg.dtype)
+    rec = _record(
+        metric="long-context paged decode (C4): HBM GB/s over 28 layers + tokens/s, Qwen2.5-7B shape bs16 ctx32k",
+        value=gbps, unit="GB/s", higher=True, args=args, ms=ms, dtype="bf16",
+        workload="C4: 28 layers (one pool each, 30 GB), batch 16, context 32768, 28 Q / 4 KV heads, D 128, "
+                 "block 16, fragmented tables",
+        extra={"steps": steps, "pct_of_hbm_peak": round(100 * gbps / HBM_PEAK_GBS, 2),
+               "tokens_per_s": round(cfg.batch / (ms * 1e-3), 1), "algorithmic_bytes_per_step": cfg.layers * per_layer,
+               "split_k": {"waves_per_head": work.waves_per_head, "partials": work.num_partial_slots,
+                           "merge_jobs": work.num_jobs},
+               "host_submit_ms": round(host_ms, 5)})
+    if not args.no_cpu_baseline:
+        from oracle import paged_kv_oracle as O  # checker/baseline only
+
+        kp, vp, otables = _oracle_pools(cache, "layer0", tables[:1])
+        qn = q[:1].float().cpu().numpy()
+        sec, n = _time_oracle(
+            lambda: O.paged_attention(qn, kp, vp, otables, [cfg.ctx], [(-1,)], scale=scale), args.cpu_budget)
+        rec["cpu_baseline"] = {"value": round(L * 2 * cfg.hkv * cfg.d * 2 / sec / 1e9, 4), "unit": "GB/s",
+                               "cores": 1, "kind": "port",
+                               "sample": f"1 sequence x 1 layer (32769 keys) x{n}, numpy oracle"}
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+class C5:
+    layers, hq, hkv, d, bs, batch = 28, 12, 2, 128, 16, 32
+    prefix, suffix, tree = 2048, (64, 512), 8
+    dtype = torch.bfloat16
+    seed = 5005
+
+
+def run_c5(args, device) -> int:
+    cfg = C5
+    rng = np.random.default_rng(cfg.seed)
+    shared_blocks = cfg.prefix // cfg.bs
+    suffix = [int(s) for s in rng.integers(cfg.suffix[0], cfg.suffix[1] + 1, size=cfg.batch)]
+    computed = [cfg.prefix + s for s in suffix]
+    q_len = 1 + cfg.tree
+    layouts, accepted = [], []
+    for _ in range(cfg.batch):
+        parents = [-1] + [int(rng.integers(0, i)) for i in range(1, cfg.tree)]
+        layouts.append(lv.QueryLayout(tuple([-1] + [0 if p == -1 else p + 1 for p in parents])))
+        leaf = int(rng.integers(0, cfg.tree))
+        path = [leaf]
+        while parents[path[-1]] != -1:
+            path.append(parents[path[-1]])
+        accepted.append((0,) + tuple(sorted(i + 1 for i in path)))
+    need = [(c + q_len + cfg.bs - 1) // cfg.bs for c in computed]
+    num_blocks = shared_blocks + sum(n - shared_blocks + 1 for n in need) + 16
+    perm = [int(b) for b in rng.permutation(num_blocks)]
+    shared = perm[:shared_blocks]
+    free = perm[shared_blocks:]
+    tables, cow_dst, off = [], [], 0
+    for n in need:
+        # The last shared block is copied on write into a private block.
+        private = free[off : off + n - shared_blocks + 1]
+        off += n - shared_blocks + 1
+        cow_dst.append(private[0])
+        tables.append(tuple(shared[:-1]) + tuple(private))
+    cow_src = [shared[-1]] * cfg.batch
+    md = lv.PagedAttentionMetadata(block_tables=tuple(tables), num_computed_tokens=tuple(computed),
+                                   query_layouts=tuple(layouts), num_readonly_prefix_blocks=(shared_blocks - 1,) * cfg.batch)
+    layer_ids = [f"layer{i}" for i in range(cfg.layers)]
+    spec = lv.ModelKVCacheSpec(tuple(lv.AttentionLayerSpec(lid, cfg.hq, cfg.hkv, cfg.d) for lid in layer_ids))
+    cache = lv.PagedKVCache(spec, lv.PagedKVCacheConfig(num_blocks=num_blocks, block_size=cfg.bs,
+                                                        dtype=cfg.dtype, device=device))
+    gen = torch.Generator(device=device).manual_seed(cfg.seed)
+    _fill_pools(cache, layer_ids, gen, cfg.dtype)
+    t = cfg.batch * q_len
+    q = torch.randn((t, cfg.hq, cfg.d), generator=gen, device=device).to(cfg.dtype)
+    k = torch.randn((t, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
+    v = torch.randn((t, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
+    scale = 1.0 / math.sqrt(cfg.d)
+    backend = lv.HipPagedAttentionBackend()
+    compacts = [dict(block_ids=tables[r], num_computed_tokens=computed[r], num_query_tokens=q_len,
+                     num_reserved_query_tokens=q_len, retained_query_indices=accepted[r],
+                     num_readonly_prefix_blocks=shared_blocks - 1) for r in range(cfg.batch)]
+
+    def attend():
+        ctx = backend.create(cache, md)
+        for lid in layer_ids:
+            ctx.forward(lid, q, k, v, scale=scale)
+
+    def step(i):
+        cache.copy_blocks(cow_src, cow_dst)
+        attend()
+        cache.compact_many(compacts)
+
+    ms, host_ms = _time_steps(step, args.steps, args.warmup)
+    cow_ms = _time_launches(lambda i: cache.copy_blocks(cow_src, cow_dst), args.steps, args.warmup, device)
+    attend_ms = _time_launches(lambda i: attend(), max(10, args.steps // 4), 2, device)
+    compact_ms = _time_launches(lambda i: cache.compact_many(compacts), args.steps, args.warmup, device)
+    row = cfg.hkv * cfg.d * 2
+    unique_kv = (cfg.prefix + sum(s + q_len for s in suffix)) * 2 * row
+    cow_bytes = 2 * cfg.batch * cfg.layers * 2 * cfg.bs * row
+    moved = sum(len(a) for a in accepted)
+    rec = _record(
+        metric="prefix-cache + tree verification step (C5): us per step, Qwen2.5-1.5B shape bs32, 28 layers",
+        value=ms * 1e3, unit="us", higher=False, args=args, ms=ms, dtype="bf16",
+        workload="C5: 28 layers, 12 Q / 2 KV heads, D 128, block 16, 32 seqs sharing a 2048-token prefix "
+                 "(last shared block copied on write), private suffix U[64,512], 8-node draft tree each, "
+                 "then compact of an accepted root-to-leaf path",
+        extra={"attention_us": round(attend_ms * 1e3, 2),
+               "attention_unique_gbps": round(cfg.layers * unique_kv / (attend_ms * 1e-3) / 1e9, 1),
+               "cow_copy_us": round(cow_ms * 1e3, 2), "cow_copy_gbps": round(cow_bytes / (cow_ms * 1e-3) / 1e9, 1),
+               "compact_us": round(compact_ms * 1e3, 2), "compact_tokens": moved,
+               "host_submit_ms": round(host_ms, 5)})
+    if not args.no_cpu_baseline:
+        from oracle import paged_kv_oracle as O  # checker/baseline only
+
+        kp, vp, otables = _oracle_pools(cache, "layer0", tables)
+        qn = q.float().cpu().numpy()
+        parents = [l.parent_indices for l in layouts]
+        sec, n = _time_oracle(lambda: O.paged_attention(qn, kp, vp, otables, computed, parents, scale=scale),
+                              args.cpu_budget)
+        rec["cpu_baseline"] = {"value": round(sec * cfg.layers * 1e6, 1), "unit": "us", "cores": 1, "kind": "port",
+                               "sample": f"tree attention of 1 layer (32 seqs) x{n}, numpy oracle, "
+                                         f"x28 layers extrapolated (COW and compact not included)"}
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -201,6 +596,8 @@ def main() -> int:
                              "copy of known size (counter calibration and the practical HBM ceiling)")
     parser.add_argument("--partition", type=int, default=None,
                         help="cap on the tokens one decode wave handles (default: spread over all resident waves)")
+    parser.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5"), default="c2",
+                        help="BASELINE config (default c2, the headline metric); the others report their own metric")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -212,6 +609,8 @@ def main() -> int:
     device = torch.device("cuda:0")
     if args.mode == "copy":
         return copy_calibration(args, device)
+    if args.config != "c2":
+        return {"c1": run_c1, "c3": run_c3, "c4": run_c4, "c5": run_c5}[args.config](args, device)
     print(f"[bench] building C2 workload, {args.sets} pool sets", file=sys.stderr, flush=True)
     metadata, caches, q, k, v, ctx = build_workload(args.sets, device)
     nbytes = algorithmic_bytes(ctx)

@@ -201,8 +201,39 @@ def hip_compact(cache, block_ids: tuple[int, ...], **kwargs) -> int:
     _require_gpu(cache)
     sources, targets = compact_slots(cache.config, block_ids, **kwargs)
     moved = [(s, t) for s, t in zip(sources, targets) if s != t]
+    _launch_compact(cache, moved)
+    return len(moved)
+
+
+def hip_compact_many(cache, requests) -> tuple[int, ...]:
+    """``hip_compact`` for several requests of one step in a single launch.
+
+    Each request is a mapping of ``hip_compact``'s keyword arguments
+    (``block_ids``, ``num_computed_tokens``, ...), validated exactly as a
+    single compact; destinations must be unique across the batch (every
+    source is read before any destination is written, as for one request).
+    Returns each request's moved-token count.
+    """
+
+    _require_gpu(cache)
+    moved: list[tuple[int, int]] = []
+    counts = []
+    for request in requests:
+        kwargs = dict(request)
+        block_ids = kwargs.pop("block_ids")
+        sources, targets = compact_slots(cache.config, tuple(block_ids), **kwargs)
+        pairs = [(s, t) for s, t in zip(sources, targets) if s != t]
+        counts.append(len(pairs))
+        moved += pairs
+    if len({t for _, t in moved}) != len(moved):
+        raise KVCacheError("compact requests of one step must not write the same slot")
+    _launch_compact(cache, moved)
+    return tuple(counts)
+
+
+def _launch_compact(cache, moved: list[tuple[int, int]]) -> None:
     if not moved:
-        return 0
+        return
     device = cache.config.device
     pairs = torch.tensor(moved, dtype=torch.int64).t().contiguous()
     if device.type == "cuda":
@@ -220,7 +251,6 @@ def hip_compact(cache, block_ids: tuple[int, ...], **kwargs) -> int:
             workspace.data_ptr() if workspace is not None else None, ws_bytes, stream,
         )
         native.check(status, "lvamd_kv_compact")
-    return n
 
 
 def hip_block_copy(cache, src_blocks, dst_blocks) -> None:
@@ -376,6 +406,13 @@ class PagedKVCache:
             retained_query_indices=retained_query_indices,
             num_readonly_prefix_blocks=num_readonly_prefix_blocks,
         )
+
+    @torch.inference_mode()
+    def compact_many(self, requests) -> tuple[int, ...]:
+        """``compact`` for every request of a step in one launch (one mapping of
+        ``compact``'s arguments, with ``block_ids``, per request)."""
+
+        return hip_compact_many(self, requests)
 
     @torch.inference_mode()
     def copy_blocks(self, src_blocks, dst_blocks) -> None:

@@ -146,6 +146,43 @@ def test_compact_matches_oracle_across_layers(n_retained) -> None:
         np.testing.assert_array_equal(_bits(cache.layer(f"l{i}").values), vb)
 
 
+@pytest.mark.parametrize("n_requests", [1, 3, 32])
+def test_compact_many_matches_per_request_oracle(n_requests) -> None:
+    # One launch for every request of a step: the same bytes as compacting the
+    # requests one by one (oracle), and the same moved counts.
+    _announce(f"compact many x{n_requests}")
+    rng = np.random.default_rng(100 + n_requests)
+    bs, layers, computed, q = 16, 3, 29, 9
+    per_req = (computed + q + bs - 1) // bs
+    nb = per_req * n_requests + 5
+    cache = _cache(hkv=2, d=128, bs=bs, nb=nb, dtype=torch.bfloat16, layers=layers, hq=12)
+    perm = [int(x) for x in rng.permutation(nb)]
+    pools = [(_bits(cache.layer(f"l{i}").keys), _bits(cache.layer(f"l{i}").values)) for i in range(layers)]
+    requests, expect = [], []
+    for r in range(n_requests):
+        table = tuple(perm[r * per_req : (r + 1) * per_req])
+        n_keep = int(rng.integers(1, q + 1))
+        retained = tuple(sorted(int(i) for i in rng.permutation(q)[:n_keep]))
+        args = dict(num_computed_tokens=computed, num_query_tokens=q, num_reserved_query_tokens=q,
+                    retained_query_indices=retained)
+        expect.append(O.compact(pools, table, num_blocks=nb, block_size=bs, **args))
+        requests.append(dict(block_ids=table, **args))
+    moved = cache.compact_many(requests)
+    torch.cuda.synchronize()
+    assert moved == tuple(expect)
+    for i, (kb, vb) in enumerate(pools):
+        np.testing.assert_array_equal(_bits(cache.layer(f"l{i}").keys), kb)
+        np.testing.assert_array_equal(_bits(cache.layer(f"l{i}").values), vb)
+
+
+def test_compact_many_rejects_a_shared_destination() -> None:
+    cache = _cache(hkv=2, d=64, bs=2, nb=8, dtype=torch.float32)
+    req = dict(block_ids=(0, 1), num_computed_tokens=1, num_query_tokens=2, num_reserved_query_tokens=2,
+               retained_query_indices=(1,))
+    with pytest.raises(lv.KVCacheError, match="same slot"):
+        cache.compact_many([req, req])
+
+
 def test_compact_identity_path_writes_nothing_and_returns_zero() -> None:
     cache = _cache(hkv=2, d=64, bs=4, nb=8, dtype=torch.float32)
     before = _bits(cache.layer("l0").keys)
