@@ -8,16 +8,16 @@
 // q head h reads kv head h / group; fp32 scores and softmax.
 //
 // Mapping onto CDNA4:
-//   * A work unit is up to 16 * kColTilesPerWave(D) * 4 MFMA columns of one
-//     request, a column being a (query, head-in-group) pair of one kv head, so
-//     the GQA group shares every K/V byte.  One 256-thread workgroup per
-//     (unit, kv head); each of its four waves owns kColTilesPerWave column
-//     tiles of 16.
-//   * Keys go in 32-token tiles: the workgroup gathers a tile's K and V rows
-//     through the block table (16-byte coalesced loads, table entries
-//     prefetched two tiles ahead) into registers, then into a double-buffered
-//     LDS tile, one barrier per tile; the loads of tile t+1 are in flight
-//     while tile t computes.
+//   * A work unit is up to 16 * prefill_col_tiles_per_wave(D) * 4 MFMA columns
+//     of one request, a column being a (query, head-in-group) pair of one kv
+//     head, so the GQA group shares every K/V byte.  One 256-thread workgroup
+//     per (unit, kv head); each of its four waves owns
+//     prefill_col_tiles_per_wave(D) column tiles of 16.
+//   * Keys go in 64-token tiles (32 for D = 256): the workgroup gathers a tile's K and V rows
+//     through the block table (16-byte coalesced loads) into registers, then
+//     into a double-buffered LDS tile, one barrier per tile.  While tile t
+//     computes, tile t+1 waits in registers, tile t+2's loads are in flight
+//     and tile t+3's table entries are being fetched.
 //   * S^T = K Q^T on MFMA 16x16x32: the K A operand is read from LDS once per
 //     wave and used for all its column tiles; the accumulator layout (lane l:
 //     column l%16, keys 4*(l/16)+r) is the B operand of O^T = V^T P^T, whose
@@ -36,25 +36,36 @@ namespace lvamd {
 namespace {
 
 constexpr float kRescaleSlack = 8.0f;  // log2 units: probabilities stay below 2^8
-constexpr int kKeyTile = 32;
 constexpr int kThreads = 256;
 
 }  // namespace
 
-// Column tiles of 16 per wave: 4 (64 columns) up to D = 128, 2 for D = 256,
-// which keeps the O^T accumulators within the accumulation registers.
-constexpr int prefill_col_tiles_per_wave(int d) { return d <= 128 ? 4 : 2; }
+#ifndef LVAMD_PREFILL_CT
+#define LVAMD_PREFILL_CT 2
+#endif
+#ifndef LVAMD_PREFILL_KT
+#define LVAMD_PREFILL_KT 64
+#endif
+// Column tiles of 16 per wave and keys per LDS tile.  Two column tiles keep
+// the wave within 256 registers, so two workgroups share a CU; measured on C3
+// (bf16, D = 128, three-stage pipeline): 190 us at two tiles / 64 keys,
+// 213 us at two tiles / 32 keys, 468 us at four tiles (one wave per SIMD).
+constexpr int prefill_col_tiles_per_wave(int d) { return d <= 128 ? LVAMD_PREFILL_CT : 2; }
+constexpr int prefill_key_tile(int d) { return d <= 128 ? LVAMD_PREFILL_KT : 32; }
 constexpr int prefill_unit_columns(int d) { return 16 * prefill_col_tiles_per_wave(d) * (kThreads / 64); }
 
 template <typename T, int D>
 struct PrefillShape {
+  static constexpr int KT = prefill_key_tile(D);               // keys per tile
+  static constexpr int KS = KT / 16;                           // 16-key groups per tile
   static constexpr int CPR = D * (int)sizeof(T) / 16;          // 16-byte chunks per row
   static constexpr int RS = D * (int)sizeof(T) + 16;           // LDS row stride in bytes (bank spread)
-  static constexpr int LPT = (kKeyTile * CPR + kThreads - 1) / kThreads;  // chunks per thread per tile
+  static constexpr int LPT = (KT * CPR + kThreads - 1) / kThreads;  // chunks per thread per tile
   static constexpr int CT = prefill_col_tiles_per_wave(D);
   static constexpr int NCH = (D + 31) / 32;                    // 16x16x32 k-steps of QK^T
   static constexpr int NT = D / 16;                            // 16-row tiles of O^T
-  static constexpr int TILE_BYTES = kKeyTile * RS;
+  static constexpr int TILE_BYTES = KT * RS;
+  static_assert(KT % 32 == 0, "PV steps take 32 keys");
   static_assert(sizeof(T) == 2, "the prefill kernel is built for 16-bit types");
 };
 
@@ -77,9 +88,10 @@ struct PrefillArgs {
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void paged_prefill_kernel(const PrefillArgs a) {
   using P = PrefillShape<T, D>;
   constexpr int CPR = P::CPR, RS = P::RS, LPT = P::LPT, CT = P::CT, NCH = P::NCH, NT = P::NT;
+  constexpr int KT = P::KT, KS = P::KS;
   using V8 = typename std::conditional<std::is_same<T, __bf16>::value, bf16x8, f16x8>::type;
   __shared__ __attribute__((aligned(16))) char klds[2][P::TILE_BYTES];
   __shared__ __attribute__((aligned(16))) char vlds[2][P::TILE_BYTES];
@@ -101,35 +113,42 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a)
   const int col_end = col0 + ncols;  // exclusive, <= q_len * G
   // Keys the unit needs: up to its last query's position.
   const int kmax = computed + (col_end - 1) / G + 1;
-  const int ntiles = (kmax + kKeyTile - 1) / kKeyTile;
+  const int ntiles = (kmax + KT - 1) / KT;
+  const int bs = a.block_size;
 
   const int64_t row_elems = (int64_t)Hkv * D;
-  const T* kbase = static_cast<const T*>(a.k_pool) + (int64_t)kvh * D;
-  const T* vbase = static_cast<const T*>(a.v_pool) + (int64_t)kvh * D;
+  const T* kbase = static_cast<const T*>(a.k_pool);
+  const T* vbase = static_cast<const T*>(a.v_pool);
+  const int32_t* table = a.tables + table_off;
 
-  auto logical_block = [&](int pos) -> int {
-    return a.bs_shift >= 0 ? (pos >> a.bs_shift) : (pos / a.block_size);
-  };
-
-  // ---- tile gather: chunk i of this thread is (row, chunk) = divmod(tid + 256 i, CPR)
-  auto chunk_pos = [&](int t, int i) -> int {
+  // ---- tile gather.  Chunk i of this thread is row rw[i], 16-byte chunk
+  // (idx % CPR) of the tile (idx = tid + 256 i); both fixed for the kernel.
+  int rw[LPT];
+  int64_t cofs[LPT];
+  bool cok[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
     const int idx = tid + kThreads * i;
-    const int pos = t * kKeyTile + (idx < kKeyTile * CPR ? idx / CPR : 0);
+    cok[i] = idx < KT * CPR;
+    rw[i] = cok[i] ? idx / CPR : 0;
+    cofs[i] = (int64_t)kvh * D + (idx % CPR) * 8;
+  }
+  auto key_pos = [&](int t, int i) -> int {
+    const int pos = t * KT + rw[i];
     return pos < kmax ? pos : kmax - 1;  // rows past the unit read its last key (masked)
   };
+  auto logical_block = [&](int pos) -> int { return a.bs_shift >= 0 ? (pos >> a.bs_shift) : (pos / bs); };
   auto load_entries = [&](int t, int (&te)[LPT]) {
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) te[i] = a.tables[table_off + logical_block(chunk_pos(t, i))];
+    for (int i = 0; i < LPT; ++i) te[i] = table[logical_block(key_pos(t, i))];
   };
   auto load_tile = [&](int t, const int (&te)[LPT], uint4 (&kr)[LPT], uint4 (&vr)[LPT]) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const int idx = tid + kThreads * i;
-      const int pos = chunk_pos(t, i);
-      const int lb = logical_block(pos);
-      const int64_t off = ((int64_t)te[i] * a.block_size + (pos - lb * a.block_size)) * row_elems +
-                          (idx % CPR) * 8;
-      if (idx < kKeyTile * CPR) {
+      const int pos = key_pos(t, i);
+      const uint32_t slot = (uint32_t)te[i] * (uint32_t)bs + (uint32_t)(pos - logical_block(pos) * bs);
+      const int64_t off = (int64_t)slot * row_elems + cofs[i];
+      if (cok[i]) {
         kr[i] = load16(kbase + off);
         vr[i] = load16(vbase + off);
       }
@@ -138,9 +157,9 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a)
   auto store_tile = [&](int b, const uint4 (&kr)[LPT], const uint4 (&vr)[LPT]) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const int idx = tid + kThreads * i;
-      if (idx < kKeyTile * CPR) {
-        const int off = (idx / CPR) * RS + (idx % CPR) * 16;
+      if (cok[i]) {
+        const int idx = tid + kThreads * i;
+        const int off = rw[i] * RS + (idx % CPR) * 16;
         *reinterpret_cast<uint4*>(klds[b] + off) = kr[i];
         *reinterpret_cast<uint4*>(vlds[b] + off) = vr[i];
       }
@@ -149,14 +168,14 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a)
 
   // ---- this wave's columns: (query qi, head) per column tile, and Q^T chunks
   int qi[CT], lin_last[CT];
-  bool cok[CT];
+  bool colok[CT];
   const uint32_t* vrow[CT];
   uint4 qf[CT][NCH];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     const int col = col0 + 16 * (CT * wave + ct) + l16;
-    cok[ct] = col < col_end;
-    const int colc = cok[ct] ? col : col_end - 1;
+    colok[ct] = col < col_end;
+    const int colc = colok[ct] ? col : col_end - 1;
     qi[ct] = colc / G;
     const int qhead = kvh * G + (colc - qi[ct] * G);
     lin_last[ct] = computed + qi[ct];
@@ -166,7 +185,7 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a)
 #pragma unroll
     for (int kk = 0; kk < NCH; ++kk) {
       const int ch = kk * 4 + g;
-      qf[ct][kk] = (cok[ct] && ch < CPR) ? load16(qrow + ch * 8) : zero_u4();
+      qf[ct][kk] = (colok[ct] && ch < CPR) ? load16(qrow + ch * 8) : zero_u4();
     }
   }
   // Keys this wave's columns can see at most (its last valid query).
@@ -175,9 +194,11 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a)
   const bool wave_active = col0 + 16 * CT * wave < col_end;
   // Tiles below this bound are visible to every column of the unit (for a
   // tree request only the computed prefix is).
-  const int full_tiles = (vis_off >= 0 ? computed : computed + col0 / G + 1) / kKeyTile;
+  const int full_tiles = (vis_off >= 0 ? computed : computed + col0 / G + 1) / KT;
+  const bool tree = vis_off >= 0;
+  const float c_log2 = a.scale_log2;
 
-  float m_run[CT], l_run[CT];
+  float m_run[CT], l_run[CT];  // m_run in the scaled log2 domain
   f32x4 acc[CT][NT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
@@ -187,93 +208,81 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a)
     for (int n = 0; n < NT; ++n) acc[ct][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // ---- prologue: tile 0 staged, entries of tiles 1 and 2 in flight
-  int te_next[LPT], te_after[LPT];
-  {
-    int te0[LPT];
-    uint4 kr[LPT], vr[LPT];
-    load_entries(0, te0);
-    load_tile(0, te0, kr, vr);
-    store_tile(0, kr, vr);
-  }
-  if (ntiles > 1) load_entries(1, te_next);
-  if (ntiles > 2) load_entries(2, te_after);
-  __syncthreads();
-
-  for (int t = 0; t < ntiles; ++t) {
-    const int b = t & 1;
-    uint4 kr[LPT], vr[LPT];
-    const bool more = t + 1 < ntiles;
-    if (more) load_tile(t + 1, te_next, kr, vr);
-
-    if (wave_active && t * kKeyTile < wave_kmax) {
-      const char* kt = klds[b];
-      const char* vt = vlds[b];
-      // S^T for each column tile, K chunks shared.
-      f32x4 st[CT][2];
+  // ---- one tile of attention from LDS buffer b
+  auto compute_tile = [&](int t, int b) {
+    if (!wave_active || t * KT >= wave_kmax) return;
+    const char* kt = klds[b];
+    const char* vt = vlds[b];
+    // S^T for each column tile, K chunks shared.
+    f32x4 st[CT][KS];
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) st[ct][0] = st[ct][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
+      for (int s = 0; s < KS; ++s) st[ct][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < NCH; ++kk) {
-          const int ch = kk * 4 + g;
-          const uint4 kc = ch < CPR ? *reinterpret_cast<const uint4*>(kt + (16 * s + l16) * RS + ch * 16)
-                                    : zero_u4();
+    for (int s = 0; s < KS; ++s)
 #pragma unroll
-          for (int ct = 0; ct < CT; ++ct) st[ct][s] = Mma<T>::qk(kc, qf[ct][kk], st[ct][s]);
-        }
-      // Mask, online softmax, P^T operands.
-      const bool need_mask = t >= full_tiles;
-      V8 pb[CT];
+      for (int kk = 0; kk < NCH; ++kk) {
+        const int ch = kk * 4 + g;
+        const uint4 kc = ch < CPR ? *reinterpret_cast<const uint4*>(kt + (16 * s + l16) * RS + ch * 16) : zero_u4();
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        float sv[2][4];
-        float mt = -INFINITY;
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int pos = t * kKeyTile + 16 * s + 4 * g + r;
-            bool vis = true;
-            if (need_mask) {
-              if (pos >= computed) {
-                if (vrow[ct] == nullptr) {
-                  vis = pos <= lin_last[ct];
-                } else {
-                  const int j = pos - computed;
-                  vis = j < q_len && ((vrow[ct][j >> 5] >> (j & 31)) & 1u);
-                }
-              }
-            }
-            const float x = vis ? st[ct][s][r] * a.scale_log2 : -INFINITY;
-            sv[s][r] = x;
-            mt = fmaxf(mt, x);
-          }
-        mt = row_max4(mt);
-        if (__any(mt > m_run[ct] + kRescaleSlack)) {
-          const float m_new = fmaxf(m_run[ct], mt);
-          const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run[ct] - m_new);
-          l_run[ct] *= alpha;
-#pragma unroll
-          for (int n = 0; n < NT; ++n) acc[ct][n] *= alpha;
-          m_run[ct] = m_new;
-        }
-        const float base = (m_run[ct] == -INFINITY) ? 0.f : m_run[ct];
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float p = fast_exp2(sv[s][r] - base);
-            l_run[ct] += p;
-            pb[ct][s * 4 + r] = from_f32<T>(p);
-          }
+        for (int ct = 0; ct < CT; ++ct) st[ct][s] = Mma<T>::qk(kc, qf[ct][kk], st[ct][s]);
       }
-      // O^T += V^T P^T: transpose reads shared by the column tiles.
-      const int q4 = l16 & 3;
+    // Masks only past the fully visible prefix: one compare per score for a
+    // linear request, the ancestor bits for a tree.
+    if (t >= full_tiles) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int pos = t * KT + 16 * s + 4 * g + r;
+            bool vis;
+            if (!tree) {
+              vis = pos <= lin_last[ct];
+            } else {
+              const int j = pos - computed;
+              vis = j < 0 || (j < q_len && ((vrow[ct][j >> 5] >> (j & 31)) & 1u));
+            }
+            if (!vis) st[ct][s][r] = -INFINITY;
+          }
+    }
+    // Online softmax on raw scores: max first, scale folded into the exp.
+    V8 pb[CT][KS / 2];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      float mt = -INFINITY;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mt = fmaxf(mt, st[ct][s][r]);
+      mt = row_max4(mt) * c_log2;
+      if (__any(mt > m_run[ct] + kRescaleSlack)) {
+        const float m_new = fmaxf(m_run[ct], mt);
+        const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run[ct] - m_new);
+        l_run[ct] *= alpha;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) acc[ct][n] *= alpha;
+        m_run[ct] = m_new;
+      }
+      const float nbase = (m_run[ct] == -INFINITY) ? 0.f : -m_run[ct];
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = fast_exp2(__builtin_fmaf(st[ct][s][r], c_log2, nbase));
+          l_run[ct] += p;
+          pb[ct][s >> 1][(s & 1) * 4 + r] = from_f32<T>(p);
+        }
+    }
+    // O^T += V^T P^T: transpose reads shared by the column tiles.
+    const int q4 = l16 & 3;
+#pragma unroll
+    for (int h = 0; h < KS / 2; ++h)
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
-        const int lo = (4 * g + (l16 >> 2)) * RS + (16 * n + 4 * q4) * 2;
+        const int lo = (32 * h + 4 * g + (l16 >> 2)) * RS + (16 * n + 4 * q4) * 2;
         const int hi = lo + 16 * RS;
         const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vt + lo));
         const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vt + hi));
@@ -282,23 +291,42 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a)
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
           if constexpr (std::is_same<T, __bf16>::value) {
-            acc[ct][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[ct], acc[ct][n], 0, 0, 0);
+            acc[ct][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[ct][h], acc[ct][n], 0, 0, 0);
           } else {
-            acc[ct][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb[ct], acc[ct][n], 0, 0, 0);
+            acc[ct][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb[ct][h], acc[ct][n], 0, 0, 0);
           }
         }
       }
-    }
+  };
 
-    if (more) {
-      // Entries two tiles ahead, then the next tile into the other buffer
-      // (read by every wave two barriers ago).
-#pragma unroll
-      for (int i = 0; i < LPT; ++i) te_next[i] = te_after[i];
-      if (t + 3 < ntiles) load_entries(t + 3, te_after);
-      store_tile(b ^ 1, kr, vr);
-    }
+  // ---- pipeline: tile t computes from LDS while tile t+1 sits in registers
+  // (stored to the other LDS buffer after the compute), tile t+2's loads are
+  // in flight and tile t+3's table entries are being fetched.  Two register
+  // sets alternate statically (a run-time swap would force waits).
+  int ea[LPT], eb[LPT];
+  uint4 ka[LPT], va[LPT], kb[LPT], vb[LPT];
+  load_entries(0, eb);
+  load_tile(0, eb, kb, vb);
+  store_tile(0, kb, vb);
+  if (ntiles > 1) {
+    load_entries(1, ea);
+    load_tile(1, ea, ka, va);
+  }
+  if (ntiles > 2) load_entries(2, eb);
+  __syncthreads();
+
+  // dc holds tile t+1, dn receives tile t+2 (entries en), ec receives tile t+3's entries.
+  auto iter = [&](int t, uint4 (&kc)[LPT], uint4 (&vc)[LPT], uint4 (&kn)[LPT], uint4 (&vn)[LPT],
+                  int (&ec)[LPT], const int (&en)[LPT]) {
+    if (t + 2 < ntiles) load_tile(t + 2, en, kn, vn);
+    if (t + 3 < ntiles) load_entries(t + 3, ec);
+    compute_tile(t, t & 1);
+    if (t + 1 < ntiles) store_tile((t + 1) & 1, kc, vc);
     __syncthreads();
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    iter(t, ka, va, kb, vb, ea, eb);
+    if (t + 1 < ntiles) iter(t + 1, kb, vb, ka, va, eb, ea);
   }
 
   // ---- normalised output rows
@@ -306,7 +334,7 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a)
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     const float l_tot = row_sum4(l_run[ct]);
-    if (!cok[ct]) continue;
+    if (!colok[ct]) continue;
     const int col = col0 + 16 * (CT * wave + ct) + l16;
     const int qhead = kvh * G + (col - qi[ct] * G);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
