@@ -690,7 +690,7 @@ def main() -> int:
             "pool_blocks": C2.num_blocks, "context": f"U[{C2.ctx_lo},{C2.ctx_hi}] seed {C2.seed}",
             "mean_context": float(ctx.mean()), "rotating_pool_sets": len(caches),
             "decode_waves": launches[0].work.waves_per_head * C2.hkv if launches[0] else None,
-            "tiles_per_wave": launches[0].work.tiles_per_wave if launches[0] else None,
+            "units_per_wave": launches[0].work.units_per_wave if launches[0] else None,
         },
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "tokens_per_s": round(C2.batch / (NUM_LAYERS * ms_per_step * 1e-3), 1),

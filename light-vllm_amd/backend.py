@@ -26,7 +26,7 @@ from torch import Tensor
 from light_vllm_amd import native
 from light_vllm_amd.errors import KVCacheError
 from light_vllm_amd.paged_cache import current_stream, dtype_code, hip_append
-from light_vllm_amd.plan import StepPlan
+from light_vllm_amd.plan import UNIT_TOKENS, StepPlan
 
 SUPPORTED_HEAD_SIZES = (32, 64, 80, 96, 128, 256)
 
@@ -239,8 +239,8 @@ class HipPagedAttentionBackend:
         resident wave)."""
 
         native.load()
-        if partition_tokens is not None and (partition_tokens <= 0 or partition_tokens % 32):
-            raise ValueError("partition_tokens must be a positive multiple of 32")
+        if partition_tokens is not None and (partition_tokens <= 0 or partition_tokens % UNIT_TOKENS):
+            raise ValueError(f"partition_tokens must be a positive multiple of {UNIT_TOKENS}")
         self._workspace = _Workspace()
         self._use_prefill = use_prefill_kernel
         self._partition_tokens = partition_tokens

@@ -395,13 +395,13 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
       for (int n = 0; n < NT; ++n) acc[n] *= alpha;
       m_run = m_new;
     }
-    const float base = (m_run == -INFINITY) ? 0.f : m_run;
+    const float nbase = (m_run == -INFINITY) ? 0.f : -m_run;
     float p4[SUB][4];
 #pragma unroll
     for (int s = 0; s < SUB; ++s)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        p4[s][r] = fast_exp2(sv[s][r] - base);
+        p4[s][r] = fast_exp2(sv[s][r] + nbase);  // sv is already scaled
         l_run += p4[s][r];
       }
 
@@ -536,7 +536,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
 
 // ---------------------------------------------------------------------------
 // Merge: one wave per (job, kv head); lane (g, l16) combines dims 16n + 4g..+3
-// of column l16 over the job's partials, four partials per round trip, by
+// of column l16 over the job's partials, MC partials per round trip, by
 // log-sum-exp in the log2 domain.
 // ---------------------------------------------------------------------------
 struct MergeArgs {
@@ -550,8 +550,10 @@ struct MergeArgs {
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(64) void paged_merge_kernel(const MergeArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void paged_merge_kernel(const MergeArgs a) {
   constexpr int NT = D / 16;
+  // Partials per round trip: as many as ~192 VGPRs of staging hold.
+  constexpr int MC = (192 / (D / 4 + 2)) < 2 ? 2 : ((192 / (D / 4 + 2)) > 8 ? 8 : 192 / (D / 4 + 2));
   const int Hkv = a.num_kv_heads;
   const int G = a.group;
   const int job = blockIdx.x / Hkv;
@@ -571,11 +573,11 @@ __global__ __launch_bounds__(64) void paged_merge_kernel(const MergeArgs a) {
   f32x4 o[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int j0 = 0; j0 < np; j0 += 4) {
-    float2 ml[4];
-    f32x4 pa[4][NT];
+  for (int j0 = 0; j0 < np; j0 += MC) {
+    float2 ml[MC];
+    f32x4 pa[MC][NT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < MC; ++i) {
       const int64_t cs = ((int64_t)(slot0 + (j0 + i < np ? j0 + i : np - 1)) * Hkv + kvh) * 16 + l16;
       ml[i] = *reinterpret_cast<const float2*>(a.part_ml + cs * 2);
 #pragma unroll
@@ -585,7 +587,7 @@ __global__ __launch_bounds__(64) void paged_merge_kernel(const MergeArgs a) {
     // together; entries past the job and empty partials weigh 0.
     float mc = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mc = fmaxf(mc, j0 + i < np ? ml[i].x : -INFINITY);
+    for (int i = 0; i < MC; ++i) mc = fmaxf(mc, j0 + i < np ? ml[i].x : -INFINITY);
     const float mnew = fmaxf(mrun, mc);
     const bool any = mnew != -INFINITY;
     const float sc = (any && mrun != -INFINITY) ? fast_exp2(mrun - mnew) : (any ? 0.f : 1.f);
@@ -593,7 +595,7 @@ __global__ __launch_bounds__(64) void paged_merge_kernel(const MergeArgs a) {
 #pragma unroll
     for (int n = 0; n < NT; ++n) o[n] *= sc;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < MC; ++i) {
       const float wt = (j0 + i < np && ml[i].x != -INFINITY) ? fast_exp2(ml[i].x - mnew) : 0.f;
       lsum += wt * ml[i].y;
 #pragma unroll

@@ -44,7 +44,11 @@ TABLE_SLICE = 256
 
 PIECE_FIELDS = 16
 MERGE_FIELDS = 8
-TILE_TOKENS = 32
+# Stream-K granularity: shares and piece boundaries fall on multiples of this
+# many tokens (the kernel's tiles may be larger; a piece's last tile is
+# masked).  Measured on C2: 16-token units made the decode slower than 32,
+# because every partial tile costs a full load round trip.
+UNIT_TOKENS = 32
 
 _BIT_WEIGHTS = (np.uint64(1) << np.arange(32, dtype=np.uint64)).astype(np.uint64)
 
@@ -58,15 +62,15 @@ def stream_k_pieces(
     num_kv_heads: int,
     resident_waves: int,
     block_size: int,
-    min_tiles_per_wave: int = 4,
-    max_tiles_per_wave: int | None = None,
+    min_units_per_wave: int = 4,
+    max_units_per_wave: int | None = None,
 ):
     """Split the decode work evenly over the waves the GPU holds at once.
 
-    A segment is one (request, column tile); it has ceil(seq / 32) tiles of 32
-    tokens.  The segments of all decode rows are laid end to end and the
-    flattened tile range is cut into ``waves_per_head`` contiguous shares
-    that differ by at most one tile (the same cut for every kv head).  A wave's share is a list of
+    A segment is one (request, column tile); it has ceil(seq / UNIT_TOKENS)
+    units.  The segments of all decode rows are laid end to end and the
+    flattened unit range is cut into ``waves_per_head`` contiguous shares
+    that differ by at most one unit (the same cut for every kv head).  A wave's share is a list of
     pieces: the part of each segment it covers.  A piece that covers a whole
     segment writes the output directly; otherwise it writes a partial
     (max, sum, acc) to its slot and a merge job combines the segment's
@@ -77,15 +81,15 @@ def stream_k_pieces(
 
     seg_req = np.repeat(np.flatnonzero(rows), nct[rows])
     seg_ctile = np.concatenate([np.arange(n) for n in nct[rows]]) if rows.any() else np.zeros(0, np.int64)
-    seg_tiles = -(-seq[seg_req] // TILE_TOKENS)
+    seg_tiles = -(-seq[seg_req] // UNIT_TOKENS)
     total = int(seg_tiles.sum())
     seg_start = np.zeros(len(seg_req) + 1, dtype=np.int64)
     np.cumsum(seg_tiles, out=seg_start[1:])
     # The block-table slice of a piece must fit the kernel's LDS copy.
-    cap = max(1, ((TABLE_SLICE - 2) * block_size) // TILE_TOKENS)
-    if max_tiles_per_wave is not None:
-        cap = max(1, min(cap, max_tiles_per_wave))
-    waves = max(1, min(max(1, resident_waves // num_kv_heads), -(-total // min_tiles_per_wave)))
+    cap = max(1, ((TABLE_SLICE - 2) * block_size) // UNIT_TOKENS)
+    if max_units_per_wave is not None:
+        cap = max(1, min(cap, max_units_per_wave))
+    waves = max(1, min(max(1, resident_waves // num_kv_heads), -(-total // min_units_per_wave)))
     waves = max(waves, -(-total // cap))
     per_wave = -(-total // waves)  # the largest share; never above cap
     # Balanced shares: wave w covers units [w * total // W, (w + 1) * total // W),
@@ -102,8 +106,8 @@ def stream_k_pieces(
     pieces = np.zeros((len(lo), PIECE_FIELDS), dtype=np.int64)
     pieces[:, 0] = req
     pieces[:, 1] = seg_ctile[seg]
-    pieces[:, 2] = (lo - seg_start[seg]) * TILE_TOKENS
-    pieces[:, 3] = np.minimum((hi - seg_start[seg]) * TILE_TOKENS, seq[req])
+    pieces[:, 2] = (lo - seg_start[seg]) * UNIT_TOKENS
+    pieces[:, 3] = np.minimum((hi - seg_start[seg]) * UNIT_TOKENS, seq[req])
     pieces[:, 4] = slot
     pieces[:, 5] = req_meta[req, 0]  # table_off
     pieces[:, 6] = req_meta[req, 2]  # computed
@@ -141,7 +145,7 @@ class DecodeWork:
     jobs: Tensor | None  # int32 [n_jobs, 8]
     num_jobs: int
     num_partial_slots: int
-    tiles_per_wave: int
+    units_per_wave: int
     prefill_units: Tensor | None  # int32 [n_prefill_units, 4]
     num_prefill_units: int
 
@@ -264,12 +268,12 @@ class StepPlan:
         waves = num_jobs = num_partial = num_prefill = per_wave = 0
         blocks = []
         if decode_rows.any():
-            max_tiles = None
+            max_units = None
             if self.partition_tokens:
-                max_tiles = max(1, self.partition_tokens // TILE_TOKENS)
+                max_units = max(1, self.partition_tokens // UNIT_TOKENS)
             piece_tab, first_tab, waves, per_wave, job_tab, num_partial = stream_k_pieces(
                 seq=seq, nct=nct, rows=decode_rows, req_meta=self._req_meta, num_kv_heads=num_kv_heads,
-                resident_waves=resident_waves, block_size=self.block_size, max_tiles_per_wave=max_tiles,
+                resident_waves=resident_waves, block_size=self.block_size, max_units_per_wave=max_units,
             )
             num_pieces = int(piece_tab.shape[0])
             num_jobs = int(job_tab.shape[0])

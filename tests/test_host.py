@@ -14,7 +14,7 @@ import torch
 
 import light_vllm_amd as lv
 from light_vllm_amd import native
-from light_vllm_amd.plan import StepPlan
+from light_vllm_amd.plan import UNIT_TOKENS, StepPlan
 from oracle import paged_kv_oracle as O
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())
@@ -165,27 +165,28 @@ def test_stream_k_pieces_cover_every_segment_once(resident, bs, group) -> None:
     first = work.wave_first.numpy()
     waves = work.waves_per_head
     assert first[0] == 0 and first[-1] == len(pieces) and np.all(np.diff(first) >= 1)
-    cap = (254 * bs) // 32  # tiles whose block-table slice fits the kernel's LDS copy
-    assert work.tiles_per_wave <= max(cap, 1)
+    u = UNIT_TOKENS
+    cap = (254 * bs) // u  # units whose block-table slice fits the kernel's LDS copy
+    assert work.units_per_wave <= max(cap, 1)
     seqs = np.asarray(md.num_computed_tokens) + np.asarray(md.query_lengths)
     nct = -(-(np.asarray(md.query_lengths) * group) // 16)
-    total_tiles = int((-(-seqs // 32) * nct).sum())
+    total_tiles = int((-(-seqs // u) * nct).sum())
     assert waves <= max(resident // 4, 1, -(-total_tiles // cap))
-    assert work.tiles_per_wave == -(-total_tiles // waves)
+    assert work.units_per_wave == -(-total_tiles // waves)
     share_sizes = []
     covered = {}
     for w in range(waves):
         tiles = 0
         for rec in pieces[first[w] : first[w + 1]]:
             req, ctile, tb, te, slot = rec[:5]
-            assert 0 <= tb < te <= seqs[req] and tb % 32 == 0
+            assert 0 <= tb < te <= seqs[req] and tb % u == 0
             assert rec[6] == md.num_computed_tokens[req] and rec[7] == md.query_lengths[req]
             assert rec[8] == md.query_start_loc[req]
             n_tab = (te - 1) // bs - tb // bs + 1
             assert n_tab <= 254, "piece exceeds the kernel's LDS table slice"
             covered.setdefault((req, ctile), []).append((tb, te, slot))
-            tiles += -(-(te - tb) // 32)
-        assert tiles <= work.tiles_per_wave
+            tiles += -(-(te - tb) // u)
+        assert tiles <= work.units_per_wave
         share_sizes.append(tiles)
         # Only a share's first and last pieces can be partial.
         wave_slots = pieces[first[w] : first[w + 1], 4]
