@@ -123,6 +123,11 @@ int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_str
  * dtype and head size: the planner's stream-K width.  Needs a GPU. */
 int lvamd_paged_decode_resident_waves(int32_t dtype, int32_t head_size);
 
+/* Tokens per decode-kernel tile for this dtype and head size (64, or 16 for
+ * rows above 256 bytes): the planner cuts pieces on multiples of it.  A piece
+ * may start anywhere; tile-aligned pieces avoid partial tiles. */
+int lvamd_paged_decode_tile_tokens(int32_t dtype, int32_t head_size);
+
 /*
  * Log-sum-exp merge of split-K partials into out, one wave per (job, kv head);
  * jobs [num_jobs][LVAMD_MERGE_FIELDS].  Same reference functions as

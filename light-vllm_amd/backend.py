@@ -158,7 +158,8 @@ class HipPagedAttention:
         code = dtype_code(dtype)
         resident = native.resident_decode_waves(code, spec.head_size)
         columns = native.prefill_unit_columns(code, spec.head_size) if self._use_prefill else 0
-        return self._plan.work(group, spec.num_kv_heads, resident, columns)
+        unit = native.decode_tile_tokens(code, spec.head_size)
+        return self._plan.work(group, spec.num_kv_heads, resident, columns, unit)
 
     def prefill(self, layer_id: str, query: Tensor, out: Tensor, *, scale: float) -> None:
         spec = self._cache.layer_spec(layer_id)

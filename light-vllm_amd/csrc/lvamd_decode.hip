@@ -727,6 +727,26 @@ static const void* decode_kernel_ptr(int head_size) {
   }
 }
 
+template <typename T>
+static int decode_tile_tokens_t(int head_size) {
+  switch (head_size) {
+    case 32: return DecodeTile<T, 32>::TT;
+    case 64: return DecodeTile<T, 64>::TT;
+    case 80: return DecodeTile<T, 80>::TT;
+    case 96: return DecodeTile<T, 96>::TT;
+    case 128: return DecodeTile<T, 128>::TT;
+    case 256: return DecodeTile<T, 256>::TT;
+    default: return LVAMD_ERR_UNSUPPORTED;
+  }
+}
+
+extern "C" int lvamd_paged_decode_tile_tokens(int32_t dtype, int32_t head_size) {
+  if (dtype_size(dtype) == 0 || !head_size_supported(head_size)) return LVAMD_ERR_UNSUPPORTED;
+  return dtype == LVAMD_BF16 ? decode_tile_tokens_t<__bf16>(head_size)
+         : dtype == LVAMD_F16 ? decode_tile_tokens_t<_Float16>(head_size)
+                              : decode_tile_tokens_t<float>(head_size);
+}
+
 extern "C" int lvamd_paged_decode_resident_waves(int32_t dtype, int32_t head_size) {
   if (dtype_size(dtype) == 0 || !head_size_supported(head_size)) return LVAMD_ERR_UNSUPPORTED;
   const void* fn = dtype == LVAMD_BF16 ? decode_kernel_ptr<__bf16>(head_size)

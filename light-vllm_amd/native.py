@@ -15,7 +15,7 @@ from pathlib import Path
 from light_vllm_amd.errors import ExecutionError, ExecutionNotReadyError
 
 LIB_NAME = "liblvamd_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
@@ -46,6 +46,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i32, _i32, _i32, _i32, _f32, _i32, _p],
     ),
     "lvamd_paged_decode_resident_waves": (ctypes.c_int, [_i32, _i32]),
+    "lvamd_paged_decode_tile_tokens": (ctypes.c_int, [_i32, _i32]),
     "lvamd_paged_attention_merge": (
         ctypes.c_int,
         [_p, _p, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p],
@@ -114,6 +115,16 @@ def resident_decode_waves(dtype_code: int, head_size: int) -> int:
     return found
 
 
+@functools.lru_cache(maxsize=None)
+def decode_tile_tokens(dtype_code: int, head_size: int) -> int:
+    """Tokens per decode-kernel tile for this dtype and head size (the planner's unit)."""
+
+    found = int(load().lvamd_paged_decode_tile_tokens(dtype_code, head_size))
+    check(min(found, 0), "lvamd_paged_decode_tile_tokens")
+    return found
+
+
+@functools.lru_cache(maxsize=None)
 def prefill_unit_columns(dtype_code: int, head_size: int) -> int:
     """Columns per prefill work unit, 0 when the prefill kernel does not cover the shape."""
 

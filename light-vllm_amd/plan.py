@@ -44,10 +44,10 @@ TABLE_SLICE = 256
 
 PIECE_FIELDS = 16
 MERGE_FIELDS = 8
-# Stream-K granularity: shares and piece boundaries fall on multiples of this
-# many tokens (the kernel's tiles may be larger; a piece's last tile is
-# masked).  Measured on C2: 16-token units made the decode slower than 32,
-# because every partial tile costs a full load round trip.
+# Default stream-K granularity: shares and piece boundaries fall on multiples
+# of this many tokens.  The backend passes the decode kernel's own tile size
+# instead, so that every piece is whole tiles (a partial tile costs a full
+# load round trip; measured on C2, 16-token units were slower than 32).
 UNIT_TOKENS = 32
 
 _BIT_WEIGHTS = (np.uint64(1) << np.arange(32, dtype=np.uint64)).astype(np.uint64)
@@ -64,10 +64,11 @@ def stream_k_pieces(
     block_size: int,
     min_units_per_wave: int = 4,
     max_units_per_wave: int | None = None,
+    unit_tokens: int = UNIT_TOKENS,
 ):
     """Split the decode work evenly over the waves the GPU holds at once.
 
-    A segment is one (request, column tile); it has ceil(seq / UNIT_TOKENS)
+    A segment is one (request, column tile); it has ceil(seq / unit_tokens)
     units.  The segments of all decode rows are laid end to end and the
     flattened unit range is cut into ``waves_per_head`` contiguous shares
     that differ by at most one unit (the same cut for every kv head).  A wave's share is a list of
@@ -81,12 +82,12 @@ def stream_k_pieces(
 
     seg_req = np.repeat(np.flatnonzero(rows), nct[rows])
     seg_ctile = np.concatenate([np.arange(n) for n in nct[rows]]) if rows.any() else np.zeros(0, np.int64)
-    seg_tiles = -(-seq[seg_req] // UNIT_TOKENS)
+    seg_tiles = -(-seq[seg_req] // unit_tokens)
     total = int(seg_tiles.sum())
     seg_start = np.zeros(len(seg_req) + 1, dtype=np.int64)
     np.cumsum(seg_tiles, out=seg_start[1:])
     # The block-table slice of a piece must fit the kernel's LDS copy.
-    cap = max(1, ((TABLE_SLICE - 2) * block_size) // UNIT_TOKENS)
+    cap = max(1, ((TABLE_SLICE - 2) * block_size) // unit_tokens)
     if max_units_per_wave is not None:
         cap = max(1, min(cap, max_units_per_wave))
     waves = max(1, min(max(1, resident_waves // num_kv_heads), -(-total // min_units_per_wave)))
@@ -106,8 +107,8 @@ def stream_k_pieces(
     pieces = np.zeros((len(lo), PIECE_FIELDS), dtype=np.int64)
     pieces[:, 0] = req
     pieces[:, 1] = seg_ctile[seg]
-    pieces[:, 2] = (lo - seg_start[seg]) * UNIT_TOKENS
-    pieces[:, 3] = np.minimum((hi - seg_start[seg]) * UNIT_TOKENS, seq[req])
+    pieces[:, 2] = (lo - seg_start[seg]) * unit_tokens
+    pieces[:, 3] = np.minimum((hi - seg_start[seg]) * unit_tokens, seq[req])
     pieces[:, 4] = slot
     pieces[:, 5] = req_meta[req, 0]  # table_off
     pieces[:, 6] = req_meta[req, 2]  # computed
@@ -238,24 +239,27 @@ class StepPlan:
 
     # -- work lists ---------------------------------------------------------
     def work(
-        self, group: int, num_kv_heads: int, resident_waves: int = 8 * NUM_CUS, prefill_columns: int = 0
+        self, group: int, num_kv_heads: int, resident_waves: int = 8 * NUM_CUS, prefill_columns: int = 0,
+        unit_tokens: int = UNIT_TOKENS,
     ) -> DecodeWork:
         """Work lists for layers of this (group, kv heads) shape.
 
-        ``resident_waves`` is how many decode waves the GPU holds at once and
+        ``resident_waves`` is how many decode waves the GPU holds at once,
         ``prefill_columns`` the prefill kernel's unit width (0: every request
-        goes through the decode kernel); the library reports both per dtype and
-        head size.
+        goes through the decode kernel) and ``unit_tokens`` the decode kernel's
+        tile; the library reports all three per dtype and head size.
         """
 
-        key = (group, num_kv_heads, resident_waves, prefill_columns)
+        key = (group, num_kv_heads, resident_waves, prefill_columns, unit_tokens)
         found = self._work.get(key)
         if found is None:
-            found = self._build_work(group, num_kv_heads, resident_waves, prefill_columns)
+            found = self._build_work(group, num_kv_heads, resident_waves, prefill_columns, unit_tokens)
             self._work[key] = found
         return found
 
-    def _build_work(self, group: int, num_kv_heads: int, resident_waves: int, prefill_columns: int) -> DecodeWork:
+    def _build_work(
+        self, group: int, num_kv_heads: int, resident_waves: int, prefill_columns: int, unit_tokens: int
+    ) -> DecodeWork:
         computed, q_lens = self._computed, self._q_lens
         batch = self.batch_size
         seq = computed + q_lens
@@ -270,10 +274,11 @@ class StepPlan:
         if decode_rows.any():
             max_units = None
             if self.partition_tokens:
-                max_units = max(1, self.partition_tokens // UNIT_TOKENS)
+                max_units = max(1, self.partition_tokens // unit_tokens)
             piece_tab, first_tab, waves, per_wave, job_tab, num_partial = stream_k_pieces(
                 seq=seq, nct=nct, rows=decode_rows, req_meta=self._req_meta, num_kv_heads=num_kv_heads,
                 resident_waves=resident_waves, block_size=self.block_size, max_units_per_wave=max_units,
+                unit_tokens=unit_tokens,
             )
             num_pieces = int(piece_tab.shape[0])
             num_jobs = int(job_tab.shape[0])

@@ -14,7 +14,7 @@ import torch
 
 import light_vllm_amd as lv
 from light_vllm_amd import native
-from light_vllm_amd.plan import UNIT_TOKENS, StepPlan
+from light_vllm_amd.plan import StepPlan
 from oracle import paged_kv_oracle as O
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())
@@ -153,19 +153,20 @@ def test_plan_request_table_matches_metadata() -> None:
         assert flat[meta[r, 0] : meta[r, 0] + meta[r, 1]].tolist() == list(table)
 
 
+@pytest.mark.parametrize("unit", (16, 32, 64))
 @pytest.mark.parametrize("resident", (7, 64, 2048))
 @pytest.mark.parametrize("bs", (1, 16))
 @pytest.mark.parametrize("group", (1, 7))
-def test_stream_k_pieces_cover_every_segment_once(resident, bs, group) -> None:
-    rng = np.random.default_rng(resident + bs + group)
+def test_stream_k_pieces_cover_every_segment_once(resident, bs, group, unit) -> None:
+    rng = np.random.default_rng(resident + bs + group + unit)
     md = _random_metadata(rng, batch=11, bs=bs)
     plan = StepPlan(md, block_size=bs, device=CPU)
-    work = plan.work(group, 4, resident)
+    work = plan.work(group, 4, resident, 0, unit)
     pieces = work.pieces.numpy()
     first = work.wave_first.numpy()
     waves = work.waves_per_head
     assert first[0] == 0 and first[-1] == len(pieces) and np.all(np.diff(first) >= 1)
-    u = UNIT_TOKENS
+    u = unit
     cap = (254 * bs) // u  # units whose block-table slice fits the kernel's LDS copy
     assert work.units_per_wave <= max(cap, 1)
     seqs = np.asarray(md.num_computed_tokens) + np.asarray(md.query_lengths)
