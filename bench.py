@@ -32,6 +32,7 @@ import os
 import sys
 import time
 from pathlib import Path
+from types import SimpleNamespace
 
 import numpy as np
 import torch
@@ -308,7 +309,7 @@ def run_c1(args, device) -> int:
     k = torch.randn((b, cfg.hkv, cfg.d), generator=gen, device=device)
     v = torch.randn((b, cfg.hkv, cfg.d), generator=gen, device=device)
     scale = 1.0 / math.sqrt(cfg.d)
-    backend = lv.HipPagedAttentionBackend()
+    backend = lv.HipPagedAttentionBackend(decode_col_tiles=args.col_tiles)
     ms, host_ms = _time_steps(lambda i: backend.create(cache, md).forward("layer0", q, k, v, scale=scale),
                               args.steps, args.warmup)
     L = np.asarray(cfg.ctx) + 1
@@ -367,7 +368,7 @@ def run_c3(args, device) -> int:
     k = torch.randn((t, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
     v = torch.randn((t, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
     scale = 1.0 / math.sqrt(cfg.d)
-    backend = lv.HipPagedAttentionBackend()
+    backend = lv.HipPagedAttentionBackend(decode_col_tiles=args.col_tiles)
     print(f"[bench] C3: {cfg.n_prefill} x {cfg.chunk} prefill + {cfg.n_decode} decode, T={t}", file=sys.stderr, flush=True)
     ms, host_ms = _time_steps(
         lambda i: backend.create(caches[i % len(caches)], md).forward("layer0", q, k, v, scale=scale),
@@ -447,7 +448,7 @@ def run_c4(args, device) -> int:
     k = torch.randn((cfg.batch, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
     v = torch.randn((cfg.batch, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
     scale = 1.0 / math.sqrt(cfg.d)
-    backend = lv.HipPagedAttentionBackend()
+    backend = lv.HipPagedAttentionBackend(decode_col_tiles=args.col_tiles)
 
     def step(i):
         ctx = backend.create(cache, md)
@@ -492,7 +493,9 @@ class C5:
     seed = 5005
 
 
-def run_c5(args, device) -> int:
+def build_c5(device, col_tiles=None):
+    """The C5 workload: pools, metadata, step inputs and the step's three parts."""
+
     cfg = C5
     rng = np.random.default_rng(cfg.seed)
     shared_blocks = cfg.prefix // cfg.bs
@@ -534,25 +537,42 @@ def run_c5(args, device) -> int:
     k = torch.randn((t, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
     v = torch.randn((t, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
     scale = 1.0 / math.sqrt(cfg.d)
-    backend = lv.HipPagedAttentionBackend()
+    backend = lv.HipPagedAttentionBackend(decode_col_tiles=col_tiles)
     compacts = [dict(block_ids=tables[r], num_computed_tokens=computed[r], num_query_tokens=q_len,
                      num_reserved_query_tokens=q_len, retained_query_indices=accepted[r],
                      num_readonly_prefix_blocks=shared_blocks - 1) for r in range(cfg.batch)]
+
+    def cow():
+        cache.copy_blocks(cow_src, cow_dst)
 
     def attend():
         ctx = backend.create(cache, md)
         for lid in layer_ids:
             ctx.forward(lid, q, k, v, scale=scale)
 
-    def step(i):
-        cache.copy_blocks(cow_src, cow_dst)
-        attend()
+    def compact():
         cache.compact_many(compacts)
 
+    return SimpleNamespace(cfg=cfg, cache=cache, md=md, q=q, k=k, v=v, scale=scale, tables=tables,
+                           computed=computed, layouts=layouts, accepted=accepted, suffix=suffix, q_len=q_len,
+                           cow=cow, attend=attend, compact=compact)
+
+
+def run_c5(args, device) -> int:
+    w = build_c5(device, args.col_tiles)
+    cfg, cache, q, tables, computed, layouts = w.cfg, w.cache, w.q, w.tables, w.computed, w.layouts
+    suffix, q_len, accepted, scale = w.suffix, w.q_len, w.accepted, w.scale
+    cow, attend, compact = w.cow, w.attend, w.compact
+
+    def step(i):
+        cow()
+        attend()
+        compact()
+
     ms, host_ms = _time_steps(step, args.steps, args.warmup)
-    cow_ms = _time_launches(lambda i: cache.copy_blocks(cow_src, cow_dst), args.steps, args.warmup, device)
+    cow_ms = _time_launches(lambda i: cow(), args.steps, args.warmup, device)
     attend_ms = _time_launches(lambda i: attend(), max(10, args.steps // 4), 2, device)
-    compact_ms = _time_launches(lambda i: cache.compact_many(compacts), args.steps, args.warmup, device)
+    compact_ms = _time_launches(lambda i: compact(), args.steps, args.warmup, device)
     row = cfg.hkv * cfg.d * 2
     unique_kv = (cfg.prefix + sum(s + q_len for s in suffix)) * 2 * row
     cow_bytes = 2 * cfg.batch * cfg.layers * 2 * cfg.bs * row
@@ -596,6 +616,8 @@ def main() -> int:
                              "copy of known size (counter calibration and the practical HBM ceiling)")
     parser.add_argument("--partition", type=int, default=None,
                         help="cap on the tokens one decode wave handles (default: spread over all resident waves)")
+    parser.add_argument("--col-tiles", type=int, choices=(1, 4), default=None,
+                        help="fix the decode kernel's column tiles per wave (default: the planner's choice)")
     parser.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5"), default="c2",
                         help="BASELINE config (default c2, the headline metric); the others report their own metric")
     args = parser.parse_args()
@@ -614,7 +636,7 @@ def main() -> int:
     print(f"[bench] building C2 workload, {args.sets} pool sets", file=sys.stderr, flush=True)
     metadata, caches, q, k, v, ctx = build_workload(args.sets, device)
     nbytes = algorithmic_bytes(ctx)
-    backend = lv.HipPagedAttentionBackend(partition_tokens=args.partition)
+    backend = lv.HipPagedAttentionBackend(partition_tokens=args.partition, decode_col_tiles=args.col_tiles)
     out = torch.empty_like(q)
 
     def step(i: int) -> torch.Tensor:

@@ -39,12 +39,13 @@ enum lvamd_dtype { LVAMD_F32 = 0, LVAMD_F16 = 1, LVAMD_BF16 = 2 };
 /* Number of int32 fields per request in the attention metadata
  * (table_off, num_table_blocks, computed, q_len, q_start, vis_off, vis_words, 0). */
 #define LVAMD_REQ_FIELDS 8
-/* Number of int32 fields per decode piece: (req, column_tile, token_begin, token_end,
+/* Number of int32 fields per decode piece: (req, column_group, token_begin, token_end,
  * partial_slot, table_off, computed, q_len, q_start, vis_off, vis_words, 0, 0, 0, 0, 0).
- * A piece with partial_slot -1 covers its whole segment. */
+ * column_group g covers column tiles [g * col_tiles, (g + 1) * col_tiles) of
+ * the request.  A piece with partial_slot -1 covers its whole segment. */
 #define LVAMD_PIECE_FIELDS 16
 /* Number of int32 fields per merge job:
- * (req, column_tile, first_partial_slot, num_partials, q_start, q_len, 0, 0). */
+ * (req, column_group, first_partial_slot, num_partials, q_start, q_len, 0, 0). */
 #define LVAMD_MERGE_FIELDS 8
 /* Number of int32 fields per prefill work unit (req, first column, columns, 0). */
 #define LVAMD_PREFILL_FIELDS 4
@@ -78,14 +79,16 @@ int lvamd_kv_append(const void* key, int64_t key_token_stride, int64_t key_head_
  * Split-K paged attention for short query runs (decode, speculative tree
  * verification), stream-K scheduled, with this step's KV append fused in.
  *
- * Work: the decode rows' (request, column tile) segments are laid end to end
- * in 32-token units and cut into waves_per_head contiguous shares; wave w of
- * kv head h (workgroup h * waves_per_head + w, one wave64 each) processes
- * pieces [wave_first[w], wave_first[w + 1]) (LVAMD_PIECE_FIELDS int32 each).
- * A piece with partial_slot -1 covers its whole segment and writes out; the
+ * Work: one wave computes col_tiles (1 or 4) column tiles of 16 MFMA columns
+ * each.  The decode rows' (request, column group) segments are laid end to
+ * end in tile-sized units (lvamd_paged_decode_tile_tokens) and cut into
+ * waves_per_head contiguous shares; wave w of kv head h (workgroup
+ * h * waves_per_head + w, one wave64 each) processes pieces
+ * [wave_first[w], wave_first[w + 1]) (LVAMD_PIECE_FIELDS int32 each).  A
+ * piece with partial_slot -1 covers its whole segment and writes out; the
  * others write fp32 (max, sum, acc) partials to part_acc
- * [slots][num_kv_heads][16][head_size] and part_ml [slots][num_kv_heads][16][2]
- * for lvamd_paged_attention_merge.
+ * [slots][num_kv_heads][16 * col_tiles][head_size] and part_ml
+ * [slots][num_kv_heads][16 * col_tiles][2] for lvamd_paged_attention_merge.
  *
  * Append: when new_key / new_value are given ([tokens][num_kv_heads][D] with
  * the given strides), keys and values at positions >= computed are read from
@@ -116,28 +119,30 @@ int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_str
                        const int32_t* pieces, const int32_t* wave_first, int32_t waves_per_head,
                        const int32_t* tables, const uint32_t* vis,
                        float* part_acc, float* part_ml, int64_t num_partial_slots,
-                       int32_t num_kv_heads, int32_t group, int32_t head_size,
+                       int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t col_tiles,
                        int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream);
 
 /* How many decode waves (workgroups) the current device holds at once for this
- * dtype and head size: the planner's stream-K width.  Needs a GPU. */
-int lvamd_paged_decode_resident_waves(int32_t dtype, int32_t head_size);
+ * dtype, head size and col_tiles: the planner's stream-K width.  Needs a GPU. */
+int lvamd_paged_decode_resident_waves(int32_t dtype, int32_t head_size, int32_t col_tiles);
 
-/* Tokens per decode-kernel tile for this dtype and head size (64, or 16 for
- * rows above 256 bytes): the planner cuts pieces on multiples of it.  A piece
- * may start anywhere; tile-aligned pieces avoid partial tiles. */
-int lvamd_paged_decode_tile_tokens(int32_t dtype, int32_t head_size);
+/* Tokens per decode-kernel tile for this dtype, head size and col_tiles (64
+ * for one column tile, 32 for four; 16 for rows above 256 bytes): the planner
+ * cuts pieces on multiples of it.  A piece may start anywhere; tile-aligned
+ * pieces avoid partial tiles. */
+int lvamd_paged_decode_tile_tokens(int32_t dtype, int32_t head_size, int32_t col_tiles);
 
 /*
- * Log-sum-exp merge of split-K partials into out, one wave per (job, kv head);
- * jobs [num_jobs][LVAMD_MERGE_FIELDS].  Same reference functions as
- * lvamd_paged_decode: the reference has no split-K, and this is the
- * cross-partition half of that computation.
+ * Log-sum-exp merge of split-K partials into out, one wave per (job, kv head,
+ * column tile); jobs [num_jobs][LVAMD_MERGE_FIELDS]; col_tiles is the value the
+ * partials were written with.  Same reference functions as lvamd_paged_decode:
+ * the reference has no split-K, and this is the cross-partition half of that
+ * computation.
  */
 int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
                                 void* out, int64_t out_token_stride, int64_t out_head_stride,
                                 const int32_t* jobs, int32_t num_jobs,
-                                int32_t num_kv_heads, int32_t group, int32_t head_size,
+                                int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t col_tiles,
                                 int32_t dtype, lvamd_stream_t stream);
 
 /*
@@ -146,8 +151,9 @@ int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
  * (units [num_units][LVAMD_PREFILL_FIELDS] = (req, first column, columns, 0))
  * is a run of MFMA columns of one request, a column being a (query,
  * head-in-group) pair, column c = query (c / group), head (c % group).  K/V
- * tiles of 32 tokens are gathered through the block table into LDS and shared
- * by the workgroup's waves; QK^T and PV on MFMA 16x16x32, fp32 online softmax.
+ * tiles (64 tokens up to head size 128, else 32) are gathered through the
+ * block table into LDS and shared by the workgroup's waves; QK^T and PV on
+ * MFMA 16x16x32, fp32 online softmax.
  * The pool must already hold this step's K/V (lvamd_kv_append).  req_meta is
  * [batch][LVAMD_REQ_FIELDS].  Replaces the prefill half of the same reference
  * functions as lvamd_paged_decode.

@@ -75,9 +75,11 @@ def _rows_aligned(t: Tensor) -> bool:
 class HipPagedAttention:
     """Per-step context: writes each layer's K/V, then runs paged attention."""
 
-    def __init__(self, cache, metadata, workspace: _Workspace, plan: StepPlan, use_prefill: bool = True) -> None:
+    def __init__(self, cache, metadata, workspace: _Workspace, plan: StepPlan, use_prefill: bool = True,
+                 col_tiles: int | None = None) -> None:
         self._cache = cache
         self._use_prefill = use_prefill
+        self._col_tiles = col_tiles
         self._metadata = metadata
         self._layer_ids: set[str] = set()
         self._workspace = workspace
@@ -146,7 +148,7 @@ class HipPagedAttention:
             return None
         part_acc = part_ml = None
         if work.num_partial_slots:
-            per_slot = spec.num_kv_heads * 16
+            per_slot = spec.num_kv_heads * 16 * work.col_tiles
             buf = self._workspace.get(work.num_partial_slots * per_slot * (spec.head_size + 2), query.device)
             part_acc = buf.data_ptr()
             part_ml = part_acc + work.num_partial_slots * per_slot * spec.head_size * 4
@@ -156,10 +158,15 @@ class HipPagedAttention:
     def _work(self, spec, dtype):
         group = spec.num_query_heads // spec.num_kv_heads
         code = dtype_code(dtype)
-        resident = native.resident_decode_waves(code, spec.head_size)
         columns = native.prefill_unit_columns(code, spec.head_size) if self._use_prefill else 0
-        unit = native.decode_tile_tokens(code, spec.head_size)
-        return self._plan.work(group, spec.num_kv_heads, resident, columns, unit)
+        max_ctw = native.decode_max_col_tiles(code, spec.head_size)
+        ctw = self._col_tiles
+        if ctw is None:
+            ctw = self._plan.choose_col_tiles(group, columns, max_ctw)
+        ctw = min(ctw, max_ctw)
+        resident = native.resident_decode_waves(code, spec.head_size, ctw)
+        unit = native.decode_tile_tokens(code, spec.head_size, ctw)
+        return self._plan.work(group, spec.num_kv_heads, resident, columns, unit, ctw)
 
     def prefill(self, layer_id: str, query: Tensor, out: Tensor, *, scale: float) -> None:
         spec = self._cache.layer_spec(layer_id)
@@ -203,7 +210,7 @@ class _DecodeLaunch:
             work.pieces.data_ptr(), work.wave_first.data_ptr(), work.waves_per_head,
             plan.tables.data_ptr(), plan.vis.data_ptr(),
             part_acc, part_ml, work.num_partial_slots,
-            spec.num_kv_heads, group, spec.head_size,
+            spec.num_kv_heads, group, spec.head_size, work.col_tiles,
             cache.config.block_size, scale, dt, stream,
         )
         self._merge_args = None
@@ -211,7 +218,7 @@ class _DecodeLaunch:
             self._merge_args = (
                 part_acc, part_ml, out.data_ptr(), out.stride(0), out.stride(1),
                 work.jobs.data_ptr(), work.num_jobs,
-                spec.num_kv_heads, group, spec.head_size, dt, stream,
+                spec.num_kv_heads, group, spec.head_size, work.col_tiles, dt, stream,
             )
 
     def decode(self) -> None:
@@ -233,18 +240,25 @@ class HipPagedAttentionBackend:
     the validated, staged plan.
     """
 
-    def __init__(self, *, use_prefill_kernel: bool = True, partition_tokens: int | None = None) -> None:
+    def __init__(
+        self, *, use_prefill_kernel: bool = True, partition_tokens: int | None = None,
+        decode_col_tiles: int | None = None,
+    ) -> None:
         """``use_prefill_kernel=False`` sends every request through the decode
         kernel; ``partition_tokens`` caps the tokens one decode wave handles (a
         tuning knob; by default the planner spreads the work over every
-        resident wave)."""
+        resident wave); ``decode_col_tiles`` (1 or 4) fixes the decode kernel's
+        column tiles per wave instead of the planner's per-step choice."""
 
         native.load()
         if partition_tokens is not None and (partition_tokens <= 0 or partition_tokens % UNIT_TOKENS):
             raise ValueError(f"partition_tokens must be a positive multiple of {UNIT_TOKENS}")
+        if decode_col_tiles is not None and decode_col_tiles not in native.DECODE_COL_TILES:
+            raise ValueError(f"decode_col_tiles must be one of {native.DECODE_COL_TILES}")
         self._workspace = _Workspace()
         self._use_prefill = use_prefill_kernel
         self._partition_tokens = partition_tokens
+        self._col_tiles = decode_col_tiles
         self._last: tuple[object, object, StepPlan] | None = None
 
     def create(self, cache, metadata) -> HipPagedAttention:
@@ -260,4 +274,4 @@ class HipPagedAttentionBackend:
             plan = StepPlan(metadata, block_size=config.block_size, device=config.device,
                             partition_tokens=self._partition_tokens)
             self._last = (key, metadata, plan)
-        return HipPagedAttention(cache, metadata, self._workspace, plan, self._use_prefill)
+        return HipPagedAttention(cache, metadata, self._workspace, plan, self._use_prefill, self._col_tiles)

@@ -11,30 +11,35 @@
 // sequence into partitions and merges their (max, sum, acc) partials.
 //
 // Mapping onto CDNA4 (one wave64 per workgroup, one workgroup per SIMD):
-//   * Stream-K: the (request, column tile) segments of all decode rows are
-//     laid end to end in 32-token units and cut into equal contiguous shares,
-//     one per wave; wave w of kv head h is workgroup h * waves_per_head + w and
-//     walks its pieces (the parts of segments inside its share).  A piece
-//     covering a whole segment writes the output; the others write partials
-//     that the merge kernel combines by log-sum-exp, one wave per (segment,
-//     kv head).  (Merging in the decode kernel, by the wave that completes a
-//     segment, put ~1000 instructions of cold code in the kernel's tail: the
-//     instruction-cache misses cost more than a separate launch.)
+//   * MFMA columns are (query, head-in-group) pairs of one kv head, 16 per
+//     column tile, so a GQA group shares every K/V byte.  A wave owns CTW
+//     column tiles of one request (CTW = 1 for decode; 4 when a request's
+//     queries x group need more than 16 columns, as in tree verification),
+//     so every K/V byte it loads serves all of them.
+//   * Stream-K: the (request, column-tile group) segments of all decode rows
+//     are laid end to end in tile-sized units and cut into balanced
+//     contiguous shares, one per wave; wave w of kv head h is workgroup
+//     h * waves_per_head + w and walks its pieces (the parts of segments
+//     inside its share).  A piece covering a whole segment writes the output;
+//     the others write partials that the merge kernel combines by
+//     log-sum-exp, one wave per (segment, kv head, column tile).  (Merging in
+//     the decode kernel, by the wave that completes a segment, put ~1000
+//     instructions of cold code in the kernel's tail: the instruction-cache
+//     misses cost more than a separate launch.)
 //   * Fused append: this step's tokens are read from the input K/V and
 //     written to their pool slots by the piece that covers them.
-//   * MFMA columns are (query, head-in-group) pairs of one kv head: 16 per
-//     column tile, so a GQA group of 7 heads shares every K/V byte.
-//   * Per tile (64 tokens, or fewer for wide rows), lane (g = l/16, l%16)
-//     loads 16-byte chunks 4kk+g of token rows 16s + l%16 of K and V: the K
-//     chunks land in VGPRs already in the A-operand layout of S^T = K Q^T
-//     (MFMA 16x16x32 bf16/fp16, 16x16x4 fp32); the V chunks are written to
-//     LDS after the current tile's PV.  (No LDS DMA: LLVM cannot tell an
-//     in-flight DMA into one buffer from reads of the other and would make
-//     every LDS read wait for the next tile's loads.)
+//   * Per tile (64 tokens for one column tile, 16 for four or for wide
+//     rows), lane (g = l/16, l%16) loads 16-byte chunks 4kk+g of token rows
+//     16s + l%16 of K and V: the K chunks land in VGPRs already in the
+//     A-operand layout of S^T = K Q^T (MFMA 16x16x32 bf16/fp16, 16x16x4
+//     fp32); the V chunks are written to LDS after the current tile's PV.
+//     (No LDS DMA: LLVM cannot tell an in-flight DMA into one buffer from
+//     reads of the other and would make every LDS read wait for the next
+//     tile's loads.)
 //   * The S^T accumulator layout (lane l: column l%16, tokens 4*(l/16)+r) is
 //     the B-operand layout of O^T = V^T P^T, so P never leaves its lane; the
 //     V^T A operand comes out of LDS with ds_read_b64_tr_b16 transpose reads
-//     (two per 16-row output tile).
+//     (two per 16-row output tile, shared by the wave's column tiles).
 //   * The block-table slice of a piece sits in LDS, so tile addresses
 //     never wait on a table load; K is double-buffered in VGPRs and V in
 //     LDS, and the next tile's K/V are in flight while the current tile
@@ -51,11 +56,12 @@
 
 namespace lvamd {
 
-// Block-table entries of one partition staged in LDS (the host keeps
-// partition_tokens / block_size + 2 within this bound).
+// Block-table entries of one piece staged in LDS (the host keeps a piece
+// within kTableSlice - 2 blocks).
 constexpr int kTableSlice = 256;
 // Lazy-rescale threshold in log2 units: probabilities stay below 2^8.
 constexpr float kRescaleSlack = 8.0f;
+
 struct DecodeArgs {
   const void* q;
   int64_t q_tok_stride, q_head_stride;
@@ -70,8 +76,8 @@ struct DecodeArgs {
   const int32_t* __restrict__ wave_first;  // [waves_per_head + 1]
   const int32_t* __restrict__ tables;
   const uint32_t* __restrict__ vis;
-  float* part_acc;
-  float* part_ml;
+  float* part_acc;  // [slots][Hkv][CTW * 16][D]
+  float* part_ml;   // [slots][Hkv][CTW * 16][2]
   int32_t waves_per_head;
   int32_t num_kv_heads;
   int32_t group;
@@ -80,21 +86,25 @@ struct DecodeArgs {
   float scale_log2;
 };
 
-// LDS slot (16-byte units) of V row r chunk c of a tile: the DMA of
-// instruction (s = r/16, kk = c/4) writes 64 consecutive slots,
-// lane 16*(c%4) + r%16 at slot 16*(c%4) + r%16.
+// LDS slot (16-byte units) of V row r chunk c of a tile: the (s = r/16,
+// kk = c/4) chunk group is 64 consecutive slots, lane 16*(c%4) + r%16 at slot
+// 16*(c%4) + r%16 (the order in which the lanes load it).
 template <int NCH>
 __device__ __forceinline__ int vslot(int r, int c) {
   return ((r >> 4) * NCH + (c >> 2)) * 64 + (c & 3) * 16 + (r & 15);
 }
 
-// Decode tile shape: a tile is TT tokens of one kv head: TT = 64 when a
-// head's row slice is at most 256 bytes (bf16/fp16 up to D = 128, fp32 up to
-// D = 64), else 16, so one tile's K (and V) take at most 64 VGPRs per lane.
-template <typename T, int D>
+// Decode tile shape: a tile is TT tokens of one kv head.  With one column
+// tile per wave, TT = 64 when a head's row slice is at most 256 bytes
+// (bf16/fp16 up to D = 128, fp32 up to D = 64), else 16, so one tile's K (and
+// V) take at most 64 VGPRs per lane; with four column tiles TT = 16, which
+// leaves registers for their Q operands and accumulators (at TT = 32 the
+// bf16 D = 128 kernel spills).
+template <typename T, int D, int CTW>
 struct DecodeTile {
   static constexpr int ROW = (int)sizeof(T) * D;
-  static constexpr int TT = ROW <= 256 ? 64 : 16;
+  static constexpr int TT1 = ROW <= 256 ? 64 : 16;
+  static constexpr int TT = CTW == 1 ? TT1 : 16;
   static constexpr int SUB = TT / 16;                                // 16-row groups per tile
   static constexpr int VSLOTS = SUB * TileShape<T, D>::NCH * 64;     // 16-byte LDS slots per V tile
   // Each workgroup reserves more than 32 KiB of LDS (two V buffers of at
@@ -106,9 +116,9 @@ struct DecodeTile {
 };
 
 // One piece of a wave's share: a contiguous token range of one
-// (request, column tile), with the request fields the kernel needs.
+// (request, column-tile group), with the request fields the kernel needs.
 struct Piece {
-  int req, ctile, tok_begin, tok_end, slot;
+  int req, cgroup, tok_begin, tok_end, slot;
   int table_off, computed, q_len, q_start, vis_off, vis_words;
 };
 
@@ -116,7 +126,7 @@ __device__ __forceinline__ Piece read_piece(const int32_t* __restrict__ pieces, 
   const int32_t* r = pieces + (int64_t)p * LVAMD_PIECE_FIELDS;
   Piece x;
   x.req = r[0];
-  x.ctile = r[1];
+  x.cgroup = r[1];
   x.tok_begin = r[2];
   x.tok_end = r[3];
   x.slot = r[4];
@@ -129,20 +139,23 @@ __device__ __forceinline__ Piece read_piece(const int32_t* __restrict__ pieces, 
   return x;
 }
 
-// This lane's MFMA column of a piece: (query qi, head h of the group).
+// This lane's MFMA column of one column tile: (query qi, head h of the group).
 struct LaneCol {
   int qi, qhead, lin_last;
   bool ok;
   const uint32_t* vrow;
 };
 
-template <typename T, int D>
+template <typename T, int D, int CTW>
 __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   using S = TileShape<T, D>;
-  using DT = DecodeTile<T, D>;
+  using DT = DecodeTile<T, D, CTW>;
   constexpr int E16 = S::E16, NCH = S::NCH, NT = S::NT, CPR = S::CPR;
   constexpr int TT = DT::TT, SUB = DT::SUB;
   constexpr int TAB_PER_LANE = kTableSlice / 64;
+  // One column tile prefetches the next piece's Q; four load theirs at the
+  // piece switch (their registers hold the extra accumulators instead).
+  constexpr bool kPrefetchQ = CTW == 1;
   __shared__ __attribute__((aligned(16))) uint4 vlds_a[DT::VALLOC];
   __shared__ __attribute__((aligned(16))) uint4 vlds_b[DT::VALLOC];
   __shared__ int32_t tab[2][kTableSlice];
@@ -164,7 +177,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   T* const vbase = static_cast<T*>(a.v_pool) + (int64_t)kvh * D;
   // Fused append: this step's tokens are read from the input K/V (so no
   // wave waits for another's pool write) and written to their pool slots by
-  // the column-tile-0 piece that covers them.
+  // the column-group-0 piece that covers them.
   const T* const knew = a.k_new ? static_cast<const T*>(a.k_new) + (int64_t)kvh * a.kn_head_stride : nullptr;
   const T* const vnew = a.v_new ? static_cast<const T*>(a.v_new) + (int64_t)kvh * a.vn_head_stride : nullptr;
 
@@ -173,8 +186,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   };
 
   // Block-table slice of a piece: loaded into registers (lane i holds entries
-  // i + 64j), stored to LDS when the piece's first tile is issued.  The host
-  // keeps a piece within kTableSlice - 2 blocks.
+  // i + 64j), stored to LDS when the piece's first tile is issued.
   auto load_table = [&](const Piece& x, int (&t)[TAB_PER_LANE]) {
     const int lb0 = logical_block(x.tok_begin);
     const int n = logical_block(x.tok_end - 1) - lb0 + 1;
@@ -189,10 +201,10 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
     for (int j = 0; j < TAB_PER_LANE; ++j) tab[b][j * 64 + lane] = t[j];
   };
 
-  auto lane_col = [&](const Piece& x) -> LaneCol {
+  auto lane_col = [&](const Piece& x, int ct) -> LaneCol {
     LaneCol c;
     const int ncols = x.q_len * G;
-    const int col = x.ctile * 16 + l16;
+    const int col = (x.cgroup * CTW + ct) * 16 + l16;
     c.ok = col < ncols;
     const int colc = c.ok ? col : ncols - 1;
     c.qi = colc / G;
@@ -202,15 +214,18 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
     return c;
   };
 
-  // B operand: Q^T chunks of this lane's column.
-  auto load_q = [&](const Piece& x, uint4 (&qdst)[NCH]) {
-    const LaneCol c = lane_col(x);
-    const T* qrow = static_cast<const T*>(a.q) + (int64_t)(x.q_start + c.qi) * a.q_tok_stride +
-                    (int64_t)c.qhead * a.q_head_stride;
+  // B operands: Q^T chunks of this lane's columns.
+  auto load_q = [&](const Piece& x, uint4 (&qdst)[CTW][NCH]) {
 #pragma unroll
-    for (int kk = 0; kk < NCH; ++kk) {
-      const int ch = kk * 4 + g;
-      qdst[kk] = (c.ok && ch < CPR) ? load16(qrow + ch * E16) : zero_u4();
+    for (int ct = 0; ct < CTW; ++ct) {
+      const LaneCol c = lane_col(x, ct);
+      const T* qrow = static_cast<const T*>(a.q) + (int64_t)(x.q_start + c.qi) * a.q_tok_stride +
+                      (int64_t)c.qhead * a.q_head_stride;
+#pragma unroll
+      for (int kk = 0; kk < NCH; ++kk) {
+        const int ch = kk * 4 + g;
+        qdst[ct][kk] = (c.ok && ch < CPR) ? load16(qrow + ch * E16) : zero_u4();
+      }
     }
   };
 
@@ -237,7 +252,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
         const int64_t t = x.q_start + (pc - x.computed);
         kp[s] = knew + t * a.kn_tok_stride;
         vp[s] = vnew + t * a.vn_tok_stride;
-        if (x.ctile == 0 && pc == pos) fresh[s] = off;
+        if (x.cgroup == 0 && pc == pos) fresh[s] = off;
       }
     }
 #pragma unroll
@@ -278,11 +293,12 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
       for (int kk = 0; kk < NCH; ++kk) vdst[(s * NCH + kk) * 64 + lane] = vr[s][kk];
   };
 
-  // Prologue: this piece's table and Q, the next piece's table and Q, then
+  // Prologue: this piece's table and Q, the next piece's table (and Q), then
   // the first tile.
   Piece cur = read_piece(a.pieces, p);
   int tb = 0;
-  uint4 qf[NCH], qn[NCH];
+  uint4 qf[CTW][NCH];
+  uint4 qn[kPrefetchQ ? CTW : 1][NCH];
   int tn[TAB_PER_LANE];
   {
     int tc[TAB_PER_LANE];
@@ -296,7 +312,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   if (have_nxt) {
     nxt = read_piece(a.pieces, p + 1);
     load_table(nxt, tn);
-    load_q(nxt, qn);
+    if constexpr (kPrefetchQ) load_q(nxt, qn);
   }
   uint4 ka[SUB][NCH], kb[SUB][NCH];
   {
@@ -307,12 +323,18 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
     store_fresh(ka, vr, fresh);
   }
 
-  LaneCol lc = lane_col(cur);
-  float m_run = -INFINITY;  // per-column base (log2 domain), uniform across the column's lanes
-  float l_run = 0.f;        // this lane's share of the column's probability sum
-  f32x4 acc[NT];
+  LaneCol lc[CTW];
+  float m_run[CTW];  // per-column base (log2 domain), uniform across the column's lanes
+  float l_run[CTW];  // this lane's share of the column's probability sum
+  f32x4 acc[CTW][NT];
 #pragma unroll
-  for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int ct = 0; ct < CTW; ++ct) {
+    lc[ct] = lane_col(cur, ct);
+    m_run[ct] = -INFINITY;
+    l_run[ct] = 0.f;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) acc[ct][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   int t0 = cur.tok_begin;
 
   // One tile: start loading the next tile into (kx, registers for vx), then
@@ -326,12 +348,23 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
     const int computed = cur.computed;
     const int tok_end = cur.tok_end;
     const bool need_mask = t0 + TT > (computed < tok_end ? computed : tok_end);
-    uint32_t vw[3] = {0u, 0u, 0u};
+    // (One-dimensional word arrays: LLVM turns a two-dimensional one into
+    // an LDS allocation.)
+    uint32_t vw0[CTW], vw1[CTW], vw2[CTW];
     const int jw0 = (t0 > computed ? t0 - computed : 0) >> 5;
-    if (need_mask && lc.vrow != nullptr) {
-      const int last_word = (cur.q_len - 1) >> 5;
 #pragma unroll
-      for (int i = 0; i < 3; ++i) vw[i] = lc.vrow[jw0 + i <= last_word ? jw0 + i : last_word];
+    for (int ct = 0; ct < CTW; ++ct) vw0[ct] = vw1[ct] = vw2[ct] = 0u;
+    if (need_mask && lc[0].vrow != nullptr) {
+      const int last_word = (cur.q_len - 1) >> 5;
+      const int w0 = jw0 <= last_word ? jw0 : last_word;
+      const int w1 = jw0 + 1 <= last_word ? jw0 + 1 : last_word;
+      const int w2 = jw0 + 2 <= last_word ? jw0 + 2 : last_word;
+#pragma unroll
+      for (int ct = 0; ct < CTW; ++ct) {
+        vw0[ct] = lc[ct].vrow[w0];
+        vw1[ct] = lc[ct].vrow[w1];
+        vw2[ct] = lc[ct].vrow[w2];
+      }
     }
 
     const int nt0 = t0 + TT;
@@ -349,72 +382,83 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
       issue_tile(nxt, tb ^ 1, nxt.tok_begin, kx, vr, fresh);
     }
 
-    // S^T tile: rows = TT tokens (16-row groups), columns = this lane's col.
-    f32x4 st[SUB];
-#pragma unroll
-    for (int s = 0; s < SUB; ++s) {
-      st[s] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < NCH; ++kk) st[s] = Mma<T>::qk(kc[s][kk], qf[kk], st[s]);
-    }
-
-    // Scale and mask.
-    float sv[SUB][4];
-    float mt = -INFINITY;
+    // S^T tiles: rows = TT tokens (16-row groups), columns = this lane's
+    // column of each column tile; the K operands serve every column tile.
+    f32x4 st[CTW][SUB];
 #pragma unroll
     for (int s = 0; s < SUB; ++s)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int pos = t0 + 16 * s + 4 * g + r;
-        bool vis = true;
-        if (need_mask) {
-          if (pos >= tok_end) {
-            vis = false;
-          } else if (pos >= computed) {
-            const int j = pos - computed;
-            if (lc.vrow == nullptr) {
-              vis = pos <= lc.lin_last;
-            } else {
-              const int wi = (j >> 5) - jw0;
-              const uint32_t word = wi == 0 ? vw[0] : (wi == 1 ? vw[1] : vw[2]);
-              vis = (word >> (j & 31)) & 1u;
+      for (int ct = 0; ct < CTW; ++ct) {
+        st[ct][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < NCH; ++kk) st[ct][s] = Mma<T>::qk(kc[s][kk], qf[ct][kk], st[ct][s]);
+      }
+
+    // Scale, mask and the online softmax of each column tile.
+    float p4[CTW][SUB][4];
+#pragma unroll
+    for (int ct = 0; ct < CTW; ++ct) {
+      float sv[SUB][4];
+      float mt = -INFINITY;
+#pragma unroll
+      for (int s = 0; s < SUB; ++s)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int pos = t0 + 16 * s + 4 * g + r;
+          bool vis = true;
+          if (need_mask) {
+            if (pos >= tok_end) {
+              vis = false;
+            } else if (pos >= computed) {
+              const int j = pos - computed;
+              if (lc[ct].vrow == nullptr) {
+                vis = pos <= lc[ct].lin_last;
+              } else {
+                const int wi = (j >> 5) - jw0;
+                const uint32_t word = wi == 0 ? vw0[ct] : (wi == 1 ? vw1[ct] : vw2[ct]);
+                vis = (word >> (j & 31)) & 1u;
+              }
             }
           }
+          const float x = vis ? st[ct][s][r] * a.scale_log2 : -INFINITY;
+          sv[s][r] = x;
+          mt = fmaxf(mt, x);
         }
-        const float x = vis ? st[s][r] * a.scale_log2 : -INFINITY;
-        sv[s][r] = x;
-        mt = fmaxf(mt, x);
-      }
-    mt = row_max4(mt);
-    // Lazy rescale: move the base only when some column's max outgrows it.
-    if (__any(mt > m_run + kRescaleSlack)) {
-      const float m_new = fmaxf(m_run, mt);
-      const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run - m_new);
-      l_run *= alpha;
+      mt = row_max4(mt);
+      // Lazy rescale: move the base only when some column's max outgrows it.
+      if (__any(mt > m_run[ct] + kRescaleSlack)) {
+        const float m_new = fmaxf(m_run[ct], mt);
+        const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run[ct] - m_new);
+        l_run[ct] *= alpha;
 #pragma unroll
-      for (int n = 0; n < NT; ++n) acc[n] *= alpha;
-      m_run = m_new;
+        for (int n = 0; n < NT; ++n) acc[ct][n] *= alpha;
+        m_run[ct] = m_new;
+      }
+      const float nbase = (m_run[ct] == -INFINITY) ? 0.f : -m_run[ct];
+#pragma unroll
+      for (int s = 0; s < SUB; ++s)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p4[ct][s][r] = fast_exp2(sv[s][r] + nbase);  // sv is already scaled
+          l_run[ct] += p4[ct][s][r];
+        }
     }
-    const float nbase = (m_run == -INFINITY) ? 0.f : -m_run;
-    float p4[SUB][4];
-#pragma unroll
-    for (int s = 0; s < SUB; ++s)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p4[s][r] = fast_exp2(sv[s][r] + nbase);  // sv is already scaled
-        l_run += p4[s][r];
-      }
 
-    // O^T += V^T P^T with V^T from the LDS tile: 32 tokens per MFMA k-step
-    // (16x16x32), or 16 (16x16x16) for a single 16-row group.
+    // O^T += V^T P^T with V^T from the LDS tile (each transpose read serves
+    // every column tile): 32 tokens per MFMA k-step (16x16x32), or 16
+    // (16x16x16) for a single 16-row group.
     char* vbytes = reinterpret_cast<char*>(vc);
     if constexpr (sizeof(T) == 2 && SUB == 1) {
       using V4 = typename std::conditional<std::is_same<T, __bf16>::value, s16x4, f16x4>::type;
       const int q4 = l16 & 3;
-      T pt[4];
+      V4 pb[CTW];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) pt[r] = from_f32<T>(p4[0][r]);
-      const V4 pb = bitcast<V4>(pt);
+      for (int ct = 0; ct < CTW; ++ct) {
+        T pt[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pt[r] = from_f32<T>(p4[ct][0][r]);
+        pb[ct] = bitcast<V4>(pt);
+      }
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
         // The transpose hands lane (g, l16) dims 16n + l16 of rows 4g + 0..3:
@@ -422,10 +466,13 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
         const int c = 2 * n + (q4 >> 1);
         const int lo = vslot<NCH>(4 * g + (l16 >> 2), c) * 16 + (q4 & 1) * 8;
         const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vbytes + lo));
-        if constexpr (std::is_same<T, __bf16>::value) {
-          acc[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v0, pb, acc[n], 0, 0, 0);
-        } else {
-          acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(bitcast<f16x4>(v0), pb, acc[n], 0, 0, 0);
+#pragma unroll
+        for (int ct = 0; ct < CTW; ++ct) {
+          if constexpr (std::is_same<T, __bf16>::value) {
+            acc[ct][n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v0, pb[ct], acc[ct][n], 0, 0, 0);
+          } else {
+            acc[ct][n] = __builtin_amdgcn_mfma_f32_16x16x16f16(bitcast<f16x4>(v0), pb[ct], acc[ct][n], 0, 0, 0);
+          }
         }
       }
     } else if constexpr (sizeof(T) == 2) {
@@ -433,11 +480,13 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
       const int q4 = l16 & 3;
 #pragma unroll
       for (int h = 0; h < SUB / 2; ++h) {
-        V8 pb;
+        V8 pb[CTW];
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
+        for (int ct = 0; ct < CTW; ++ct)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) pb[s * 4 + r] = from_f32<T>(p4[2 * h + s][r]);
+          for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pb[ct][s * 4 + r] = from_f32<T>(p4[ct][2 * h + s][r]);
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
           // Lane (g, l16) addresses row 32h + 16j + 4g + l16/4, dims
@@ -450,10 +499,13 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
           const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vbytes + hi));
           const s16x4 both[2] = {v0, v1};
           const V8 av = bitcast<V8>(both);
-          if constexpr (std::is_same<T, __bf16>::value) {
-            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb, acc[n], 0, 0, 0);
-          } else {
-            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb, acc[n], 0, 0, 0);
+#pragma unroll
+          for (int ct = 0; ct < CTW; ++ct) {
+            if constexpr (std::is_same<T, __bf16>::value) {
+              acc[ct][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[ct], acc[ct][n], 0, 0, 0);
+            } else {
+              acc[ct][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb[ct], acc[ct][n], 0, 0, 0);
+            }
           }
         }
       }
@@ -467,7 +519,9 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float av = vfl[vslot<NCH>(16 * s + 4 * g + r, d >> 2) * 4 + (d & 3)];
-            acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, p4[s][r], acc[n], 0, 0, 0);
+#pragma unroll
+            for (int ct = 0; ct < CTW; ++ct)
+              acc[ct][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, p4[ct][s][r], acc[ct][n], 0, 0, 0);
           }
       }
     }
@@ -482,38 +536,50 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
     return !next_in_cur;
   };
 
-  // Piece finished: write the output (whole segment) or its partial, then
+  // Piece finished: write the outputs (whole segment) or its partials, then
   // switch to the next piece (its first tile is already staged) and start
   // fetching the one after.  Returns false after the wave's last piece.
   auto end_piece = [&]() -> bool {
-    const float l_tot = row_sum4(l_run);
-    if (cur.slot < 0) {
-      if (lc.ok) {
-        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-        T* orow = static_cast<T*>(a.out) + (int64_t)(cur.q_start + lc.qi) * a.out_tok_stride +
-                  (int64_t)lc.qhead * a.out_head_stride;
 #pragma unroll
-        for (int n = 0; n < NT; ++n)
+    for (int ct = 0; ct < CTW; ++ct) {
+      const float l_tot = row_sum4(l_run[ct]);
+      if (cur.slot < 0) {
+        if (lc[ct].ok) {
+          const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+          T* orow = static_cast<T*>(a.out) + (int64_t)(cur.q_start + lc[ct].qi) * a.out_tok_stride +
+                    (int64_t)lc[ct].qhead * a.out_head_stride;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) orow[16 * n + 4 * g + r] = from_f32<T>(acc[n][r] * inv);
+          for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) orow[16 * n + 4 * g + r] = from_f32<T>(acc[ct][n][r] * inv);
+        }
+      } else if (lc[ct].ok) {
+        const int64_t cs = ((int64_t)cur.slot * Hkv + kvh) * (16 * CTW) + ct * 16 + l16;
+        float* pacc = a.part_acc + cs * D;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(pacc + 16 * n + 4 * g) = acc[ct][n];
+        if (g == 0) *reinterpret_cast<float2*>(a.part_ml + cs * 2) = make_float2(m_run[ct], l_tot);
       }
-    } else if (lc.ok) {
-      const int64_t cs = ((int64_t)cur.slot * Hkv + kvh) * 16 + l16;
-      float* pacc = a.part_acc + cs * D;
-#pragma unroll
-      for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(pacc + 16 * n + 4 * g) = acc[n];
-      if (g == 0) *reinterpret_cast<float2*>(a.part_ml + cs * 2) = make_float2(m_run, l_tot);
     }
     if (!have_nxt) return false;
     cur = nxt;
     tb ^= 1;
+    if constexpr (kPrefetchQ) {
 #pragma unroll
-    for (int kk = 0; kk < NCH; ++kk) qf[kk] = qn[kk];
-    lc = lane_col(cur);
-    m_run = -INFINITY;
-    l_run = 0.f;
+      for (int ct = 0; ct < CTW; ++ct)
 #pragma unroll
-    for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int kk = 0; kk < NCH; ++kk) qf[ct][kk] = qn[ct][kk];
+    } else {
+      load_q(cur, qf);
+    }
+#pragma unroll
+    for (int ct = 0; ct < CTW; ++ct) {
+      lc[ct] = lane_col(cur, ct);
+      m_run[ct] = -INFINITY;
+      l_run[ct] = 0.f;
+#pragma unroll
+      for (int n = 0; n < NT; ++n) acc[ct][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     t0 = cur.tok_begin;
     ++p;
     have_nxt = p + 1 < p_end;
@@ -521,7 +587,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
     if (have_nxt) {
       nxt = read_piece(a.pieces, p + 1);
       load_table(nxt, tn);
-      load_q(nxt, qn);
+      if constexpr (kPrefetchQ) load_q(nxt, qn);
     }
     return true;
   };
@@ -535,9 +601,9 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Merge: one wave per (job, kv head); lane (g, l16) combines dims 16n + 4g..+3
-// of column l16 over the job's partials, MC partials per round trip, by
-// log-sum-exp in the log2 domain.
+// Merge: one wave per (job, kv head, column tile of the job's group); lane
+// (g, l16) combines dims 16n + 4g..+3 of column l16 over the job's partials,
+// MC partials per round trip, by log-sum-exp in the log2 domain.
 // ---------------------------------------------------------------------------
 struct MergeArgs {
   const float* part_acc;
@@ -547,6 +613,7 @@ struct MergeArgs {
   const int32_t* __restrict__ jobs;  // [num_jobs][LVAMD_MERGE_FIELDS]
   int32_t num_kv_heads;
   int32_t group;
+  int32_t col_tiles;  // column tiles per partial slot (the decode launch's)
 };
 
 template <typename T, int D>
@@ -556,14 +623,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
   constexpr int MC = (192 / (D / 4 + 2)) < 2 ? 2 : ((192 / (D / 4 + 2)) > 8 ? 8 : 192 / (D / 4 + 2));
   const int Hkv = a.num_kv_heads;
   const int G = a.group;
-  const int job = blockIdx.x / Hkv;
-  const int kvh = blockIdx.x - job * Hkv;
+  const int ctw = a.col_tiles;
+  const int wave = blockIdx.x;
+  const int ct = wave % ctw;
+  const int jh = wave / ctw;
+  const int job = jh / Hkv;
+  const int kvh = jh - job * Hkv;
   const int lane = threadIdx.x;
   const int l16 = lane & 15;
   const int g = lane >> 4;
   const int32_t* jb = a.jobs + (int64_t)job * LVAMD_MERGE_FIELDS;
-  const int ctile = jb[1], slot0 = jb[2], np = jb[3], q_start = jb[4], q_len = jb[5];
-  const int col = ctile * 16 + l16;
+  const int cgroup = jb[1], slot0 = jb[2], np = jb[3], q_start = jb[4], q_len = jb[5];
+  const int col = (cgroup * ctw + ct) * 16 + l16;
   if (col >= q_len * G) return;
   const int qi = col / G;
   const int qhead = kvh * G + (col - qi * G);
@@ -578,7 +649,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
     f32x4 pa[MC][NT];
 #pragma unroll
     for (int i = 0; i < MC; ++i) {
-      const int64_t cs = ((int64_t)(slot0 + (j0 + i < np ? j0 + i : np - 1)) * Hkv + kvh) * 16 + l16;
+      const int slot = slot0 + (j0 + i < np ? j0 + i : np - 1);
+      const int64_t cs = ((int64_t)slot * Hkv + kvh) * (16 * ctw) + ct * 16 + l16;
       ml[i] = *reinterpret_cast<const float2*>(a.part_ml + cs * 2);
 #pragma unroll
       for (int n = 0; n < NT; ++n) pa[i][n] = *reinterpret_cast<const f32x4*>(a.part_acc + cs * D + 16 * n + 4 * g);
@@ -611,18 +683,60 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
     for (int r = 0; r < 4; ++r) orow[16 * n + 4 * g + r] = from_f32<T>(o[n][r] * inv);
 }
 
-template <typename T>
-static int launch_decode_t(int head_size, dim3 grid, hipStream_t s, const DecodeArgs& a) {
+// ---------------------------------------------------------------------------
+// Launch tables: (dtype, head size, column tiles per wave) -> kernel.
+// ---------------------------------------------------------------------------
+static bool head_size_supported(int d) {
+  return d == 32 || d == 64 || d == 80 || d == 96 || d == 128 || d == 256;
+}
+static bool col_tiles_supported(int ctw) { return ctw == 1 || ctw == 4; }
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Four column tiles per wave are built for rows of at most 256 bytes: wider
+// rows leave no registers for four accumulator sets.
+template <typename T, int D, int CTW>
+constexpr bool decode_built = CTW == 1 || (int)sizeof(T) * D <= 256;
+
+template <typename T, int D, int CTW, typename F>
+static int with_kernel(F& f) {
+  if constexpr (decode_built<T, D, CTW>) {
+    return f.template operator()<T, D, CTW>();
+  } else {
+    return LVAMD_ERR_UNSUPPORTED;
+  }
+}
+
+// Calls F.template operator()<T, D, CTW>() for the run-time triple; returns
+// LVAMD_ERR_UNSUPPORTED for a combination without a kernel.
+template <typename T, int CTW, typename F>
+static int with_head_size(int head_size, F& f) {
   switch (head_size) {
-    case 32: hipLaunchKernelGGL((paged_decode_kernel<T, 32>), grid, dim3(64), 0, s, a); break;
-    case 64: hipLaunchKernelGGL((paged_decode_kernel<T, 64>), grid, dim3(64), 0, s, a); break;
-    case 80: hipLaunchKernelGGL((paged_decode_kernel<T, 80>), grid, dim3(64), 0, s, a); break;
-    case 96: hipLaunchKernelGGL((paged_decode_kernel<T, 96>), grid, dim3(64), 0, s, a); break;
-    case 128: hipLaunchKernelGGL((paged_decode_kernel<T, 128>), grid, dim3(64), 0, s, a); break;
-    case 256: hipLaunchKernelGGL((paged_decode_kernel<T, 256>), grid, dim3(64), 0, s, a); break;
+    case 32: return with_kernel<T, 32, CTW>(f);
+    case 64: return with_kernel<T, 64, CTW>(f);
+    case 80: return with_kernel<T, 80, CTW>(f);
+    case 96: return with_kernel<T, 96, CTW>(f);
+    case 128: return with_kernel<T, 128, CTW>(f);
+    case 256: return with_kernel<T, 256, CTW>(f);
     default: return LVAMD_ERR_UNSUPPORTED;
   }
-  return launch_status();
+}
+template <typename F>
+static int dispatch_decode(int dtype, int head_size, int col_tiles, F f) {
+  if (dtype_size(dtype) == 0 || !head_size_supported(head_size) || !col_tiles_supported(col_tiles))
+    return LVAMD_ERR_UNSUPPORTED;
+  if (col_tiles == 4) {
+    switch (dtype) {
+      case LVAMD_BF16: return with_head_size<__bf16, 4>(head_size, f);
+      case LVAMD_F16: return with_head_size<_Float16, 4>(head_size, f);
+      default: return with_head_size<float, 4>(head_size, f);
+    }
+  }
+  switch (dtype) {
+    case LVAMD_BF16: return with_head_size<__bf16, 1>(head_size, f);
+    case LVAMD_F16: return with_head_size<_Float16, 1>(head_size, f);
+    default: return with_head_size<float, 1>(head_size, f);
+  }
 }
 
 template <typename T>
@@ -639,12 +753,6 @@ static int launch_merge_t(int head_size, dim3 grid, hipStream_t s, const MergeAr
   return launch_status();
 }
 
-static bool head_size_supported(int d) {
-  return d == 32 || d == 64 || d == 80 || d == 96 || d == 128 || d == 256;
-}
-
-static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
-
 }  // namespace lvamd
 
 using namespace lvamd;
@@ -658,10 +766,10 @@ extern "C" int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t
                                   const int32_t* pieces, const int32_t* wave_first, int32_t waves_per_head,
                                   const int32_t* tables, const uint32_t* vis,
                                   float* part_acc, float* part_ml, int64_t num_partial_slots,
-                                  int32_t num_kv_heads, int32_t group, int32_t head_size,
+                                  int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t col_tiles,
                                   int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream) {
   const int es = dtype_size(dtype);
-  if (es == 0 || !head_size_supported(head_size)) return LVAMD_ERR_UNSUPPORTED;
+  if (es == 0 || !head_size_supported(head_size) || !col_tiles_supported(col_tiles)) return LVAMD_ERR_UNSUPPORTED;
   if (waves_per_head < 0 || num_kv_heads <= 0 || group <= 0 || block_size <= 0 || num_partial_slots < 0)
     return LVAMD_ERR_INVALID_ARGUMENT;
   if (waves_per_head == 0) return LVAMD_OK;
@@ -707,68 +815,41 @@ extern "C" int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t
   a.scale_log2 = scale * 1.4426950408889634f;
   const dim3 grid((unsigned)(waves_per_head * num_kv_heads));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (dtype) {
-    case LVAMD_BF16: return launch_decode_t<__bf16>(head_size, grid, s, a);
-    case LVAMD_F16: return launch_decode_t<_Float16>(head_size, grid, s, a);
-    default: return launch_decode_t<float>(head_size, grid, s, a);
-  }
+  return dispatch_decode(dtype, head_size, col_tiles, [&]<typename T, int D, int CTW>() -> int {
+    hipLaunchKernelGGL((paged_decode_kernel<T, D, CTW>), grid, dim3(64), 0, s, a);
+    return launch_status();
+  });
 }
 
-template <typename T>
-static const void* decode_kernel_ptr(int head_size) {
-  switch (head_size) {
-    case 32: return reinterpret_cast<const void*>(&paged_decode_kernel<T, 32>);
-    case 64: return reinterpret_cast<const void*>(&paged_decode_kernel<T, 64>);
-    case 80: return reinterpret_cast<const void*>(&paged_decode_kernel<T, 80>);
-    case 96: return reinterpret_cast<const void*>(&paged_decode_kernel<T, 96>);
-    case 128: return reinterpret_cast<const void*>(&paged_decode_kernel<T, 128>);
-    case 256: return reinterpret_cast<const void*>(&paged_decode_kernel<T, 256>);
-    default: return nullptr;
-  }
+extern "C" int lvamd_paged_decode_tile_tokens(int32_t dtype, int32_t head_size, int32_t col_tiles) {
+  return dispatch_decode(dtype, head_size, col_tiles,
+                         []<typename T, int D, int CTW>() -> int { return DecodeTile<T, D, CTW>::TT; });
 }
 
-template <typename T>
-static int decode_tile_tokens_t(int head_size) {
-  switch (head_size) {
-    case 32: return DecodeTile<T, 32>::TT;
-    case 64: return DecodeTile<T, 64>::TT;
-    case 80: return DecodeTile<T, 80>::TT;
-    case 96: return DecodeTile<T, 96>::TT;
-    case 128: return DecodeTile<T, 128>::TT;
-    case 256: return DecodeTile<T, 256>::TT;
-    default: return LVAMD_ERR_UNSUPPORTED;
-  }
-}
-
-extern "C" int lvamd_paged_decode_tile_tokens(int32_t dtype, int32_t head_size) {
-  if (dtype_size(dtype) == 0 || !head_size_supported(head_size)) return LVAMD_ERR_UNSUPPORTED;
-  return dtype == LVAMD_BF16 ? decode_tile_tokens_t<__bf16>(head_size)
-         : dtype == LVAMD_F16 ? decode_tile_tokens_t<_Float16>(head_size)
-                              : decode_tile_tokens_t<float>(head_size);
-}
-
-extern "C" int lvamd_paged_decode_resident_waves(int32_t dtype, int32_t head_size) {
-  if (dtype_size(dtype) == 0 || !head_size_supported(head_size)) return LVAMD_ERR_UNSUPPORTED;
-  const void* fn = dtype == LVAMD_BF16 ? decode_kernel_ptr<__bf16>(head_size)
-                   : dtype == LVAMD_F16 ? decode_kernel_ptr<_Float16>(head_size)
-                                        : decode_kernel_ptr<float>(head_size);
-  int device = 0, cus = 0, per_cu = 0;
-  if (hipGetDevice(&device) != hipSuccess) return LVAMD_ERR_LAUNCH;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return LVAMD_ERR_LAUNCH;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64, 0) != hipSuccess) return LVAMD_ERR_LAUNCH;
-  return per_cu * cus;
+extern "C" int lvamd_paged_decode_resident_waves(int32_t dtype, int32_t head_size, int32_t col_tiles) {
+  return dispatch_decode(dtype, head_size, col_tiles, []<typename T, int D, int CTW>() -> int {
+    int device = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&device) != hipSuccess) return LVAMD_ERR_LAUNCH;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+      return LVAMD_ERR_LAUNCH;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(&paged_decode_kernel<T, D, CTW>), 64, 0) != hipSuccess)
+      return LVAMD_ERR_LAUNCH;
+    return per_cu * cus;
+  });
 }
 
 extern "C" int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
                                            void* out, int64_t out_token_stride, int64_t out_head_stride,
                                            const int32_t* jobs, int32_t num_jobs,
-                                           int32_t num_kv_heads, int32_t group, int32_t head_size,
+                                           int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t col_tiles,
                                            int32_t dtype, lvamd_stream_t stream) {
-  if (dtype_size(dtype) == 0 || !head_size_supported(head_size)) return LVAMD_ERR_UNSUPPORTED;
+  if (dtype_size(dtype) == 0 || !head_size_supported(head_size) || !col_tiles_supported(col_tiles))
+    return LVAMD_ERR_UNSUPPORTED;
   if (num_jobs < 0 || num_kv_heads <= 0 || group <= 0) return LVAMD_ERR_INVALID_ARGUMENT;
   if (num_jobs == 0) return LVAMD_OK;
   if (!part_acc || !part_ml || !out || !jobs) return LVAMD_ERR_INVALID_ARGUMENT;
-  if ((int64_t)num_jobs * num_kv_heads > 0x7fffffffLL) return LVAMD_ERR_INVALID_ARGUMENT;
+  if ((int64_t)num_jobs * num_kv_heads * col_tiles > 0x7fffffffLL) return LVAMD_ERR_INVALID_ARGUMENT;
   MergeArgs a;
   a.part_acc = part_acc;
   a.part_ml = part_ml;
@@ -778,7 +859,8 @@ extern "C" int lvamd_paged_attention_merge(const float* part_acc, const float* p
   a.jobs = jobs;
   a.num_kv_heads = num_kv_heads;
   a.group = group;
-  const dim3 grid((unsigned)(num_jobs * num_kv_heads));
+  a.col_tiles = col_tiles;
+  const dim3 grid((unsigned)(num_jobs * num_kv_heads * col_tiles));
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case LVAMD_BF16: return launch_merge_t<__bf16>(head_size, grid, s, a);

@@ -15,7 +15,7 @@ from pathlib import Path
 from light_vllm_amd.errors import ExecutionError, ExecutionNotReadyError
 
 LIB_NAME = "liblvamd_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
@@ -43,13 +43,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i64,
          _p, _p, _i32, _p, _p, _p, _p, _i64,
-         _i32, _i32, _i32, _i32, _f32, _i32, _p],
+         _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p],
     ),
-    "lvamd_paged_decode_resident_waves": (ctypes.c_int, [_i32, _i32]),
-    "lvamd_paged_decode_tile_tokens": (ctypes.c_int, [_i32, _i32]),
+    "lvamd_paged_decode_resident_waves": (ctypes.c_int, [_i32, _i32, _i32]),
+    "lvamd_paged_decode_tile_tokens": (ctypes.c_int, [_i32, _i32, _i32]),
     "lvamd_paged_attention_merge": (
         ctypes.c_int,
-        [_p, _p, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p],
+        [_p, _p, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p],
     ),
     "lvamd_paged_prefill": (
         ctypes.c_int,
@@ -100,28 +100,42 @@ def load() -> ctypes.CDLL:
     return lib
 
 
-_RESIDENT: dict[tuple[int, int], int] = {}
+# Column tiles per decode wave the library builds: 1, and 4 for narrow rows.
+DECODE_COL_TILES = (1, 4)
+
+_RESIDENT: dict[tuple[int, int, int], int] = {}
 
 
-def resident_decode_waves(dtype_code: int, head_size: int) -> int:
-    """Decode waves the current GPU holds at once (cached per dtype and head size)."""
+def resident_decode_waves(dtype_code: int, head_size: int, col_tiles: int = 1) -> int:
+    """Decode waves the current GPU holds at once (cached per kernel)."""
 
-    key = (dtype_code, head_size)
+    key = (dtype_code, head_size, col_tiles)
     found = _RESIDENT.get(key)
     if found is None:
-        found = load().lvamd_paged_decode_resident_waves(dtype_code, head_size)
+        found = load().lvamd_paged_decode_resident_waves(dtype_code, head_size, col_tiles)
         check(min(found, 0), "lvamd_paged_decode_resident_waves")
         _RESIDENT[key] = found
     return found
 
 
 @functools.lru_cache(maxsize=None)
-def decode_tile_tokens(dtype_code: int, head_size: int) -> int:
-    """Tokens per decode-kernel tile for this dtype and head size (the planner's unit)."""
+def decode_tile_tokens(dtype_code: int, head_size: int, col_tiles: int = 1) -> int:
+    """Tokens per decode-kernel tile for this kernel (the planner's unit)."""
 
-    found = int(load().lvamd_paged_decode_tile_tokens(dtype_code, head_size))
+    found = int(load().lvamd_paged_decode_tile_tokens(dtype_code, head_size, col_tiles))
     check(min(found, 0), "lvamd_paged_decode_tile_tokens")
     return found
+
+
+@functools.lru_cache(maxsize=None)
+def decode_max_col_tiles(dtype_code: int, head_size: int) -> int:
+    """The widest column-tile count a decode kernel is built with for this shape."""
+
+    lib = load()
+    for ctw in sorted(DECODE_COL_TILES, reverse=True):
+        if lib.lvamd_paged_decode_tile_tokens(dtype_code, head_size, ctw) > 0:
+            return ctw
+    raise ExecutionError(f"no decode kernel for dtype {dtype_code}, head size {head_size}")
 
 
 @functools.lru_cache(maxsize=None)

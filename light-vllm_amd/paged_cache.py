@@ -174,7 +174,11 @@ def compact_slots(
     required = (num_computed_tokens + num_reserved_query_tokens + bs - 1) // bs
     if len(block_ids) != required:
         raise KVCacheError("block table does not exactly cover the reserved query slots")
-    if any(type(b) is not int or not 0 <= b < config.num_blocks for b in block_ids):
+    # Every id an int (not a bool or numpy scalar) in [0, num_blocks); checked
+    # with C-level passes (map/min/max) since tables run to thousands of ids.
+    if block_ids and (
+        set(map(type, block_ids)) != {int} or min(block_ids) < 0 or max(block_ids) >= config.num_blocks
+    ):
         raise KVCacheError("block table contains an invalid physical block")
     if len(set(block_ids)) != len(block_ids):
         raise KVCacheError("block table aliases a physical block within one request")
@@ -266,7 +270,8 @@ def hip_block_copy(cache, src_blocks, dst_blocks) -> None:
     if len(src) != len(dst):
         raise ValueError("block copy needs one destination per source")
     num_blocks = cache.config.num_blocks
-    if any(type(b) is not int or not 0 <= b < num_blocks for b in src + dst):
+    both = src + dst
+    if both and (set(map(type, both)) != {int} or min(both) < 0 or max(both) >= num_blocks):
         raise KVCacheError("block copy names an invalid physical block")
     if len(set(dst)) != len(dst):
         raise KVCacheError("block copy writes the same physical block twice")

@@ -49,6 +49,13 @@ MERGE_FIELDS = 8
 # instead, so that every piece is whole tiles (a partial tile costs a full
 # load round trip; measured on C2, 16-token units were slower than 32).
 UNIT_TOKENS = 32
+# Relative cost per K/V token of the four-column-tile decode kernel against
+# the one-tile kernel (16-token tiles and four accumulator sets).  The
+# planner uses four column tiles per wave when
+#   sum(seq * ceil(tiles / 4)) * COL_TILES4_COST < sum(seq * tiles)
+# over the decode rows, i.e. when the K/V re-reads it saves outweigh its
+# slower tiles.
+COL_TILES4_COST = 1.5
 
 _BIT_WEIGHTS = (np.uint64(1) << np.arange(32, dtype=np.uint64)).astype(np.uint64)
 
@@ -56,7 +63,7 @@ _BIT_WEIGHTS = (np.uint64(1) << np.arange(32, dtype=np.uint64)).astype(np.uint64
 def stream_k_pieces(
     *,
     seq: np.ndarray,
-    nct: np.ndarray,
+    ngroups: np.ndarray,
     rows: np.ndarray,
     req_meta: np.ndarray,
     num_kv_heads: int,
@@ -68,20 +75,21 @@ def stream_k_pieces(
 ):
     """Split the decode work evenly over the waves the GPU holds at once.
 
-    A segment is one (request, column tile); it has ceil(seq / unit_tokens)
-    units.  The segments of all decode rows are laid end to end and the
+    A segment is one (request, column group), a column group being the
+    ``col_tiles`` column tiles one decode wave computes together (``ngroups``
+    per request); it has ceil(seq / unit_tokens) units.  The segments of all decode rows are laid end to end and the
     flattened unit range is cut into ``waves_per_head`` contiguous shares
     that differ by at most one unit (the same cut for every kv head).  A wave's share is a list of
     pieces: the part of each segment it covers.  A piece that covers a whole
     segment writes the output directly; otherwise it writes a partial
     (max, sum, acc) to its slot and a merge job combines the segment's
-    partials, which a merge job per segment combines.  Returns (pieces
-    [n, 16] int64, wave_first [W + 1], W, largest share, jobs [m, 8] =
-    (req, column tile, first slot, partials, q_start, q_len, 0, 0), num_slots).
+    partials.  Returns (pieces [n, 16] int64, wave_first [W + 1], W, largest
+    share, jobs [m, 8] = (req, column group, first slot, partials, q_start,
+    q_len, 0, 0), num_slots).
     """
 
-    seg_req = np.repeat(np.flatnonzero(rows), nct[rows])
-    seg_ctile = np.concatenate([np.arange(n) for n in nct[rows]]) if rows.any() else np.zeros(0, np.int64)
+    seg_req = np.repeat(np.flatnonzero(rows), ngroups[rows])
+    seg_group = np.concatenate([np.arange(n) for n in ngroups[rows]]) if rows.any() else np.zeros(0, np.int64)
     seg_tiles = -(-seq[seg_req] // unit_tokens)
     total = int(seg_tiles.sum())
     seg_start = np.zeros(len(seg_req) + 1, dtype=np.int64)
@@ -106,7 +114,7 @@ def stream_k_pieces(
     req = seg_req[seg]
     pieces = np.zeros((len(lo), PIECE_FIELDS), dtype=np.int64)
     pieces[:, 0] = req
-    pieces[:, 1] = seg_ctile[seg]
+    pieces[:, 1] = seg_group[seg]
     pieces[:, 2] = (lo - seg_start[seg]) * unit_tokens
     pieces[:, 3] = np.minimum((hi - seg_start[seg]) * unit_tokens, seq[req])
     pieces[:, 4] = slot
@@ -121,7 +129,7 @@ def stream_k_pieces(
     jreq = req[first]
     jobs = np.zeros((int(first.sum()), MERGE_FIELDS), dtype=np.int64)
     jobs[:, 0] = jreq
-    jobs[:, 1] = seg_ctile[seg[first]]
+    jobs[:, 1] = seg_group[seg[first]]
     jobs[:, 2] = slot[first]
     jobs[:, 3] = npieces[seg[first]]
     jobs[:, 4] = req_meta[jreq, 4]  # q_start
@@ -147,6 +155,7 @@ class DecodeWork:
     num_jobs: int
     num_partial_slots: int
     units_per_wave: int
+    col_tiles: int  # column tiles per decode wave (partials hold 16 * col_tiles columns)
     prefill_units: Tensor | None  # int32 [n_prefill_units, 4]
     num_prefill_units: int
 
@@ -238,36 +247,57 @@ class StepPlan:
         self._work: dict[tuple[int, int], DecodeWork] = {}
 
     # -- work lists ---------------------------------------------------------
+    def decode_rows(self, prefill_columns: int) -> np.ndarray:
+        """Requests the decode kernel serves (all of them without a prefill kernel)."""
+
+        if prefill_columns > 0:
+            return self._q_lens <= DECODE_MAX_QUERIES
+        return np.ones(self.batch_size, dtype=bool)
+
+    def choose_col_tiles(self, group: int, prefill_columns: int, max_col_tiles: int) -> int:
+        """Column tiles per decode wave for layers with this group size: 4 when
+        the decode rows' K/V re-reads at one tile per wave cost more than the
+        four-tile kernel's slower tiles (``COL_TILES4_COST``), else 1."""
+
+        if max_col_tiles < 4:
+            return 1
+        rows = self.decode_rows(prefill_columns)
+        seq = (self._computed + self._q_lens)[rows]
+        nct = -(-(self._q_lens[rows] * group) // 16)
+        one = float((seq * nct).sum())
+        four = float((seq * -(-nct // 4)).sum()) * COL_TILES4_COST
+        return 4 if four < one else 1
+
     def work(
         self, group: int, num_kv_heads: int, resident_waves: int = 8 * NUM_CUS, prefill_columns: int = 0,
-        unit_tokens: int = UNIT_TOKENS,
+        unit_tokens: int = UNIT_TOKENS, col_tiles: int = 1,
     ) -> DecodeWork:
         """Work lists for layers of this (group, kv heads) shape.
 
         ``resident_waves`` is how many decode waves the GPU holds at once,
         ``prefill_columns`` the prefill kernel's unit width (0: every request
-        goes through the decode kernel) and ``unit_tokens`` the decode kernel's
-        tile; the library reports all three per dtype and head size.
+        goes through the decode kernel), ``unit_tokens`` the decode kernel's
+        tile and ``col_tiles`` its column tiles per wave; the library reports
+        the kernel figures per dtype, head size and column tiles.
         """
 
-        key = (group, num_kv_heads, resident_waves, prefill_columns, unit_tokens)
+        key = (group, num_kv_heads, resident_waves, prefill_columns, unit_tokens, col_tiles)
         found = self._work.get(key)
         if found is None:
-            found = self._build_work(group, num_kv_heads, resident_waves, prefill_columns, unit_tokens)
+            found = self._build_work(group, num_kv_heads, resident_waves, prefill_columns, unit_tokens, col_tiles)
             self._work[key] = found
         return found
 
     def _build_work(
-        self, group: int, num_kv_heads: int, resident_waves: int, prefill_columns: int, unit_tokens: int
+        self, group: int, num_kv_heads: int, resident_waves: int, prefill_columns: int, unit_tokens: int,
+        col_tiles: int,
     ) -> DecodeWork:
         computed, q_lens = self._computed, self._q_lens
         batch = self.batch_size
         seq = computed + q_lens
-        if prefill_columns > 0:
-            decode_rows = q_lens <= DECODE_MAX_QUERIES
-        else:
-            decode_rows = np.ones(batch, dtype=bool)
+        decode_rows = self.decode_rows(prefill_columns)
         nct = -(-(q_lens * group) // 16)
+        ngroups = -(-nct // col_tiles)
         pieces = wave_first = jobs = prefill_units = None
         waves = num_jobs = num_partial = num_prefill = per_wave = 0
         blocks = []
@@ -276,7 +306,7 @@ class StepPlan:
             if self.partition_tokens:
                 max_units = max(1, self.partition_tokens // unit_tokens)
             piece_tab, first_tab, waves, per_wave, job_tab, num_partial = stream_k_pieces(
-                seq=seq, nct=nct, rows=decode_rows, req_meta=self._req_meta, num_kv_heads=num_kv_heads,
+                seq=seq, ngroups=ngroups, rows=decode_rows, req_meta=self._req_meta, num_kv_heads=num_kv_heads,
                 resident_waves=resident_waves, block_size=self.block_size, max_units_per_wave=max_units,
                 unit_tokens=unit_tokens,
             )
@@ -316,4 +346,5 @@ class StepPlan:
             off += MERGE_FIELDS * num_jobs
         if num_prefill:
             prefill_units = blob[off : off + 4 * num_prefill].view(num_prefill, 4)
-        return DecodeWork(pieces, wave_first, waves, jobs, num_jobs, num_partial, per_wave, prefill_units, num_prefill)
+        return DecodeWork(pieces, wave_first, waves, jobs, num_jobs, num_partial, per_wave, col_tiles, prefill_units,
+                          num_prefill)

@@ -233,3 +233,58 @@ def test_two_split_k_layers_share_the_workspace() -> None:
         torch.cuda.synchronize()
         err = np.abs(out.float().cpu().numpy() - oracle_attention(step, lid))
         assert err.max() <= max_tol and err.mean() <= mean_tol
+
+
+# ------------------------------------------------------ four column tiles per decode wave
+@pytest.mark.parametrize("dtype", ("fp32", "fp16", "bf16"))
+@pytest.mark.parametrize("head_size", (32, 64, 80, 96, 128))
+def test_four_column_tiles_across_dtypes_and_head_sizes(dtype, head_size) -> None:
+    # Eight queries x group 4 = 32 columns: two column tiles of a four-tile group.
+    _announce(f"col_tiles=4 d={head_size} {dtype}")
+    step = make_step(hq=8, hkv=2, d=head_size, bs=16, dtype=DTYPES[dtype], computed=[700, 3, 1500, 64],
+                     layouts=_lin(8, 1, 9, 2), seed=head_size + 5)
+    _run_and_check(step, backend=lv.HipPagedAttentionBackend(decode_col_tiles=4))
+
+
+@pytest.mark.parametrize("col_tiles", (1, 4))
+@pytest.mark.parametrize("partition", (None, 32))
+def test_tree_verification_by_column_tiles(col_tiles, partition) -> None:
+    # 9-token trees at group 7 = 63 columns: four column tiles, split into
+    # many partials when partitions are short.
+    _announce(f"tree verify col_tiles={col_tiles} partition={partition}")
+    rng = np.random.default_rng(51)
+    layouts, computed = [], []
+    for _ in range(6):
+        parents = [-1] + [int(rng.integers(0, i)) for i in range(1, 8)]
+        layouts.append(tuple([-1] + [0 if p == -1 else p + 1 for p in parents]))
+        computed.append(256 + int(rng.integers(0, 900)))
+    step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=computed, layouts=layouts,
+                     shared_prefix_blocks=16, seed=52)
+    backend = lv.HipPagedAttentionBackend(decode_col_tiles=col_tiles, partition_tokens=partition)
+    _, ctx = _run_and_check(step, backend=backend)
+    work = ctx.plan.work(7, 4, lv.native.resident_decode_waves(2, 128, col_tiles), 0,
+                         lv.native.decode_tile_tokens(2, 128, col_tiles), col_tiles)
+    assert work.col_tiles == col_tiles
+
+
+@pytest.mark.parametrize("bs", (1, 3, 16))
+def test_four_column_tiles_long_queries_without_prefill_kernel(bs) -> None:
+    # 40 queries x group 7 = 280 columns = 18 column tiles: four full groups
+    # and a partial one, all through the decode kernel.
+    _announce(f"col_tiles=4 long queries bs={bs}")
+    step = make_step(hq=28, hkv=4, d=128, bs=bs, dtype=torch.bfloat16, computed=[0, 300, 1000],
+                     layouts=_lin(40, 17, 5), seed=60 + bs)
+    backend = lv.HipPagedAttentionBackend(use_prefill_kernel=False, decode_col_tiles=4, partition_tokens=256)
+    _run_and_check(step, backend=backend)
+
+
+def test_auto_column_tiles_pick_four_for_trees_and_one_for_decode() -> None:
+    _announce("auto column tiles")
+    step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[500, 900],
+                     layouts=_lin(8, 8), seed=71)
+    _, ctx = _run_and_check(step)
+    assert ctx.plan.choose_col_tiles(7, 0, 4) == 4
+    step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[500, 900],
+                     layouts=_lin(1, 1), seed=72)
+    _, ctx = _run_and_check(step)
+    assert ctx.plan.choose_col_tiles(7, 0, 4) == 1

@@ -153,15 +153,16 @@ def test_plan_request_table_matches_metadata() -> None:
         assert flat[meta[r, 0] : meta[r, 0] + meta[r, 1]].tolist() == list(table)
 
 
-@pytest.mark.parametrize("unit", (16, 32, 64))
+@pytest.mark.parametrize("unit,ctw", ((16, 1), (32, 1), (64, 1), (16, 4), (64, 4)))
 @pytest.mark.parametrize("resident", (7, 64, 2048))
 @pytest.mark.parametrize("bs", (1, 16))
 @pytest.mark.parametrize("group", (1, 7))
-def test_stream_k_pieces_cover_every_segment_once(resident, bs, group, unit) -> None:
-    rng = np.random.default_rng(resident + bs + group + unit)
+def test_stream_k_pieces_cover_every_segment_once(resident, bs, group, unit, ctw) -> None:
+    rng = np.random.default_rng(resident + bs + group + unit + ctw)
     md = _random_metadata(rng, batch=11, bs=bs)
     plan = StepPlan(md, block_size=bs, device=CPU)
-    work = plan.work(group, 4, resident, 0, unit)
+    work = plan.work(group, 4, resident, 0, unit, ctw)
+    assert work.col_tiles == ctw
     pieces = work.pieces.numpy()
     first = work.wave_first.numpy()
     waves = work.waves_per_head
@@ -170,8 +171,8 @@ def test_stream_k_pieces_cover_every_segment_once(resident, bs, group, unit) -> 
     cap = (254 * bs) // u  # units whose block-table slice fits the kernel's LDS copy
     assert work.units_per_wave <= max(cap, 1)
     seqs = np.asarray(md.num_computed_tokens) + np.asarray(md.query_lengths)
-    nct = -(-(np.asarray(md.query_lengths) * group) // 16)
-    total_tiles = int((-(-seqs // u) * nct).sum())
+    ngroups = -(-(-(-(np.asarray(md.query_lengths) * group) // 16)) // ctw)
+    total_tiles = int((-(-seqs // u) * ngroups).sum())
     assert waves <= max(resident // 4, 1, -(-total_tiles // cap))
     assert work.units_per_wave == -(-total_tiles // waves)
     share_sizes = []
@@ -199,7 +200,7 @@ def test_stream_k_pieces_cover_every_segment_once(resident, bs, group, unit) -> 
         assert j[4] == md.query_start_loc[j[0]] and j[5] == md.query_lengths[j[0]]
     slots_seen = []
     for r, q in enumerate(md.query_lengths):
-        for ct in range(-(-(q * group) // 16)):
+        for ct in range(ngroups[r]):
             spans = sorted(covered[(r, ct)])
             assert spans[0][0] == 0 and spans[-1][1] == seqs[r]
             assert all(a[1] == b[0] for a, b in zip(spans, spans[1:]))
@@ -210,6 +211,30 @@ def test_stream_k_pieces_cover_every_segment_once(resident, bs, group, unit) -> 
                 assert [sp[2] for sp in spans] == list(range(s0, s0 + n)) and n == len(spans)
                 slots_seen += list(range(s0, s0 + n))
     assert sorted(slots_seen) == list(range(work.num_partial_slots))
+
+
+def _uniform_metadata(*, batch, computed, q, bs=16):
+    layouts = tuple(lv.QueryLayout(tuple(range(-1, q - 1))) for _ in range(batch))
+    need = -(-(computed + q) // bs)
+    tables = tuple(tuple(range(r * need, (r + 1) * need)) for r in range(batch))
+    return lv.PagedAttentionMetadata(
+        block_tables=tables, num_computed_tokens=(computed,) * batch, query_layouts=layouts,
+        num_reserved_query_tokens=(q,) * batch,
+    )
+
+
+def test_col_tiles_choice_follows_the_reread_cost() -> None:
+    from light_vllm_amd.plan import COL_TILES4_COST
+    # One column tile per request (decode at group 7): nothing to share.
+    plan = StepPlan(_uniform_metadata(batch=4, computed=500, q=1), block_size=16, device=CPU)
+    assert plan.choose_col_tiles(7, 0, 4) == 1
+    # Eight queries x group 7 = 4 column tiles: one wave reads K/V once, not 4 times.
+    plan = StepPlan(_uniform_metadata(batch=4, computed=500, q=8), block_size=16, device=CPU)
+    assert plan.choose_col_tiles(7, 0, 4) == (4 if COL_TILES4_COST < 4 else 1)
+    assert plan.choose_col_tiles(7, 0, 1) == 1  # the kernel is not built for this shape
+    # Three queries x group 7 = 2 column tiles: four tiles pay off only below cost 2.
+    plan = StepPlan(_uniform_metadata(batch=4, computed=500, q=3), block_size=16, device=CPU)
+    assert plan.choose_col_tiles(7, 0, 4) == (4 if COL_TILES4_COST < 2 else 1)
 
 
 @pytest.mark.parametrize("group,columns", ((7, 256), (1, 256), (4, 128)))
@@ -254,10 +279,21 @@ def test_library_loads_and_exports_every_header_function() -> None:
     assert lib.lvamd_kv_append(None, 0, 0, None, 0, 0, None, None, None, 1, 2, 64, 2, None) == -1
     no_append = (None, 0, 0, None, 0, 0)
     assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 1, None, None,
-                                  None, None, 0, 4, 7, 72, 16, ctypes.c_float(0.1), 2, None) == -2
+                                  None, None, 0, 4, 7, 72, 1, 16, ctypes.c_float(0.1), 2, None) == -2
     assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 1, None, None,
-                                  None, None, 0, 4, 7, 128, 16, ctypes.c_float(0.1), 2, None) == -1
-    assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 2, None) == -1
+                                  None, None, 0, 4, 7, 128, 1, 16, ctypes.c_float(0.1), 2, None) == -1
+    assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 1, None, None,
+                                  None, None, 0, 4, 7, 128, 2, 16, ctypes.c_float(0.1), 2, None) == -2
+    assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 1, 2, None) == -1
+    assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 3, 2, None) == -2
+    # Tile sizes per kernel; four column tiles only for rows of at most 256 bytes.
+    assert lib.lvamd_paged_decode_tile_tokens(2, 128, 1) == 64
+    assert lib.lvamd_paged_decode_tile_tokens(2, 128, 4) == 16
+    assert lib.lvamd_paged_decode_tile_tokens(2, 256, 1) == 16
+    assert lib.lvamd_paged_decode_tile_tokens(2, 256, 4) == -2
+    assert lib.lvamd_paged_decode_tile_tokens(0, 64, 4) == 16
+    assert lib.lvamd_paged_decode_tile_tokens(0, 128, 4) == -2
+    assert native.decode_max_col_tiles(2, 128) == 4 and native.decode_max_col_tiles(2, 256) == 1
 
 def test_backend_refuses_a_cpu_cache() -> None:
     spec = lv.ModelKVCacheSpec((lv.AttentionLayerSpec("attention", 4, 2, 64),))
