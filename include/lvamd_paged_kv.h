@@ -40,15 +40,23 @@ enum lvamd_dtype { LVAMD_F32 = 0, LVAMD_F16 = 1, LVAMD_BF16 = 2 };
  * (table_off, num_table_blocks, computed, q_len, q_start, vis_off, vis_words, 0). */
 #define LVAMD_REQ_FIELDS 8
 /* Number of int32 fields per decode piece: (req, column_group, token_begin, token_end,
- * partial_slot, table_off, computed, q_len, q_start, vis_off, vis_words, 0, 0, 0, 0, 0).
+ * partial_slot, table_off, computed, q_len, q_start, vis_off, vis_words, b0, b1, b2, b3, b4).
  * column_group g covers column tiles [g * col_tiles, (g + 1) * col_tiles) of
- * the request.  A piece with partial_slot -1 covers its whole segment. */
+ * the request.  A piece with partial_slot -1 covers its whole segment.
+ * b0..b4 are the physical ids of the piece's first five logical blocks
+ * (token_begin / block_size onwards; 0 past the request's table): the kernel
+ * issues the piece's first tile from them when that tile spans at most five
+ * blocks, without waiting for the block table. */
 #define LVAMD_PIECE_FIELDS 16
 /* Number of int32 fields per merge job:
  * (req, column_group, first_partial_slot, num_partials, q_start, q_len, 0, 0). */
 #define LVAMD_MERGE_FIELDS 8
-/* Number of int32 fields per prefill work unit (req, first column, columns, 0). */
-#define LVAMD_PREFILL_FIELDS 4
+/* Number of int32 fields per prefill work unit:
+ * (req, first column, columns, key_begin, key_end, partial_slot, 0, 0).
+ * key_begin and key_end are multiples of lvamd_paged_prefill_key_tokens();
+ * key_end 0 means up to the unit's last visible key.  A unit with partial_slot -1 covers
+ * all its keys and writes out; the others write partials. */
+#define LVAMD_PREFILL_FIELDS 8
 
 const char* lvamd_status_string(int status);
 
@@ -134,8 +142,9 @@ int lvamd_paged_decode_tile_tokens(int32_t dtype, int32_t head_size, int32_t col
 
 /*
  * Log-sum-exp merge of split-K partials into out, one wave per (job, kv head,
- * column tile); jobs [num_jobs][LVAMD_MERGE_FIELDS]; col_tiles is the value the
- * partials were written with.  Same reference functions as lvamd_paged_decode:
+ * column tile); jobs [num_jobs][LVAMD_MERGE_FIELDS]; col_tiles (1 to 16) is
+ * the number of 16-column tiles per partial slot the partials were written
+ * with (the decode kernel's col_tiles, or prefill unit columns / 16).  Same reference functions as lvamd_paged_decode:
  * the reference has no split-K, and this is the cross-partition half of that
  * computation.
  */
@@ -146,14 +155,18 @@ int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
                                 int32_t dtype, lvamd_stream_t stream);
 
 /*
- * Chunked-prefill paged attention for long query runs (bf16 / fp16, head sizes
- * 64, 80, 96, 128, 256): one 256-thread workgroup per (unit, kv head); a unit
- * (units [num_units][LVAMD_PREFILL_FIELDS] = (req, first column, columns, 0))
- * is a run of MFMA columns of one request, a column being a (query,
- * head-in-group) pair, column c = query (c / group), head (c % group).  K/V
- * tiles (64 tokens up to head size 128, else 32) are gathered through the
- * block table into LDS and shared by the workgroup's waves; QK^T and PV on
- * MFMA 16x16x32, fp32 online softmax.
+ * Chunked-prefill paged attention for query runs of more than one column
+ * tile (prompt chunks, tree verification; bf16 / fp16, head sizes 64, 80, 96,
+ * 128, 256): one 256-thread workgroup per (unit, kv head); a unit
+ * (units [num_units][LVAMD_PREFILL_FIELDS]) is a run of MFMA columns of one
+ * request over a key range, a column being a (query, head-in-group) pair,
+ * column c = query (c / group), head (c % group).  K/V tiles (64 tokens up to
+ * head size 128, else 32) are gathered through the block table into LDS and
+ * shared by the workgroup's waves; QK^T and PV on MFMA 16x16x32, fp32 online
+ * softmax.  Units with a partial slot write fp32 partials to part_acc
+ * [slots][num_kv_heads][unit columns][head_size] and part_ml
+ * [slots][num_kv_heads][unit columns][2]; lvamd_paged_attention_merge with
+ * col_tiles = unit columns / 16 combines them.
  * The pool must already hold this step's K/V (lvamd_kv_append).  req_meta is
  * [batch][LVAMD_REQ_FIELDS].  Replaces the prefill half of the same reference
  * functions as lvamd_paged_decode.
@@ -163,12 +176,20 @@ int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_st
                         void* out, int64_t out_token_stride, int64_t out_head_stride,
                         const int32_t* req_meta, const int32_t* tables, const uint32_t* vis,
                         const int32_t* units, int32_t num_units,
+                        float* part_acc, float* part_ml, int64_t num_partial_slots,
                         int32_t num_kv_heads, int32_t group, int32_t head_size,
                         int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream);
 
 /* Columns per prefill unit for this dtype and head size (the planner's unit
  * width), or 0 when the prefill kernel does not support them. */
 int lvamd_paged_prefill_unit_columns(int32_t dtype, int32_t head_size);
+
+/* Keys per prefill tile (unit key ranges start on multiples of it). */
+int lvamd_paged_prefill_key_tokens(int32_t dtype, int32_t head_size);
+
+/* Prefill workgroups the current device holds at once for this dtype and head
+ * size: the planner splits units' key ranges to fill them.  Needs a GPU. */
+int lvamd_paged_prefill_resident_units(int32_t dtype, int32_t head_size);
 
 /*
  * Tree-KV compact across all layers: for every layer l and pair i,

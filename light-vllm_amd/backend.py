@@ -32,7 +32,11 @@ SUPPORTED_HEAD_SIZES = (32, 64, 80, 96, 128, 256)
 
 
 def validate_paged_attention_tensors(cache, metadata, layer_id: str, query: Tensor, key: Tensor, value: Tensor):
-    """Shape checks shared by every backend (paged_attention.py:226-247)."""
+    """Shape checks shared by every backend (paged_attention.py:226-247).
+
+    ``metadata`` is anything with ``num_query_tokens``: the step's
+    ``PagedAttentionMetadata`` or its ``StepPlan`` (which holds the count).
+    """
 
     layer_spec = cache.layer_spec(layer_id)
     if query.ndim != 3:
@@ -62,6 +66,9 @@ class _Workspace:
             self._buffer = torch.empty(max(num_floats, 1), dtype=torch.float32, device=device)
         return self._buffer
 
+    def ptr(self) -> int | None:
+        return None if self._buffer is None else self._buffer.data_ptr()
+
 
 def _rows_aligned(t: Tensor) -> bool:
     """Rows of 16-byte chunks: contiguous last dim, 16-byte aligned base and strides."""
@@ -72,14 +79,82 @@ def _rows_aligned(t: Tensor) -> bool:
     ) % 16 == 0
 
 
+class _LayerLaunch:
+    """Launch facts shared by every layer of one shape in one step plan.
+
+    Holds the work lists and every kernel argument that does not depend on
+    the layer's tensors, so a layer's ``forward`` only reads tensor pointers
+    and strides.
+    """
+
+    __slots__ = ("work", "group", "dtype", "decode_args", "merge_args", "prefill_args", "prefill_merge_args",
+                 "workspace_ptr")
+
+    @staticmethod
+    def workspace_floats(work, spec, prefill_columns: int) -> tuple[int, int]:
+        """(decode partial floats, prefill partial floats) of this work."""
+
+        per_row = spec.head_size + 2
+        dec = work.num_partial_slots * spec.num_kv_heads * 16 * work.col_tiles * per_row
+        pre = work.num_prefill_partial_slots * spec.num_kv_heads * prefill_columns * per_row
+        return dec, pre
+
+    def __init__(self, plan: StepPlan, work, spec, group: int, dtype: int, block_size: int,
+                 workspace_ptr: int | None, prefill_columns: int) -> None:
+        self.work = work
+        self.group = group
+        self.dtype = dtype
+        self.workspace_ptr = workspace_ptr
+        self.decode_args = None
+        self.merge_args = None
+        self.prefill_args = None
+        self.prefill_merge_args = None
+        dec_floats, pre_floats = self.workspace_floats(work, spec, prefill_columns)
+        part_acc = part_ml = pre_acc = pre_ml = None
+        if dec_floats:
+            part_acc = workspace_ptr
+            part_ml = part_acc + work.num_partial_slots * spec.num_kv_heads * 16 * work.col_tiles * spec.head_size * 4
+        if pre_floats:
+            pre_acc = workspace_ptr + dec_floats * 4
+            pre_ml = pre_acc + work.num_prefill_partial_slots * spec.num_kv_heads * prefill_columns * spec.head_size * 4
+        if work.waves_per_head:
+            # lvamd_paged_decode arguments after the output strides, up to the scale.
+            self.decode_args = (
+                work.pieces.data_ptr(), work.wave_first.data_ptr(), work.waves_per_head,
+                plan.tables.data_ptr(), plan.vis.data_ptr(),
+                part_acc, part_ml, work.num_partial_slots,
+                spec.num_kv_heads, group, spec.head_size, work.col_tiles, block_size,
+            )
+        if work.num_jobs:
+            # lvamd_paged_attention_merge arguments after the output strides, up to the stream.
+            self.merge_args = (part_acc, part_ml) + (
+                work.jobs.data_ptr(), work.num_jobs, spec.num_kv_heads, group, spec.head_size, work.col_tiles, dtype,
+            )
+        if work.num_prefill_units:
+            # lvamd_paged_prefill arguments after the output strides, up to the scale.
+            self.prefill_args = (
+                plan.req_meta.data_ptr(), plan.tables.data_ptr(), plan.vis.data_ptr(),
+                work.prefill_units.data_ptr(), work.num_prefill_units,
+                pre_acc, pre_ml, work.num_prefill_partial_slots,
+                spec.num_kv_heads, group, spec.head_size, block_size,
+            )
+        if work.num_prefill_jobs:
+            self.prefill_merge_args = (pre_acc, pre_ml) + (
+                work.prefill_jobs.data_ptr(), work.num_prefill_jobs, spec.num_kv_heads, group, spec.head_size,
+                prefill_columns // 16, dtype,
+            )
+
+
 class HipPagedAttention:
     """Per-step context: writes each layer's K/V, then runs paged attention."""
 
     def __init__(self, cache, metadata, workspace: _Workspace, plan: StepPlan, use_prefill: bool = True,
-                 col_tiles: int | None = None) -> None:
+                 col_tiles: int | None = None, split_prefill: bool = True) -> None:
         self._cache = cache
+        self._config = cache.config
         self._use_prefill = use_prefill
         self._col_tiles = col_tiles
+        self._split_prefill = split_prefill
         self._metadata = metadata
         self._layer_ids: set[str] = set()
         self._workspace = workspace
@@ -98,8 +173,8 @@ class HipPagedAttention:
         if layer_id in self._layer_ids:
             raise KVCacheError(f"paged attention layer {layer_id!r} ran more than once")
         self._layer_ids.add(layer_id)
-        spec = validate_paged_attention_tensors(self._cache, self._metadata, layer_id, query, key, value)
-        config = self._cache.config
+        spec = validate_paged_attention_tensors(self._cache, self._plan, layer_id, query, key, value)
+        config = self._config
         if query.device != config.device or query.dtype != config.dtype:
             raise KVCacheError("HIP paged attention query dtype and device must match the KV cache")
         if key.dtype != config.dtype or value.dtype != config.dtype or key.device != config.device or (
@@ -114,22 +189,44 @@ class HipPagedAttention:
         if not _rows_aligned(query):
             query = query.contiguous()
         out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
-        work = self._work(spec, query.dtype)
-        if work.num_prefill_units:
+        launch = self._launch(spec, query.dtype)
+        layer = self._cache.layer(layer_id)
+        stream = current_stream(query.device)
+        lib = self._lib
+        if launch.prefill_args is not None:
             # Prefill rows read the pool, so the whole step is appended first.
             hip_append(self._cache, layer_id, key, value, self._plan.slots)
-            launch = self.decode_launch(layer_id, query, out, scale=scale)
+            new_kv = (None, 0, 0, None, 0, 0)
         else:
             if not _rows_aligned(key):
                 key = key.contiguous()
             if not _rows_aligned(value):
                 value = value.contiguous()
-            launch = self.decode_launch(layer_id, query, out, scale=scale, key=key, value=value)
-        if launch is not None:
-            launch.decode()
-            launch.merge()
-        self.prefill(layer_id, query, out, scale=scale)
+            new_kv = (key.data_ptr(), key.stride(0), key.stride(1), value.data_ptr(), value.stride(0), value.stride(1))
+        scale = float(scale)
+        o_args = (out.data_ptr(), out.stride(0), out.stride(1))
+        if launch.decode_args is not None:
+            native.check(lib.lvamd_paged_decode(
+                query.data_ptr(), query.stride(0), query.stride(1), *new_kv,
+                layer.keys.data_ptr(), layer.values.data_ptr(), *o_args,
+                *launch.decode_args, scale, launch.dtype, stream,
+            ), "lvamd_paged_decode")
+            if launch.merge_args is not None:
+                m = launch.merge_args
+                native.check(lib.lvamd_paged_attention_merge(m[0], m[1], *o_args, *m[2:], stream),
+                             "lvamd_paged_attention_merge")
+        if launch.prefill_args is not None:
+            native.check(lib.lvamd_paged_prefill(
+                query.data_ptr(), query.stride(0), query.stride(1),
+                layer.keys.data_ptr(), layer.values.data_ptr(), *o_args,
+                *launch.prefill_args, scale, launch.dtype, stream,
+            ), "lvamd_paged_prefill")
+            if launch.prefill_merge_args is not None:
+                m = launch.prefill_merge_args
+                native.check(lib.lvamd_paged_attention_merge(m[0], m[1], *o_args, *m[2:], stream),
+                             "lvamd_paged_attention_merge")
         return out
+
 
     def decode_launch(
         self, layer_id: str, query: Tensor, out: Tensor, *, scale: float, key: Tensor | None = None,
@@ -142,18 +239,52 @@ class HipPagedAttention:
         """
 
         spec = self._cache.layer_spec(layer_id)
-        group = spec.num_query_heads // spec.num_kv_heads
-        work = self._work(spec, query.dtype)
-        if not work.waves_per_head:
+        launch = self._launch(spec, query.dtype)
+        if launch.decode_args is None:
             return None
-        part_acc = part_ml = None
-        if work.num_partial_slots:
-            per_slot = spec.num_kv_heads * 16 * work.col_tiles
-            buf = self._workspace.get(work.num_partial_slots * per_slot * (spec.head_size + 2), query.device)
-            part_acc = buf.data_ptr()
-            part_ml = part_acc + work.num_partial_slots * per_slot * spec.head_size * 4
-        return _DecodeLaunch(self._lib, self._cache, self._plan, work, spec, group, self._cache.layer(layer_id),
-                             query, key, value, out, float(scale), part_acc, part_ml)
+        return _DecodeLaunch(self._lib, launch, self._cache.layer(layer_id), query, key, value, out, float(scale))
+
+    def prefill(self, layer_id: str, query: Tensor, out: Tensor, *, scale: float) -> None:
+        """Only the prefill kernel of this layer (the pool must hold the step's K/V)."""
+
+        spec = self._cache.layer_spec(layer_id)
+        launch = self._launch(spec, query.dtype)
+        if launch.prefill_args is None:
+            return
+        layer = self._cache.layer(layer_id)
+        stream = current_stream(query.device)
+        o_args = (out.data_ptr(), out.stride(0), out.stride(1))
+        native.check(self._lib.lvamd_paged_prefill(
+            query.data_ptr(), query.stride(0), query.stride(1),
+            layer.keys.data_ptr(), layer.values.data_ptr(), *o_args,
+            *launch.prefill_args, float(scale), launch.dtype, stream,
+        ), "lvamd_paged_prefill")
+        if launch.prefill_merge_args is not None:
+            m = launch.prefill_merge_args
+            native.check(self._lib.lvamd_paged_attention_merge(m[0], m[1], *o_args, *m[2:], stream),
+                         "lvamd_paged_attention_merge")
+
+    def _launch(self, spec, dtype) -> _LayerLaunch:
+        """The launch facts of this layer shape, built once per plan and options."""
+
+        code = dtype_code(dtype)
+        key = (spec.num_query_heads, spec.num_kv_heads, spec.head_size, code, self._use_prefill, self._col_tiles,
+               self._split_prefill)
+        plan = self._plan
+        found = plan.launches.get(key)
+        if found is not None and found.workspace_ptr is not None and found.workspace_ptr != self._workspace.ptr():
+            found = None  # the workspace (shared by all plans) was regrown since
+        if found is None:
+            work = self._work(spec, dtype)
+            group = spec.num_query_heads // spec.num_kv_heads
+            columns = native.prefill_unit_columns(code, spec.head_size) if self._use_prefill else 0
+            dec_floats, pre_floats = _LayerLaunch.workspace_floats(work, spec, columns)
+            ptr = None
+            if dec_floats + pre_floats:
+                ptr = self._workspace.get(dec_floats + pre_floats, self._config.device).data_ptr()
+            found = _LayerLaunch(plan, work, spec, group, code, self._config.block_size, ptr, columns)
+            plan.launches[key] = found
+        return found
 
     def _work(self, spec, dtype):
         group = spec.num_query_heads // spec.num_kv_heads
@@ -166,60 +297,35 @@ class HipPagedAttention:
         ctw = min(ctw, max_ctw)
         resident = native.resident_decode_waves(code, spec.head_size, ctw)
         unit = native.decode_tile_tokens(code, spec.head_size, ctw)
-        return self._plan.work(group, spec.num_kv_heads, resident, columns, unit, ctw)
-
-    def prefill(self, layer_id: str, query: Tensor, out: Tensor, *, scale: float) -> None:
-        spec = self._cache.layer_spec(layer_id)
-        group = spec.num_query_heads // spec.num_kv_heads
-        work = self._work(spec, query.dtype)
-        if not work.num_prefill_units:
-            return
-        layer = self._cache.layer(layer_id)
-        plan = self._plan
-        status = self._lib.lvamd_paged_prefill(
-            query.data_ptr(), query.stride(0), query.stride(1),
-            layer.keys.data_ptr(), layer.values.data_ptr(),
-            out.data_ptr(), out.stride(0), out.stride(1),
-            plan.req_meta.data_ptr(), plan.tables.data_ptr(), plan.vis.data_ptr(),
-            work.prefill_units.data_ptr(), work.num_prefill_units,
-            spec.num_kv_heads, group, spec.head_size,
-            self._cache.config.block_size, float(scale), dtype_code(query.dtype), current_stream(query.device),
-        )
-        native.check(status, "lvamd_paged_prefill")
+        key_tokens = prefill_resident = 0
+        if columns:
+            key_tokens = native.prefill_key_tokens(code, spec.head_size)
+            if self._split_prefill:
+                prefill_resident = native.prefill_resident_units(code, spec.head_size)
+        return self._plan.work(group, spec.num_kv_heads, resident, columns, unit, ctw, key_tokens, prefill_resident)
 
 
 class _DecodeLaunch:
     """The decode and merge kernel launches of one layer, with bound arguments."""
 
-    def __init__(self, lib, cache, plan, work, spec, group, layer, query, key, value, out, scale,
-                 part_acc, part_ml) -> None:
-        self.work = work
+    def __init__(self, lib, launch: _LayerLaunch, layer, query, key, value, out, scale) -> None:
+        self.work = launch.work
         stream = current_stream(query.device)
-        dt = dtype_code(query.dtype)
         self._lib = lib
         if key is None:
-            new_k, new_v, ks, vs = None, None, (0, 0), (0, 0)
+            new_kv = (None, 0, 0, None, 0, 0)
         else:
-            new_k, new_v = key.data_ptr(), value.data_ptr()
-            ks, vs = (key.stride(0), key.stride(1)), (value.stride(0), value.stride(1))
+            new_kv = (key.data_ptr(), key.stride(0), key.stride(1), value.data_ptr(), value.stride(0), value.stride(1))
+        o_args = (out.data_ptr(), out.stride(0), out.stride(1))
         self._decode_args = (
-            query.data_ptr(), query.stride(0), query.stride(1),
-            new_k, ks[0], ks[1], new_v, vs[0], vs[1],
-            layer.keys.data_ptr(), layer.values.data_ptr(),
-            out.data_ptr(), out.stride(0), out.stride(1),
-            work.pieces.data_ptr(), work.wave_first.data_ptr(), work.waves_per_head,
-            plan.tables.data_ptr(), plan.vis.data_ptr(),
-            part_acc, part_ml, work.num_partial_slots,
-            spec.num_kv_heads, group, spec.head_size, work.col_tiles,
-            cache.config.block_size, scale, dt, stream,
+            query.data_ptr(), query.stride(0), query.stride(1), *new_kv,
+            layer.keys.data_ptr(), layer.values.data_ptr(), *o_args,
+            *launch.decode_args, scale, launch.dtype, stream,
         )
         self._merge_args = None
-        if work.num_jobs:
-            self._merge_args = (
-                part_acc, part_ml, out.data_ptr(), out.stride(0), out.stride(1),
-                work.jobs.data_ptr(), work.num_jobs,
-                spec.num_kv_heads, group, spec.head_size, work.col_tiles, dt, stream,
-            )
+        if launch.merge_args is not None:
+            m = launch.merge_args
+            self._merge_args = (m[0], m[1], *o_args, *m[2:], stream)
 
     def decode(self) -> None:
         native.check(self._lib.lvamd_paged_decode(*self._decode_args), "lvamd_paged_decode")
@@ -242,13 +348,15 @@ class HipPagedAttentionBackend:
 
     def __init__(
         self, *, use_prefill_kernel: bool = True, partition_tokens: int | None = None,
-        decode_col_tiles: int | None = None,
+        decode_col_tiles: int | None = None, split_prefill: bool = True,
     ) -> None:
         """``use_prefill_kernel=False`` sends every request through the decode
         kernel; ``partition_tokens`` caps the tokens one decode wave handles (a
         tuning knob; by default the planner spreads the work over every
         resident wave); ``decode_col_tiles`` (1 or 4) fixes the decode kernel's
-        column tiles per wave instead of the planner's per-step choice."""
+        column tiles per wave instead of the planner's per-step choice;
+        ``split_prefill=False`` keeps every prefill unit's keys in one
+        workgroup (no split-K partials)."""
 
         native.load()
         if partition_tokens is not None and (partition_tokens <= 0 or partition_tokens % UNIT_TOKENS):
@@ -259,6 +367,7 @@ class HipPagedAttentionBackend:
         self._use_prefill = use_prefill_kernel
         self._partition_tokens = partition_tokens
         self._col_tiles = decode_col_tiles
+        self._split_prefill = split_prefill
         self._last: tuple[object, object, StepPlan] | None = None
 
     def create(self, cache, metadata) -> HipPagedAttention:
@@ -274,4 +383,5 @@ class HipPagedAttentionBackend:
             plan = StepPlan(metadata, block_size=config.block_size, device=config.device,
                             partition_tokens=self._partition_tokens)
             self._last = (key, metadata, plan)
-        return HipPagedAttention(cache, metadata, self._workspace, plan, self._use_prefill, self._col_tiles)
+        return HipPagedAttention(cache, metadata, self._workspace, plan, self._use_prefill, self._col_tiles,
+                                 self._split_prefill)

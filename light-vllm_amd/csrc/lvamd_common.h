@@ -22,10 +22,26 @@ __device__ __forceinline__ To bitcast(const From& v) {
 
 __device__ __forceinline__ uint4 zero_u4() { return make_uint4(0u, 0u, 0u, 0u); }
 
-// 16-byte global load/store of a row chunk.
+// 16-byte global load of a row chunk.  The pointer is cast to the global
+// address space: callers select between pools and input tensors at run time,
+// and a generic pointer would make LLVM emit a flat load (which also counts
+// against the LDS wait counter).
+template <typename T>
+using gptr = __attribute__((address_space(1))) T*;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ uint4 load16(gptr<const T> p) {
+  const u32x4 v = *(gptr<const u32x4>)(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 template <typename T>
 __device__ __forceinline__ uint4 load16(const T* p) {
-  return *reinterpret_cast<const uint4*>(p);
+  return load16((gptr<const T>)(p));
+}
+template <typename T>
+__device__ __forceinline__ void store16(gptr<T> p, uint4 v) {
+  *(gptr<u32x4>)(p) = u32x4{v.x, v.y, v.z, v.w};
 }
 
 // fp32 -> storage type with round-to-nearest-even (matches torch's .to()).

@@ -61,6 +61,15 @@ namespace lvamd {
 constexpr int kTableSlice = 256;
 // Lazy-rescale threshold in log2 units: probabilities stay below 2^8.
 constexpr float kRescaleSlack = 8.0f;
+// Piece fields 11..15: physical ids of the piece's first logical blocks.
+constexpr int kPieceBlockField = 11;
+constexpr int kPieceBlocks = 5;
+#ifndef LVAMD_DECODE_DIRECT_FIRST
+#define LVAMD_DECODE_DIRECT_FIRST 1
+#endif
+#ifndef LVAMD_DECODE_NT_PARTIALS
+#define LVAMD_DECODE_NT_PARTIALS 0
+#endif
 
 struct DecodeArgs {
   const void* q;
@@ -160,7 +169,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint4 vlds_b[DT::VALLOC];
   __shared__ int32_t tab[2][kTableSlice];
 
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;  // (the mask tells LLVM lane < 64)
   const int l16 = lane & 15;
   const int g = lane >> 4;
   const int Hkv = a.num_kv_heads;
@@ -173,13 +182,17 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   if (p >= p_end) return;
 
   const int64_t row_elems = (int64_t)Hkv * D;
-  T* const kbase = static_cast<T*>(a.k_pool) + (int64_t)kvh * D;
-  T* const vbase = static_cast<T*>(a.v_pool) + (int64_t)kvh * D;
+  // Global-address-space pointers: the tile loads select between the pool
+  // and the input K/V per lane, and generic pointers would become flat loads.
+  gptr<T> const kbase = (gptr<T>)(a.k_pool) + (int64_t)kvh * D;
+  gptr<T> const vbase = (gptr<T>)(a.v_pool) + (int64_t)kvh * D;
   // Fused append: this step's tokens are read from the input K/V (so no
   // wave waits for another's pool write) and written to their pool slots by
   // the column-group-0 piece that covers them.
-  const T* const knew = a.k_new ? static_cast<const T*>(a.k_new) + (int64_t)kvh * a.kn_head_stride : nullptr;
-  const T* const vnew = a.v_new ? static_cast<const T*>(a.v_new) + (int64_t)kvh * a.vn_head_stride : nullptr;
+  gptr<const T> const knew =
+      a.k_new ? (gptr<const T>)(a.k_new) + (int64_t)kvh * a.kn_head_stride : nullptr;
+  gptr<const T> const vnew =
+      a.v_new ? (gptr<const T>)(a.v_new) + (int64_t)kvh * a.vn_head_stride : nullptr;
 
   auto logical_block = [&](int pos) -> int {
     return a.bs_shift >= 0 ? (pos >> a.bs_shift) : (pos / a.block_size);
@@ -234,17 +247,17 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   // (finite data, masked to probability 0, already in cache).  All row
   // offsets are read from LDS before any load is issued.  fresh[s] is the
   // pool offset of row group s's row when this tile must append it, else -1.
-  auto issue_tile = [&](const Piece& x, int tb, int t0, uint4 (&kdst)[SUB][NCH], uint4 (&vdst)[SUB][NCH],
-                        int64_t (&fresh)[SUB]) {
+  auto issue_tile_ids = [&](const Piece& x, int t0, auto block_id, uint4 (&kdst)[SUB][NCH],
+                            uint4 (&vdst)[SUB][NCH], int64_t (&fresh)[SUB]) {
     const int lb0 = logical_block(x.tok_begin);
-    const T* kp[SUB];
-    const T* vp[SUB];
+    gptr<const T> kp[SUB];
+    gptr<const T> vp[SUB];
 #pragma unroll
     for (int s = 0; s < SUB; ++s) {
       const int pos = t0 + 16 * s + l16;
       const int pc = pos < x.tok_end ? pos : x.tok_end - 1;
       const int lb = logical_block(pc);
-      const int64_t off = ((int64_t)tab[tb][lb - lb0] * a.block_size + (pc - lb * a.block_size)) * row_elems;
+      const int64_t off = ((int64_t)block_id(lb - lb0) * a.block_size + (pc - lb * a.block_size)) * row_elems;
       kp[s] = kbase + off;
       vp[s] = vbase + off;
       fresh[s] = -1;
@@ -269,6 +282,10 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
         }
       }
   };
+  auto issue_tile = [&](const Piece& x, int tb, int t0, uint4 (&kdst)[SUB][NCH], uint4 (&vdst)[SUB][NCH],
+                        int64_t (&fresh)[SUB]) {
+    issue_tile_ids(x, t0, [&](int rel) { return tab[tb][rel]; }, kdst, vdst, fresh);
+  };
   // Append the tile's fresh rows to the pool (bit-exact row copies).
   auto store_fresh = [&](const uint4 (&kr)[SUB][NCH], const uint4 (&vr)[SUB][NCH], const int64_t (&fresh)[SUB]) {
 #pragma unroll
@@ -278,8 +295,8 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
         for (int kk = 0; kk < NCH; ++kk) {
           const int c = kk * 4 + g;
           if (c < CPR) {
-            *reinterpret_cast<uint4*>(kbase + fresh[s] + c * E16) = kr[s][kk];
-            *reinterpret_cast<uint4*>(vbase + fresh[s] + c * E16) = vr[s][kk];
+            store16(kbase + fresh[s] + c * E16, kr[s][kk]);
+            store16(vbase + fresh[s] + c * E16, vr[s][kk]);
           }
         }
       }
@@ -293,17 +310,33 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
       for (int kk = 0; kk < NCH; ++kk) vdst[(s * NCH + kk) * 64 + lane] = vr[s][kk];
   };
 
-  // Prologue: this piece's table and Q, the next piece's table (and Q), then
-  // the first tile.
+  // Prologue.  The first tile is issued straight from the block ids the
+  // piece record carries (when the tile spans at most kPieceBlocks blocks),
+  // so it does not wait for the table slice; then this piece's table and Q,
+  // the next piece's table (and Q).
   Piece cur = read_piece(a.pieces, p);
   int tb = 0;
   uint4 qf[CTW][NCH];
   uint4 qn[kPrefetchQ ? CTW : 1][NCH];
   int tn[TAB_PER_LANE];
-  {
-    int tc[TAB_PER_LANE];
+  uint4 ka[SUB][NCH], kb[SUB][NCH];
+  uint4 vr0[SUB][NCH];
+  int64_t fresh0[SUB];
+  int tc[TAB_PER_LANE];
+  const int first_span = logical_block(min(cur.tok_begin + TT, cur.tok_end) - 1) - logical_block(cur.tok_begin);
+  const bool direct = LVAMD_DECODE_DIRECT_FIRST && first_span < kPieceBlocks;
+  if (direct) {
+    const int32_t* ids = a.pieces + (int64_t)p * LVAMD_PIECE_FIELDS + kPieceBlockField;
+    const int b0 = ids[0], b1 = ids[1], b2 = ids[2], b3 = ids[3], b4 = ids[4];
+    issue_tile_ids(
+        cur, cur.tok_begin,
+        [&](int rel) { return rel == 0 ? b0 : rel == 1 ? b1 : rel == 2 ? b2 : rel == 3 ? b3 : b4; }, ka, vr0,
+        fresh0);
+    load_table(cur, tc);
+  } else {
     load_table(cur, tc);
     store_table(tb, tc);
+    issue_tile(cur, tb, cur.tok_begin, ka, vr0, fresh0);
   }
   load_q(cur, qf);
   bool have_nxt = p + 1 < p_end;
@@ -314,14 +347,9 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
     load_table(nxt, tn);
     if constexpr (kPrefetchQ) load_q(nxt, qn);
   }
-  uint4 ka[SUB][NCH], kb[SUB][NCH];
-  {
-    uint4 vr[SUB][NCH];
-    int64_t fresh[SUB];
-    issue_tile(cur, tb, cur.tok_begin, ka, vr, fresh);
-    stage_v(vlds_a, vr);
-    store_fresh(ka, vr, fresh);
-  }
+  if (direct) store_table(tb, tc);
+  stage_v(vlds_a, vr0);
+  store_fresh(ka, vr0, fresh0);
 
   LaneCol lc[CTW];
   float m_run[CTW];  // per-column base (log2 domain), uniform across the column's lanes
@@ -556,9 +584,19 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
       } else if (lc[ct].ok) {
         const int64_t cs = ((int64_t)cur.slot * Hkv + kvh) * (16 * CTW) + ct * 16 + l16;
         float* pacc = a.part_acc + cs * D;
+#if LVAMD_DECODE_NT_PARTIALS
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+          __builtin_nontemporal_store(acc[ct][n], reinterpret_cast<f32x4*>(pacc + 16 * n + 4 * g));
+        if (g == 0) {
+          __builtin_nontemporal_store(m_run[ct], a.part_ml + cs * 2);
+          __builtin_nontemporal_store(l_tot, a.part_ml + cs * 2 + 1);
+        }
+#else
 #pragma unroll
         for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(pacc + 16 * n + 4 * g) = acc[ct][n];
         if (g == 0) *reinterpret_cast<float2*>(a.part_ml + cs * 2) = make_float2(m_run[ct], l_tot);
+#endif
       }
     }
     if (!have_nxt) return false;
@@ -629,7 +667,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
   const int jh = wave / ctw;
   const int job = jh / Hkv;
   const int kvh = jh - job * Hkv;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;  // (the mask tells LLVM lane < 64)
   const int l16 = lane & 15;
   const int g = lane >> 4;
   const int32_t* jb = a.jobs + (int64_t)job * LVAMD_MERGE_FIELDS;
@@ -844,7 +882,7 @@ extern "C" int lvamd_paged_attention_merge(const float* part_acc, const float* p
                                            const int32_t* jobs, int32_t num_jobs,
                                            int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t col_tiles,
                                            int32_t dtype, lvamd_stream_t stream) {
-  if (dtype_size(dtype) == 0 || !head_size_supported(head_size) || !col_tiles_supported(col_tiles))
+  if (dtype_size(dtype) == 0 || !head_size_supported(head_size) || col_tiles < 1 || col_tiles > 16)
     return LVAMD_ERR_UNSUPPORTED;
   if (num_jobs < 0 || num_kv_heads <= 0 || group <= 0) return LVAMD_ERR_INVALID_ARGUMENT;
   if (num_jobs == 0) return LVAMD_OK;

@@ -25,6 +25,11 @@
 //     shared by the column tiles.
 //   * Online softmax in the log2 domain with lazy rescaling (wave vote), max
 //     and sum across the four 16-lane rows with permlane swaps.
+//   * Split-K: a unit may cover a key range of its request (a piece); a piece
+//     that is not the whole range writes fp32 (max, sum, acc) partials that
+//     lvamd_paged_attention_merge combines.  The host splits units when there
+//     are fewer units than resident workgroups (tree verification, short
+//     chunks), so each workgroup's waves share fewer, wider K/V tiles.
 
 #include <cmath>
 #include <type_traits>
@@ -80,6 +85,8 @@ struct PrefillArgs {
   const int32_t* __restrict__ tables;
   const uint32_t* __restrict__ vis;
   const int32_t* __restrict__ units;     // [n][LVAMD_PREFILL_FIELDS]
+  float* part_acc;                       // [slots][Hkv][unit columns][D]
+  float* part_ml;                        // [slots][Hkv][unit columns][2]
   int32_t num_kv_heads;
   int32_t group;
   int32_t block_size;
@@ -106,14 +113,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
   const int unit = blockIdx.x / Hkv;
   const int kvh = blockIdx.x - unit * Hkv;
   const int32_t* u = a.units + (int64_t)unit * LVAMD_PREFILL_FIELDS;
-  const int req = u[0], col0 = u[1], ncols = u[2];
+  const int req = u[0], col0 = u[1], ncols = u[2], key_begin = u[3], key_end = u[4], slot = u[5];
   const int32_t* rm = a.req_meta + (int64_t)req * LVAMD_REQ_FIELDS;
   const int table_off = rm[0], computed = rm[2], q_len = rm[3], q_start = rm[4], vis_off = rm[5],
             vis_words = rm[6];
   const int col_end = col0 + ncols;  // exclusive, <= q_len * G
-  // Keys the unit needs: up to its last query's position.
-  const int kmax = computed + (col_end - 1) / G + 1;
-  const int ntiles = (kmax + KT - 1) / KT;
+  // Keys the unit needs: up to its last query's position, within the piece's
+  // key range [key_begin, key_end) (key_begin a multiple of KT; key_end 0 =
+  // no bound).  Tiles are numbered from position 0.
+  const int kneed = computed + (col_end - 1) / G + 1;
+  const int kmax = key_end > 0 && key_end < kneed ? key_end : kneed;
+  const int tile0 = key_begin / KT;
+  const int ntiles = (kmax + KT - 1) / KT - tile0;  // tiles of this piece
   const int bs = a.block_size;
 
   const int64_t row_elems = (int64_t)Hkv * D;
@@ -134,8 +145,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     cofs[i] = (int64_t)kvh * D + (idx % CPR) * 8;
   }
   auto key_pos = [&](int t, int i) -> int {
-    const int pos = t * KT + rw[i];
-    return pos < kmax ? pos : kmax - 1;  // rows past the unit read its last key (masked)
+    const int pos = (tile0 + t) * KT + rw[i];
+    return pos < kmax ? pos : kmax - 1;  // rows past the piece read its last key (masked)
   };
   auto logical_block = [&](int pos) -> int { return a.bs_shift >= 0 ? (pos >> a.bs_shift) : (pos / bs); };
   auto load_entries = [&](int t, int (&te)[LPT]) {
@@ -208,8 +219,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     for (int n = 0; n < NT; ++n) acc[ct][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // ---- one tile of attention from LDS buffer b
-  auto compute_tile = [&](int t, int b) {
+  // ---- one tile of attention from LDS buffer b (t: tile of the piece)
+  auto compute_tile = [&](int tr, int b) {
+    const int t = tile0 + tr;
     if (!wave_active || t * KT >= wave_kmax) return;
     const char* kt = klds[b];
     const char* vt = vlds[b];
@@ -229,7 +241,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
         for (int ct = 0; ct < CT; ++ct) st[ct][s] = Mma<T>::qk(kc, qf[ct][kk], st[ct][s]);
       }
     // Masks only past the fully visible prefix: one compare per score for a
-    // linear request, the ancestor bits for a tree.
+    // linear request, the ancestor bits for a tree.  (A piece ends on a tile
+    // boundary or at the unit's last key, so no unmasked tile reaches past
+    // it; rows past kmax in a masked tile fail the visibility test.)
     if (t >= full_tiles) {
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
@@ -329,12 +343,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     if (t + 1 < ntiles) iter(t + 1, kb, vb, ka, va, eb, ea);
   }
 
-  // ---- normalised output rows
+  // ---- normalised output rows, or this piece's partials
   if (!wave_active) return;
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     const float l_tot = row_sum4(l_run[ct]);
     if (!colok[ct]) continue;
+    if (slot >= 0) {
+      constexpr int UC = prefill_unit_columns(D);
+      const int64_t cs = ((int64_t)slot * Hkv + kvh) * UC + 16 * (CT * wave + ct) + l16;
+      float* pacc = a.part_acc + cs * D;
+#pragma unroll
+      for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(pacc + 16 * n + 4 * g) = acc[ct][n];
+      if (g == 0) *reinterpret_cast<float2*>(a.part_ml + cs * 2) = make_float2(m_run[ct], l_tot);
+      continue;
+    }
     const int col = col0 + 16 * (CT * wave + ct) + l16;
     const int qhead = kvh * G + (col - qi[ct] * G);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
@@ -374,18 +397,44 @@ extern "C" int lvamd_paged_prefill_unit_columns(int32_t dtype, int32_t head_size
   return prefill_unit_columns(head_size);
 }
 
+extern "C" int lvamd_paged_prefill_key_tokens(int32_t dtype, int32_t head_size) {
+  if (!prefill_supported(dtype, head_size)) return LVAMD_ERR_UNSUPPORTED;
+  return prefill_key_tile(head_size);
+}
+
+extern "C" int lvamd_paged_prefill_resident_units(int32_t dtype, int32_t head_size) {
+  if (!prefill_supported(dtype, head_size)) return LVAMD_ERR_UNSUPPORTED;
+  const void* fn = nullptr;
+  const bool bf = dtype == LVAMD_BF16;
+  switch (head_size) {
+    case 64: fn = bf ? (const void*)&paged_prefill_kernel<__bf16, 64> : (const void*)&paged_prefill_kernel<_Float16, 64>; break;
+    case 80: fn = bf ? (const void*)&paged_prefill_kernel<__bf16, 80> : (const void*)&paged_prefill_kernel<_Float16, 80>; break;
+    case 96: fn = bf ? (const void*)&paged_prefill_kernel<__bf16, 96> : (const void*)&paged_prefill_kernel<_Float16, 96>; break;
+    case 128: fn = bf ? (const void*)&paged_prefill_kernel<__bf16, 128> : (const void*)&paged_prefill_kernel<_Float16, 128>; break;
+    default: fn = bf ? (const void*)&paged_prefill_kernel<__bf16, 256> : (const void*)&paged_prefill_kernel<_Float16, 256>; break;
+  }
+  int device = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&device) != hipSuccess) return LVAMD_ERR_LAUNCH;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return LVAMD_ERR_LAUNCH;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, 0) != hipSuccess) return LVAMD_ERR_LAUNCH;
+  return per_cu * cus;
+}
+
 extern "C" int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stride,
                                    const void* key_pool, const void* value_pool,
                                    void* out, int64_t out_token_stride, int64_t out_head_stride,
                                    const int32_t* req_meta, const int32_t* tables, const uint32_t* vis,
                                    const int32_t* units, int32_t num_units,
+                                   float* part_acc, float* part_ml, int64_t num_partial_slots,
                                    int32_t num_kv_heads, int32_t group, int32_t head_size,
                                    int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream) {
-  if (num_units < 0 || num_kv_heads <= 0 || group <= 0 || block_size <= 0) return LVAMD_ERR_INVALID_ARGUMENT;
+  if (num_units < 0 || num_kv_heads <= 0 || group <= 0 || block_size <= 0 || num_partial_slots < 0)
+    return LVAMD_ERR_INVALID_ARGUMENT;
   if (num_units == 0) return LVAMD_OK;
   if (!prefill_supported(dtype, head_size)) return LVAMD_ERR_UNSUPPORTED;
   if (!q || !key_pool || !value_pool || !out || !req_meta || !tables || !vis || !units)
     return LVAMD_ERR_INVALID_ARGUMENT;
+  if (num_partial_slots > 0 && (!part_acc || !part_ml)) return LVAMD_ERR_WORKSPACE;
   const int es = dtype_size(dtype);
   if (((uintptr_t)q & 15u) || ((uintptr_t)key_pool & 15u) || ((uintptr_t)value_pool & 15u) ||
       (q_token_stride * es) % 16 != 0 || (q_head_stride * es) % 16 != 0)
@@ -404,6 +453,8 @@ extern "C" int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_
   a.tables = tables;
   a.vis = vis;
   a.units = units;
+  a.part_acc = part_acc;
+  a.part_ml = part_ml;
   a.num_kv_heads = num_kv_heads;
   a.group = group;
   a.block_size = block_size;

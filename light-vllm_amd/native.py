@@ -15,7 +15,7 @@ from pathlib import Path
 from light_vllm_amd.errors import ExecutionError, ExecutionNotReadyError
 
 LIB_NAME = "liblvamd_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
@@ -24,7 +24,7 @@ DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 REQ_FIELDS = 8
 PIECE_FIELDS = 16
 MERGE_FIELDS = 8
-PREFILL_FIELDS = 4
+PREFILL_FIELDS = 8
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -53,10 +53,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "lvamd_paged_prefill": (
         ctypes.c_int,
-        [_p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i32,
+        [_p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i32, _p, _p, _i64,
          _i32, _i32, _i32, _i32, _f32, _i32, _p],
     ),
     "lvamd_paged_prefill_unit_columns": (ctypes.c_int, [_i32, _i32]),
+    "lvamd_paged_prefill_key_tokens": (ctypes.c_int, [_i32, _i32]),
+    "lvamd_paged_prefill_resident_units": (ctypes.c_int, [_i32, _i32]),
     "lvamd_kv_compact": (
         ctypes.c_int,
         [_p, _p, _i32, _i64, _p, _p, _i64, _p, _i64, _p],
@@ -143,6 +145,24 @@ def prefill_unit_columns(dtype_code: int, head_size: int) -> int:
     """Columns per prefill work unit, 0 when the prefill kernel does not cover the shape."""
 
     return int(load().lvamd_paged_prefill_unit_columns(dtype_code, head_size))
+
+
+@functools.lru_cache(maxsize=None)
+def prefill_key_tokens(dtype_code: int, head_size: int) -> int:
+    """Keys per prefill tile (split-K key ranges start on multiples of it)."""
+
+    found = int(load().lvamd_paged_prefill_key_tokens(dtype_code, head_size))
+    check(min(found, 0), "lvamd_paged_prefill_key_tokens")
+    return found
+
+
+@functools.lru_cache(maxsize=None)
+def prefill_resident_units(dtype_code: int, head_size: int) -> int:
+    """Prefill workgroups the current GPU holds at once."""
+
+    found = int(load().lvamd_paged_prefill_resident_units(dtype_code, head_size))
+    check(min(found, 0), "lvamd_paged_prefill_resident_units")
+    return found
 
 
 def check(status: int, what: str) -> None:

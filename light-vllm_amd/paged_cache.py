@@ -35,8 +35,17 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise KVCacheError(f"HIP paged KV supports float32, float16 and bfloat16, not {dtype}") from exc
 
 
-def current_stream(device: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def current_stream(device: torch.device) -> int:
+    """The current HIP stream of ``device`` as a raw handle (torch's own
+    accessor when present: it skips building a Stream object per call)."""
+
+    if _raw_stream is not None:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(index)
+    return torch.cuda.current_stream(device).cuda_stream
 
 
 @dataclass(frozen=True, slots=True)

@@ -33,9 +33,14 @@ from torch import Tensor
 
 from light_vllm_amd.layout import is_linear, query_visibility
 
-# Requests with at most this many queries use the split-K decode kernel;
-# longer runs use the MFMA prefill kernel when it covers the layer's shape.
-DECODE_MAX_QUERIES = 16
+# Requests whose queries x group fit one 16-column MFMA tile use the split-K
+# decode kernel; wider ones (prompt chunks, tree verification) use the MFMA
+# prefill kernel when it covers the layer's shape, whose four waves share
+# each K/V tile.
+DECODE_MAX_COLUMNS = 16
+# Smallest key range (in prefill key tiles) the planner gives one prefill
+# workgroup when it splits units to fill the GPU.
+PREFILL_MIN_TILES = 4
 # Compute units of an MI355X; the planner aims for several waves per CU.
 NUM_CUS = 256
 # Block-table entries a decode partition may span (the kernel's LDS slice).
@@ -43,6 +48,8 @@ TABLE_SLICE = 256
 
 
 PIECE_FIELDS = 16
+PREFILL_FIELDS = 8
+PIECE_BLOCKS = 5  # first-tile block ids carried in piece fields 11..15
 MERGE_FIELDS = 8
 # Default stream-K granularity: shares and piece boundaries fall on multiples
 # of this many tokens.  The backend passes the decode kernel's own tile size
@@ -66,6 +73,7 @@ def stream_k_pieces(
     ngroups: np.ndarray,
     rows: np.ndarray,
     req_meta: np.ndarray,
+    flat_tables: np.ndarray,
     num_kv_heads: int,
     resident_waves: int,
     block_size: int,
@@ -124,6 +132,14 @@ def stream_k_pieces(
     pieces[:, 8] = req_meta[req, 4]  # q_start
     pieces[:, 9] = req_meta[req, 5]  # vis_off
     pieces[:, 10] = req_meta[req, 6]  # vis_words
+    # Physical ids of each piece's first PIECE_BLOCKS logical blocks (0 past
+    # the request's table): the kernel issues the first tile from them.
+    lb0 = pieces[:, 2] // block_size
+    nblk = req_meta[req, 1]
+    j = np.arange(PIECE_BLOCKS)
+    ok = lb0[:, None] + j[None, :] < nblk[:, None]
+    idx = np.where(ok, req_meta[req, 0][:, None] + lb0[:, None] + j[None, :], 0)
+    pieces[:, 11 : 11 + PIECE_BLOCKS] = np.where(ok, flat_tables[idx] if flat_tables.size else 0, 0)
     wave_first = np.searchsorted(wave, np.arange(waves + 1), side="left")
     first = multi & (lo == seg_start[seg])
     jreq = req[first]
@@ -135,6 +151,78 @@ def stream_k_pieces(
     jobs[:, 4] = req_meta[jreq, 4]  # q_start
     jobs[:, 5] = req_meta[jreq, 3]  # q_len
     return pieces, wave_first, waves, per_wave, jobs, int(multi.sum())
+
+
+def prefill_pieces(
+    *,
+    q_lens: np.ndarray,
+    computed: np.ndarray,
+    rows: np.ndarray,
+    req_meta: np.ndarray,
+    group: int,
+    columns: int,
+    key_tokens: int,
+    slots_per_head: int,
+    min_tiles: int = PREFILL_MIN_TILES,
+):
+    """Prefill work units of the ``rows`` requests, split over keys when the
+    units alone cannot fill the GPU.
+
+    A unit is up to ``columns`` MFMA columns (query, head-in-group pairs) of
+    one request; it needs the keys up to its last query, ceil(kneed /
+    key_tokens) tiles.  When there are fewer units than ``slots_per_head``
+    (resident prefill workgroups per kv head), every unit's tile range is cut
+    into near-equal pieces of at least ``min_tiles`` tiles so that all slots
+    get work; the pieces of a split unit write partials (consecutive slots)
+    and one merge job per unit combines them.  Returns (units [n, 8] int64,
+    heaviest first, as (req, first column, columns, key_begin, key_end, slot,
+    0, 0); merge jobs [m, 8] as (req, column group, first slot, pieces,
+    q_start, q_len, 0, 0); number of partial slots).
+    """
+
+    ncols = q_lens * group
+    nunit = np.where(rows, -(-ncols // columns), 0)
+    n = int(nunit.sum())
+    req = np.repeat(np.arange(len(q_lens)), nunit)
+    starts = np.zeros(len(q_lens), dtype=np.int64)
+    np.cumsum(nunit[:-1], out=starts[1:])
+    col0 = (np.arange(n) - starts[req]) * columns
+    cols = np.minimum(columns, ncols[req] - col0)
+    kneed = computed[req] + (col0 + cols - 1) // group + 1
+    tiles = -(-kneed // key_tokens)
+    npieces = np.ones(n, dtype=np.int64)
+    if slots_per_head and n < slots_per_head:
+        target = max(min_tiles, -(-int(tiles.sum()) // slots_per_head))
+        npieces = np.maximum(1, -(-tiles // target))
+    total = int(npieces.sum())
+    unit = np.repeat(np.arange(n), npieces)
+    pstart = np.zeros(n, dtype=np.int64)
+    np.cumsum(npieces[:-1], out=pstart[1:])
+    i = np.arange(total) - pstart[unit]
+    t0 = (i * tiles[unit]) // npieces[unit]
+    t1 = ((i + 1) * tiles[unit]) // npieces[unit]
+    split = npieces[unit] > 1
+    slot = np.where(split, np.cumsum(split) - 1, -1)
+    ptab = np.zeros((total, PREFILL_FIELDS), dtype=np.int64)
+    ptab[:, 0] = req[unit]
+    ptab[:, 1] = col0[unit]
+    ptab[:, 2] = cols[unit]
+    ptab[:, 3] = t0 * key_tokens
+    ptab[:, 4] = np.where(i + 1 < npieces[unit], t1 * key_tokens, 0)
+    ptab[:, 5] = slot
+    # Heaviest first (keys x columns): better tail balance.
+    work = (t1 - t0) * cols[unit]
+    order = np.argsort(-work, kind="stable")
+    first = split & (i == 0)
+    ju = unit[first]
+    jobs = np.zeros((int(first.sum()), MERGE_FIELDS), dtype=np.int64)
+    jobs[:, 0] = req[ju]
+    jobs[:, 1] = col0[ju] // columns
+    jobs[:, 2] = slot[first]
+    jobs[:, 3] = npieces[ju]
+    jobs[:, 4] = req_meta[req[ju], 4]  # q_start
+    jobs[:, 5] = req_meta[req[ju], 3]  # q_len
+    return ptab[order], jobs, int(split.sum())
 
 
 def _stage_int32(array: np.ndarray, device: torch.device) -> Tensor:
@@ -156,8 +244,11 @@ class DecodeWork:
     num_partial_slots: int
     units_per_wave: int
     col_tiles: int  # column tiles per decode wave (partials hold 16 * col_tiles columns)
-    prefill_units: Tensor | None  # int32 [n_prefill_units, 4]
+    prefill_units: Tensor | None  # int32 [n_prefill_units, 8]
     num_prefill_units: int
+    prefill_jobs: Tensor | None = None  # int32 [n, 8] merge jobs of split prefill units
+    num_prefill_jobs: int = 0
+    num_prefill_partial_slots: int = 0
 
 
 class StepPlan:
@@ -244,14 +335,22 @@ class StepPlan:
         self._computed = computed
         self._q_lens = q_lens
         self._req_meta = req_meta
-        self._work: dict[tuple[int, int], DecodeWork] = {}
+        self._flat = flat
+        self._work: dict[tuple[int, ...], DecodeWork] = {}
+        self._col_tiles: dict[tuple[int, int, int], int] = {}
+        # Bound launch arguments per layer shape, filled by the backend.
+        self.launches: dict[tuple, object] = {}
+
+    @property
+    def num_query_tokens(self) -> int:
+        return self.num_tokens
 
     # -- work lists ---------------------------------------------------------
-    def decode_rows(self, prefill_columns: int) -> np.ndarray:
+    def decode_rows(self, prefill_columns: int, group: int = 1) -> np.ndarray:
         """Requests the decode kernel serves (all of them without a prefill kernel)."""
 
         if prefill_columns > 0:
-            return self._q_lens <= DECODE_MAX_QUERIES
+            return self._q_lens * group <= DECODE_MAX_COLUMNS
         return np.ones(self.batch_size, dtype=bool)
 
     def choose_col_tiles(self, group: int, prefill_columns: int, max_col_tiles: int) -> int:
@@ -261,7 +360,14 @@ class StepPlan:
 
         if max_col_tiles < 4:
             return 1
-        rows = self.decode_rows(prefill_columns)
+        key = (group, prefill_columns, max_col_tiles)
+        found = self._col_tiles.get(key)
+        if found is None:
+            found = self._col_tiles[key] = self._choose_col_tiles(group, prefill_columns)
+        return found
+
+    def _choose_col_tiles(self, group: int, prefill_columns: int) -> int:
+        rows = self.decode_rows(prefill_columns, group)
         seq = (self._computed + self._q_lens)[rows]
         nct = -(-(self._q_lens[rows] * group) // 16)
         one = float((seq * nct).sum())
@@ -270,32 +376,37 @@ class StepPlan:
 
     def work(
         self, group: int, num_kv_heads: int, resident_waves: int = 8 * NUM_CUS, prefill_columns: int = 0,
-        unit_tokens: int = UNIT_TOKENS, col_tiles: int = 1,
+        unit_tokens: int = UNIT_TOKENS, col_tiles: int = 1, prefill_key_tokens: int = 64,
+        prefill_resident: int = 0,
     ) -> DecodeWork:
         """Work lists for layers of this (group, kv heads) shape.
 
         ``resident_waves`` is how many decode waves the GPU holds at once,
         ``prefill_columns`` the prefill kernel's unit width (0: every request
         goes through the decode kernel), ``unit_tokens`` the decode kernel's
-        tile and ``col_tiles`` its column tiles per wave; the library reports
-        the kernel figures per dtype, head size and column tiles.
+        tile and ``col_tiles`` its column tiles per wave; ``prefill_key_tokens``
+        is the prefill kernel's key tile and ``prefill_resident`` how many
+        prefill workgroups the GPU holds (0: never split prefill units).  The
+        library reports the kernel figures per dtype and head size.
         """
 
-        key = (group, num_kv_heads, resident_waves, prefill_columns, unit_tokens, col_tiles)
+        key = (group, num_kv_heads, resident_waves, prefill_columns, unit_tokens, col_tiles, prefill_key_tokens,
+               prefill_resident)
         found = self._work.get(key)
         if found is None:
-            found = self._build_work(group, num_kv_heads, resident_waves, prefill_columns, unit_tokens, col_tiles)
+            found = self._build_work(group, num_kv_heads, resident_waves, prefill_columns, unit_tokens, col_tiles,
+                                     prefill_key_tokens, prefill_resident)
             self._work[key] = found
         return found
 
     def _build_work(
         self, group: int, num_kv_heads: int, resident_waves: int, prefill_columns: int, unit_tokens: int,
-        col_tiles: int,
+        col_tiles: int, prefill_key_tokens: int, prefill_resident: int,
     ) -> DecodeWork:
         computed, q_lens = self._computed, self._q_lens
         batch = self.batch_size
         seq = computed + q_lens
-        decode_rows = self.decode_rows(prefill_columns)
+        decode_rows = self.decode_rows(prefill_columns, group)
         nct = -(-(q_lens * group) // 16)
         ngroups = -(-nct // col_tiles)
         pieces = wave_first = jobs = prefill_units = None
@@ -306,7 +417,8 @@ class StepPlan:
             if self.partition_tokens:
                 max_units = max(1, self.partition_tokens // unit_tokens)
             piece_tab, first_tab, waves, per_wave, job_tab, num_partial = stream_k_pieces(
-                seq=seq, ngroups=ngroups, rows=decode_rows, req_meta=self._req_meta, num_kv_heads=num_kv_heads,
+                seq=seq, ngroups=ngroups, rows=decode_rows, req_meta=self._req_meta, flat_tables=self._flat,
+                num_kv_heads=num_kv_heads,
                 resident_waves=resident_waves, block_size=self.block_size, max_units_per_wave=max_units,
                 unit_tokens=unit_tokens,
             )
@@ -316,21 +428,19 @@ class StepPlan:
             if num_jobs:
                 blocks.append(job_tab.reshape(-1))
         prefill_rows = ~decode_rows
+        ptab = pjobs = None
+        num_pjobs = num_pslots = 0
         if prefill_rows.any():
-            # Units of prefill_columns (query, head-in-group) columns.
-            ncols = q_lens * group
-            nunit = np.where(prefill_rows, -(-ncols // prefill_columns), 0)
-            num_prefill = int(nunit.sum())
-            req = np.repeat(np.arange(batch), nunit)
-            starts = np.zeros(batch, dtype=np.int64)
-            np.cumsum(nunit[:-1], out=starts[1:])
-            col0 = (np.arange(num_prefill) - starts[req]) * prefill_columns
-            cols = np.minimum(prefill_columns, ncols[req] - col0)
-            # Heaviest units (keys x columns) first: better tail balance.
-            work = (computed[req] + (col0 + cols - 1) // group + 1) * cols
-            order = np.argsort(-work, kind="stable")
-            ptab = np.stack([req[order], col0[order], cols[order], np.zeros(num_prefill, dtype=np.int64)], axis=1)
+            ptab, pjobs, num_pslots = prefill_pieces(
+                q_lens=q_lens, computed=computed, rows=prefill_rows, req_meta=self._req_meta, group=group,
+                columns=prefill_columns, key_tokens=prefill_key_tokens,
+                slots_per_head=prefill_resident // num_kv_heads if prefill_resident else 0,
+            )
+            num_prefill = int(ptab.shape[0])
+            num_pjobs = int(pjobs.shape[0])
             blocks.append(ptab.reshape(-1))
+            if num_pjobs:
+                blocks.append(pjobs.reshape(-1))
         if blocks:
             blob = _stage_int32(np.concatenate(blocks), self.device)
         else:
@@ -344,7 +454,11 @@ class StepPlan:
         if num_jobs:
             jobs = blob[off : off + MERGE_FIELDS * num_jobs].view(num_jobs, MERGE_FIELDS)
             off += MERGE_FIELDS * num_jobs
+        prefill_jobs = None
         if num_prefill:
-            prefill_units = blob[off : off + 4 * num_prefill].view(num_prefill, 4)
+            prefill_units = blob[off : off + PREFILL_FIELDS * num_prefill].view(num_prefill, PREFILL_FIELDS)
+            off += PREFILL_FIELDS * num_prefill
+        if num_pjobs:
+            prefill_jobs = blob[off : off + MERGE_FIELDS * num_pjobs].view(num_pjobs, MERGE_FIELDS)
         return DecodeWork(pieces, wave_first, waves, jobs, num_jobs, num_partial, per_wave, col_tiles, prefill_units,
-                          num_prefill)
+                          num_prefill, prefill_jobs, num_pjobs, num_pslots)

@@ -243,7 +243,7 @@ def test_four_column_tiles_across_dtypes_and_head_sizes(dtype, head_size) -> Non
     _announce(f"col_tiles=4 d={head_size} {dtype}")
     step = make_step(hq=8, hkv=2, d=head_size, bs=16, dtype=DTYPES[dtype], computed=[700, 3, 1500, 64],
                      layouts=_lin(8, 1, 9, 2), seed=head_size + 5)
-    _run_and_check(step, backend=lv.HipPagedAttentionBackend(decode_col_tiles=4))
+    _run_and_check(step, backend=lv.HipPagedAttentionBackend(use_prefill_kernel=False, decode_col_tiles=4))
 
 
 @pytest.mark.parametrize("col_tiles", (1, 4))
@@ -260,7 +260,8 @@ def test_tree_verification_by_column_tiles(col_tiles, partition) -> None:
         computed.append(256 + int(rng.integers(0, 900)))
     step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=computed, layouts=layouts,
                      shared_prefix_blocks=16, seed=52)
-    backend = lv.HipPagedAttentionBackend(decode_col_tiles=col_tiles, partition_tokens=partition)
+    backend = lv.HipPagedAttentionBackend(use_prefill_kernel=False, decode_col_tiles=col_tiles,
+                                          partition_tokens=partition)
     _, ctx = _run_and_check(step, backend=backend)
     work = ctx.plan.work(7, 4, lv.native.resident_decode_waves(2, 128, col_tiles), 0,
                          lv.native.decode_tile_tokens(2, 128, col_tiles), col_tiles)
@@ -279,10 +280,12 @@ def test_four_column_tiles_long_queries_without_prefill_kernel(bs) -> None:
 
 
 def test_auto_column_tiles_pick_four_for_trees_and_one_for_decode() -> None:
+    # Without the prefill kernel (as for fp32 layers) multi-tile rows take
+    # the four-column-tile decode kernel.
     _announce("auto column tiles")
     step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[500, 900],
                      layouts=_lin(8, 8), seed=71)
-    _, ctx = _run_and_check(step)
+    _, ctx = _run_and_check(step, backend=lv.HipPagedAttentionBackend(use_prefill_kernel=False))
     assert ctx.plan.choose_col_tiles(7, 0, 4) == 4
     step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[500, 900],
                      layouts=_lin(1, 1), seed=72)

@@ -1,7 +1,9 @@
 """GPU parity of the MFMA chunked-prefill kernel against the CPU oracle.
 
-Requests with more than 16 queries of a bf16/fp16 layer take the prefill
-kernel; shorter ones take the decode kernel in the same step.  Tolerances as in
+Requests whose queries x group exceed one 16-column MFMA tile take the
+prefill kernel in a bf16/fp16 layer; the others take the decode kernel in the
+same step.  When there are fewer prefill units than resident workgroups the
+planner splits their key ranges (split-K) and a merge combines the partials.  Tolerances as in
 paged_cases.tolerances (bf16 max-abs 2e-2 / mean-abs 2e-3, fp16 3e-3 / 3e-4).
 Large steps are checked against the independent fp64 dense oracle.
 """
@@ -134,3 +136,70 @@ def test_fp32_layers_use_the_decode_kernel() -> None:
     _announce("fp32 long queries")
     step = make_step(hq=4, hkv=2, d=64, bs=16, dtype=torch.float32, computed=[20], layouts=_lin(40), seed=5)
     _check(step, expect_prefill=False)
+
+
+# ------------------------------------------------------ split-K prefill (key-range pieces + merge)
+def _tree(rng, n):
+    parents = [-1] + [int(rng.integers(0, i)) for i in range(1, n - 1)]
+    return tuple([-1] + [0 if p == -1 else p + 1 for p in parents])  # 1 input token + (n-1)-node tree
+
+
+def _split_work(step):
+    backend = lv.HipPagedAttentionBackend()
+    ctx = backend.create(step.cache, step.metadata)
+    return backend, ctx._work(step.cache.layer_spec(step.layer_ids[0]), step.query.dtype)
+
+
+@pytest.mark.parametrize("dtype", ("bf16", "fp16"))
+@pytest.mark.parametrize("head_size", (64, 80, 96, 128, 256))
+def test_split_k_tree_verification_head_sizes(dtype, head_size) -> None:
+    _announce(f"split-K prefill tree d={head_size} {dtype}")
+    rng = np.random.default_rng(head_size)
+    step = make_step(hq=12, hkv=2, d=head_size, bs=16, dtype=DTYPES[dtype], computed=[900, 1500, 370, 2100],
+                     layouts=[_tree(rng, 9) for _ in range(4)], seed=head_size + 31)
+    backend, work = _split_work(step)
+    assert work.num_prefill_partial_slots > 0 and work.num_prefill_jobs == 4
+    _check(step, backend=backend)
+
+
+def test_split_k_c5_shape_shared_prefix() -> None:
+    # BASELINE C5 at reduced batch: 8 requests share a 2048-token prefix,
+    # private suffixes, 9-token trees (1 input + 8 drafts) at group 6.
+    _announce("split-K C5 shape")
+    rng = np.random.default_rng(55)
+    computed = [2048 + int(rng.integers(64, 513)) for _ in range(8)]
+    step = make_step(hq=12, hkv=2, d=128, bs=16, dtype=torch.bfloat16, computed=computed,
+                     layouts=[_tree(rng, 9) for _ in range(8)], shared_prefix_blocks=128, seed=55)
+    backend, work = _split_work(step)
+    assert work.num_prefill_partial_slots > 0
+    _check(step, backend=backend)
+
+
+@pytest.mark.parametrize("bs", (1, 3, 16))
+def test_split_k_causal_chunks_and_block_sizes(bs) -> None:
+    # Causal chunks with long prior context: 40 x 7 = 280 columns (three units,
+    # the last partial), split over keys; plus decode rows in the same step.
+    _announce(f"split-K causal chunks bs={bs}")
+    step = make_step(hq=28, hkv=4, d=128, bs=bs, dtype=torch.bfloat16, computed=[3000, 700, 1200],
+                     layouts=_lin(40, 3, 1), seed=80 + bs)
+    backend, work = _split_work(step)
+    assert work.num_prefill_partial_slots > 0 and work.waves_per_head > 0
+    _check(step, backend=backend, dense=True)
+
+
+def test_split_k_matches_the_unsplit_kernel() -> None:
+    # The same step through split pieces and through whole units agrees
+    # within the bf16 tolerance (both are checked against the oracle too).
+    _announce("split-K vs whole units")
+    rng = np.random.default_rng(90)
+    step = make_step(hq=12, hkv=2, d=128, bs=16, dtype=torch.bfloat16, computed=[1800, 2500],
+                     layouts=[_tree(rng, 9), _tree(rng, 9)], seed=90)
+    backend, work = _split_work(step)
+    assert work.num_prefill_partial_slots > 0
+    a = _check(step, backend=backend)
+    whole = lv.HipPagedAttentionBackend(split_prefill=False)
+    ctx = whole.create(step.cache, step.metadata)
+    w2 = ctx._work(step.cache.layer_spec(step.layer_ids[0]), step.query.dtype)
+    assert w2.num_prefill_partial_slots == 0 and w2.num_prefill_units == 2
+    b = _check(step, backend=whole)
+    assert (a.float() - b.float()).abs().max().item() <= 2e-2

@@ -187,6 +187,10 @@ def test_stream_k_pieces_cover_every_segment_once(resident, bs, group, unit, ctw
             n_tab = (te - 1) // bs - tb // bs + 1
             assert n_tab <= 254, "piece exceeds the kernel's LDS table slice"
             covered.setdefault((req, ctile), []).append((tb, te, slot))
+            table = md.block_tables[req]
+            for j in range(5):  # first-tile block ids carried by the piece
+                lb = tb // bs + j
+                assert rec[11 + j] == (table[lb] if lb < len(table) else 0)
             tiles += -(-(te - tb) // u)
         assert tiles <= work.units_per_wave
         share_sizes.append(tiles)
@@ -238,30 +242,71 @@ def test_col_tiles_choice_follows_the_reread_cost() -> None:
 
 
 @pytest.mark.parametrize("group,columns", ((7, 256), (1, 256), (4, 128)))
-def test_prefill_units_tile_every_long_request(group, columns) -> None:
-    rng = np.random.default_rng(12 + group)
+@pytest.mark.parametrize("resident", (0, 64, 4096))
+@pytest.mark.parametrize("key_tokens", (32, 64))
+def test_prefill_pieces_cover_every_wide_request_once(group, columns, resident, key_tokens) -> None:
+    """Every (column, key) pair of a wide request is in exactly one prefill
+    piece; split units' pieces own consecutive partial slots that one merge
+    job names; pieces are heaviest first."""
+
+    rng = np.random.default_rng(12 + group + resident)
     md = _random_metadata(rng, batch=6, bs=16)
     plan = StepPlan(md, block_size=16, device=CPU)
-    work = plan.work(group, 4, 2048, columns)
-    seen = {}
-    keys_prev = None
+    work = plan.work(group, 4, 2048, columns, 64, 1, key_tokens, resident)
     computed = np.asarray(md.num_computed_tokens)
-    for req, c0, n, _ in (work.prefill_units.numpy() if work.num_prefill_units else []):
-        assert 0 < n <= columns
-        seen.setdefault(int(req), []).extend(range(c0, c0 + n))
-        keys = (computed[req] + (c0 + n - 1) // group + 1) * n
-        assert keys_prev is None or keys <= keys_prev  # heaviest first
-        keys_prev = keys
+    units = work.prefill_units.numpy() if work.num_prefill_units else np.zeros((0, 8), np.int32)
+    spans: dict[tuple[int, int], list] = {}
+    work_prev = None
+    for req, c0, n, kb, ke, slot, z0, z1 in units:
+        assert 0 < n <= columns and c0 % columns == 0 and z0 == z1 == 0
+        kneed = computed[req] + (c0 + n - 1) // group + 1
+        end = ke if ke else kneed
+        assert kb % key_tokens == 0 and kb < end <= kneed and (ke == 0 or ke % key_tokens == 0)
+        spans.setdefault((int(req), int(c0)), []).append((int(kb), int(end), int(slot), int(n)))
+        w = -(-(end - kb) // key_tokens) * n
+        assert work_prev is None or w <= work_prev  # heaviest first
+        work_prev = w
+    jobs = {(int(j[0]), int(j[1])): j for j in (work.prefill_jobs.numpy() if work.num_prefill_jobs else [])}
+    slots = []
+    for (req, c0), sp in spans.items():
+        sp.sort()
+        kneed = computed[req] + (c0 + sp[0][3] - 1) // group + 1
+        assert sp[0][0] == 0 and sp[-1][1] == kneed
+        assert all(a[1] == b[0] for a, b in zip(sp, sp[1:]))
+        if len(sp) == 1:
+            assert sp[0][2] == -1 and (req, c0 // columns) not in jobs
+        else:
+            j = jobs[(req, c0 // columns)]
+            assert [x[2] for x in sp] == list(range(j[2], j[2] + j[3])) and j[3] == len(sp)
+            assert j[4] == md.query_start_loc[req] and j[5] == md.query_lengths[req]
+            assert all(-(-(x[1] - x[0]) // key_tokens) >= 4 or x is sp[-1] for x in sp)
+            slots += [x[2] for x in sp]
+    assert sorted(slots) == list(range(work.num_prefill_partial_slots))
+    if resident == 0:
+        assert work.num_prefill_partial_slots == 0  # no split without a resident count
     decode_reqs = set()
     if work.waves_per_head:
         decode_reqs = {int(r) for r in work.pieces.numpy()[:, 0]}
     for r, q in enumerate(md.query_lengths):
-        if q > 16:
-            assert sorted(seen[r]) == list(range(q * group)) and r not in decode_reqs
+        if q * group > 16:
+            cols = sorted(c for (rr, c0), sp in spans.items() if rr == r for c in range(c0, c0 + sp[0][3]))
+            assert cols == list(range(q * group)) and r not in decode_reqs
         else:
-            assert r not in seen and r in decode_reqs
+            assert all(rr != r for rr, _ in spans) and r in decode_reqs
     # Without the prefill kernel every request is a decode row.
     assert plan.work(group, 4, 2048, 0).num_prefill_units == 0
+
+
+def test_prefill_split_fills_the_resident_workgroups() -> None:
+    # C5-like: tree verification of 9 queries at group 6 = 54 columns, one
+    # unit per request; 4 requests x 32 key tiles over 16 slots per kv head.
+    plan = StepPlan(_uniform_metadata(batch=4, computed=2000, q=9), block_size=16, device=CPU)
+    work = plan.work(6, 2, 2048, 128, 64, 1, 64, 32)
+    assert work.waves_per_head == 0 and work.num_prefill_units == 16
+    assert work.num_prefill_jobs == 4 and work.num_prefill_partial_slots == 16
+    units = work.prefill_units.numpy()
+    assert sorted(units[:, 3].tolist()) == sorted([0, 512, 1024, 1536] * 4)
+    assert sorted(units[:, 4].tolist()) == sorted([512, 1024, 1536, 0] * 4)
 
 
 def test_library_loads_and_exports_every_header_function() -> None:
@@ -285,7 +330,9 @@ def test_library_loads_and_exports_every_header_function() -> None:
     assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 1, None, None,
                                   None, None, 0, 4, 7, 128, 2, 16, ctypes.c_float(0.1), 2, None) == -2
     assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 1, 2, None) == -1
-    assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 3, 2, None) == -2
+    assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 17, 2, None) == -2
+    assert lib.lvamd_paged_prefill_key_tokens(2, 128) == 64 and lib.lvamd_paged_prefill_key_tokens(2, 256) == 32
+    assert lib.lvamd_paged_prefill_key_tokens(0, 128) == -2  # no fp32 prefill kernel
     # Tile sizes per kernel; four column tiles only for rows of at most 256 bytes.
     assert lib.lvamd_paged_decode_tile_tokens(2, 128, 1) == 64
     assert lib.lvamd_paged_decode_tile_tokens(2, 128, 4) == 16
