@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
   __shared__ __attribute__((aligned(16))) char klds[2][P::TILE_BYTES];
   __shared__ __attribute__((aligned(16))) char vlds[2][P::TILE_BYTES];
 
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x & (kThreads - 1);  // (the mask tells LLVM tid < 256)
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int l16 = lane & 15;
@@ -132,20 +132,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
   const T* vbase = static_cast<const T*>(a.v_pool);
   const int32_t* table = a.tables + table_off;
 
-  // ---- tile gather.  Chunk i of this thread is row rw[i], 16-byte chunk
-  // (idx % CPR) of the tile (idx = tid + 256 i); both fixed for the kernel.
-  int rw[LPT];
-  int64_t cofs[LPT];
-  bool cok[LPT];
-#pragma unroll
-  for (int i = 0; i < LPT; ++i) {
-    const int idx = tid + kThreads * i;
-    cok[i] = idx < KT * CPR;
-    rw[i] = cok[i] ? idx / CPR : 0;
-    cofs[i] = (int64_t)kvh * D + (idx % CPR) * 8;
-  }
+  // ---- tile gather.  Chunk i of this thread is chunk idx = tid + 256 i of
+  // the tile: row idx / CPR, 16-byte chunk idx % CPR (recomputed where used:
+  // cheaper than holding them in registers).
+  auto chunk_ok = [&](int i) { return tid + kThreads * i < KT * CPR; };
+  auto chunk_row = [&](int i) { return chunk_ok(i) ? (tid + kThreads * i) / CPR : 0; };
+  auto chunk_col = [&](int i) { return (tid + kThreads * i) % CPR; };
   auto key_pos = [&](int t, int i) -> int {
-    const int pos = (tile0 + t) * KT + rw[i];
+    const int pos = (tile0 + t) * KT + chunk_row(i);
     return pos < kmax ? pos : kmax - 1;  // rows past the piece read its last key (masked)
   };
   auto logical_block = [&](int pos) -> int { return a.bs_shift >= 0 ? (pos >> a.bs_shift) : (pos / bs); };
@@ -158,8 +152,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     for (int i = 0; i < LPT; ++i) {
       const int pos = key_pos(t, i);
       const uint32_t slot = (uint32_t)te[i] * (uint32_t)bs + (uint32_t)(pos - logical_block(pos) * bs);
-      const int64_t off = (int64_t)slot * row_elems + cofs[i];
-      if (cok[i]) {
+      const int64_t off = (int64_t)slot * row_elems + kvh * D + chunk_col(i) * 8;
+      if (chunk_ok(i)) {
         kr[i] = load16(kbase + off);
         vr[i] = load16(vbase + off);
       }
@@ -168,9 +162,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
   auto store_tile = [&](int b, const uint4 (&kr)[LPT], const uint4 (&vr)[LPT]) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      if (cok[i]) {
-        const int idx = tid + kThreads * i;
-        const int off = rw[i] * RS + (idx % CPR) * 16;
+      if (chunk_ok(i)) {
+        const int off = chunk_row(i) * RS + chunk_col(i) * 16;
         *reinterpret_cast<uint4*>(klds[b] + off) = kr[i];
         *reinterpret_cast<uint4*>(vlds[b] + off) = vr[i];
       }
@@ -178,9 +171,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
   };
 
   // ---- this wave's columns: (query qi, head) per column tile, and Q^T chunks
-  int qi[CT], lin_last[CT];
+  int qi[CT];
   bool colok[CT];
-  const uint32_t* vrow[CT];
   uint4 qf[CT][NCH];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
@@ -189,8 +181,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     const int colc = colok[ct] ? col : col_end - 1;
     qi[ct] = colc / G;
     const int qhead = kvh * G + (colc - qi[ct] * G);
-    lin_last[ct] = computed + qi[ct];
-    vrow[ct] = vis_off >= 0 ? a.vis + vis_off + (int64_t)qi[ct] * vis_words : nullptr;
     const T* qrow = static_cast<const T*>(a.q) + (int64_t)(q_start + qi[ct]) * a.q_tok_stride +
                     (int64_t)qhead * a.q_head_stride;
 #pragma unroll
@@ -240,11 +230,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) st[ct][s] = Mma<T>::qk(kc, qf[ct][kk], st[ct][s]);
       }
+    const bool masked = t >= full_tiles;
     // Masks only past the fully visible prefix: one compare per score for a
     // linear request, the ancestor bits for a tree.  (A piece ends on a tile
     // boundary or at the unit's last key, so no unmasked tile reaches past
     // it; rows past kmax in a masked tile fail the visibility test.)
-    if (t >= full_tiles) {
+    if (masked) {
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
@@ -254,10 +245,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
             const int pos = t * KT + 16 * s + 4 * g + r;
             bool vis;
             if (!tree) {
-              vis = pos <= lin_last[ct];
+              vis = pos <= computed + qi[ct];
             } else {
               const int j = pos - computed;
-              vis = j < 0 || (j < q_len && ((vrow[ct][j >> 5] >> (j & 31)) & 1u));
+              vis = j < 0 || (j < q_len && ((a.vis[vis_off + qi[ct] * vis_words + (j >> 5)] >> (j & 31)) & 1u));
             }
             if (!vis) st[ct][s][r] = -INFINITY;
           }
@@ -317,16 +308,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
   // (stored to the other LDS buffer after the compute), tile t+2's loads are
   // in flight and tile t+3's table entries are being fetched.  Two register
   // sets alternate statically (a run-time swap would force waits).
+  // Prologue in two round trips: the table entries of tiles 0 and 1, then
+  // both tiles' loads (and tile 2's entries); tile 0 goes to LDS.
   int ea[LPT], eb[LPT];
   uint4 ka[LPT], va[LPT], kb[LPT], vb[LPT];
   load_entries(0, eb);
+  if (ntiles > 1) load_entries(1, ea);
   load_tile(0, eb, kb, vb);
-  store_tile(0, kb, vb);
-  if (ntiles > 1) {
-    load_entries(1, ea);
-    load_tile(1, ea, ka, va);
-  }
+  if (ntiles > 1) load_tile(1, ea, ka, va);
   if (ntiles > 2) load_entries(2, eb);
+  store_tile(0, kb, vb);
   __syncthreads();
 
   // dc holds tile t+1, dn receives tile t+2 (entries en), ec receives tile t+3's entries.
