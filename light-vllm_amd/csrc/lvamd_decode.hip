@@ -655,10 +655,12 @@ struct MergeArgs {
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void paged_merge_kernel(const MergeArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void paged_merge_kernel(const MergeArgs a) {
   constexpr int NT = D / 16;
-  // Partials per round trip: as many as ~192 VGPRs of staging hold.
-  constexpr int MC = (192 / (D / 4 + 2)) < 2 ? 2 : ((192 / (D / 4 + 2)) > 8 ? 8 : 192 / (D / 4 + 2));
+  // Partials per round trip: as many as ~384 registers of staging hold (one
+  // wave per SIMD: a merge launch has a few hundred waves, so occupancy is
+  // not what bounds it; the round trips are).
+  constexpr int MC = (384 / (D / 4 + 2)) < 2 ? 2 : ((384 / (D / 4 + 2)) > 12 ? 12 : 384 / (D / 4 + 2));
   const int Hkv = a.num_kv_heads;
   const int G = a.group;
   const int ctw = a.col_tiles;
