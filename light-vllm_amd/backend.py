@@ -379,8 +379,7 @@ class HipPagedAttentionBackend:
         else:
             if config.device.type != "cuda":
                 raise KVCacheError("HIP paged attention requires a GPU KV cache")
-            metadata.validate_block_tables(num_blocks=config.num_blocks, block_size=config.block_size)
-            plan = StepPlan(metadata, block_size=config.block_size, device=config.device,
+            plan = StepPlan(metadata, block_size=config.block_size, device=config.device, num_blocks=config.num_blocks,
                             partition_tokens=self._partition_tokens)
             self._last = (key, metadata, plan)
         return HipPagedAttention(cache, metadata, self._workspace, plan, self._use_prefill, self._col_tiles,

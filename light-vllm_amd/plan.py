@@ -31,6 +31,7 @@ import numpy as np
 import torch
 from torch import Tensor
 
+from light_vllm_amd.errors import KVCacheError
 from light_vllm_amd.layout import is_linear, query_visibility
 
 # Requests whose queries x group fit one 16-column MFMA tile use the split-K
@@ -227,6 +228,59 @@ def prefill_pieces(
     return ptab[order], jobs, int(split.sum())
 
 
+def tables_valid(
+    flat: np.ndarray,
+    counts: np.ndarray,
+    computed: np.ndarray,
+    reserved: np.ndarray,
+    readonly: np.ndarray,
+    *,
+    num_blocks: int,
+    block_size: int,
+) -> bool:
+    """Whether ``PagedAttentionMetadata.validate_block_tables`` would pass
+    (paged_attention.py:138-173), checked with array passes over the flat
+    tables instead of a Python loop per block id:
+
+    * every table has exactly ceil((computed + reserved) / block_size) blocks;
+    * every id is < num_blocks;
+    * readonly prefix blocks fit the table and the computed prefix;
+    * no id repeats within a table;
+    * an id shared by several tables sits at the same logical index and is
+      in the readonly prefix of every one of them.
+    """
+
+    if len(counts) == 0:
+        return True
+    required = (computed + reserved + block_size - 1) // block_size
+    if np.any(counts != required):
+        return False
+    if flat.size and (int(flat.max()) >= num_blocks or int(flat.min()) < 0):
+        return False
+    if np.any((readonly > counts) | (readonly * block_size > computed)):
+        return False
+    if flat.size == 0:
+        return True
+    uses = np.bincount(flat, minlength=num_blocks)
+    if int(uses.max()) <= 1:
+        return True  # no id appears twice anywhere
+    # Only the ids that repeat need the per-occurrence checks.
+    rep = np.flatnonzero(uses[flat] > 1)
+    req = np.searchsorted(np.cumsum(counts), rep, side="right")
+    starts = np.zeros(len(counts), dtype=np.int64)
+    np.cumsum(counts[:-1], out=starts[1:])
+    logical = rep - starts[req]
+    ro = logical < readonly[req]
+    order = np.lexsort((req, flat[rep]))  # by block id, then request
+    b, r, lg, o = flat[rep][order], req[order], logical[order], ro[order]
+    same = b[1:] == b[:-1]
+    if np.any(same & (r[1:] == r[:-1])):
+        return False  # repeated within one table
+    # Across tables: every occurrence of a shared id (each one after the
+    # first compared with the previous) at the same logical index, readonly.
+    return not np.any(same & ((lg[1:] != lg[:-1]) | ~o[1:] | ~o[:-1]))
+
+
 def _stage_int32(array: np.ndarray, device: torch.device) -> Tensor:
     """One pinned host buffer, one non-blocking copy on the current stream."""
 
@@ -263,7 +317,13 @@ class StepPlan:
         block_size: int,
         device: torch.device,
         partition_tokens: int | None = None,
+        num_blocks: int | None = None,
     ) -> None:
+        """With ``num_blocks`` the block tables are validated first, with the
+        rules and messages of ``PagedAttentionMetadata.validate_block_tables``
+        (paged_attention.py:138-173): a vectorised check over the flat tables,
+        and the metadata's own method to raise the exact error when it fails."""
+
         self.block_size = block_size
         self.device = device
         layouts = tuple(metadata.query_layouts)
@@ -274,6 +334,14 @@ class StepPlan:
         table_off = np.zeros(batch, dtype=np.int64)
         np.cumsum(counts[:-1], out=table_off[1:])
         computed = np.asarray(metadata.num_computed_tokens, dtype=np.int64)
+        if num_blocks is not None and not tables_valid(
+            flat, counts, computed, np.asarray(metadata.num_reserved_query_tokens, dtype=np.int64),
+            np.asarray(metadata.num_readonly_prefix_blocks, dtype=np.int64), num_blocks=num_blocks,
+            block_size=block_size,
+        ):
+            metadata.validate_block_tables(num_blocks=num_blocks, block_size=block_size)
+            # Only a negative id gets here (the metadata constructor rejects them).
+            raise KVCacheError("block table contains an out-of-range physical block")
         q_lens = np.fromiter((len(layout) for layout in layouts), dtype=np.int64, count=batch)
         q_start = np.zeros(batch, dtype=np.int64)
         np.cumsum(q_lens[:-1], out=q_start[1:])

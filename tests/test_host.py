@@ -358,3 +358,72 @@ def test_backend_refuses_a_cpu_cache() -> None:
 def test_kv_cache_bytes_per_block() -> None:
     spec = lv.ModelKVCacheSpec((lv.AttentionLayerSpec("attention", 2, 2, 4),))
     assert lv.kv_cache_bytes_per_block(spec, block_size=2, dtype=torch.float32) == 128
+
+
+def _tables_valid_of(md, num_blocks, bs):
+    from light_vllm_amd.plan import tables_valid
+    counts = np.asarray([len(t) for t in md.block_tables], dtype=np.int64)
+    flat = np.asarray([b for t in md.block_tables for b in t], dtype=np.int64)
+    return tables_valid(flat, counts, np.asarray(md.num_computed_tokens, dtype=np.int64),
+                        np.asarray(md.num_reserved_query_tokens, dtype=np.int64),
+                        np.asarray(md.num_readonly_prefix_blocks, dtype=np.int64),
+                        num_blocks=num_blocks, block_size=bs)
+
+
+@pytest.mark.parametrize("seed", range(54))
+def test_vectorised_table_check_agrees_with_validate_block_tables(seed) -> None:
+    """The step plan's array check passes exactly when the metadata's own
+    validate_block_tables does, on valid steps and on each kind of mistake
+    (short/long tables, out-of-range ids, aliasing within and across
+    requests, readonly sharing at another logical index or of a writable
+    block or at another logical index, readonly counts past the prefix)."""
+
+    rng = np.random.default_rng(seed)
+    bs = int(rng.choice([1, 4, 16]))
+    batch = int(rng.integers(1, 7))
+    shared = int(rng.integers(0, 3))
+    computed = [shared * bs + int(rng.integers(0, 40)) for _ in range(batch)]
+    reserved = [int(rng.integers(1, 5)) for _ in range(batch)]
+    need = [(c + r + bs - 1) // bs for c, r in zip(computed, reserved)]
+    pool = [int(x) for x in rng.permutation(sum(need) + 8)]
+    prefix, rest, tables = pool[:shared], pool[shared:], []
+    for n in need:
+        tables.append(list(prefix) + rest[: n - shared])
+        rest = rest[n - shared :]
+    readonly = [shared] * batch
+    num_blocks = len(pool)
+    kind = seed % 9
+    r = int(rng.integers(0, batch))
+    if kind == 1:
+        tables[r] = tables[r][:-1] or tables[r]
+    elif kind == 2:
+        tables[r] = tables[r] + [rest[0] if rest else num_blocks - 1]
+    elif kind == 3:
+        tables[r][-1] = num_blocks + int(rng.integers(0, 3))
+    elif kind == 4 and len(tables[r]) > 1:
+        tables[r][-1] = tables[r][0]
+    elif kind == 5 and batch > 1:
+        other = (r + 1) % batch
+        tables[r][-1] = tables[other][-1]
+    elif kind == 6 and shared and batch > 1:
+        readonly[r] = 0  # a shared block that this request may write
+    elif kind == 7:
+        readonly[r] = len(tables[r]) + 1
+    elif kind == 8 and shared == 2:  # a shared readonly block at another logical index
+        tables[r][0], tables[r][1] = tables[r][1], tables[r][0]
+    md = lv.PagedAttentionMetadata(
+        block_tables=tuple(tuple(t) for t in tables), num_computed_tokens=tuple(computed),
+        query_layouts=tuple(lv.QueryLayout((-1,)) for _ in range(batch)),
+        num_reserved_query_tokens=tuple(reserved), num_readonly_prefix_blocks=tuple(readonly),
+    )
+    try:
+        md.validate_block_tables(num_blocks=num_blocks, block_size=bs)
+        ok = True
+    except lv.KVCacheError:
+        ok = False
+    assert _tables_valid_of(md, num_blocks, bs) == ok
+    if not ok:  # the plan raises the metadata's own message
+        with pytest.raises(lv.KVCacheError):
+            StepPlan(md, block_size=bs, device=CPU, num_blocks=num_blocks)
+    else:
+        StepPlan(md, block_size=bs, device=CPU, num_blocks=num_blocks)
