@@ -142,7 +142,7 @@ int lvamd_paged_decode_tile_tokens(int32_t dtype, int32_t head_size, int32_t col
 
 /*
  * Log-sum-exp merge of split-K partials into out, one wave per (job, kv head,
- * column tile); jobs [num_jobs][LVAMD_MERGE_FIELDS]; col_tiles (1 to 16) is
+ * column), four columns per workgroup; jobs [num_jobs][LVAMD_MERGE_FIELDS]; col_tiles (1 to 16) is
  * the number of 16-column tiles per partial slot the partials were written
  * with (the decode kernel's col_tiles, or prefill unit columns / 16).  Same reference functions as lvamd_paged_decode:
  * the reference has no split-K, and this is the cross-partition half of that

@@ -639,9 +639,12 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Merge: one wave per (job, kv head, column tile of the job's group); lane
-// (g, l16) combines dims 16n + 4g..+3 of column l16 over the job's partials,
-// MC partials per round trip, by log-sum-exp in the log2 domain.
+// Merge: one wave per (job, kv head, column); a workgroup holds the four
+// waves of four consecutive columns.  Lane l combines dims EPL*l..+EPL-1 of
+// its column over the job's partials, MCP partials per round trip (their
+// (max, sum) pairs and acc rows are all requested before any is used), by
+// log-sum-exp in the log2 domain.  Every lane computes the chunk's weights
+// itself from the same (max, sum) values, so no cross-lane step is needed.
 // ---------------------------------------------------------------------------
 struct MergeArgs {
   const float* part_acc;
@@ -654,73 +657,92 @@ struct MergeArgs {
   int32_t col_tiles;  // column tiles per partial slot (the decode launch's)
 };
 
+constexpr int kMergeWaves = 4;  // columns (waves) per merge workgroup
+
+template <int EPL>
+__device__ __forceinline__ void load_acc(const float* p, float (&v)[EPL]) {
+  if constexpr (EPL == 1) {
+    v[0] = *p;
+  } else if constexpr (EPL == 2) {
+    const float2 x = *reinterpret_cast<const float2*>(p);
+    v[0] = x.x;
+    v[1] = x.y;
+  } else {
+    const float4 x = *reinterpret_cast<const float4*>(p);
+    v[0] = x.x;
+    v[1] = x.y;
+    v[2] = x.z;
+    v[3] = x.w;
+  }
+}
+
 template <typename T, int D>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void paged_merge_kernel(const MergeArgs a) {
-  constexpr int NT = D / 16;
-  // Partials per round trip: as many as ~384 registers of staging hold (one
-  // wave per SIMD: a merge launch has a few hundred waves, so occupancy is
-  // not what bounds it; the round trips are).
-  constexpr int MC = (384 / (D / 4 + 2)) < 2 ? 2 : ((384 / (D / 4 + 2)) > 12 ? 12 : 384 / (D / 4 + 2));
+__global__ __launch_bounds__(64 * kMergeWaves) void paged_merge_kernel(const MergeArgs a) {
+  constexpr int EPL = D <= 64 ? 1 : (D <= 128 ? 2 : 4);  // dims per lane
+  constexpr int MCP = 16;
   const int Hkv = a.num_kv_heads;
   const int G = a.group;
-  const int ctw = a.col_tiles;
-  const int wave = blockIdx.x;
-  const int ct = wave % ctw;
-  const int jh = wave / ctw;
+  const int cols = 16 * a.col_tiles;  // columns per partial slot
+  const int quads = cols / kMergeWaves;
+  const int jh = (int)blockIdx.x / quads;
+  const int c = ((int)blockIdx.x - jh * quads) * kMergeWaves +
+                __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int job = jh / Hkv;
   const int kvh = jh - job * Hkv;
-  const int lane = threadIdx.x & 63;  // (the mask tells LLVM lane < 64)
-  const int l16 = lane & 15;
-  const int g = lane >> 4;
+  const int lane = threadIdx.x & 63;
   const int32_t* jb = a.jobs + (int64_t)job * LVAMD_MERGE_FIELDS;
   const int cgroup = jb[1], slot0 = jb[2], np = jb[3], q_start = jb[4], q_len = jb[5];
-  const int col = (cgroup * ctw + ct) * 16 + l16;
+  const int col = cgroup * cols + c;
   if (col >= q_len * G) return;
   const int qi = col / G;
   const int qhead = kvh * G + (col - qi * G);
+  const int e0 = lane * EPL;
+  const bool act = e0 < D;
 
   float mrun = -INFINITY;
   float lsum = 0.f;
-  f32x4 o[NT];
+  float o[EPL];
 #pragma unroll
-  for (int n = 0; n < NT; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int j0 = 0; j0 < np; j0 += MC) {
-    float2 ml[MC];
-    f32x4 pa[MC][NT];
+  for (int k = 0; k < EPL; ++k) o[k] = 0.f;
+  for (int p0 = 0; p0 < np; p0 += MCP) {
+    const int n = np - p0 < MCP ? np - p0 : MCP;
+    float2 ml[MCP];
+    float pa[MCP][EPL];
 #pragma unroll
-    for (int i = 0; i < MC; ++i) {
-      const int slot = slot0 + (j0 + i < np ? j0 + i : np - 1);
-      const int64_t cs = ((int64_t)slot * Hkv + kvh) * (16 * ctw) + ct * 16 + l16;
-      ml[i] = *reinterpret_cast<const float2*>(a.part_ml + cs * 2);
+    for (int i = 0; i < MCP; ++i) {
+      ml[i] = make_float2(-INFINITY, 0.f);
 #pragma unroll
-      for (int n = 0; n < NT; ++n) pa[i][n] = *reinterpret_cast<const f32x4*>(a.part_acc + cs * D + 16 * n + 4 * g);
+      for (int k = 0; k < EPL; ++k) pa[i][k] = 0.f;
+      if (i < n) {
+        const int64_t r = ((int64_t)(slot0 + p0 + i) * Hkv + kvh) * cols + c;
+        ml[i] = *reinterpret_cast<const float2*>(a.part_ml + r * 2);
+        if (act) load_acc<EPL>(a.part_acc + r * D + e0, pa[i]);
+      }
     }
-    // One rescale per chunk, branch-free so the chunk's loads are issued
-    // together; entries past the job and empty partials weigh 0.
     float mc = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < MC; ++i) mc = fmaxf(mc, j0 + i < np ? ml[i].x : -INFINITY);
+    for (int i = 0; i < MCP; ++i) mc = fmaxf(mc, ml[i].x);
     const float mnew = fmaxf(mrun, mc);
     const bool any = mnew != -INFINITY;
     const float sc = (any && mrun != -INFINITY) ? fast_exp2(mrun - mnew) : (any ? 0.f : 1.f);
     lsum *= sc;
 #pragma unroll
-    for (int n = 0; n < NT; ++n) o[n] *= sc;
+    for (int k = 0; k < EPL; ++k) o[k] *= sc;
 #pragma unroll
-    for (int i = 0; i < MC; ++i) {
-      const float wt = (j0 + i < np && ml[i].x != -INFINITY) ? fast_exp2(ml[i].x - mnew) : 0.f;
+    for (int i = 0; i < MCP; ++i) {
+      // Entries past the job and empty partials carry max -inf: weight 0.
+      const float wt = ml[i].x != -INFINITY ? fast_exp2(ml[i].x - mnew) : 0.f;
       lsum += wt * ml[i].y;
 #pragma unroll
-      for (int n = 0; n < NT; ++n) o[n] += wt * pa[i][n];
+      for (int k = 0; k < EPL; ++k) o[k] += wt * pa[i][k];
     }
     mrun = mnew;
   }
+  if (!act) return;
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   T* orow = static_cast<T*>(a.out) + (int64_t)(q_start + qi) * a.out_tok_stride + (int64_t)qhead * a.out_head_stride;
 #pragma unroll
-  for (int n = 0; n < NT; ++n)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) orow[16 * n + 4 * g + r] = from_f32<T>(o[n][r] * inv);
+  for (int k = 0; k < EPL; ++k) orow[e0 + k] = from_f32<T>(o[k] * inv);
 }
 
 // ---------------------------------------------------------------------------
@@ -782,12 +804,12 @@ static int dispatch_decode(int dtype, int head_size, int col_tiles, F f) {
 template <typename T>
 static int launch_merge_t(int head_size, dim3 grid, hipStream_t s, const MergeArgs& a) {
   switch (head_size) {
-    case 32: hipLaunchKernelGGL((paged_merge_kernel<T, 32>), grid, dim3(64), 0, s, a); break;
-    case 64: hipLaunchKernelGGL((paged_merge_kernel<T, 64>), grid, dim3(64), 0, s, a); break;
-    case 80: hipLaunchKernelGGL((paged_merge_kernel<T, 80>), grid, dim3(64), 0, s, a); break;
-    case 96: hipLaunchKernelGGL((paged_merge_kernel<T, 96>), grid, dim3(64), 0, s, a); break;
-    case 128: hipLaunchKernelGGL((paged_merge_kernel<T, 128>), grid, dim3(64), 0, s, a); break;
-    case 256: hipLaunchKernelGGL((paged_merge_kernel<T, 256>), grid, dim3(64), 0, s, a); break;
+    case 32: hipLaunchKernelGGL((paged_merge_kernel<T, 32>), grid, dim3(64 * kMergeWaves), 0, s, a); break;
+    case 64: hipLaunchKernelGGL((paged_merge_kernel<T, 64>), grid, dim3(64 * kMergeWaves), 0, s, a); break;
+    case 80: hipLaunchKernelGGL((paged_merge_kernel<T, 80>), grid, dim3(64 * kMergeWaves), 0, s, a); break;
+    case 96: hipLaunchKernelGGL((paged_merge_kernel<T, 96>), grid, dim3(64 * kMergeWaves), 0, s, a); break;
+    case 128: hipLaunchKernelGGL((paged_merge_kernel<T, 128>), grid, dim3(64 * kMergeWaves), 0, s, a); break;
+    case 256: hipLaunchKernelGGL((paged_merge_kernel<T, 256>), grid, dim3(64 * kMergeWaves), 0, s, a); break;
     default: return LVAMD_ERR_UNSUPPORTED;
   }
   return launch_status();
@@ -889,7 +911,7 @@ extern "C" int lvamd_paged_attention_merge(const float* part_acc, const float* p
   if (num_jobs < 0 || num_kv_heads <= 0 || group <= 0) return LVAMD_ERR_INVALID_ARGUMENT;
   if (num_jobs == 0) return LVAMD_OK;
   if (!part_acc || !part_ml || !out || !jobs) return LVAMD_ERR_INVALID_ARGUMENT;
-  if ((int64_t)num_jobs * num_kv_heads * col_tiles > 0x7fffffffLL) return LVAMD_ERR_INVALID_ARGUMENT;
+  if ((int64_t)num_jobs * num_kv_heads * col_tiles * (16 / kMergeWaves) > 0x7fffffffLL) return LVAMD_ERR_INVALID_ARGUMENT;
   MergeArgs a;
   a.part_acc = part_acc;
   a.part_ml = part_ml;
@@ -900,7 +922,8 @@ extern "C" int lvamd_paged_attention_merge(const float* part_acc, const float* p
   a.num_kv_heads = num_kv_heads;
   a.group = group;
   a.col_tiles = col_tiles;
-  const dim3 grid((unsigned)(num_jobs * num_kv_heads * col_tiles));
+  // One workgroup per (job, kv head, kMergeWaves columns).
+  const dim3 grid((unsigned)(num_jobs * num_kv_heads * col_tiles * (16 / kMergeWaves)));
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case LVAMD_BF16: return launch_merge_t<__bf16>(head_size, grid, s, a);

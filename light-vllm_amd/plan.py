@@ -112,6 +112,12 @@ def stream_k_pieces(
     waves = max(1, min(max(1, resident_waves // num_kv_heads), -(-total // min_units_per_wave)))
     waves = max(waves, -(-total // cap))
     per_wave = -(-total // waves)  # the largest share; never above cap
+    # As few waves as give that largest share: every wave then carries a
+    # full share (C2: 237 waves per head of 10 tiles, not 256 of 9 or 10),
+    # so the memory system stays busy until the end and no wave runs a
+    # lone extra tile after the others finish.
+    if per_wave:
+        waves = -(-total // per_wave)
     # Balanced shares: wave w covers units [w * total // W, (w + 1) * total // W),
     # so shares differ by at most one unit and every wave has work.
     bounds = (np.arange(waves + 1, dtype=np.int64) * total) // waves
