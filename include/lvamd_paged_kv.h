@@ -229,6 +229,16 @@ int lvamd_kv_block_copy(const uint64_t* layer_key_ptrs, const uint64_t* layer_va
                         const int64_t* src_blocks, const int64_t* dst_blocks, int64_t num_pairs,
                         lvamd_stream_t stream);
 
+/*
+ * Measurement only: streams bytes (a multiple of 16) of buf from HBM with
+ * workgroups x 64 lanes, 16-byte loads, and writes the XOR of every lane's
+ * words to sink[workgroups * 64] (so the XOR of sink equals the XOR of buf).
+ * bench.py times it to report the practical HBM read ceiling beside the
+ * decode kernel's bandwidth.  No counterpart in the reference.
+ */
+int lvamd_hbm_read_probe(const void* buf, int64_t bytes, uint32_t* sink, int32_t workgroups,
+                         lvamd_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

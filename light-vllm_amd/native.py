@@ -69,6 +69,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_p, _p, _i32, _i64, _p, _p, _i64, _p],
     ),
+    "lvamd_hbm_read_probe": (ctypes.c_int, [_p, _i64, _p, _i32, _p]),
 }
 
 

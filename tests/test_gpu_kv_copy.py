@@ -230,3 +230,25 @@ def test_block_copy_rejects_overlap_and_duplicates() -> None:
         cache.copy_blocks([1, 2], [4, 4])
     with pytest.raises(lv.KVCacheError, match="invalid physical block"):
         cache.copy_blocks([1], [8])
+
+
+@pytest.mark.parametrize("nbytes, workgroups", [(16, 1), (4096, 3), ((1 << 20) + 48, 512), (64 << 20, 1024)])
+def test_read_probe_reads_every_chunk_once(nbytes, workgroups) -> None:
+    """The bandwidth probe bench.py times reads each 16-byte chunk exactly
+    once: the XOR of its per-lane words equals the XOR of the buffer."""
+
+    from light_vllm_amd import native
+
+    _announce(f"read probe {nbytes} B, {workgroups} workgroups")
+    rng = np.random.default_rng(nbytes)
+    words = rng.integers(0, 2**32, size=nbytes // 4, dtype=np.uint64).astype(np.uint32)
+    buf = torch.from_numpy(words.view(np.int32)).to(DEV)
+    sink = torch.empty(workgroups * 64, dtype=torch.int32, device=DEV)
+    lib = native.load()
+    stream = torch.cuda.current_stream(DEV).cuda_stream
+    native.check(lib.lvamd_hbm_read_probe(buf.data_ptr(), nbytes, sink.data_ptr(), workgroups, stream),
+                 "lvamd_hbm_read_probe")
+    got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))
+    assert got == np.bitwise_xor.reduce(words)
+    # A size that is not a multiple of 16 is refused (LVAMD_ERR_INVALID_ARGUMENT).
+    assert lib.lvamd_hbm_read_probe(buf.data_ptr(), 8, sink.data_ptr(), workgroups, stream) == -1
