@@ -100,6 +100,42 @@ def algorithmic_bytes(ctx: np.ndarray) -> dict:
             "step": kv + q + o + tables + append, "decode": kv + q + o + tables, "flops": flops}
 
 
+ROPE_THETA = 1_000_000.0  # Qwen2.5's rope_theta
+
+
+def rope_rows(positions, head_size: int, dtype: torch.dtype, device: torch.device):
+    """Per-token cos/sin rows as Qwen2 builds them (qwen2.py:690-705)."""
+
+    pos = torch.as_tensor(np.asarray(positions), dtype=torch.float32)
+    freqs = 1.0 / (ROPE_THETA ** (torch.arange(0, head_size, 2, dtype=torch.float32) / head_size))
+    emb = torch.outer(pos, freqs)
+    emb = torch.cat((emb, emb), dim=-1)
+    return emb.cos().to(dtype).to(device), emb.sin().to(dtype).to(device)
+
+
+def torch_rotary(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
+    """apply_rotary's PyTorch path (_qwen2_kernels.py:214-224): the model-side
+    rotation an unfused step runs before attention."""
+
+    q1, q2 = q.chunk(2, dim=-1)
+    k1, k2 = k.chunk(2, dim=-1)
+    c, s = cos.unsqueeze(1), sin.unsqueeze(1)
+    return q * c + torch.cat((-q2, q1), dim=-1) * s, k * c + torch.cat((-k2, k1), dim=-1) * s
+
+
+def time_steps(step, steps: int, warmup: int) -> float:
+    """ms per step of ``step(i)`` with host timing bracketed by synchronisation."""
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(i)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e3
+
+
 def cpu_baseline(metadata, cache, q, k, v, ctx, budget_s: float) -> dict:
     """Time the CPU oracle (append + per-query online softmax) on the same step."""
 
@@ -585,9 +621,25 @@ def build_c5(device, col_tiles=None):
     def compact():
         cache.compact_many(compacts)
 
+    # RoPE at each draft node's position (computed + tree depth).
+    positions = [p for c, l in zip(computed, layouts) for p in lv.semantic_positions(l, prefix_length=c)]
+    cos, sin = rope_rows(positions, cfg.d, cfg.dtype, device)
+
+    def attend_rotary():
+        ctx = backend.create(cache, md)
+        for lid in layer_ids:
+            ctx.forward(lid, q, k, v, scale=scale, rotary=(cos, sin))
+
+    def attend_torch_rotary():
+        ctx = backend.create(cache, md)
+        for lid in layer_ids:
+            qr, kr = torch_rotary(q, k, cos, sin)
+            ctx.forward(lid, qr, kr, v, scale=scale)
+
     return SimpleNamespace(cfg=cfg, cache=cache, md=md, q=q, k=k, v=v, scale=scale, tables=tables,
                            computed=computed, layouts=layouts, accepted=accepted, suffix=suffix, q_len=q_len,
-                           cow=cow, attend=attend, compact=compact)
+                           cow=cow, attend=attend, compact=compact, attend_rotary=attend_rotary,
+                           attend_torch_rotary=attend_torch_rotary)
 
 
 def run_c5(args, device) -> int:
@@ -605,6 +657,8 @@ def run_c5(args, device) -> int:
     cow_ms = _time_launches(lambda i: cow(), args.steps, args.warmup, device)
     attend_ms = _time_launches(lambda i: attend(), max(10, args.steps // 4), 2, device)
     compact_ms = _time_launches(lambda i: compact(), args.steps, args.warmup, device)
+    rotary_ms = _time_launches(lambda i: w.attend_rotary(), max(10, args.steps // 4), 2, device)
+    torch_rotary_ms = _time_launches(lambda i: w.attend_torch_rotary(), max(10, args.steps // 4), 2, device)
     row = cfg.hkv * cfg.d * 2
     unique_kv = (cfg.prefix + sum(s + q_len for s in suffix)) * 2 * row
     cow_bytes = 2 * cfg.batch * cfg.layers * 2 * cfg.bs * row
@@ -619,6 +673,10 @@ def run_c5(args, device) -> int:
                "attention_unique_gbps": round(cfg.layers * unique_kv / (attend_ms * 1e-3) / 1e9, 1),
                "cow_copy_us": round(cow_ms * 1e3, 2), "cow_copy_gbps": round(cow_bytes / (cow_ms * 1e-3) / 1e9, 1),
                "compact_us": round(compact_ms * 1e3, 2), "compact_tokens": moved,
+               "rotary": {"fused_attention_us": round(rotary_ms * 1e3, 2),
+                          "unfused_attention_us": round(torch_rotary_ms * 1e3, 2),
+                          "note": "28 layers with RoPE: lvamd_kv_append_rotary + attention, against "
+                                  "apply_rotary's PyTorch path + attention"},
                "host_submit_ms": round(host_ms, 5)})
     if not args.no_cpu_baseline:
         from oracle import paged_kv_oracle as O  # checker/baseline only
@@ -761,6 +819,25 @@ def main() -> int:
             "kernel": "paged_decode_kernel<bf16,128>",
             "algorithmic_bytes_per_launch": nbytes["decode"],
         },
+    }
+    # RoPE fused into the append (lvamd_kv_append_rotary) against the model's
+    # PyTorch rotation followed by the same attention step.
+    cos, sin = rope_rows(ctx, C2.d, C2.dtype, device)  # the new token sits at position ctx
+    scale = 1.0 / math.sqrt(C2.d)
+
+    def fused(i: int) -> torch.Tensor:
+        return backend.create(caches[i % len(caches)], metadata).forward(
+            "layer0", q, k, v, scale=scale, rotary=(cos, sin))
+
+    def unfused(i: int) -> torch.Tensor:
+        qr, kr = torch_rotary(q, k, cos, sin)
+        return backend.create(caches[i % len(caches)], metadata).forward("layer0", qr, kr, v, scale=scale)
+
+    record["rotary"] = {
+        "fused_ms_per_step": round(time_steps(fused, args.steps, args.warmup), 5),
+        "unfused_ms_per_step": round(time_steps(unfused, args.steps, args.warmup), 5),
+        "note": "step with RoPE: lvamd_kv_append_rotary + attention, against apply_rotary's PyTorch path + "
+                "the fused-append attention step",
     }
     ceiling = read_ceiling(device)
     record["hbm_read_ceiling"] = {

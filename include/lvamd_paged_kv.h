@@ -84,6 +84,32 @@ int lvamd_kv_append(const void* key, int64_t key_token_stride, int64_t key_head_
                     lvamd_stream_t stream);
 
 /*
+ * Rotary append: the RoPE half rotation fused with the KV append.  For every
+ * packed token t (cosines / sines rows t, head_size wide, in the cache dtype):
+ *   query_out[t, h] = rotate(query[t, h])         for h < num_query_heads
+ *   key_pool[slots[t], h] = rotate(key[t, h])     for h < num_kv_heads
+ *   value_pool[slots[t], h] = value[t, h]         (bit-exact copy)
+ * with rotate(x)[d] = x[d]*cos[d] + r[d]*sin[d], r = (-x[D/2:], x[:D/2]),
+ * rounded as the PyTorch path rounds it: each product to the dtype, then the
+ * sum (fp32 add) to the dtype.  Negative slots skip the pool writes.
+ * query_out may alias query (each thread reads a chunk pair before writing
+ * it).  One launch replaces the model's rotary kernel and the append.
+ *
+ * Replaces: apply_rotary (src/light_vllm/modeling/models/_qwen2_kernels.py:205-245,
+ *   called at src/light_vllm/modeling/models/qwen2.py:411) followed by
+ *   PagedKVCache.write_prepared (src/light_vllm/runtime/execution/paged_cache.py:209-248).
+ */
+int lvamd_kv_append_rotary(const void* query, int64_t query_token_stride, int64_t query_head_stride,
+                           void* query_out, int64_t query_out_token_stride, int64_t query_out_head_stride,
+                           const void* key, int64_t key_token_stride, int64_t key_head_stride,
+                           const void* value, int64_t value_token_stride, int64_t value_head_stride,
+                           const void* cosines, int64_t cosines_token_stride,
+                           const void* sines, int64_t sines_token_stride,
+                           void* key_pool, void* value_pool, const int64_t* slots, int64_t num_tokens,
+                           int32_t num_query_heads, int32_t num_kv_heads, int32_t head_size, int32_t dtype,
+                           lvamd_stream_t stream);
+
+/*
  * Split-K paged attention for short query runs (decode, speculative tree
  * verification), stream-K scheduled, with this step's KV append fused in.
  *

@@ -25,7 +25,7 @@ from torch import Tensor
 
 from light_vllm_amd import native
 from light_vllm_amd.errors import KVCacheError
-from light_vllm_amd.paged_cache import current_stream, dtype_code, hip_append
+from light_vllm_amd.paged_cache import current_stream, dtype_code, hip_append, hip_append_rotary
 from light_vllm_amd.plan import UNIT_TOKENS, StepPlan
 
 SUPPORTED_HEAD_SIZES = (32, 64, 80, 96, 128, 256)
@@ -169,7 +169,18 @@ class HipPagedAttention:
     def plan(self) -> StepPlan:
         return self._plan
 
-    def forward(self, layer_id: str, query: Tensor, key: Tensor, value: Tensor, *, scale: float) -> Tensor:
+    def forward(self, layer_id: str, query: Tensor, key: Tensor, value: Tensor, *, scale: float,
+                rotary: tuple[Tensor, Tensor] | None = None) -> Tensor:
+        """Append this layer's K/V, then attend (paged_attention.py:268-380).
+
+        ``rotary=(cosines, sines)`` ([tokens, head_size] rows in the cache
+        dtype, as Qwen2's ``_rotary_embeddings`` returns them) takes unrotated
+        ``query``/``key`` and applies ``apply_rotary``'s half rotation
+        (_qwen2_kernels.py:205-245) inside the append: one launch rotates the
+        queries and writes the rotated keys and the values to their slots.
+        The result equals ``apply_rotary`` followed by ``forward``.
+        """
+
         if layer_id in self._layer_ids:
             raise KVCacheError(f"paged attention layer {layer_id!r} ran more than once")
         self._layer_ids.add(layer_id)
@@ -193,7 +204,12 @@ class HipPagedAttention:
         layer = self._cache.layer(layer_id)
         stream = current_stream(query.device)
         lib = self._lib
-        if launch.prefill_args is not None:
+        if rotary is not None:
+            # The rotated queries go to a fresh buffer and the pool receives
+            # the whole step's rotated K and V, so attention reads the pool.
+            query = hip_append_rotary(self._cache, layer_id, query, key, value, rotary, self._plan.slots)
+            new_kv = (None, 0, 0, None, 0, 0)
+        elif launch.prefill_args is not None:
             # Prefill rows read the pool, so the whole step is appended first.
             hip_append(self._cache, layer_id, key, value, self._plan.slots)
             new_kv = (None, 0, 0, None, 0, 0)

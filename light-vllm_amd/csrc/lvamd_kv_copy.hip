@@ -9,6 +9,7 @@
 //   block copy has no reference counterpart (copy-on-write of a whole block).
 
 #include <initializer_list>
+#include <type_traits>
 
 #include "lvamd_common.h"
 
@@ -48,6 +49,144 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const AppendArgs a) {
     char* dst = (is_v ? a.value_pool : a.key_pool) + slot * row_bytes + (int64_t)h * a.head_bytes;
     reinterpret_cast<V*>(dst)[c] = reinterpret_cast<const V*>(src)[c];
   }
+}
+
+// ---------------------------------------------------------------------------
+// Rotary append: one workgroup per packed token.  The token's query heads and
+// key heads get the half rotation of light-vllm's apply_rotary
+//   out[d]     = x[d] * cos[d]     + (-x[d + D/2]) * sin[d]       (d < D/2)
+//   out[d+D/2] = x[d+D/2] * cos[d+D/2] + x[d] * sin[d+D/2]
+// with the rounding of its PyTorch path (_qwen2_kernels.py:214-224): each
+// product is rounded to the tensor dtype, then their sum is (an fp32 add,
+// rounded to the dtype).  Rotated queries go to query_out; rotated keys and
+// the values are written to their pool slots (negative slot: no pool write).
+// A thread takes one chunk pair (d, d + D/2) of one head, or one value chunk.
+// ---------------------------------------------------------------------------
+struct RotaryArgs {
+  const char* q;
+  char* q_out;
+  const char* key;
+  const char* value;
+  const char* cosines;
+  const char* sines;
+  int64_t q_tok_bytes, q_head_bytes, qo_tok_bytes, qo_head_bytes;
+  int64_t key_tok_bytes, key_head_bytes, value_tok_bytes, value_head_bytes;
+  int64_t cos_tok_bytes, sin_tok_bytes;
+  char* key_pool;
+  char* value_pool;
+  const int64_t* slots;
+  int32_t num_q_heads, num_kv_heads;
+  int32_t head_bytes;
+};
+
+template <int VB> struct RawChunk;
+template <> struct RawChunk<16> { using type = uint4; };
+template <> struct RawChunk<8> { using type = uint2; };
+template <> struct RawChunk<4> { using type = uint32_t; };
+template <> struct RawChunk<2> { using type = uint16_t; };
+
+// One product of the rotation, rounded as the PyTorch expression rounds it.
+// The rounded product passes through an empty asm statement: the device
+// code generator fuses a multiply feeding an add into an FMA whatever the
+// contraction flags say (also the mixed-precision fma_mix / packed forms it
+// builds from a 16-bit product extended into an fp32 add), which would skip
+// the product's rounding.  The asm makes the product an opaque register.
+template <typename T>
+__device__ __forceinline__ float rope_product(float x, float y) {
+  float p;
+  if constexpr (std::is_same_v<T, float>) {
+    p = x * y;
+  } else {
+    p = to_f32(from_f32<T>(x * y));  // exact in fp32, then rounded to T
+  }
+  __asm__("" : "+v"(p));
+  return p;
+}
+
+template <typename T, int VB>
+__device__ __forceinline__ void rotate_pair(const char* src, char* dst_lo, char* dst_hi, int64_t half_bytes,
+                                            const char* cs, const char* sn) {
+  using R = typename RawChunk<VB>::type;
+  constexpr int W = VB / (int)sizeof(T);
+  const R xl = *reinterpret_cast<const R*>(src);
+  const R xh = *reinterpret_cast<const R*>(src + half_bytes);
+  const R cl = *reinterpret_cast<const R*>(cs);
+  const R ch = *reinterpret_cast<const R*>(cs + half_bytes);
+  const R sl = *reinterpret_cast<const R*>(sn);
+  const R sh = *reinterpret_cast<const R*>(sn + half_bytes);
+  T x0[W], x1[W], c0[W], c1[W], s0[W], s1[W], o0[W], o1[W];
+  __builtin_memcpy(x0, &xl, VB);
+  __builtin_memcpy(x1, &xh, VB);
+  __builtin_memcpy(c0, &cl, VB);
+  __builtin_memcpy(c1, &ch, VB);
+  __builtin_memcpy(s0, &sl, VB);
+  __builtin_memcpy(s1, &sh, VB);
+#pragma unroll
+  for (int e = 0; e < W; ++e) {
+    const float lo = to_f32(x0[e]), hi = to_f32(x1[e]);
+    // x + round(-h*s) is x - round(h*s) exactly (rounding is sign-symmetric).
+    o0[e] = from_f32<T>(rope_product<T>(lo, to_f32(c0[e])) - rope_product<T>(hi, to_f32(s0[e])));
+    o1[e] = from_f32<T>(rope_product<T>(hi, to_f32(c1[e])) + rope_product<T>(lo, to_f32(s1[e])));
+  }
+  R rl, rh;
+  __builtin_memcpy(&rl, o0, VB);
+  __builtin_memcpy(&rh, o1, VB);
+  *reinterpret_cast<R*>(dst_lo) = rl;
+  *reinterpret_cast<R*>(dst_hi) = rh;
+}
+
+template <typename T, int VB>
+__global__ __launch_bounds__(256) void kv_append_rotary_kernel(const RotaryArgs a) {
+  const int64_t t = blockIdx.x;
+  const int64_t slot = a.slots[t];
+  const int half_bytes = a.head_bytes / 2;
+  const int pairs = half_bytes / VB;  // chunk pairs per head row
+  const int vchunks = a.head_bytes / VB;
+  const int q_items = a.num_q_heads * pairs;
+  const int k_items = a.num_kv_heads * pairs;
+  const int items = q_items + (slot >= 0 ? k_items + a.num_kv_heads * vchunks : 0);
+  const int64_t row_bytes = (int64_t)a.num_kv_heads * a.head_bytes;
+  const char* cs = a.cosines + t * a.cos_tok_bytes;
+  const char* sn = a.sines + t * a.sin_tok_bytes;
+  for (int i = threadIdx.x; i < items; i += blockDim.x) {
+    if (i < q_items) {
+      const int h = i / pairs;
+      const int off = (i - h * pairs) * VB;
+      const char* src = a.q + t * a.q_tok_bytes + h * a.q_head_bytes + off;
+      char* dst = a.q_out + t * a.qo_tok_bytes + h * a.qo_head_bytes + off;
+      rotate_pair<T, VB>(src, dst, dst + half_bytes, half_bytes, cs + off, sn + off);
+    } else if (i < q_items + k_items) {
+      const int j = i - q_items;
+      const int h = j / pairs;
+      const int off = (j - h * pairs) * VB;
+      const char* src = a.key + t * a.key_tok_bytes + h * a.key_head_bytes + off;
+      char* dst = a.key_pool + slot * row_bytes + (int64_t)h * a.head_bytes + off;
+      rotate_pair<T, VB>(src, dst, dst + half_bytes, half_bytes, cs + off, sn + off);
+    } else {
+      const int j = i - q_items - k_items;
+      const int h = j / vchunks;
+      const int off = (j - h * vchunks) * VB;
+      using R = typename RawChunk<VB>::type;
+      *reinterpret_cast<R*>(a.value_pool + slot * row_bytes + (int64_t)h * a.head_bytes + off) =
+          *reinterpret_cast<const R*>(a.value + t * a.value_tok_bytes + h * a.value_head_bytes + off);
+    }
+  }
+}
+
+template <typename T>
+static int launch_rotary(int width, dim3 grid, dim3 block, hipStream_t s, const RotaryArgs& a) {
+  switch (width) {
+    case 16: hipLaunchKernelGGL((kv_append_rotary_kernel<T, 16>), grid, block, 0, s, a); break;
+    case 8: hipLaunchKernelGGL((kv_append_rotary_kernel<T, 8>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((kv_append_rotary_kernel<T, 4>), grid, block, 0, s, a); break;
+    default:
+      if constexpr (sizeof(T) == 2) {
+        hipLaunchKernelGGL((kv_append_rotary_kernel<T, 2>), grid, block, 0, s, a);
+        break;
+      }
+      return LVAMD_ERR_INVALID_ARGUMENT;
+  }
+  return launch_status();
 }
 
 // Largest access width (16/8/4/2 bytes) dividing every address and stride.
@@ -218,6 +357,65 @@ int lvamd_kv_append(const void* key, int64_t key_token_stride, int64_t key_head_
   LVAMD_LAUNCH_BY_WIDTH(kv_append_kernel, width, dim3((unsigned)num_tokens), dim3(threads),
                         static_cast<hipStream_t>(stream), a);
   return launch_status();
+}
+
+int lvamd_kv_append_rotary(const void* query, int64_t query_token_stride, int64_t query_head_stride,
+                           void* query_out, int64_t query_out_token_stride, int64_t query_out_head_stride,
+                           const void* key, int64_t key_token_stride, int64_t key_head_stride,
+                           const void* value, int64_t value_token_stride, int64_t value_head_stride,
+                           const void* cosines, int64_t cosines_token_stride,
+                           const void* sines, int64_t sines_token_stride,
+                           void* key_pool, void* value_pool, const int64_t* slots, int64_t num_tokens,
+                           int32_t num_query_heads, int32_t num_kv_heads, int32_t head_size, int32_t dtype,
+                           lvamd_stream_t stream) {
+  const int es = dtype_size(dtype);
+  if (es == 0) return LVAMD_ERR_UNSUPPORTED;
+  if (num_tokens < 0 || num_query_heads <= 0 || num_kv_heads <= 0 || head_size <= 0 || head_size % 2 != 0)
+    return LVAMD_ERR_INVALID_ARGUMENT;
+  if (num_tokens == 0) return LVAMD_OK;
+  if (!query || !query_out || !key || !value || !cosines || !sines || !key_pool || !value_pool || !slots)
+    return LVAMD_ERR_INVALID_ARGUMENT;
+  if (num_tokens > 0x7fffffffLL) return LVAMD_ERR_INVALID_ARGUMENT;
+  RotaryArgs a;
+  a.q = static_cast<const char*>(query);
+  a.q_out = static_cast<char*>(query_out);
+  a.key = static_cast<const char*>(key);
+  a.value = static_cast<const char*>(value);
+  a.cosines = static_cast<const char*>(cosines);
+  a.sines = static_cast<const char*>(sines);
+  a.q_tok_bytes = query_token_stride * es;
+  a.q_head_bytes = query_head_stride * es;
+  a.qo_tok_bytes = query_out_token_stride * es;
+  a.qo_head_bytes = query_out_head_stride * es;
+  a.key_tok_bytes = key_token_stride * es;
+  a.key_head_bytes = key_head_stride * es;
+  a.value_tok_bytes = value_token_stride * es;
+  a.value_head_bytes = value_head_stride * es;
+  a.cos_tok_bytes = cosines_token_stride * es;
+  a.sin_tok_bytes = sines_token_stride * es;
+  a.key_pool = static_cast<char*>(key_pool);
+  a.value_pool = static_cast<char*>(value_pool);
+  a.slots = slots;
+  a.num_q_heads = num_query_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.head_bytes = head_size * es;
+  const int width = common_vector_bytes(
+      {(uint64_t)(uintptr_t)query, (uint64_t)(uintptr_t)query_out, (uint64_t)(uintptr_t)key,
+       (uint64_t)(uintptr_t)value, (uint64_t)(uintptr_t)cosines, (uint64_t)(uintptr_t)sines,
+       (uint64_t)(uintptr_t)key_pool, (uint64_t)(uintptr_t)value_pool, (uint64_t)a.q_tok_bytes,
+       (uint64_t)a.q_head_bytes, (uint64_t)a.qo_tok_bytes, (uint64_t)a.qo_head_bytes, (uint64_t)a.key_tok_bytes,
+       (uint64_t)a.key_head_bytes, (uint64_t)a.value_tok_bytes, (uint64_t)a.value_head_bytes,
+       (uint64_t)a.cos_tok_bytes, (uint64_t)a.sin_tok_bytes, (uint64_t)(a.head_bytes / 2)});
+  if (width < es) return LVAMD_ERR_INVALID_ARGUMENT;  // misaligned element rows
+  const int items = (num_query_heads + num_kv_heads) * (a.head_bytes / 2 / width) + num_kv_heads * (a.head_bytes / width);
+  const int threads = items >= 256 ? 256 : ((items + 63) / 64) * 64;
+  const dim3 grid((unsigned)num_tokens);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case LVAMD_BF16: return launch_rotary<__bf16>(width, grid, dim3(threads), s, a);
+    case LVAMD_F16: return launch_rotary<_Float16>(width, grid, dim3(threads), s, a);
+    default: return launch_rotary<float>(width, grid, dim3(threads), s, a);
+  }
 }
 
 int64_t lvamd_kv_compact_inline_pairs(void) { return kCompactInline; }

@@ -39,6 +39,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i32, _i32, _i32, _p],
     ),
+    "lvamd_kv_append_rotary": (
+        ctypes.c_int,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _p, _i64,
+         _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _p],
+    ),
     "lvamd_paged_decode": (
         ctypes.c_int,
         [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i64,

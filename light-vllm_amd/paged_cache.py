@@ -151,6 +151,51 @@ def hip_append(cache, layer_id: str, key: Tensor, value: Tensor, slots: Tensor) 
     native.check(status, "lvamd_kv_append")
 
 
+def hip_append_rotary(cache, layer_id: str, query: Tensor, key: Tensor, value: Tensor,
+                      rotary: tuple[Tensor, Tensor], slots: Tensor) -> Tensor:
+    """Rotate ``query`` and ``key`` (Qwen2's half rotation, rounded as
+    apply_rotary's PyTorch path rounds it) and append: ``flatK[slots[t]] =
+    rotate(key[t])``, ``flatV[slots[t]] = value[t]``; returns the rotated
+    queries as a new tensor.  One kernel on the current stream.
+
+    apply_rotary: src/light_vllm/modeling/models/_qwen2_kernels.py:205-245;
+    append: src/light_vllm/runtime/execution/paged_cache.py:209-248.
+    """
+
+    spec = cache.layer_spec(layer_id)
+    cosines, sines = rotary
+    tokens = query.shape[0]
+    for name, t in (("cosines", cosines), ("sines", sines)):
+        if not isinstance(t, Tensor) or t.dim() != 2 or tuple(t.shape) != (tokens, spec.head_size):
+            raise KVCacheError(f"rotary {name} must have shape [{tokens}, {spec.head_size}]")
+        if t.dtype != query.dtype or t.device != query.device:
+            raise KVCacheError(f"rotary {name} dtype and device must match the query")
+    if cosines.stride(1) != 1:
+        cosines = cosines.contiguous()
+    if sines.stride(1) != 1:
+        sines = sines.contiguous()
+    if query.stride(2) != 1:
+        query = query.contiguous()
+    if key.stride(2) != 1 or value.stride(2) != 1:
+        key = key.contiguous()
+        value = value.contiguous()
+    layer = cache.layer(layer_id)
+    rotated = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    lib = native.load()
+    status = lib.lvamd_kv_append_rotary(
+        query.data_ptr(), query.stride(0), query.stride(1),
+        rotated.data_ptr(), rotated.stride(0), rotated.stride(1),
+        key.data_ptr(), key.stride(0), key.stride(1),
+        value.data_ptr(), value.stride(0), value.stride(1),
+        cosines.data_ptr(), cosines.stride(0), sines.data_ptr(), sines.stride(0),
+        layer.keys.data_ptr(), layer.values.data_ptr(), slots.data_ptr(), slots.numel(),
+        spec.num_query_heads, spec.num_kv_heads, spec.head_size, dtype_code(query.dtype),
+        current_stream(query.device),
+    )
+    native.check(status, "lvamd_kv_append_rotary")
+    return rotated
+
+
 def compact_slots(
     config,
     block_ids: tuple[int, ...],

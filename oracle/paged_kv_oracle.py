@@ -21,12 +21,17 @@ path (paths relative to light-vllm's source tree):
                                 softmax, here in fp64 over the gathered keys)
 * ``block_copy``                no reference function (copy-on-write of whole
                                 blocks); its definition is the closed form below.
+* ``rotary_half``               src/light_vllm/modeling/models/_qwen2_kernels.py:214-224
+                                (apply_rotary's PyTorch path, with its rounding)
 
 How each function is pinned (tests/test_oracle.py):
 * slot mapping, validation, visibility, request indices, layouts and compact:
   the reference tests' known answers (tests/golden/reference_known_answers.json);
 * append, compact, block copy: closed-form invariants (every untouched byte
   unchanged, moved rows byte-equal) on random pools;
+* rotary_half: torch's own CPU arithmetic in the tensor dtype running the
+  reference expression, closed forms (cos 1 / sin 0 is the identity, cos 0 /
+  sin 1 the pure half swap), norm preservation, and planted mistakes;
 * paged_attention: the fp64 dense softmax on random inputs (GQA, tree masks,
   multi-block, shared prefix, lookahead), plus closed forms (one visible key
   gives that key's value; identical keys give the mean of the visible values),
@@ -132,6 +137,49 @@ def validate_block_tables(block_tables, computed, reserved, readonly, *, num_blo
             if prev is not None and (prev[0] != idx or not prev[1] or not is_ro):
                 raise OracleKVCacheError("block tables alias a physical block across requests")
             owners[b] = (idx, is_ro)
+
+
+# --------------------------------------------------------------------------- rotary
+def _bits_to_f32(bits: np.ndarray, dtype: str) -> np.ndarray:
+    """Element bits (uint16 for bf16/f16, float32 for f32) as float32 values."""
+
+    if dtype == "bf16":
+        return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+    if dtype == "f16":
+        return np.asarray(bits, dtype=np.uint16).view(np.float16).astype(np.float32)
+    return np.asarray(bits, dtype=np.float32)
+
+
+def _round_to(values: np.ndarray, dtype: str) -> np.ndarray:
+    """float32 values rounded to nearest-even in ``dtype``, returned as element bits."""
+
+    values = np.asarray(values, dtype=np.float32)
+    if dtype == "bf16":
+        u = values.view(np.uint32).astype(np.uint64)
+        rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        return np.where(np.isnan(values), np.uint16(0x7FC0), rounded)
+    if dtype == "f16":
+        return values.astype(np.float16).view(np.uint16)
+    return values
+
+
+def rotary_half(x: np.ndarray, cosines: np.ndarray, sines: np.ndarray, dtype: str) -> np.ndarray:
+    """Qwen2's half rotation of x [T, H, D] by per-token cos/sin rows [T, D]
+    (_qwen2_kernels.py:214-224): ``x * cos + cat(-x[D/2:], x[:D/2]) * sin``.
+
+    Element bits in and out.  As in PyTorch's evaluation of that expression in
+    the tensor dtype, each product is rounded to the dtype, then the float32
+    sum of the two is rounded to the dtype.
+    """
+
+    xf = _bits_to_f32(x, dtype)
+    c = _bits_to_f32(cosines, dtype)[:, None, :]
+    s = _bits_to_f32(sines, dtype)[:, None, :]
+    half = xf.shape[-1] // 2
+    rotated = np.concatenate((-xf[..., half:], xf[..., :half]), axis=-1)
+    first = _bits_to_f32(_round_to(xf * c, dtype), dtype)
+    second = _bits_to_f32(_round_to(rotated * s, dtype), dtype)
+    return _round_to(first + second, dtype)
 
 
 # --------------------------------------------------------------------------- KV movement

@@ -314,3 +314,103 @@ def test_planted_oracle_mistakes_fail_the_dense_check(name) -> None:
     bad = mutant(query, kpool, vpool, tables, case["computed"], case["layouts"], scale=0.25)
     assert np.abs(good - dense).max() < 2e-6
     assert np.abs(bad - dense).max() > 1e-2
+
+
+# --------------------------------------------------------------------------- rotary
+TORCH_DTYPES = {"bf16": "bfloat16", "f16": "float16", "f32": "float32"}
+
+
+def _rotary_inputs(rng, dtype, tokens=5, heads=3, d=16, theta=10000.0):
+    import torch
+
+    tdt = getattr(torch, TORCH_DTYPES[dtype])
+    x = torch.randn(tokens, heads, d, generator=torch.Generator().manual_seed(int(rng.integers(1 << 30)))).to(tdt)
+    pos = torch.as_tensor(rng.integers(0, 40000, size=tokens), dtype=torch.float32)
+    freqs = 1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    angles = torch.outer(pos, freqs)
+    emb = torch.cat((angles, angles), dim=-1)
+    return x, emb.cos().to(tdt), emb.sin().to(tdt)
+
+
+def _as_bits(t):
+    import torch
+
+    if t.dtype == torch.float32:
+        return t.numpy()
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("seed", range(4))
+def test_rotary_matches_torch_dtype_arithmetic(dtype, seed) -> None:
+    """The oracle's rounding emulation equals torch's own CPU arithmetic in the
+    tensor dtype on the reference's expression (what the reference runs
+    without Triton), bit for bit."""
+
+    import torch
+
+    rng = np.random.default_rng(seed)
+    x, cos, sin = _rotary_inputs(rng, dtype, d=[16, 64, 128, 80][seed])
+    if seed == 3:
+        x = x * 300.0  # large magnitudes: the float32 sum can round twice
+    first, second = x.chunk(2, dim=-1)
+    expected = x * cos.unsqueeze(1) + torch.cat((-second, first), dim=-1) * sin.unsqueeze(1)
+    got = O.rotary_half(_as_bits(x), _as_bits(cos), _as_bits(sin), dtype)
+    np.testing.assert_array_equal(got, _as_bits(expected))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+def test_rotary_closed_forms(dtype) -> None:
+    """cos 1 / sin 0 is the identity; cos 0 / sin 1 is the half swap with the
+    first half negated; cos -1 / sin 0 negates."""
+
+    import torch
+
+    rng = np.random.default_rng(7)
+    x, cos, sin = _rotary_inputs(rng, dtype)
+    xb = _as_bits(x)
+    one, zero = torch.ones_like(cos), torch.zeros_like(cos)
+    np.testing.assert_array_equal(O.rotary_half(xb, _as_bits(one), _as_bits(zero), dtype), xb)
+    swapped = torch.cat((-x[..., 8:], x[..., :8]), dim=-1)
+    np.testing.assert_array_equal(O.rotary_half(xb, _as_bits(zero), _as_bits(one), dtype), _as_bits(swapped))
+    np.testing.assert_array_equal(O.rotary_half(xb, _as_bits(-one), _as_bits(zero), dtype), _as_bits(-x))
+
+
+def test_rotary_preserves_pair_norms() -> None:
+    """Each (d, d + D/2) pair is rotated by one angle: its norm is kept (fp32)."""
+
+    rng = np.random.default_rng(9)
+    x, cos, sin = _rotary_inputs(rng, "f32", tokens=7, heads=2, d=32)
+    out = O.rotary_half(_as_bits(x), _as_bits(cos), _as_bits(sin), "f32").astype(np.float64)
+    xin = x.numpy().astype(np.float64)
+    norm_in = xin[..., :16] ** 2 + xin[..., 16:] ** 2
+    norm_out = out[..., :16] ** 2 + out[..., 16:] ** 2
+    np.testing.assert_allclose(norm_out, norm_in, rtol=2e-6, atol=1e-9)
+
+
+ROTARY_MUTATIONS = {
+    "sign": ("(-xf[..., half:], xf[..., :half])", "(xf[..., half:], xf[..., :half])"),
+    "pairing": ("np.concatenate((-xf[..., half:], xf[..., :half]), axis=-1)",
+                "np.stack((-xf[..., 1::2], xf[..., ::2]), axis=-1).reshape(xf.shape)"),
+    "single_rounding": ("first + second", "xf * c + rotated * s"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(ROTARY_MUTATIONS))
+def test_planted_rotary_mistakes_fail(name) -> None:
+    import torch
+
+    old, new = ROTARY_MUTATIONS[name]
+    source = textwrap.dedent(inspect.getsource(O.rotary_half))
+    assert old in source, f"mutation anchor for {name} not found"
+    namespace = dict(vars(O))
+    exec(compile(source.replace(old, new), "<mutant>", "exec"), namespace)
+    mutant = namespace["rotary_half"]
+    rng = np.random.default_rng(11)
+    x, cos, sin = _rotary_inputs(rng, "bf16", tokens=16, heads=4, d=64)
+    first, second = x.chunk(2, dim=-1)
+    expected = _as_bits(x * cos.unsqueeze(1) + torch.cat((-second, first), dim=-1) * sin.unsqueeze(1))
+    good = O.rotary_half(_as_bits(x), _as_bits(cos), _as_bits(sin), "bf16")
+    bad = mutant(_as_bits(x), _as_bits(cos), _as_bits(sin), "bf16")
+    np.testing.assert_array_equal(good, expected)
+    assert (bad != expected).any()
