@@ -657,8 +657,15 @@ def run_c5(args, device) -> int:
     cow_ms = _time_launches(lambda i: cow(), args.steps, args.warmup, device)
     attend_ms = _time_launches(lambda i: attend(), max(10, args.steps // 4), 2, device)
     compact_ms = _time_launches(lambda i: compact(), args.steps, args.warmup, device)
-    rotary_ms = _time_launches(lambda i: w.attend_rotary(), max(10, args.steps // 4), 2, device)
-    torch_rotary_ms = _time_launches(lambda i: w.attend_torch_rotary(), max(10, args.steps // 4), 2, device)
+    rotary = None
+    if not args.no_rotary:
+        rotary = {"fused_attention_us": _time_launches(lambda i: w.attend_rotary(), max(10, args.steps // 4), 2,
+                                                       device) * 1e3,
+                  "unfused_attention_us": _time_launches(lambda i: w.attend_torch_rotary(), max(10, args.steps // 4),
+                                                         2, device) * 1e3}
+        rotary = {k: round(v, 2) for k, v in rotary.items()}
+        rotary["note"] = ("28 layers with RoPE: lvamd_kv_append_rotary + attention, against apply_rotary's "
+                          "PyTorch path + attention")
     row = cfg.hkv * cfg.d * 2
     unique_kv = (cfg.prefix + sum(s + q_len for s in suffix)) * 2 * row
     cow_bytes = 2 * cfg.batch * cfg.layers * 2 * cfg.bs * row
@@ -673,10 +680,7 @@ def run_c5(args, device) -> int:
                "attention_unique_gbps": round(cfg.layers * unique_kv / (attend_ms * 1e-3) / 1e9, 1),
                "cow_copy_us": round(cow_ms * 1e3, 2), "cow_copy_gbps": round(cow_bytes / (cow_ms * 1e-3) / 1e9, 1),
                "compact_us": round(compact_ms * 1e3, 2), "compact_tokens": moved,
-               "rotary": {"fused_attention_us": round(rotary_ms * 1e3, 2),
-                          "unfused_attention_us": round(torch_rotary_ms * 1e3, 2),
-                          "note": "28 layers with RoPE: lvamd_kv_append_rotary + attention, against "
-                                  "apply_rotary's PyTorch path + attention"},
+               "rotary": rotary,
                "host_submit_ms": round(host_ms, 5)})
     if not args.no_cpu_baseline:
         from oracle import paged_kv_oracle as O  # checker/baseline only
@@ -701,6 +705,8 @@ def main() -> int:
     parser.add_argument("--sets", type=int, default=4, help="rotating pool sets (1 GiB each)")
     parser.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline work")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-rotary", action="store_true",
+                        help="skip the RoPE-fused step timing (keeps a kernel trace to the attention step)")
     parser.add_argument("--mode", choices=("full", "decode", "copy"), default="full",
                         help="decode: only the decode kernel (counter runs); copy: a plain 1 GiB device "
                              "copy of known size (counter calibration and the practical HBM ceiling)")
@@ -833,12 +839,13 @@ def main() -> int:
         qr, kr = torch_rotary(q, k, cos, sin)
         return backend.create(caches[i % len(caches)], metadata).forward("layer0", qr, kr, v, scale=scale)
 
-    record["rotary"] = {
-        "fused_ms_per_step": round(time_steps(fused, args.steps, args.warmup), 5),
-        "unfused_ms_per_step": round(time_steps(unfused, args.steps, args.warmup), 5),
-        "note": "step with RoPE: lvamd_kv_append_rotary + attention, against apply_rotary's PyTorch path + "
-                "the fused-append attention step",
-    }
+    if not args.no_rotary:
+        record["rotary"] = {
+            "fused_ms_per_step": round(time_steps(fused, args.steps, args.warmup), 5),
+            "unfused_ms_per_step": round(time_steps(unfused, args.steps, args.warmup), 5),
+            "note": "step with RoPE: lvamd_kv_append_rotary + attention, against apply_rotary's PyTorch path + "
+                    "the fused-append attention step",
+        }
     ceiling = read_ceiling(device)
     record["hbm_read_ceiling"] = {
         **ceiling, "decode_kernel_frac": round(achieved / ceiling["GBps"], 4),

@@ -148,6 +148,9 @@ class _LayerLaunch:
 class HipPagedAttention:
     """Per-step context: writes each layer's K/V, then runs paged attention."""
 
+    # forward accepts rotary=(cosines, sines): RoPE is applied inside the append.
+    supports_rotary = True
+
     def __init__(self, cache, metadata, workspace: _Workspace, plan: StepPlan, use_prefill: bool = True,
                  col_tiles: int | None = None, split_prefill: bool = True) -> None:
         self._cache = cache
