@@ -189,7 +189,9 @@ int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
  * column c = query (c / group), head (c % group).  K/V tiles (64 tokens up to
  * head size 128, else 32) are gathered through the block table into LDS and
  * shared by the workgroup's waves; QK^T and PV on MFMA 16x16x32, fp32 online
- * softmax.  Units with a partial slot write fp32 partials to part_acc
+ * softmax.  waves (4 or 8) picks the workgroup shape for the same unit: four
+ * waves of two 16-column tiles or eight waves of one (8 only where
+ * lvamd_paged_prefill_waves_built says so).  Units with a partial slot write fp32 partials to part_acc
  * [slots][num_kv_heads][unit columns][head_size] and part_ml
  * [slots][num_kv_heads][unit columns][2]; lvamd_paged_attention_merge with
  * col_tiles = unit columns / 16 combines them.
@@ -203,7 +205,7 @@ int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_st
                         const int32_t* req_meta, const int32_t* tables, const uint32_t* vis,
                         const int32_t* units, int32_t num_units,
                         float* part_acc, float* part_ml, int64_t num_partial_slots,
-                        int32_t num_kv_heads, int32_t group, int32_t head_size,
+                        int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t waves,
                         int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream);
 
 /* Columns per prefill unit for this dtype and head size (the planner's unit
@@ -213,9 +215,14 @@ int lvamd_paged_prefill_unit_columns(int32_t dtype, int32_t head_size);
 /* Keys per prefill tile (unit key ranges start on multiples of it). */
 int lvamd_paged_prefill_key_tokens(int32_t dtype, int32_t head_size);
 
-/* Prefill workgroups the current device holds at once for this dtype and head
- * size: the planner splits units' key ranges to fill them.  Needs a GPU. */
-int lvamd_paged_prefill_resident_units(int32_t dtype, int32_t head_size);
+/* Prefill workgroups of the given shape (waves 4 or 8) the current device
+ * holds at once for this dtype and head size: the planner splits units' key
+ * ranges to fill them.  Needs a GPU. */
+int lvamd_paged_prefill_resident_units(int32_t dtype, int32_t head_size, int32_t waves);
+
+/* 1 when the prefill kernel is built with that many waves per workgroup for
+ * this dtype and head size (4 always; 8 up to head size 128), else 0. */
+int lvamd_paged_prefill_waves_built(int32_t dtype, int32_t head_size, int32_t waves);
 
 /*
  * Tree-KV compact across all layers: for every layer l and pair i,

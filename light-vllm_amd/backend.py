@@ -136,7 +136,7 @@ class _LayerLaunch:
                 plan.req_meta.data_ptr(), plan.tables.data_ptr(), plan.vis.data_ptr(),
                 work.prefill_units.data_ptr(), work.num_prefill_units,
                 pre_acc, pre_ml, work.num_prefill_partial_slots,
-                spec.num_kv_heads, group, spec.head_size, block_size,
+                spec.num_kv_heads, group, spec.head_size, work.prefill_waves, block_size,
             )
         if work.num_prefill_jobs:
             self.prefill_merge_args = (pre_acc, pre_ml) + (
@@ -152,12 +152,13 @@ class HipPagedAttention:
     supports_rotary = True
 
     def __init__(self, cache, metadata, workspace: _Workspace, plan: StepPlan, use_prefill: bool = True,
-                 col_tiles: int | None = None, split_prefill: bool = True) -> None:
+                 col_tiles: int | None = None, split_prefill: bool = True, prefill_waves: int | None = None) -> None:
         self._cache = cache
         self._config = cache.config
         self._use_prefill = use_prefill
         self._col_tiles = col_tiles
         self._split_prefill = split_prefill
+        self._prefill_waves = prefill_waves
         self._metadata = metadata
         self._layer_ids: set[str] = set()
         self._workspace = workspace
@@ -288,7 +289,7 @@ class HipPagedAttention:
 
         code = dtype_code(dtype)
         key = (spec.num_query_heads, spec.num_kv_heads, spec.head_size, code, self._use_prefill, self._col_tiles,
-               self._split_prefill)
+               self._split_prefill, self._prefill_waves)
         plan = self._plan
         found = plan.launches.get(key)
         if found is not None and found.workspace_ptr is not None and found.workspace_ptr != self._workspace.ptr():
@@ -317,11 +318,20 @@ class HipPagedAttention:
         resident = native.resident_decode_waves(code, spec.head_size, ctw)
         unit = native.decode_tile_tokens(code, spec.head_size, ctw)
         key_tokens = prefill_resident = 0
+        waves = 4
         if columns:
             key_tokens = native.prefill_key_tokens(code, spec.head_size)
             if self._split_prefill:
-                prefill_resident = native.prefill_resident_units(code, spec.head_size)
-        return self._plan.work(group, spec.num_kv_heads, resident, columns, unit, ctw, key_tokens, prefill_resident)
+                prefill_resident = native.prefill_resident_units(code, spec.head_size, 4)
+            wide = native.prefill_waves_built(code, spec.head_size, 8)
+            if self._prefill_waves is not None:
+                waves = 8 if self._prefill_waves == 8 and wide else 4
+            else:
+                waves = self._plan.prefill_waves(group, spec.num_kv_heads, columns, key_tokens, prefill_resident, wide)
+            if waves != 4 and self._split_prefill:
+                prefill_resident = native.prefill_resident_units(code, spec.head_size, waves)
+        return self._plan.work(group, spec.num_kv_heads, resident, columns, unit, ctw, key_tokens, prefill_resident,
+                               waves)
 
 
 class _DecodeLaunch:
@@ -367,7 +377,7 @@ class HipPagedAttentionBackend:
 
     def __init__(
         self, *, use_prefill_kernel: bool = True, partition_tokens: int | None = None,
-        decode_col_tiles: int | None = None, split_prefill: bool = True,
+        decode_col_tiles: int | None = None, split_prefill: bool = True, prefill_waves: int | None = None,
     ) -> None:
         """``use_prefill_kernel=False`` sends every request through the decode
         kernel; ``partition_tokens`` caps the tokens one decode wave handles (a
@@ -375,7 +385,9 @@ class HipPagedAttentionBackend:
         resident wave); ``decode_col_tiles`` (1 or 4) fixes the decode kernel's
         column tiles per wave instead of the planner's per-step choice;
         ``split_prefill=False`` keeps every prefill unit's keys in one
-        workgroup (no split-K partials)."""
+        workgroup (no split-K partials); ``prefill_waves`` (4 or 8) fixes the
+        prefill workgroup shape instead of the planner's per-step choice (8
+        falls back to 4 where it is not built)."""
 
         native.load()
         if partition_tokens is not None and (partition_tokens <= 0 or partition_tokens % UNIT_TOKENS):
@@ -386,7 +398,10 @@ class HipPagedAttentionBackend:
         self._use_prefill = use_prefill_kernel
         self._partition_tokens = partition_tokens
         self._col_tiles = decode_col_tiles
+        if prefill_waves not in (None, 4, 8):
+            raise ValueError("prefill_waves must be 4 or 8")
         self._split_prefill = split_prefill
+        self._prefill_waves = prefill_waves
         self._last: tuple[object, object, StepPlan] | None = None
 
     def create(self, cache, metadata) -> HipPagedAttention:
@@ -402,4 +417,4 @@ class HipPagedAttentionBackend:
                             partition_tokens=self._partition_tokens)
             self._last = (key, metadata, plan)
         return HipPagedAttention(cache, metadata, self._workspace, plan, self._use_prefill, self._col_tiles,
-                                 self._split_prefill)
+                                 self._split_prefill, self._prefill_waves)

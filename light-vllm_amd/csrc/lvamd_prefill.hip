@@ -8,11 +8,10 @@
 // q head h reads kv head h / group; fp32 scores and softmax.
 //
 // Mapping onto CDNA4:
-//   * A work unit is up to 16 * prefill_col_tiles_per_wave(D) * 4 MFMA columns
-//     of one request, a column being a (query, head-in-group) pair of one kv
-//     head, so the GQA group shares every K/V byte.  One 256-thread workgroup
-//     per (unit, kv head); each of its four waves owns
-//     prefill_col_tiles_per_wave(D) column tiles of 16.
+//   * A work unit is up to 128 MFMA columns of one request, a column being a
+//     (query, head-in-group) pair of one kv head, so the GQA group shares
+//     every K/V byte.  One workgroup per (unit, kv head): four waves of two
+//     16-column tiles, or eight waves of one (the host picks per step).
 //   * Keys go in 64-token tiles (32 for D = 256): the workgroup gathers a tile's K and V rows
 //     through the block table (16-byte coalesced loads) into registers, then
 //     into a double-buffered LDS tile, one barrier per tile.  While tile t
@@ -41,7 +40,6 @@ namespace lvamd {
 namespace {
 
 constexpr float kRescaleSlack = 8.0f;  // log2 units: probabilities stay below 2^8
-constexpr int kThreads = 256;
 
 }  // namespace
 
@@ -51,28 +49,35 @@ constexpr int kThreads = 256;
 #ifndef LVAMD_PREFILL_PAD
 #define LVAMD_PREFILL_PAD 32
 #endif
-#ifndef LVAMD_PREFILL_CT
-#define LVAMD_PREFILL_CT 2
-#endif
+
 #ifndef LVAMD_PREFILL_KT
 #define LVAMD_PREFILL_KT 64
 #endif
-// Column tiles of 16 per wave and keys per LDS tile.  Two column tiles keep
-// the wave within 256 registers, so two workgroups share a CU; measured on C3
-// (bf16, D = 128, three-stage pipeline): 190 us at two tiles / 64 keys,
-// 213 us at two tiles / 32 keys, 468 us at four tiles (one wave per SIMD).
-constexpr int prefill_col_tiles_per_wave(int d) { return d <= 128 ? LVAMD_PREFILL_CT : 2; }
+// Two shapes of the same 128-column unit, chosen per step by the planner:
+// * W = 4 waves of two 16-column tiles: each K/V LDS read feeds two MFMAs;
+//   256 registers per wave, two waves per SIMD (two workgroups per CU).
+// * W = 8 waves of one column tile: half the registers (128), four waves per
+//   SIMD to hide the softmax's dependency chain, twice the LDS reads per MFMA.
+// Measured (bf16, D = 128): W = 8 is faster on split-K and short units (tree
+// verification 8K context 126 vs 142 us, 512-query chunks without history
+// 42 vs 47 us, 512-query chunks at 16K history (split) 419 vs 460 us); W = 4
+// on long unsplit units (C3: 171 vs 183 us).  Keys per LDS tile: 64 (32 for
+// D = 256, which is built for W = 4 only).
+constexpr int prefill_col_tiles_per_wave(int d, int w) { return w == 8 ? 1 : 2; }
+constexpr bool prefill_built(int d, int w) { return w == 4 || (w == 8 && d <= 128); }
 constexpr int prefill_key_tile(int d) { return d <= 128 ? LVAMD_PREFILL_KT : 32; }
-constexpr int prefill_unit_columns(int d) { return 16 * prefill_col_tiles_per_wave(d) * (kThreads / 64); }
+constexpr int prefill_unit_columns(int d) { return 16 * prefill_col_tiles_per_wave(d, 4) * 4; }
+static_assert(16 * 1 * 8 == 16 * 2 * 4, "both shapes cover the same unit columns");
 
-template <typename T, int D>
+template <typename T, int D, int W>
 struct PrefillShape {
   static constexpr int KT = prefill_key_tile(D);               // keys per tile
   static constexpr int KS = KT / 16;                           // 16-key groups per tile
   static constexpr int CPR = D * (int)sizeof(T) / 16;          // 16-byte chunks per row
   static constexpr int RS = D * (int)sizeof(T) + LVAMD_PREFILL_PAD;  // LDS row stride in bytes (bank spread)
-  static constexpr int LPT = (KT * CPR + kThreads - 1) / kThreads;  // chunks per thread per tile
-  static constexpr int CT = prefill_col_tiles_per_wave(D);
+  static constexpr int THREADS = 64 * W;
+  static constexpr int LPT = (KT * CPR + THREADS - 1) / THREADS;  // chunks per thread per tile
+  static constexpr int CT = prefill_col_tiles_per_wave(D, W);
   static constexpr int NCH = (D + 31) / 32;                    // 16x16x32 k-steps of QK^T
   static constexpr int NT = D / 16;                            // 16-row tiles of O^T
   static constexpr int TILE_BYTES = KT * RS;
@@ -100,16 +105,17 @@ struct PrefillArgs {
   float scale_log2;
 };
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void paged_prefill_kernel(const PrefillArgs a) {
-  using P = PrefillShape<T, D>;
+template <typename T, int D, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ? 4 : (D <= 128 ? 2 : 1)))) void paged_prefill_kernel(const PrefillArgs a) {
+  using P = PrefillShape<T, D, W>;
   constexpr int CPR = P::CPR, RS = P::RS, LPT = P::LPT, CT = P::CT, NCH = P::NCH, NT = P::NT;
   constexpr int KT = P::KT, KS = P::KS;
   using V8 = typename std::conditional<std::is_same<T, __bf16>::value, bf16x8, f16x8>::type;
   __shared__ __attribute__((aligned(16))) char klds[2][P::TILE_BYTES];
   __shared__ __attribute__((aligned(16))) char vlds[2][P::TILE_BYTES];
 
-  const int tid = threadIdx.x & (kThreads - 1);  // (the mask tells LLVM tid < 256)
+  constexpr int kThreads = P::THREADS;
+  const int tid = threadIdx.x & (kThreads - 1);  // (the mask tells LLVM the thread range)
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int l16 = lane & 15;
@@ -367,17 +373,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
   }
 }
 
+template <typename T, int D>
+static int launch_prefill_d(int waves, dim3 grid, hipStream_t s, const PrefillArgs& a) {
+  if (waves == 8) {
+    if constexpr (prefill_built(D, 8)) {
+      hipLaunchKernelGGL((paged_prefill_kernel<T, D, 8>), grid, dim3(512), 0, s, a);
+      return launch_status();
+    }
+    return LVAMD_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL((paged_prefill_kernel<T, D, 4>), grid, dim3(256), 0, s, a);
+  return launch_status();
+}
+
 template <typename T>
-static int launch_prefill_t(int head_size, dim3 grid, hipStream_t s, const PrefillArgs& a) {
+static int launch_prefill_t(int head_size, int waves, dim3 grid, hipStream_t s, const PrefillArgs& a) {
   switch (head_size) {
-    case 64: hipLaunchKernelGGL((paged_prefill_kernel<T, 64>), grid, dim3(kThreads), 0, s, a); break;
-    case 80: hipLaunchKernelGGL((paged_prefill_kernel<T, 80>), grid, dim3(kThreads), 0, s, a); break;
-    case 96: hipLaunchKernelGGL((paged_prefill_kernel<T, 96>), grid, dim3(kThreads), 0, s, a); break;
-    case 128: hipLaunchKernelGGL((paged_prefill_kernel<T, 128>), grid, dim3(kThreads), 0, s, a); break;
-    case 256: hipLaunchKernelGGL((paged_prefill_kernel<T, 256>), grid, dim3(kThreads), 0, s, a); break;
+    case 64: return launch_prefill_d<T, 64>(waves, grid, s, a);
+    case 80: return launch_prefill_d<T, 80>(waves, grid, s, a);
+    case 96: return launch_prefill_d<T, 96>(waves, grid, s, a);
+    case 128: return launch_prefill_d<T, 128>(waves, grid, s, a);
+    case 256: return launch_prefill_d<T, 256>(waves, grid, s, a);
     default: return LVAMD_ERR_UNSUPPORTED;
   }
-  return launch_status();
+}
+
+template <typename T, int D>
+static const void* prefill_fn(int waves) {
+  if (waves == 8) {
+    if constexpr (prefill_built(D, 8)) return (const void*)&paged_prefill_kernel<T, D, 8>;
+    return nullptr;
+  }
+  return (const void*)&paged_prefill_kernel<T, D, 4>;
+}
+
+template <typename T>
+static const void* prefill_fn_t(int head_size, int waves) {
+  switch (head_size) {
+    case 64: return prefill_fn<T, 64>(waves);
+    case 80: return prefill_fn<T, 80>(waves);
+    case 96: return prefill_fn<T, 96>(waves);
+    case 128: return prefill_fn<T, 128>(waves);
+    case 256: return prefill_fn<T, 256>(waves);
+    default: return nullptr;
+  }
 }
 
 static bool prefill_supported(int dtype, int head_size) {
@@ -399,22 +438,21 @@ extern "C" int lvamd_paged_prefill_key_tokens(int32_t dtype, int32_t head_size) 
   return prefill_key_tile(head_size);
 }
 
-extern "C" int lvamd_paged_prefill_resident_units(int32_t dtype, int32_t head_size) {
+extern "C" int lvamd_paged_prefill_resident_units(int32_t dtype, int32_t head_size, int32_t waves) {
   if (!prefill_supported(dtype, head_size)) return LVAMD_ERR_UNSUPPORTED;
-  const void* fn = nullptr;
-  const bool bf = dtype == LVAMD_BF16;
-  switch (head_size) {
-    case 64: fn = bf ? (const void*)&paged_prefill_kernel<__bf16, 64> : (const void*)&paged_prefill_kernel<_Float16, 64>; break;
-    case 80: fn = bf ? (const void*)&paged_prefill_kernel<__bf16, 80> : (const void*)&paged_prefill_kernel<_Float16, 80>; break;
-    case 96: fn = bf ? (const void*)&paged_prefill_kernel<__bf16, 96> : (const void*)&paged_prefill_kernel<_Float16, 96>; break;
-    case 128: fn = bf ? (const void*)&paged_prefill_kernel<__bf16, 128> : (const void*)&paged_prefill_kernel<_Float16, 128>; break;
-    default: fn = bf ? (const void*)&paged_prefill_kernel<__bf16, 256> : (const void*)&paged_prefill_kernel<_Float16, 256>; break;
-  }
+  if (waves != 4 && waves != 8) return LVAMD_ERR_INVALID_ARGUMENT;
+  const void* fn = dtype == LVAMD_BF16 ? prefill_fn_t<__bf16>(head_size, waves) : prefill_fn_t<_Float16>(head_size, waves);
+  if (fn == nullptr) return LVAMD_ERR_UNSUPPORTED;
   int device = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&device) != hipSuccess) return LVAMD_ERR_LAUNCH;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return LVAMD_ERR_LAUNCH;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, 0) != hipSuccess) return LVAMD_ERR_LAUNCH;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * waves, 0) != hipSuccess) return LVAMD_ERR_LAUNCH;
   return per_cu * cus;
+}
+
+extern "C" int lvamd_paged_prefill_waves_built(int32_t dtype, int32_t head_size, int32_t waves) {
+  if (!prefill_supported(dtype, head_size)) return 0;
+  return (waves == 4 || (waves == 8 && head_size <= 128)) ? 1 : 0;
 }
 
 extern "C" int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stride,
@@ -423,10 +461,11 @@ extern "C" int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_
                                    const int32_t* req_meta, const int32_t* tables, const uint32_t* vis,
                                    const int32_t* units, int32_t num_units,
                                    float* part_acc, float* part_ml, int64_t num_partial_slots,
-                                   int32_t num_kv_heads, int32_t group, int32_t head_size,
+                                   int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t waves,
                                    int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream) {
   if (num_units < 0 || num_kv_heads <= 0 || group <= 0 || block_size <= 0 || num_partial_slots < 0)
     return LVAMD_ERR_INVALID_ARGUMENT;
+  if (waves != 4 && waves != 8) return LVAMD_ERR_INVALID_ARGUMENT;
   if (num_units == 0) return LVAMD_OK;
   if (!prefill_supported(dtype, head_size)) return LVAMD_ERR_UNSUPPORTED;
   if (!q || !key_pool || !value_pool || !out || !req_meta || !tables || !vis || !units)
@@ -459,6 +498,6 @@ extern "C" int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_
   a.scale_log2 = scale * 1.4426950408889634f;
   const dim3 grid((unsigned)(num_units * num_kv_heads));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return dtype == LVAMD_BF16 ? launch_prefill_t<__bf16>(head_size, grid, s, a)
-                             : launch_prefill_t<_Float16>(head_size, grid, s, a);
+  return dtype == LVAMD_BF16 ? launch_prefill_t<__bf16>(head_size, waves, grid, s, a)
+                             : launch_prefill_t<_Float16>(head_size, waves, grid, s, a);
 }

@@ -15,7 +15,7 @@ from pathlib import Path
 from light_vllm_amd.errors import ExecutionError, ExecutionNotReadyError
 
 LIB_NAME = "liblvamd_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
@@ -59,11 +59,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lvamd_paged_prefill": (
         ctypes.c_int,
         [_p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i32, _p, _p, _i64,
-         _i32, _i32, _i32, _i32, _f32, _i32, _p],
+         _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p],
     ),
     "lvamd_paged_prefill_unit_columns": (ctypes.c_int, [_i32, _i32]),
     "lvamd_paged_prefill_key_tokens": (ctypes.c_int, [_i32, _i32]),
-    "lvamd_paged_prefill_resident_units": (ctypes.c_int, [_i32, _i32]),
+    "lvamd_paged_prefill_resident_units": (ctypes.c_int, [_i32, _i32, _i32]),
+    "lvamd_paged_prefill_waves_built": (ctypes.c_int, [_i32, _i32, _i32]),
     "lvamd_kv_compact": (
         ctypes.c_int,
         [_p, _p, _i32, _i64, _p, _p, _i64, _p, _i64, _p],
@@ -163,12 +164,19 @@ def prefill_key_tokens(dtype_code: int, head_size: int) -> int:
 
 
 @functools.lru_cache(maxsize=None)
-def prefill_resident_units(dtype_code: int, head_size: int) -> int:
-    """Prefill workgroups the current GPU holds at once."""
+def prefill_resident_units(dtype_code: int, head_size: int, waves: int = 4) -> int:
+    """Prefill workgroups of ``waves`` waves the current GPU holds at once."""
 
-    found = int(load().lvamd_paged_prefill_resident_units(dtype_code, head_size))
+    found = int(load().lvamd_paged_prefill_resident_units(dtype_code, head_size, waves))
     check(min(found, 0), "lvamd_paged_prefill_resident_units")
     return found
+
+
+@functools.lru_cache(maxsize=None)
+def prefill_waves_built(dtype_code: int, head_size: int, waves: int) -> bool:
+    """Whether the prefill kernel is built with ``waves`` waves per workgroup."""
+
+    return bool(load().lvamd_paged_prefill_waves_built(dtype_code, head_size, waves))
 
 
 def check(status: int, what: str) -> None:

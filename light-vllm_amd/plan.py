@@ -162,6 +162,35 @@ def stream_k_pieces(
     return pieces, wave_first, waves, per_wave, jobs, int(multi.sum())
 
 
+PREFILL_WIDE_MAX_TILES = 20  # mean key tiles per unit up to which 8-wave prefill workgroups win
+
+
+def choose_prefill_waves(
+    *, q_lens: np.ndarray, computed: np.ndarray, rows: np.ndarray, group: int, columns: int, key_tokens: int,
+    slots_per_head: int, wide_built: bool,
+) -> int:
+    """Workgroup shape of the prefill kernel for these rows: 8 waves of one
+    column tile when the units will be split over the resident workgroups or
+    are short (mean key tiles per unit at most PREFILL_WIDE_MAX_TILES), where
+    latency hiding pays; else 4 waves of two column tiles, whose K/V LDS reads
+    each feed two MFMAs.  Measured per workload in the prefill kernel's notes.
+    """
+
+    if not wide_built or not rows.any():
+        return 4
+    ncols = q_lens * group
+    nunit = np.where(rows, -(-ncols // columns), 0)
+    n = int(nunit.sum())
+    req = np.repeat(np.arange(len(q_lens)), nunit)
+    starts = np.zeros(len(q_lens), dtype=np.int64)
+    np.cumsum(nunit[:-1], out=starts[1:])
+    col0 = (np.arange(n) - starts[req]) * columns
+    last = np.minimum(col0 + columns, ncols[req]) - 1
+    tiles = -(-(computed[req] + last // group + 1) // key_tokens)
+    split = bool(slots_per_head) and n < slots_per_head
+    return 8 if split or float(tiles.mean()) <= PREFILL_WIDE_MAX_TILES else 4
+
+
 def prefill_pieces(
     *,
     q_lens: np.ndarray,
@@ -311,6 +340,7 @@ class DecodeWork:
     prefill_jobs: Tensor | None = None  # int32 [n, 8] merge jobs of split prefill units
     num_prefill_jobs: int = 0
     num_prefill_partial_slots: int = 0
+    prefill_waves: int = 4  # prefill workgroup shape: 4 waves x 2 column tiles or 8 x 1
 
 
 class StepPlan:
@@ -453,7 +483,7 @@ class StepPlan:
     def work(
         self, group: int, num_kv_heads: int, resident_waves: int = 8 * NUM_CUS, prefill_columns: int = 0,
         unit_tokens: int = UNIT_TOKENS, col_tiles: int = 1, prefill_key_tokens: int = 64,
-        prefill_resident: int = 0,
+        prefill_resident: int = 0, prefill_waves: int = 4,
     ) -> DecodeWork:
         """Work lists for layers of this (group, kv heads) shape.
 
@@ -462,22 +492,34 @@ class StepPlan:
         goes through the decode kernel), ``unit_tokens`` the decode kernel's
         tile and ``col_tiles`` its column tiles per wave; ``prefill_key_tokens``
         is the prefill kernel's key tile and ``prefill_resident`` how many
-        prefill workgroups the GPU holds (0: never split prefill units).  The
-        library reports the kernel figures per dtype and head size.
+        prefill workgroups of shape ``prefill_waves`` the GPU holds (0: never
+        split prefill units).  The library reports the kernel figures per
+        dtype and head size.
         """
 
         key = (group, num_kv_heads, resident_waves, prefill_columns, unit_tokens, col_tiles, prefill_key_tokens,
-               prefill_resident)
+               prefill_resident, prefill_waves)
         found = self._work.get(key)
         if found is None:
             found = self._build_work(group, num_kv_heads, resident_waves, prefill_columns, unit_tokens, col_tiles,
-                                     prefill_key_tokens, prefill_resident)
+                                     prefill_key_tokens, prefill_resident, prefill_waves)
             self._work[key] = found
         return found
 
+    def prefill_waves(self, group: int, num_kv_heads: int, prefill_columns: int, prefill_key_tokens: int,
+                      prefill_resident: int, wide_built: bool) -> int:
+        """The prefill workgroup shape (4 or 8 waves) for this step's wide rows."""
+
+        rows = ~self.decode_rows(prefill_columns, group)
+        return choose_prefill_waves(
+            q_lens=self._q_lens, computed=self._computed, rows=rows, group=group, columns=prefill_columns,
+            key_tokens=prefill_key_tokens,
+            slots_per_head=prefill_resident // num_kv_heads if prefill_resident else 0, wide_built=wide_built,
+        )
+
     def _build_work(
         self, group: int, num_kv_heads: int, resident_waves: int, prefill_columns: int, unit_tokens: int,
-        col_tiles: int, prefill_key_tokens: int, prefill_resident: int,
+        col_tiles: int, prefill_key_tokens: int, prefill_resident: int, prefill_waves: int = 4,
     ) -> DecodeWork:
         computed, q_lens = self._computed, self._q_lens
         batch = self.batch_size
@@ -537,4 +579,4 @@ class StepPlan:
         if num_pjobs:
             prefill_jobs = blob[off : off + MERGE_FIELDS * num_pjobs].view(num_pjobs, MERGE_FIELDS)
         return DecodeWork(pieces, wave_first, waves, jobs, num_jobs, num_partial, per_wave, col_tiles, prefill_units,
-                          num_prefill, prefill_jobs, num_pjobs, num_pslots)
+                          num_prefill, prefill_jobs, num_pjobs, num_pslots, prefill_waves)

@@ -34,8 +34,11 @@ def _lin(*lengths):
     return [tuple(range(-1, n - 1)) for n in lengths]
 
 
-def _check(step, *, backend=None, dense=False, expect_prefill=True):
-    backend = backend or lv.HipPagedAttentionBackend()
+WAVES = (4, 8)  # both prefill workgroup shapes (8 falls back to 4 at head size 256)
+
+
+def _check(step, *, backend=None, dense=False, expect_prefill=True, waves=None):
+    backend = backend or lv.HipPagedAttentionBackend(prefill_waves=waves)
     ctx = backend.create(step.cache, step.metadata)
     lid = step.layer_ids[0]
     out = ctx.forward(lid, step.query, step.key, step.value, scale=step.scale)
@@ -43,6 +46,8 @@ def _check(step, *, backend=None, dense=False, expect_prefill=True):
     spec = step.cache.layer_spec(lid)
     work = ctx._work(spec, step.query.dtype)
     assert (work.num_prefill_units > 0) == expect_prefill
+    if waves is not None and expect_prefill:
+        assert work.prefill_waves == (waves if spec.head_size <= 128 else 4)
     slots = step.metadata.slot_mapping(block_size=step.cache.config.block_size, device=DEV)
     layer = step.cache.layer(lid)
     nslots = step.cache.config.num_blocks * step.cache.config.block_size
@@ -59,39 +64,43 @@ def _check(step, *, backend=None, dense=False, expect_prefill=True):
     return out
 
 
+@pytest.mark.parametrize("waves", WAVES)
 @pytest.mark.parametrize("dtype", ("bf16", "fp16"))
 @pytest.mark.parametrize("head_size", (64, 80, 96, 128, 256))
-def test_prefill_head_sizes_and_dtypes(dtype, head_size) -> None:
-    _announce(f"prefill d={head_size} {dtype}")
+def test_prefill_head_sizes_and_dtypes(dtype, head_size, waves) -> None:
+    _announce(f"prefill d={head_size} {dtype} waves={waves}")
     step = make_step(hq=8, hkv=2, d=head_size, bs=16, dtype=DTYPES[dtype], computed=[0, 37, 300, 90],
                      layouts=_lin(40, 100, 17, 1), seed=head_size + 7)
-    _check(step)
+    _check(step, waves=waves)
 
 
+@pytest.mark.parametrize("waves", WAVES)
 @pytest.mark.parametrize("bs", (1, 3, 16, 32))
-def test_prefill_block_sizes(bs) -> None:
-    _announce(f"prefill block size {bs}")
+def test_prefill_block_sizes(bs, waves) -> None:
+    _announce(f"prefill block size {bs} waves={waves}")
     step = make_step(hq=28, hkv=4, d=128, bs=bs, dtype=torch.bfloat16, computed=[5, 140, 0],
                      layouts=_lin(70, 33, 1), seed=100 + bs)
-    _check(step)
+    _check(step, waves=waves)
 
 
-def test_prefill_unit_boundaries_and_group_sizes() -> None:
+@pytest.mark.parametrize("waves", WAVES)
+def test_prefill_unit_boundaries_and_group_sizes(waves) -> None:
     # 37 queries x 7 heads = 259 columns: two units, the second with 3 columns;
     # the group of 7 splits queries across column tiles and units.
-    _announce("prefill unit boundaries")
+    _announce(f"prefill unit boundaries waves={waves}")
     step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[64, 0],
                      layouts=_lin(37, 73), seed=7)
-    _check(step)
+    _check(step, waves=waves)
 
 
-def test_prefill_tree_visibility() -> None:
-    _announce("prefill tree")
+@pytest.mark.parametrize("waves", WAVES)
+def test_prefill_tree_visibility(waves) -> None:
+    _announce(f"prefill tree waves={waves}")
     rng = np.random.default_rng(11)
     parents = tuple([-1] + [int(rng.integers(0, i)) for i in range(1, 40)])
     step = make_step(hq=12, hkv=2, d=128, bs=16, dtype=torch.bfloat16, computed=[100, 33],
                      layouts=[parents, tuple(range(-1, 20))], seed=11)
-    _check(step)
+    _check(step, waves=waves)
 
 
 def test_prefill_lookahead_slots_are_not_read() -> None:
@@ -112,15 +121,16 @@ def test_prefill_lookahead_slots_are_not_read() -> None:
     _check(step)
 
 
-def test_c3_shape_mixed_batch() -> None:
+@pytest.mark.parametrize("waves", WAVES)
+def test_c3_shape_mixed_batch(waves) -> None:
     # BASELINE C3 at reduced batch: 2 prefill chunks of 512 queries with prior
     # context, plus 6 decode tokens, Qwen2.5-7B attention shape.
-    _announce("C3-shape mixed batch")
+    _announce(f"C3-shape mixed batch waves={waves}")
     rng = np.random.default_rng(3)
     computed = [int(c) for c in rng.integers(0, 3073, size=2)] + [int(c) for c in rng.integers(256, 4097, size=6)]
     step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=computed,
                      layouts=_lin(512, 512, *([1] * 6)), seed=3)
-    _check(step, dense=True)
+    _check(step, dense=True, waves=waves)
 
 
 def test_prefill_kernel_agrees_with_the_decode_path() -> None:
@@ -144,21 +154,23 @@ def _tree(rng, n):
     return tuple([-1] + [0 if p == -1 else p + 1 for p in parents])  # 1 input token + (n-1)-node tree
 
 
-def _split_work(step):
-    backend = lv.HipPagedAttentionBackend()
+def _split_work(step, waves=None):
+    backend = lv.HipPagedAttentionBackend(prefill_waves=waves)
     ctx = backend.create(step.cache, step.metadata)
     return backend, ctx._work(step.cache.layer_spec(step.layer_ids[0]), step.query.dtype)
 
 
+@pytest.mark.parametrize("waves", WAVES)
 @pytest.mark.parametrize("dtype", ("bf16", "fp16"))
 @pytest.mark.parametrize("head_size", (64, 80, 96, 128, 256))
-def test_split_k_tree_verification_head_sizes(dtype, head_size) -> None:
-    _announce(f"split-K prefill tree d={head_size} {dtype}")
+def test_split_k_tree_verification_head_sizes(dtype, head_size, waves) -> None:
+    _announce(f"split-K prefill tree d={head_size} {dtype} waves={waves}")
     rng = np.random.default_rng(head_size)
     step = make_step(hq=12, hkv=2, d=head_size, bs=16, dtype=DTYPES[dtype], computed=[900, 1500, 370, 2100],
                      layouts=[_tree(rng, 9) for _ in range(4)], seed=head_size + 31)
-    backend, work = _split_work(step)
+    backend, work = _split_work(step, waves)
     assert work.num_prefill_partial_slots > 0 and work.num_prefill_jobs == 4
+    assert work.prefill_waves == (waves if head_size <= 128 else 4)
     _check(step, backend=backend)
 
 
@@ -175,14 +187,15 @@ def test_split_k_c5_shape_shared_prefix() -> None:
     _check(step, backend=backend)
 
 
+@pytest.mark.parametrize("waves", WAVES)
 @pytest.mark.parametrize("bs", (1, 3, 16))
-def test_split_k_causal_chunks_and_block_sizes(bs) -> None:
+def test_split_k_causal_chunks_and_block_sizes(bs, waves) -> None:
     # Causal chunks with long prior context: 40 x 7 = 280 columns (three units,
     # the last partial), split over keys; plus decode rows in the same step.
     _announce(f"split-K causal chunks bs={bs}")
     step = make_step(hq=28, hkv=4, d=128, bs=bs, dtype=torch.bfloat16, computed=[3000, 700, 1200],
                      layouts=_lin(40, 3, 1), seed=80 + bs)
-    backend, work = _split_work(step)
+    backend, work = _split_work(step, waves)
     assert work.num_prefill_partial_slots > 0 and work.waves_per_head > 0
     _check(step, backend=backend, dense=True)
 

@@ -427,3 +427,24 @@ def test_vectorised_table_check_agrees_with_validate_block_tables(seed) -> None:
             StepPlan(md, block_size=bs, device=CPU, num_blocks=num_blocks)
     else:
         StepPlan(md, block_size=bs, device=CPU, num_blocks=num_blocks)
+
+
+def test_prefill_shape_choice_follows_the_measured_workloads() -> None:
+    """8-wave prefill workgroups for split-K or short units, 4-wave for long
+    unsplit units (the kernel notes hold the measurements)."""
+
+    from light_vllm_amd.plan import choose_prefill_waves
+
+    def pick(q_lens, computed, group, slots_per_head=128, wide=True):
+        q_lens = np.asarray(q_lens, dtype=np.int64)
+        return choose_prefill_waves(q_lens=q_lens, computed=np.asarray(computed, dtype=np.int64),
+                                    rows=q_lens * group > 16, group=group, columns=128, key_tokens=64,
+                                    slots_per_head=slots_per_head, wide_built=wide)
+
+    assert pick([512] * 8, [3072] * 8, 7) == 4           # long chunks, no split
+    assert pick([512] * 8, [0] * 8, 7) == 8              # short units
+    assert pick([9] * 32, [2300] * 32, 6, 256) == 8      # C5 tree verification: split
+    assert pick([512] * 2, [16384] * 2, 7) == 8          # few units over long history: split
+    assert pick([512] * 8, [3072] * 8, 7, 0) == 4        # splitting disabled, long units
+    assert pick([9] * 32, [2300] * 32, 6, 256, wide=False) == 4
+    assert pick([1] * 8, [100] * 8, 7) == 4              # no prefill rows
