@@ -168,7 +168,9 @@ int lvamd_paged_decode_tile_tokens(int32_t dtype, int32_t head_size, int32_t col
 
 /*
  * Log-sum-exp merge of split-K partials into out, one wave per (job, kv head,
- * column), four columns per workgroup; jobs [num_jobs][LVAMD_MERGE_FIELDS]; col_tiles (1 to 16) is
+ * column), four columns per workgroup, over the first max_columns (1 to
+ * 16 * col_tiles) columns of each job (the most any job has; the host knows
+ * it); jobs [num_jobs][LVAMD_MERGE_FIELDS]; col_tiles (1 to 16) is
  * the number of 16-column tiles per partial slot the partials were written
  * with (the decode kernel's col_tiles, or prefill unit columns / 16).  Same reference functions as lvamd_paged_decode:
  * the reference has no split-K, and this is the cross-partition half of that
@@ -178,7 +180,7 @@ int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
                                 void* out, int64_t out_token_stride, int64_t out_head_stride,
                                 const int32_t* jobs, int32_t num_jobs,
                                 int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t col_tiles,
-                                int32_t dtype, lvamd_stream_t stream);
+                                int32_t max_columns, int32_t dtype, lvamd_stream_t stream);
 
 /*
  * Chunked-prefill paged attention for query runs of more than one column

@@ -128,7 +128,8 @@ class _LayerLaunch:
         if work.num_jobs:
             # lvamd_paged_attention_merge arguments after the output strides, up to the stream.
             self.merge_args = (part_acc, part_ml) + (
-                work.jobs.data_ptr(), work.num_jobs, spec.num_kv_heads, group, spec.head_size, work.col_tiles, dtype,
+                work.jobs.data_ptr(), work.num_jobs, spec.num_kv_heads, group, spec.head_size, work.col_tiles,
+                work.merge_columns, dtype,
             )
         if work.num_prefill_units:
             # lvamd_paged_prefill arguments after the output strides, up to the scale.
@@ -141,7 +142,7 @@ class _LayerLaunch:
         if work.num_prefill_jobs:
             self.prefill_merge_args = (pre_acc, pre_ml) + (
                 work.prefill_jobs.data_ptr(), work.num_prefill_jobs, spec.num_kv_heads, group, spec.head_size,
-                prefill_columns // 16, dtype,
+                prefill_columns // 16, work.prefill_merge_columns, dtype,
             )
 
 

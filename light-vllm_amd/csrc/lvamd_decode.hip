@@ -655,6 +655,7 @@ struct MergeArgs {
   int32_t num_kv_heads;
   int32_t group;
   int32_t col_tiles;  // column tiles per partial slot (the decode launch's)
+  int32_t quads;      // workgroups (of kMergeWaves columns) per (job, kv head)
 };
 
 constexpr int kMergeWaves = 4;  // columns (waves) per merge workgroup
@@ -683,7 +684,7 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_merge_kernel(const Mer
   const int Hkv = a.num_kv_heads;
   const int G = a.group;
   const int cols = 16 * a.col_tiles;  // columns per partial slot
-  const int quads = cols / kMergeWaves;
+  const int quads = a.quads;
   const int jh = (int)blockIdx.x / quads;
   const int c = ((int)blockIdx.x - jh * quads) * kMergeWaves +
                 __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -905,13 +906,15 @@ extern "C" int lvamd_paged_attention_merge(const float* part_acc, const float* p
                                            void* out, int64_t out_token_stride, int64_t out_head_stride,
                                            const int32_t* jobs, int32_t num_jobs,
                                            int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t col_tiles,
-                                           int32_t dtype, lvamd_stream_t stream) {
+                                           int32_t max_columns, int32_t dtype, lvamd_stream_t stream) {
   if (dtype_size(dtype) == 0 || !head_size_supported(head_size) || col_tiles < 1 || col_tiles > 16)
     return LVAMD_ERR_UNSUPPORTED;
+  if (max_columns < 1 || max_columns > 16 * col_tiles) return LVAMD_ERR_INVALID_ARGUMENT;
   if (num_jobs < 0 || num_kv_heads <= 0 || group <= 0) return LVAMD_ERR_INVALID_ARGUMENT;
   if (num_jobs == 0) return LVAMD_OK;
   if (!part_acc || !part_ml || !out || !jobs) return LVAMD_ERR_INVALID_ARGUMENT;
-  if ((int64_t)num_jobs * num_kv_heads * col_tiles * (16 / kMergeWaves) > 0x7fffffffLL) return LVAMD_ERR_INVALID_ARGUMENT;
+  const int64_t quads = (max_columns + kMergeWaves - 1) / kMergeWaves;
+  if ((int64_t)num_jobs * num_kv_heads * quads > 0x7fffffffLL) return LVAMD_ERR_INVALID_ARGUMENT;
   MergeArgs a;
   a.part_acc = part_acc;
   a.part_ml = part_ml;
@@ -922,8 +925,10 @@ extern "C" int lvamd_paged_attention_merge(const float* part_acc, const float* p
   a.num_kv_heads = num_kv_heads;
   a.group = group;
   a.col_tiles = col_tiles;
-  // One workgroup per (job, kv head, kMergeWaves columns).
-  const dim3 grid((unsigned)(num_jobs * num_kv_heads * col_tiles * (16 / kMergeWaves)));
+  a.quads = (int32_t)quads;
+  // One workgroup per (job, kv head, kMergeWaves columns), over the columns
+  // the jobs use; columns past a job's own count exit at once.
+  const dim3 grid((unsigned)(num_jobs * num_kv_heads * quads));
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case LVAMD_BF16: return launch_merge_t<__bf16>(head_size, grid, s, a);

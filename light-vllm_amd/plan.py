@@ -325,6 +325,15 @@ def _stage_int32(array: np.ndarray, device: torch.device) -> Tensor:
     return host.to(device, non_blocking=True)
 
 
+def _job_columns(jobs: np.ndarray, group: int, per_slot: int) -> int:
+    """Most columns any merge job covers: its query run times the group, past
+    the columns of earlier column groups, at most a slot's columns.  Jobs are
+    (req, column group, first slot, partials, q_start, q_len, 0, 0)."""
+
+    cols = np.minimum(per_slot, jobs[:, 5] * group - jobs[:, 1] * per_slot)
+    return int(max(1, cols.max()))
+
+
 @dataclass(frozen=True, slots=True)
 class DecodeWork:
     pieces: Tensor | None  # int32 [n_pieces, 16]
@@ -341,6 +350,8 @@ class DecodeWork:
     num_prefill_jobs: int = 0
     num_prefill_partial_slots: int = 0
     prefill_waves: int = 4  # prefill workgroup shape: 4 waves x 2 column tiles or 8 x 1
+    merge_columns: int = 1  # most columns any decode merge job has
+    prefill_merge_columns: int = 1  # most columns any prefill merge job has
 
 
 class StepPlan:
@@ -578,5 +589,10 @@ class StepPlan:
             off += PREFILL_FIELDS * num_prefill
         if num_pjobs:
             prefill_jobs = blob[off : off + MERGE_FIELDS * num_pjobs].view(num_pjobs, MERGE_FIELDS)
+        merge_cols = pmerge_cols = 1
+        if num_jobs:
+            merge_cols = _job_columns(job_tab, group, 16 * col_tiles)
+        if num_pjobs:
+            pmerge_cols = _job_columns(pjobs, group, prefill_columns)
         return DecodeWork(pieces, wave_first, waves, jobs, num_jobs, num_partial, per_wave, col_tiles, prefill_units,
-                          num_prefill, prefill_jobs, num_pjobs, num_pslots, prefill_waves)
+                          num_prefill, prefill_jobs, num_pjobs, num_pslots, prefill_waves, merge_cols, pmerge_cols)

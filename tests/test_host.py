@@ -309,6 +309,21 @@ def test_prefill_split_fills_the_resident_workgroups() -> None:
     assert sorted(units[:, 4].tolist()) == sorted([512, 1024, 1536, 0] * 4)
 
 
+def test_merge_grids_cover_only_the_columns_jobs_use() -> None:
+    # Tree verification at group 6: 9 x 6 = 54 of a prefill slot's 128 columns.
+    plan = StepPlan(_uniform_metadata(batch=4, computed=2000, q=9), block_size=16, device=CPU)
+    work = plan.work(6, 2, 2048, 128, 64, 1, 64, 32)
+    assert work.num_prefill_jobs == 4 and work.prefill_merge_columns == 54
+    # Decode at group 7: 7 of a decode slot's 16 columns.
+    plan = StepPlan(_uniform_metadata(batch=8, computed=3000, q=1), block_size=16, device=CPU)
+    work = plan.work(7, 4, 1024, 128, 64, 1, 64, 32)
+    assert work.num_jobs > 0 and work.merge_columns == 7
+    # 40 queries at group 7 = 280 columns: units of 128, 128 and 24.
+    plan = StepPlan(_uniform_metadata(batch=1, computed=3000, q=40), block_size=16, device=CPU)
+    work = plan.work(7, 4, 1024, 128, 64, 1, 64, 256)
+    assert work.num_prefill_jobs == 3 and work.prefill_merge_columns == 128
+
+
 def test_library_loads_and_exports_every_header_function() -> None:
     lib = native.load()
     declared = native.header_functions()
@@ -329,8 +344,11 @@ def test_library_loads_and_exports_every_header_function() -> None:
                                   None, None, 0, 4, 7, 128, 1, 16, ctypes.c_float(0.1), 2, None) == -1
     assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 1, None, None,
                                   None, None, 0, 4, 7, 128, 2, 16, ctypes.c_float(0.1), 2, None) == -2
-    assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 1, 2, None) == -1
-    assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 17, 2, None) == -2
+    assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 1, 16, 2, None) == -1
+    assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 17, 16, 2, None) == -2
+    for bad_columns in (0, 17):  # the used columns must lie within a slot's 16 * col_tiles
+        assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 1, bad_columns, 2,
+                                               None) == -1
     assert lib.lvamd_paged_prefill_key_tokens(2, 128) == 64 and lib.lvamd_paged_prefill_key_tokens(2, 256) == 32
     assert lib.lvamd_paged_prefill_key_tokens(0, 128) == -2  # no fp32 prefill kernel
     # Tile sizes per kernel; four column tiles only for rows of at most 256 bytes.
