@@ -18,11 +18,12 @@
 //     so every K/V byte it loads serves all of them.
 //   * Stream-K: the (request, column-tile group) segments of all decode rows
 //     are laid end to end in tile-sized units and cut into balanced
-//     contiguous shares, one per wave; wave w of kv head h is workgroup
+//     contiguous shares (the fewest shares that give the largest share the
+//     resident waves would get), one per wave; wave w of kv head h is workgroup
 //     h * waves_per_head + w and walks its pieces (the parts of segments
 //     inside its share).  A piece covering a whole segment writes the output;
 //     the others write partials that the merge kernel combines by
-//     log-sum-exp, one wave per (segment, kv head, column tile).  (Merging in
+//     log-sum-exp, one wave per (segment, kv head, output column).  (Merging in
 //     the decode kernel, by the wave that completes a segment, put ~1000
 //     instructions of cold code in the kernel's tail: the instruction-cache
 //     misses cost more than a separate launch.)
