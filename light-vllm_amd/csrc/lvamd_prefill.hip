@@ -76,7 +76,9 @@ struct PrefillShape {
   static constexpr int CPR = D * (int)sizeof(T) / 16;          // 16-byte chunks per row
   static constexpr int RS = D * (int)sizeof(T) + LVAMD_PREFILL_PAD;  // LDS row stride in bytes (bank spread)
   static constexpr int THREADS = 64 * W;
-  static constexpr int LPT = (KT * CPR + THREADS - 1) / THREADS;  // chunks per thread per tile
+  static constexpr int TPR = THREADS / KT;                     // gather threads per tile row
+  static constexpr int LPT = (CPR + TPR - 1) / TPR;             // chunks per thread per tile
+  static_assert(THREADS % KT == 0, "every tile row gets the same number of gather threads");
   static constexpr int CT = prefill_col_tiles_per_wave(D, W);
   static constexpr int NCH = (D + 31) / 32;                    // 16x16x32 k-steps of QK^T
   static constexpr int NT = D / 16;                            // 16-row tiles of O^T
@@ -108,7 +110,7 @@ struct PrefillArgs {
 template <typename T, int D, int W>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ? 4 : (D <= 128 ? 2 : 1)))) void paged_prefill_kernel(const PrefillArgs a) {
   using P = PrefillShape<T, D, W>;
-  constexpr int CPR = P::CPR, RS = P::RS, LPT = P::LPT, CT = P::CT, NCH = P::NCH, NT = P::NT;
+  constexpr int CPR = P::CPR, RS = P::RS, LPT = P::LPT, TPR = P::TPR, CT = P::CT, NCH = P::NCH, NT = P::NT;
   constexpr int KT = P::KT, KS = P::KS;
   using V8 = typename std::conditional<std::is_same<T, __bf16>::value, bf16x8, f16x8>::type;
   __shared__ __attribute__((aligned(16))) char klds[2][P::TILE_BYTES];
@@ -144,40 +146,37 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
   const T* vbase = static_cast<const T*>(a.v_pool);
   const int32_t* table = a.tables + table_off;
 
-  // ---- tile gather.  Chunk i of this thread is chunk idx = tid + 256 i of
-  // the tile: row idx / CPR, 16-byte chunk idx % CPR (recomputed where used:
-  // cheaper than holding them in registers).
-  auto chunk_ok = [&](int i) { return tid + kThreads * i < KT * CPR; };
-  auto chunk_row = [&](int i) { return chunk_ok(i) ? (tid + kThreads * i) / CPR : 0; };
-  auto chunk_col = [&](int i) { return (tid + kThreads * i) % CPR; };
-  auto key_pos = [&](int t, int i) -> int {
-    const int pos = (tile0 + t) * KT + chunk_row(i);
+  // ---- tile gather.  Thread tid owns row tid / TPR of every tile and its
+  // 16-byte chunks (tid % TPR) + TPR i: one table entry and one row address
+  // per tile, the chunk loads and LDS stores at immediate offsets.
+  const int grow = tid / TPR;
+  const int gcol = tid - grow * TPR;
+  auto chunk_ok = [&](int i) { return gcol + TPR * i < CPR; };
+  auto key_pos = [&](int t) -> int {
+    const int pos = (tile0 + t) * KT + grow;
     return pos < kmax ? pos : kmax - 1;  // rows past the piece read its last key (masked)
   };
   auto logical_block = [&](int pos) -> int { return a.bs_shift >= 0 ? (pos >> a.bs_shift) : (pos / bs); };
-  auto load_entries = [&](int t, int (&te)[LPT]) {
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) te[i] = table[logical_block(key_pos(t, i))];
-  };
-  auto load_tile = [&](int t, const int (&te)[LPT], uint4 (&kr)[LPT], uint4 (&vr)[LPT]) {
+  auto load_entry = [&](int t) -> int { return table[logical_block(key_pos(t))]; };
+  auto load_tile = [&](int t, int te, uint4 (&kr)[LPT], uint4 (&vr)[LPT]) {
+    const int pos = key_pos(t);
+    const uint32_t slot = (uint32_t)te * (uint32_t)bs + (uint32_t)(pos - logical_block(pos) * bs);
+    const int64_t off = (int64_t)slot * row_elems + kvh * D + gcol * 8;
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const int pos = key_pos(t, i);
-      const uint32_t slot = (uint32_t)te[i] * (uint32_t)bs + (uint32_t)(pos - logical_block(pos) * bs);
-      const int64_t off = (int64_t)slot * row_elems + kvh * D + chunk_col(i) * 8;
       if (chunk_ok(i)) {
-        kr[i] = load16(kbase + off);
-        vr[i] = load16(vbase + off);
+        kr[i] = load16(kbase + off + TPR * 8 * i);
+        vr[i] = load16(vbase + off + TPR * 8 * i);
       }
     }
   };
   auto store_tile = [&](int b, const uint4 (&kr)[LPT], const uint4 (&vr)[LPT]) {
+    const int off = grow * RS + gcol * 16;
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       if (chunk_ok(i)) {
-        const int off = chunk_row(i) * RS + chunk_col(i) * 16;
-        *reinterpret_cast<uint4*>(klds[b] + off) = kr[i];
-        *reinterpret_cast<uint4*>(vlds[b] + off) = vr[i];
+        *reinterpret_cast<uint4*>(klds[b] + off + TPR * 16 * i) = kr[i];
+        *reinterpret_cast<uint4*>(vlds[b] + off + TPR * 16 * i) = vr[i];
       }
     }
   };
@@ -322,21 +321,21 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
   // sets alternate statically (a run-time swap would force waits).
   // Prologue in two round trips: the table entries of tiles 0 and 1, then
   // both tiles' loads (and tile 2's entries); tile 0 goes to LDS.
-  int ea[LPT], eb[LPT];
+  int ea = 0, eb = 0;
   uint4 ka[LPT], va[LPT], kb[LPT], vb[LPT];
-  load_entries(0, eb);
-  if (ntiles > 1) load_entries(1, ea);
+  eb = load_entry(0);
+  if (ntiles > 1) ea = load_entry(1);
   load_tile(0, eb, kb, vb);
   if (ntiles > 1) load_tile(1, ea, ka, va);
-  if (ntiles > 2) load_entries(2, eb);
+  if (ntiles > 2) eb = load_entry(2);
   store_tile(0, kb, vb);
   __syncthreads();
 
-  // dc holds tile t+1, dn receives tile t+2 (entries en), ec receives tile t+3's entries.
-  auto iter = [&](int t, uint4 (&kc)[LPT], uint4 (&vc)[LPT], uint4 (&kn)[LPT], uint4 (&vn)[LPT],
-                  int (&ec)[LPT], const int (&en)[LPT]) {
+  // dc holds tile t+1, dn receives tile t+2 (entry en), ec receives tile t+3's entry.
+  auto iter = [&](int t, uint4 (&kc)[LPT], uint4 (&vc)[LPT], uint4 (&kn)[LPT], uint4 (&vn)[LPT], int& ec,
+                  const int en) {
     if (t + 2 < ntiles) load_tile(t + 2, en, kn, vn);
-    if (t + 3 < ntiles) load_entries(t + 3, ec);
+    if (t + 3 < ntiles) ec = load_entry(t + 3);
     compute_tile(t, t & 1);
     if (t + 1 < ntiles) store_tile((t + 1) & 1, kc, vc);
     __syncthreads();
