@@ -565,42 +565,83 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
     return !next_in_cur;
   };
 
-  // Piece finished: write the outputs (whole segment) or its partials, then
-  // switch to the next piece (its first tile is already staged) and start
-  // fetching the one after.  Returns false after the wave's last piece.
-  auto end_piece = [&]() -> bool {
+  // Results of a finished piece: the normalised output rows (a whole
+  // segment) or its (max, sum, acc) partials.
+  auto write_piece = [&](const Piece& x, const LaneCol (&lx)[CTW], const f32x4 (&ax)[CTW][NT],
+                         const float (&mx)[CTW], const float (&sx)[CTW]) {
 #pragma unroll
     for (int ct = 0; ct < CTW; ++ct) {
-      const float l_tot = row_sum4(l_run[ct]);
-      if (cur.slot < 0) {
-        if (lc[ct].ok) {
-          const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-          T* orow = static_cast<T*>(a.out) + (int64_t)(cur.q_start + lc[ct].qi) * a.out_tok_stride +
-                    (int64_t)lc[ct].qhead * a.out_head_stride;
+      if (!lx[ct].ok) continue;
+      if (x.slot < 0) {
+        const float inv = sx[ct] > 0.f ? 1.f / sx[ct] : 0.f;
+        T* orow = static_cast<T*>(a.out) + (int64_t)(x.q_start + lx[ct].qi) * a.out_tok_stride +
+                  (int64_t)lx[ct].qhead * a.out_head_stride;
 #pragma unroll
-          for (int n = 0; n < NT; ++n)
+        for (int n = 0; n < NT; ++n)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) orow[16 * n + 4 * g + r] = from_f32<T>(acc[ct][n][r] * inv);
-        }
-      } else if (lc[ct].ok) {
-        const int64_t cs = ((int64_t)cur.slot * Hkv + kvh) * (16 * CTW) + ct * 16 + l16;
+          for (int r = 0; r < 4; ++r) orow[16 * n + 4 * g + r] = from_f32<T>(ax[ct][n][r] * inv);
+      } else {
+        const int64_t cs = ((int64_t)x.slot * Hkv + kvh) * (16 * CTW) + ct * 16 + l16;
         float* pacc = a.part_acc + cs * D;
 #if LVAMD_DECODE_NT_PARTIALS
 #pragma unroll
         for (int n = 0; n < NT; ++n)
-          __builtin_nontemporal_store(acc[ct][n], reinterpret_cast<f32x4*>(pacc + 16 * n + 4 * g));
+          __builtin_nontemporal_store(ax[ct][n], reinterpret_cast<f32x4*>(pacc + 16 * n + 4 * g));
         if (g == 0) {
-          __builtin_nontemporal_store(m_run[ct], a.part_ml + cs * 2);
-          __builtin_nontemporal_store(l_tot, a.part_ml + cs * 2 + 1);
+          __builtin_nontemporal_store(mx[ct], a.part_ml + cs * 2);
+          __builtin_nontemporal_store(sx[ct], a.part_ml + cs * 2 + 1);
         }
 #else
 #pragma unroll
-        for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(pacc + 16 * n + 4 * g) = acc[ct][n];
-        if (g == 0) *reinterpret_cast<float2*>(a.part_ml + cs * 2) = make_float2(m_run[ct], l_tot);
+        for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(pacc + 16 * n + 4 * g) = ax[ct][n];
+        if (g == 0) *reinterpret_cast<float2*>(a.part_ml + cs * 2) = make_float2(mx[ct], sx[ct]);
 #endif
       }
     }
-    if (!have_nxt) return false;
+  };
+
+  // With one column tile a piece that is not the wave's last keeps its
+  // results in registers and writes them after the wave's last piece: its
+  // stores would otherwise enter the memory queues behind every wave's
+  // in-flight tile loads, and reusing the accumulators would wait for them
+  // (about 2 us per switch, measured).  Four column tiles and rows above 256
+  // bytes have no registers to spare and write at once.
+  constexpr bool kDeferWrite = CTW == 1 && (int)sizeof(T) * D <= 256;
+  bool pend = false;
+  Piece pend_piece = cur;
+  LaneCol pend_lc[CTW];
+  f32x4 pend_acc[CTW][kDeferWrite ? NT : 1];
+  float pend_m[CTW], pend_s[CTW];
+
+  // Piece finished: write (or keep) its results, then switch to the next
+  // piece (its first tile is already staged) and start fetching the one
+  // after.  Returns false after the wave's last piece.
+  auto end_piece = [&]() -> bool {
+    float l_tot[CTW];
+#pragma unroll
+    for (int ct = 0; ct < CTW; ++ct) l_tot[ct] = row_sum4(l_run[ct]);
+    if (!have_nxt) {
+      write_piece(cur, lc, acc, m_run, l_tot);
+      if constexpr (kDeferWrite) {
+        if (pend) write_piece(pend_piece, pend_lc, pend_acc, pend_m, pend_s);
+      }
+      return false;
+    }
+    if constexpr (kDeferWrite) {
+      if (pend) write_piece(pend_piece, pend_lc, pend_acc, pend_m, pend_s);
+      pend = true;
+      pend_piece = cur;
+#pragma unroll
+      for (int ct = 0; ct < CTW; ++ct) {
+        pend_lc[ct] = lc[ct];
+        pend_m[ct] = m_run[ct];
+        pend_s[ct] = l_tot[ct];
+#pragma unroll
+        for (int n = 0; n < NT; ++n) pend_acc[ct][n] = acc[ct][n];
+      }
+    } else {
+      write_piece(cur, lc, acc, m_run, l_tot);
+    }
     cur = nxt;
     tb ^= 1;
     if constexpr (kPrefetchQ) {
