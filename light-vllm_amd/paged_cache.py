@@ -14,7 +14,6 @@ so light-vllm's own ``PagedKVCache`` can use them unchanged.
 
 from __future__ import annotations
 
-import ctypes
 import weakref
 from dataclasses import dataclass
 
