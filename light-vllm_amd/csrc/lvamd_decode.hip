@@ -65,12 +65,6 @@ constexpr float kRescaleSlack = 8.0f;
 // Piece fields 11..15: physical ids of the piece's first logical blocks.
 constexpr int kPieceBlockField = 11;
 constexpr int kPieceBlocks = 5;
-#ifndef LVAMD_DECODE_DIRECT_FIRST
-#define LVAMD_DECODE_DIRECT_FIRST 1
-#endif
-#ifndef LVAMD_DECODE_NT_PARTIALS
-#define LVAMD_DECODE_NT_PARTIALS 0
-#endif
 
 struct DecodeArgs {
   const void* q;
@@ -325,7 +319,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   int64_t fresh0[SUB];
   int tc[TAB_PER_LANE];
   const int first_span = logical_block(min(cur.tok_begin + TT, cur.tok_end) - 1) - logical_block(cur.tok_begin);
-  const bool direct = LVAMD_DECODE_DIRECT_FIRST && first_span < kPieceBlocks;
+  const bool direct = first_span < kPieceBlocks;
   if (direct) {
     const int32_t* ids = a.pieces + (int64_t)p * LVAMD_PIECE_FIELDS + kPieceBlockField;
     const int b0 = ids[0], b1 = ids[1], b2 = ids[2], b3 = ids[3], b4 = ids[4];
@@ -583,19 +577,9 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
       } else {
         const int64_t cs = ((int64_t)x.slot * Hkv + kvh) * (16 * CTW) + ct * 16 + l16;
         float* pacc = a.part_acc + cs * D;
-#if LVAMD_DECODE_NT_PARTIALS
-#pragma unroll
-        for (int n = 0; n < NT; ++n)
-          __builtin_nontemporal_store(ax[ct][n], reinterpret_cast<f32x4*>(pacc + 16 * n + 4 * g));
-        if (g == 0) {
-          __builtin_nontemporal_store(mx[ct], a.part_ml + cs * 2);
-          __builtin_nontemporal_store(sx[ct], a.part_ml + cs * 2 + 1);
-        }
-#else
 #pragma unroll
         for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(pacc + 16 * n + 4 * g) = ax[ct][n];
         if (g == 0) *reinterpret_cast<float2*>(a.part_ml + cs * 2) = make_float2(mx[ct], sx[ct]);
-#endif
       }
     }
   };

@@ -46,13 +46,9 @@ constexpr float kRescaleSlack = 8.0f;  // log2 units: probabilities stay below 2
 // LDS row padding in bytes.  32 makes every tile access conflict-free
 // (measured SQ_LDS_BANK_CONFLICT 13.8M -> 0 per C3 launch; 16 left 2.3
 // conflict cycles per LDS instruction on the transpose reads).
-#ifndef LVAMD_PREFILL_PAD
-#define LVAMD_PREFILL_PAD 32
-#endif
-
-#ifndef LVAMD_PREFILL_KT
-#define LVAMD_PREFILL_KT 64
-#endif
+constexpr int kPrefillPad = 32;
+// Keys per LDS tile up to head size 128 (32 above).
+constexpr int kPrefillKeyTile = 64;
 // Two shapes of the same 128-column unit, chosen per step by the planner:
 // * W = 4 waves of two 16-column tiles: each K/V LDS read feeds two MFMAs;
 //   256 registers per wave, two waves per SIMD (two workgroups per CU).
@@ -65,7 +61,7 @@ constexpr float kRescaleSlack = 8.0f;  // log2 units: probabilities stay below 2
 // D = 256, which is built for W = 4 only).
 constexpr int prefill_col_tiles_per_wave(int d, int w) { return w == 8 ? 1 : 2; }
 constexpr bool prefill_built(int d, int w) { return w == 4 || (w == 8 && d <= 128); }
-constexpr int prefill_key_tile(int d) { return d <= 128 ? LVAMD_PREFILL_KT : 32; }
+constexpr int prefill_key_tile(int d) { return d <= 128 ? kPrefillKeyTile : 32; }
 constexpr int prefill_unit_columns(int d) { return 16 * prefill_col_tiles_per_wave(d, 4) * 4; }
 static_assert(16 * 1 * 8 == 16 * 2 * 4, "both shapes cover the same unit columns");
 
@@ -74,7 +70,7 @@ struct PrefillShape {
   static constexpr int KT = prefill_key_tile(D);               // keys per tile
   static constexpr int KS = KT / 16;                           // 16-key groups per tile
   static constexpr int CPR = D * (int)sizeof(T) / 16;          // 16-byte chunks per row
-  static constexpr int RS = D * (int)sizeof(T) + LVAMD_PREFILL_PAD;  // LDS row stride in bytes (bank spread)
+  static constexpr int RS = D * (int)sizeof(T) + kPrefillPad;  // LDS row stride in bytes (bank spread)
   static constexpr int THREADS = 64 * W;
   static constexpr int TPR = THREADS / KT;                     // gather threads per tile row
   static constexpr int LPT = (CPR + TPR - 1) / TPR;             // chunks per thread per tile
