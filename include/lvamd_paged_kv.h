@@ -197,12 +197,19 @@ int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
  * [slots][num_kv_heads][unit columns][head_size] and part_ml
  * [slots][num_kv_heads][unit columns][2]; lvamd_paged_attention_merge with
  * col_tiles = unit columns / 16 combines them.
- * The pool must already hold this step's K/V (lvamd_kv_append).  req_meta is
+ * Append (waves == 8 only): when new_key / new_value are given
+ * ([tokens][num_kv_heads][D] with the given strides), keys at positions >=
+ * computed are read from them, and each such token's row is written to its
+ * pool slot by the unit that holds the token's own query (bit-exact copy).
+ * When they are NULL the pool must already hold this step's K/V
+ * (lvamd_kv_append).  req_meta is
  * [batch][LVAMD_REQ_FIELDS].  Replaces the prefill half of the same reference
  * functions as lvamd_paged_decode.
  */
 int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stride,
-                        const void* key_pool, const void* value_pool,
+                        const void* new_key, int64_t new_key_token_stride, int64_t new_key_head_stride,
+                        const void* new_value, int64_t new_value_token_stride, int64_t new_value_head_stride,
+                        void* key_pool, void* value_pool,
                         void* out, int64_t out_token_stride, int64_t out_head_stride,
                         const int32_t* req_meta, const int32_t* tables, const uint32_t* vis,
                         const int32_t* units, int32_t num_units,

@@ -10,10 +10,12 @@ once per layer by the model (src/light_vllm/modeling/models/qwen2.py:417-423):
    (paged_attention.py:226-247) plus the dtype/device rule of the Triton
    backend (triton_paged_attention.py:475-478);
 2. attend with write-before-attend semantics: the stream-K decode kernel
-   reads this step's K/V from the inputs and appends them to their pool slots
-   itself, and a merge kernel combines its split partials; a step with
-   prefill rows appends first (HIP ``lvamd_kv_append``) and runs the MFMA
-   prefill kernel for them.  Everything is on the current stream with no host
+   (short query runs) and the MFMA prefill kernel (long ones) in its 8-wave
+   shape read this step's K/V from the inputs and append their own requests'
+   tokens to their pool slots themselves, and a merge kernel combines split
+   partials; a step whose prefill rows take the 4-wave shape appends first
+   (HIP ``lvamd_kv_append``), and with ``rotary=`` one rotary-append launch
+   writes the pool first.  Everything is on the current stream with no host
    synchronisation.
 
 """
@@ -214,11 +216,15 @@ class HipPagedAttention:
             # the whole step's rotated K and V, so attention reads the pool.
             query = hip_append_rotary(self._cache, layer_id, query, key, value, rotary, self._plan.slots)
             new_kv = (None, 0, 0, None, 0, 0)
-        elif launch.prefill_args is not None:
-            # Prefill rows read the pool, so the whole step is appended first.
+        elif launch.prefill_args is not None and launch.work.prefill_waves != 8:
+            # The 4-wave prefill shape reads this step's K/V from the pool, so
+            # the whole step is appended first.
             hip_append(self._cache, layer_id, key, value, self._plan.slots)
             new_kv = (None, 0, 0, None, 0, 0)
         else:
+            # The decode kernel and the 8-wave prefill shape append their own
+            # requests' tokens (fused append): they read this step's keys and
+            # values from the inputs and write each token's row to its slot.
             if not _rows_aligned(key):
                 key = key.contiguous()
             if not _rows_aligned(value):
@@ -238,7 +244,7 @@ class HipPagedAttention:
                              "lvamd_paged_attention_merge")
         if launch.prefill_args is not None:
             native.check(lib.lvamd_paged_prefill(
-                query.data_ptr(), query.stride(0), query.stride(1),
+                query.data_ptr(), query.stride(0), query.stride(1), *new_kv,
                 layer.keys.data_ptr(), layer.values.data_ptr(), *o_args,
                 *launch.prefill_args, scale, launch.dtype, stream,
             ), "lvamd_paged_prefill")
@@ -276,7 +282,7 @@ class HipPagedAttention:
         stream = current_stream(query.device)
         o_args = (out.data_ptr(), out.stride(0), out.stride(1))
         native.check(self._lib.lvamd_paged_prefill(
-            query.data_ptr(), query.stride(0), query.stride(1),
+            query.data_ptr(), query.stride(0), query.stride(1), None, 0, 0, None, 0, 0,
             layer.keys.data_ptr(), layer.values.data_ptr(), *o_args,
             *launch.prefill_args, float(scale), launch.dtype, stream,
         ), "lvamd_paged_prefill")

@@ -323,7 +323,7 @@ const char* lvamd_status_string(int status) {
   }
 }
 
-int lvamd_abi_version(void) { return 10; }
+int lvamd_abi_version(void) { return 11; }
 
 int lvamd_kv_append(const void* key, int64_t key_token_stride, int64_t key_head_stride,
                     const void* value, int64_t value_token_stride, int64_t value_head_stride,

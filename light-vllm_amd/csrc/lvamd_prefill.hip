@@ -86,8 +86,11 @@ struct PrefillShape {
 struct PrefillArgs {
   const void* q;
   int64_t q_tok_stride, q_head_stride;
-  const void* k_pool;
-  const void* v_pool;
+  const void* k_new;  // this step's K/V, or null when the pool already holds them
+  const void* v_new;
+  int64_t kn_tok_stride, kn_head_stride, vn_tok_stride, vn_head_stride;
+  void* k_pool;
+  void* v_pool;
   void* out;
   int64_t out_tok_stride, out_head_stride;
   const int32_t* __restrict__ req_meta;  // [B][LVAMD_REQ_FIELDS]
@@ -138,8 +141,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
   const int bs = a.block_size;
 
   const int64_t row_elems = (int64_t)Hkv * D;
-  const T* kbase = static_cast<const T*>(a.k_pool);
-  const T* vbase = static_cast<const T*>(a.v_pool);
+  // Global-address-space pointers: the gather picks the pool or the step's
+  // input per row, and generic pointers would become flat loads.
+  gptr<T> const kbase = (gptr<T>)(a.k_pool);
+  gptr<T> const vbase = (gptr<T>)(a.v_pool);
   const int32_t* table = a.tables + table_off;
 
   // ---- tile gather.  Thread tid owns row tid / TPR of every tile and its
@@ -147,6 +152,17 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
   // per tile, the chunk loads and LDS stores at immediate offsets.
   const int grow = tid / TPR;
   const int gcol = tid - grow * TPR;
+  // Fused append (8-wave shape only): keys at positions >= computed are this
+  // step's tokens, read from the input K/V; the unit that holds a token's own
+  // query (its first column) also writes the row to its pool slot, so no
+  // other launch appends.  The 4-wave shape serves long units, where the
+  // append launch is small next to the kernel and the extra registers (three
+  // more spills at D = 128) cost more: there the pool holds the step's K/V.
+  constexpr bool kAppend = W == 8;
+  gptr<const T> const knew =
+      (kAppend && a.k_new) ? (gptr<const T>)(a.k_new) + (int64_t)kvh * a.kn_head_stride : nullptr;
+  gptr<const T> const vnew =
+      (kAppend && a.v_new) ? (gptr<const T>)(a.v_new) + (int64_t)kvh * a.vn_head_stride : nullptr;
   auto chunk_ok = [&](int i) { return gcol + TPR * i < CPR; };
   auto key_pos = [&](int t) -> int {
     const int pos = (tile0 + t) * KT + grow;
@@ -154,25 +170,48 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
   };
   auto logical_block = [&](int pos) -> int { return a.bs_shift >= 0 ? (pos >> a.bs_shift) : (pos / bs); };
   auto load_entry = [&](int t) -> int { return table[logical_block(key_pos(t))]; };
-  auto load_tile = [&](int t, int te, uint4 (&kr)[LPT], uint4 (&vr)[LPT]) {
+  // Loads tile t's row; returns the row's pool slot when this thread must
+  // append it, else -1.
+  auto load_tile = [&](int t, int te, uint4 (&kr)[LPT], uint4 (&vr)[LPT]) -> int {
     const int pos = key_pos(t);
     const uint32_t slot = (uint32_t)te * (uint32_t)bs + (uint32_t)(pos - logical_block(pos) * bs);
     const int64_t off = (int64_t)slot * row_elems + kvh * D + gcol * 8;
+    gptr<const T> kp = kbase + off;
+    gptr<const T> vp = vbase + off;
+    int append = -1;
+    if (knew != nullptr && pos >= computed) {
+      const int j = pos - computed;  // query index of the row's token
+      kp = knew + (int64_t)(q_start + j) * a.kn_tok_stride + gcol * 8;
+      vp = vnew + (int64_t)(q_start + j) * a.vn_tok_stride + gcol * 8;
+      const int raw = (tile0 + t) * KT + grow;
+      if (raw == pos && j * G >= col0) append = (int)slot;  // (j * G < col_end: pos < kmax <= kneed)
+    }
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       if (chunk_ok(i)) {
-        kr[i] = load16(kbase + off + TPR * 8 * i);
-        vr[i] = load16(vbase + off + TPR * 8 * i);
+        kr[i] = load16(kp + TPR * 8 * i);
+        vr[i] = load16(vp + TPR * 8 * i);
       }
     }
+    return append;
   };
-  auto store_tile = [&](int b, const uint4 (&kr)[LPT], const uint4 (&vr)[LPT]) {
+  auto store_tile = [&](int b, const uint4 (&kr)[LPT], const uint4 (&vr)[LPT], int append) {
     const int off = grow * RS + gcol * 16;
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       if (chunk_ok(i)) {
         *reinterpret_cast<uint4*>(klds[b] + off + TPR * 16 * i) = kr[i];
         *reinterpret_cast<uint4*>(vlds[b] + off + TPR * 16 * i) = vr[i];
+      }
+    }
+    if (append >= 0) {
+      const int64_t po = (int64_t)append * row_elems + kvh * D + gcol * 8;
+#pragma unroll
+      for (int i = 0; i < LPT; ++i) {
+        if (chunk_ok(i)) {
+          store16(kbase + po + TPR * 8 * i, kr[i]);
+          store16(vbase + po + TPR * 8 * i, vr[i]);
+        }
       }
     }
   };
@@ -318,27 +357,28 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
   // Prologue in two round trips: the table entries of tiles 0 and 1, then
   // both tiles' loads (and tile 2's entries); tile 0 goes to LDS.
   int ea = 0, eb = 0;
+  int wa = -1, wb = -1;  // pool slots to append the staged rows at (-1: none)
   uint4 ka[LPT], va[LPT], kb[LPT], vb[LPT];
   eb = load_entry(0);
   if (ntiles > 1) ea = load_entry(1);
-  load_tile(0, eb, kb, vb);
-  if (ntiles > 1) load_tile(1, ea, ka, va);
+  wb = load_tile(0, eb, kb, vb);
+  if (ntiles > 1) wa = load_tile(1, ea, ka, va);
   if (ntiles > 2) eb = load_entry(2);
-  store_tile(0, kb, vb);
+  store_tile(0, kb, vb, wb);
   __syncthreads();
 
   // dc holds tile t+1, dn receives tile t+2 (entry en), ec receives tile t+3's entry.
-  auto iter = [&](int t, uint4 (&kc)[LPT], uint4 (&vc)[LPT], uint4 (&kn)[LPT], uint4 (&vn)[LPT], int& ec,
-                  const int en) {
-    if (t + 2 < ntiles) load_tile(t + 2, en, kn, vn);
+  auto iter = [&](int t, uint4 (&kc)[LPT], uint4 (&vc)[LPT], int& wc, uint4 (&kn)[LPT], uint4 (&vn)[LPT],
+                  int& wn, int& ec, const int en) {
+    if (t + 2 < ntiles) wn = load_tile(t + 2, en, kn, vn);
     if (t + 3 < ntiles) ec = load_entry(t + 3);
     compute_tile(t, t & 1);
-    if (t + 1 < ntiles) store_tile((t + 1) & 1, kc, vc);
+    if (t + 1 < ntiles) store_tile((t + 1) & 1, kc, vc, wc);
     __syncthreads();
   };
   for (int t = 0; t < ntiles; t += 2) {
-    iter(t, ka, va, kb, vb, ea, eb);
-    if (t + 1 < ntiles) iter(t + 1, kb, vb, ka, va, eb, ea);
+    iter(t, ka, va, wa, kb, vb, wb, ea, eb);
+    if (t + 1 < ntiles) iter(t + 1, kb, vb, wb, ka, va, wa, eb, ea);
   }
 
   // ---- normalised output rows, or this piece's partials
@@ -451,7 +491,9 @@ extern "C" int lvamd_paged_prefill_waves_built(int32_t dtype, int32_t head_size,
 }
 
 extern "C" int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stride,
-                                   const void* key_pool, const void* value_pool,
+                                   const void* new_key, int64_t new_key_token_stride, int64_t new_key_head_stride,
+                                   const void* new_value, int64_t new_value_token_stride,
+                                   int64_t new_value_head_stride, void* key_pool, void* value_pool,
                                    void* out, int64_t out_token_stride, int64_t out_head_stride,
                                    const int32_t* req_meta, const int32_t* tables, const uint32_t* vis,
                                    const int32_t* units, int32_t num_units,
@@ -471,10 +513,22 @@ extern "C" int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_
       (q_token_stride * es) % 16 != 0 || (q_head_stride * es) % 16 != 0)
     return LVAMD_ERR_INVALID_ARGUMENT;
   if ((int64_t)num_units * num_kv_heads > 0x7fffffffLL) return LVAMD_ERR_INVALID_ARGUMENT;
+  if ((new_key == nullptr) != (new_value == nullptr)) return LVAMD_ERR_INVALID_ARGUMENT;
+  if (new_key && waves != 8) return LVAMD_ERR_INVALID_ARGUMENT;  // only the 8-wave shape appends
+  if (new_key && (((uintptr_t)new_key & 15u) || ((uintptr_t)new_value & 15u) ||
+                  (new_key_token_stride * es) % 16 != 0 || (new_key_head_stride * es) % 16 != 0 ||
+                  (new_value_token_stride * es) % 16 != 0 || (new_value_head_stride * es) % 16 != 0))
+    return LVAMD_ERR_INVALID_ARGUMENT;
   PrefillArgs a;
   a.q = q;
   a.q_tok_stride = q_token_stride;
   a.q_head_stride = q_head_stride;
+  a.k_new = new_key;
+  a.v_new = new_value;
+  a.kn_tok_stride = new_key_token_stride;
+  a.kn_head_stride = new_key_head_stride;
+  a.vn_tok_stride = new_value_token_stride;
+  a.vn_head_stride = new_value_head_stride;
   a.k_pool = key_pool;
   a.v_pool = value_pool;
   a.out = out;

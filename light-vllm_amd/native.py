@@ -15,7 +15,7 @@ from pathlib import Path
 from light_vllm_amd.errors import ExecutionError, ExecutionNotReadyError
 
 LIB_NAME = "liblvamd_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
@@ -58,7 +58,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "lvamd_paged_prefill": (
         ctypes.c_int,
-        [_p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i32, _p, _p, _i64,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i32, _p, _p, _i64,
          _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p],
     ),
     "lvamd_paged_prefill_unit_columns": (ctypes.c_int, [_i32, _i32]),
