@@ -349,6 +349,20 @@ def test_library_loads_and_exports_every_header_function() -> None:
     for bad_columns in (0, 17):  # the used columns must lie within a slot's 16 * col_tiles
         assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 1, bad_columns, 2,
                                                None) == -1
+    # Prefill: the workgroup shape must be 4 or 8 waves, and only the 8-wave
+    # shape takes this step's K/V (fused append); K without V is refused.
+    x = ctypes.c_void_p(16)  # (never dereferenced: the checks run first)
+    prefill = lambda nk, nv, waves: lib.lvamd_paged_prefill(  # noqa: E731
+        x, 0, 0, nk, 0, 0, nv, 0, 0, x, x, x, 0, 0, x, x, x, x, 1, None, None, 0, 2, 7, 128, waves, 16,
+        ctypes.c_float(0.1), 2, None)
+    assert prefill(None, None, 5) == -1
+    assert prefill(x, None, 8) == -1
+    assert prefill(x, x, 4) == -1
+    assert lib.lvamd_paged_prefill_waves_built(2, 128, 8) == 1 and lib.lvamd_paged_prefill_waves_built(2, 256, 8) == 0
+    assert lib.lvamd_paged_prefill_waves_built(2, 256, 4) == 1 and lib.lvamd_paged_prefill_waves_built(0, 128, 4) == 0
+    assert lib.lvamd_kv_append_rotary(None, 0, 0, None, 0, 0, None, 0, 0, None, 0, 0, None, 0, None, 0, None, None,
+                                      None, 1, 4, 2, 127, 2, None) == -1  # odd head size
+    assert lib.lvamd_hbm_read_probe(None, 16, None, 1, None) == -1
     assert lib.lvamd_paged_prefill_key_tokens(2, 128) == 64 and lib.lvamd_paged_prefill_key_tokens(2, 256) == 32
     assert lib.lvamd_paged_prefill_key_tokens(0, 128) == -2  # no fp32 prefill kernel
     # Tile sizes per kernel; four column tiles only for rows of at most 256 bytes.
