@@ -255,6 +255,56 @@ def read_ceiling(device: torch.device, nbytes: int = 2 << 30) -> dict:
     return {"GBps": round(best[0], 1), "workgroups": best[1], "bytes": nbytes}
 
 
+def kv_move_sweep(args, device: torch.device) -> int:
+    """Bandwidth-scale sweep of the KV movement kernels on a C5-shaped cache
+    (28 layers, 2 KV heads, D 128, bf16, block 16): copy-on-write block copy
+    over n blocks and compact over n moved rows, bytes read + written."""
+
+    from light_vllm_amd import native
+    from light_vllm_amd.paged_cache import _layer_pointers, current_stream
+
+    layers, hkv, d, bs, nb = 28, 2, 128, 16, 20000
+    spec = lv.ModelKVCacheSpec(tuple(lv.AttentionLayerSpec(f"layer{i}", 12, hkv, d) for i in range(layers)))
+    cache = lv.PagedKVCache(spec, lv.PagedKVCacheConfig(num_blocks=nb, block_size=bs, dtype=torch.bfloat16,
+                                                        device=device))
+    rng = np.random.default_rng(5)
+    row = hkv * d * 2
+    out = {"mode": "kv-sweep", "layers": layers, "block_bytes": bs * row, "row_bytes": row, "block_copy": [],
+           "compact": []}
+    # Both kernels are called through the C ABI with their index arrays and
+    # workspace already on the GPU, so the sweep times the kernels and not
+    # the host-side validation and list conversion of the Python entry points.
+    lib = native.load()
+    _, num_layers, ptrs = _layer_pointers(cache).groups[0]
+    for n in (32, 256, 2048, 8192):
+        blocks = torch.from_numpy(rng.permutation(nb)[: 2 * n].astype(np.int64)).to(device)
+
+        def block_copy(i: int) -> None:
+            native.check(lib.lvamd_kv_block_copy(
+                ptrs[0].data_ptr(), ptrs[1].data_ptr(), num_layers, row * bs, blocks[:n].data_ptr(),
+                blocks[n:].data_ptr(), n, current_stream(device)), "lvamd_kv_block_copy")
+
+        ms = _time_launches(block_copy, 20, 3, device, batch=5)
+        moved = 2 * n * layers * 2 * bs * row
+        out["block_copy"].append({"blocks": n, "us": round(ms * 1e3, 2), "GBps": round(moved / (ms * 1e-3) / 1e9, 1)})
+    for n in (16, 128, 1024, 8192):
+        slots = torch.from_numpy(rng.permutation(nb * bs)[: 2 * n].astype(np.int64)).to(device)
+        ws_bytes = lib.lvamd_kv_compact_workspace_size(n, num_layers, row)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+
+        def compact(i: int) -> None:
+            native.check(lib.lvamd_kv_compact(
+                ptrs[0].data_ptr(), ptrs[1].data_ptr(), num_layers, row, slots[:n].data_ptr(),
+                slots[n:].data_ptr(), n, ws.data_ptr() if ws_bytes else None, ws_bytes,
+                current_stream(device)), "lvamd_kv_compact")
+
+        ms = _time_launches(compact, 20, 3, device, batch=5)
+        moved = 2 * n * layers * 2 * row
+        out["compact"].append({"rows": n, "us": round(ms * 1e3, 2), "GBps": round(moved / (ms * 1e-3) / 1e9, 1)})
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def copy_calibration(args, device: torch.device) -> int:
     """A plain device-to-device copy of 1 GiB: counter calibration and practical ceiling."""
 
@@ -719,6 +769,7 @@ def run_c5(args, device) -> int:
                           "PyTorch path + attention")
     row = cfg.hkv * cfg.d * 2
     unique_kv = (cfg.prefix + sum(s + q_len for s in suffix)) * 2 * row
+    logical_kv = sum(cfg.prefix + s + q_len for s in suffix) * 2 * row  # shared prefix counted per sequence
     cow_bytes = 2 * cfg.batch * cfg.layers * 2 * cfg.bs * row
     moved = sum(len(a) for a in accepted)
     rec = _record(
@@ -729,6 +780,7 @@ def run_c5(args, device) -> int:
                  "then compact of an accepted root-to-leaf path",
         extra={"attention_us": round(attend_ms * 1e3, 2),
                "attention_unique_gbps": round(cfg.layers * unique_kv / (attend_ms * 1e-3) / 1e9, 1),
+               "attention_logical_gbps": round(cfg.layers * logical_kv / (attend_ms * 1e-3) / 1e9, 1),
                "cow_copy_us": round(cow_ms * 1e3, 2), "cow_copy_gbps": round(cow_bytes / (cow_ms * 1e-3) / 1e9, 1),
                "compact_us": round(compact_ms * 1e3, 2), "compact_tokens": moved,
                "rotary": rotary,
@@ -758,9 +810,10 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-rotary", action="store_true",
                         help="skip the RoPE-fused step timing (keeps a kernel trace to the attention step)")
-    parser.add_argument("--mode", choices=("full", "decode", "copy"), default="full",
+    parser.add_argument("--mode", choices=("full", "decode", "copy", "kv-sweep"), default="full",
                         help="decode: only the decode kernel (counter runs); copy: a plain 1 GiB device "
-                             "copy of known size (counter calibration and the practical HBM ceiling)")
+                             "copy of known size (counter calibration and the practical HBM ceiling); kv-sweep: "
+                             "block copy and compact bandwidth over sizes")
     parser.add_argument("--partition", type=int, default=None,
                         help="cap on the tokens one decode wave handles (default: spread over all resident waves)")
     parser.add_argument("--col-tiles", type=int, choices=(1, 4), default=None,
@@ -778,6 +831,8 @@ def main() -> int:
     device = torch.device("cuda:0")
     if args.mode == "copy":
         return copy_calibration(args, device)
+    if args.mode == "kv-sweep":
+        return kv_move_sweep(args, device)
     if args.config != "c2":
         return {"c1": run_c1, "c3": run_c3, "c4": run_c4, "c5": run_c5}[args.config](args, device)
     print(f"[bench] building C2 workload, {args.sets} pool sets", file=sys.stderr, flush=True)
