@@ -261,7 +261,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
     if (!wave_active || t * KT >= wave_kmax) return;
     const char* kt = klds[b];
     const char* vt = vlds[b];
-    // S^T for each column tile, K chunks shared.
+    // S^T for each column tile, K chunks shared.  Each MFMA block runs at
+    // raised wave priority: the SIMD's other wave then does its softmax
+    // VALU work while this one feeds the matrix core, and the two phases
+    // overlap (measured 7% on a chunked-prefill step in both shapes).
+    __builtin_amdgcn_s_setprio(1);
     f32x4 st[CT][KS];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct)
@@ -276,6 +280,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) st[ct][s] = Mma<T>::qk(kc, qf[ct][kk], st[ct][s]);
       }
+    __builtin_amdgcn_s_setprio(0);
     const bool masked = t >= full_tiles;
     // Masks only past the fully visible prefix: one compare per score for a
     // linear request, the ancestor bits for a tree.  (A piece ends on a tile
@@ -328,6 +333,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
         }
     }
     // O^T += V^T P^T: transpose reads shared by the column tiles.
+    __builtin_amdgcn_s_setprio(1);
     const int q4 = l16 & 3;
 #pragma unroll
     for (int h = 0; h < KS / 2; ++h)
@@ -348,6 +354,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
           }
         }
       }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   // ---- pipeline: tile t computes from LDS while tile t+1 sits in registers
