@@ -344,20 +344,21 @@ def copy_calibration(args, device: torch.device) -> int:
 
 
 TRAFFIC_SUMMARY = Path(__file__).resolve().parent / "profiles" / "paged_decode_c2_traffic.json"
+PREFILL_TRAFFIC_SUMMARY = Path(__file__).resolve().parent / "profiles" / "paged_prefill_c3_traffic.json"
 
 
-def measured_traffic() -> dict | None:
-    """HBM bytes per decode launch from the committed rocprofv3 counter runs.
+def measured_traffic(summary_path: Path = TRAFFIC_SUMMARY) -> dict | None:
+    """HBM bytes per launch of a kernel from the committed rocprofv3 counter runs.
 
-    FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the decode kernel, each
-    scaled by what the same counter reads for a plain copy of known size
-    (the summary file records both runs and the factors).
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the kernel, each scaled
+    by what the same counter reads for a plain copy of known size (the
+    summary file records both runs and the factors).
     """
 
-    if not TRAFFIC_SUMMARY.exists():
+    if not summary_path.exists():
         return None
-    summary = json.loads(TRAFFIC_SUMMARY.read_text())
-    return {"bytes_per_launch": summary["hbm_bytes_per_launch"], "source": TRAFFIC_SUMMARY.name}
+    summary = json.loads(summary_path.read_text())
+    return {"bytes_per_launch": summary["hbm_bytes_per_launch"], "source": summary_path.name}
 
 
 # ---------------------------------------------------------------------------
@@ -558,6 +559,9 @@ def run_c3(args, device) -> int:
     flops = 4 * cfg.hq * cfg.d * int(sum(cfg.chunk * (c + 1) + cfg.chunk * (cfg.chunk - 1) // 2 for c in pre))
     dec_L = comp[cfg.n_prefill:] + 1
     dec_bytes = int(dec_L.sum()) * 2 * cfg.hkv * cfg.d * 2 + 2 * cfg.n_decode * cfg.hq * cfg.d * 2
+    # Prefill launch bytes: each prefill request's visible K/V rows once, Q and O.
+    prefill_bytes = (int((pre + cfg.chunk).sum()) * 2 * cfg.hkv * cfg.d * 2
+                     + 2 * cfg.n_prefill * cfg.chunk * cfg.hq * cfg.d * 2)
     tflops = flops / (prefill_ms * 1e-3) / 1e12
     rec = _record(
         metric="chunked-prefill mixed step (C3): prefill kernel TFLOP/s vs bf16 MFMA peak, Qwen2.5-7B shape",
@@ -567,12 +571,17 @@ def run_c3(args, device) -> int:
         extra={
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-                         "kernel": "paged_prefill_kernel<bf16,128>", "algorithmic_flops_per_launch": flops},
+                         "kernel": "paged_prefill_kernel<bf16,128>", "algorithmic_flops_per_launch": flops,
+                         "algorithmic_bytes_per_launch": prefill_bytes},
             "prefill_kernel_us": round(prefill_ms * 1e3, 2),
             "decode_rows_us": round(decode_ms * 1e3, 2),
             "decode_rows_gbps": round(dec_bytes / (decode_ms * 1e-3) / 1e9, 1),
             "step_ms": round(ms, 4), "host_submit_ms": round(host_ms, 5),
         })
+    traffic = measured_traffic(PREFILL_TRAFFIC_SUMMARY)
+    if traffic is not None:
+        rec["roofline"]["traffic"] = traffic["bytes_per_launch"]
+        rec["roofline"]["traffic_source"] = traffic["source"]
     if not args.no_cpu_baseline:
         from oracle import paged_kv_oracle as O  # checker/baseline only
 

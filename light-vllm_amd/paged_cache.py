@@ -23,6 +23,7 @@ from torch import Tensor
 from light_vllm_amd import native
 from light_vllm_amd.errors import KVCacheError
 from light_vllm_amd.interfaces import AttentionLayerSpec, ModelKVCacheSpec
+from light_vllm_amd.plan import table_proven
 
 _DTYPE_CODES = {torch.float32: native.DTYPE_F32, torch.float16: native.DTYPE_F16, torch.bfloat16: native.DTYPE_BF16}
 
@@ -227,14 +228,17 @@ def compact_slots(
     required = (num_computed_tokens + num_reserved_query_tokens + bs - 1) // bs
     if len(block_ids) != required:
         raise KVCacheError("block table does not exactly cover the reserved query slots")
-    # Every id an int (not a bool or numpy scalar) in [0, num_blocks); checked
-    # with C-level passes (map/min/max) since tables run to thousands of ids.
-    if block_ids and (
-        set(map(type, block_ids)) != {int} or min(block_ids) < 0 or max(block_ids) >= config.num_blocks
-    ):
-        raise KVCacheError("block table contains an invalid physical block")
-    if len(set(block_ids)) != len(block_ids):
-        raise KVCacheError("block table aliases a physical block within one request")
+    # Every id an int (not a bool or numpy scalar) in [0, num_blocks), none
+    # repeated; checked with C-level passes (map/min/max/set) since tables run
+    # to thousands of ids, and skipped for a table object that the step's
+    # attention context has already proven (plan.table_proven).
+    if not table_proven(block_ids, config.num_blocks):
+        if block_ids and (
+            set(map(type, block_ids)) != {int} or min(block_ids) < 0 or max(block_ids) >= config.num_blocks
+        ):
+            raise KVCacheError("block table contains an invalid physical block")
+        if len(set(block_ids)) != len(block_ids):
+            raise KVCacheError("block table aliases a physical block within one request")
     if num_readonly_prefix_blocks * bs > num_computed_tokens:
         raise KVCacheError("readonly prefix blocks exceed the computed prefix")
 

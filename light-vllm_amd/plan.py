@@ -25,6 +25,7 @@ copy on the current stream; the work lists of each group size add one more.
 from __future__ import annotations
 
 import itertools
+from collections import OrderedDict
 from dataclasses import dataclass
 
 import numpy as np
@@ -263,6 +264,32 @@ def prefill_pieces(
     return ptab[order], jobs, int(split.sum())
 
 
+# Block tables already proven to hold unique int ids in [0, num_blocks):
+# id(table) -> (table, num_blocks).  An entry holds its tuple, so the id
+# cannot pass to another object while it is listed, and a tuple of ints
+# cannot change, so a listed table needs no second pass.  compact() consults
+# it for the tables that the step's attention context has already checked.
+_PROVEN_TABLES: "OrderedDict[int, tuple[tuple, int]]" = OrderedDict()
+_PROVEN_LIMIT = 1024
+
+
+def note_proven_tables(tables, num_blocks: int) -> None:
+    """Record tables that passed the block-table rules for ``num_blocks``
+    (their ids are ints, as the metadata constructor requires)."""
+
+    for table in tables:
+        if type(table) is tuple:
+            _PROVEN_TABLES[id(table)] = (table, num_blocks)
+            _PROVEN_TABLES.move_to_end(id(table))
+    while len(_PROVEN_TABLES) > _PROVEN_LIMIT:
+        _PROVEN_TABLES.popitem(last=False)
+
+
+def table_proven(table, num_blocks: int) -> bool:
+    entry = _PROVEN_TABLES.get(id(table))
+    return entry is not None and entry[0] is table and entry[1] == num_blocks
+
+
 def tables_valid(
     flat: np.ndarray,
     counts: np.ndarray,
@@ -389,6 +416,8 @@ class StepPlan:
             metadata.validate_block_tables(num_blocks=num_blocks, block_size=block_size)
             # Only a negative id gets here (the metadata constructor rejects them).
             raise KVCacheError("block table contains an out-of-range physical block")
+        if num_blocks is not None:
+            note_proven_tables(tables, num_blocks)
         q_lens = np.fromiter((len(layout) for layout in layouts), dtype=np.int64, count=batch)
         q_start = np.zeros(batch, dtype=np.int64)
         np.cumsum(q_lens[:-1], out=q_start[1:])

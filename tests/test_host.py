@@ -480,3 +480,51 @@ def test_prefill_shape_choice_follows_the_measured_workloads() -> None:
     assert pick([512] * 8, [3072] * 8, 7, 0) == 4        # splitting disabled, long units
     assert pick([9] * 32, [2300] * 32, 6, 256, wide=False) == 4
     assert pick([1] * 8, [100] * 8, 7) == 4              # no prefill rows
+
+
+def test_compact_slots_known_answer_and_rules() -> None:
+    """compact's slot pairs and its table errors (paged_cache.py:269-312) on
+    the reference test's case: table (1, 3, 0, 2), computed 2, block size 2,
+    retained (0, 2, 4) -> targets (6, 7, 0) (tests/test_paged_attention.py:178-228)."""
+
+    from types import SimpleNamespace
+
+    from light_vllm_amd.paged_cache import compact_slots
+
+    cfg = SimpleNamespace(block_size=2, num_blocks=4)
+    kw = dict(num_computed_tokens=2, num_query_tokens=5, num_reserved_query_tokens=5,
+              retained_query_indices=(0, 2, 4))
+    assert compact_slots(cfg, (1, 3, 0, 2), **kw) == ((6, 0, 4), (6, 7, 0))
+    for table, message in (((1, 3, True, 2), "invalid physical block"), ((1, 3, 0, 4), "invalid physical block"),
+                           ((1, 3, 1, 2), "aliases a physical block"), ((1, 3, 0), "exactly cover")):
+        with pytest.raises(lv.KVCacheError, match=message):
+            compact_slots(cfg, table, **kw)
+
+
+def test_compact_trusts_only_the_table_objects_a_step_plan_proved() -> None:
+    """A step plan that validated its tables lists those tuple objects, and
+    compact then skips their id checks; an equal tuple that is another object,
+    or another pool size, is checked again.  The list is bounded."""
+
+    from types import SimpleNamespace
+
+    from light_vllm_amd import plan as P
+    from light_vllm_amd.paged_cache import compact_slots
+
+    rng = np.random.default_rng(3)
+    md = _random_metadata(rng, batch=4, bs=4)
+    num_blocks = max(max(t) for t in md.block_tables) + 1
+    StepPlan(md, block_size=4, device=CPU, num_blocks=num_blocks)
+    cfg = SimpleNamespace(block_size=4, num_blocks=num_blocks)
+    for r, table in enumerate(md.block_tables):
+        copy = tuple(list(table))
+        assert P.table_proven(table, num_blocks)
+        assert not P.table_proven(table, num_blocks + 1)
+        assert not P.table_proven(copy, num_blocks)
+        q = md.query_lengths[r]
+        kw = dict(num_computed_tokens=md.num_computed_tokens[r], num_query_tokens=q,
+                  num_reserved_query_tokens=md.num_reserved_query_tokens[r],
+                  retained_query_indices=tuple(range(q))[::-1])
+        assert compact_slots(cfg, table, **kw) == compact_slots(cfg, copy, **kw)
+    P.note_proven_tables([(i,) for i in range(P._PROVEN_LIMIT + 10)], 1 << 20)
+    assert len(P._PROVEN_TABLES) == P._PROVEN_LIMIT
