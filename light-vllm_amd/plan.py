@@ -269,8 +269,10 @@ def prefill_pieces(
 # cannot pass to another object while it is listed, and a tuple of ints
 # cannot change, so a listed table needs no second pass.  compact() consults
 # it for the tables that the step's attention context has already checked.
+# The list keeps its tables alive, so it is bounded to about one step's
+# requests; a table that fell out is simply checked again.
 _PROVEN_TABLES: "OrderedDict[int, tuple[tuple, int]]" = OrderedDict()
-_PROVEN_LIMIT = 1024
+_PROVEN_LIMIT = 256
 
 
 def note_proven_tables(tables, num_blocks: int) -> None:
