@@ -639,7 +639,7 @@ def run_c4(args, device) -> int:
     per_layer = cfg.batch * L * 2 * cfg.hkv * cfg.d * 2 + 2 * cfg.batch * cfg.hq * cfg.d * 2 + \
         cfg.batch * per_seq * 4 + 4 * cfg.batch * cfg.hkv * cfg.d * 2
     gbps = cfg.layers * per_layer / (ms * 1e-3) / 1e9
-    work = backend.create(cache, md)._work(spec.layers[0], cfg.dtype)
+    work = backend.create(cache, md).work_of(spec.layers[0])
     rec = _record(
         metric="long-context paged decode (C4): HBM GB/s over 28 layers + tokens/s, Qwen2.5-7B shape bs16 ctx32k",
         value=gbps, unit="GB/s", higher=True, args=args, ms=ms, dtype="bf16",

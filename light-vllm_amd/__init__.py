@@ -11,12 +11,7 @@ import sys as _sys
 _sys.modules.setdefault("light_vllm_amd", _sys.modules[__name__])
 
 from light_vllm_amd.backend import HipPagedAttention, HipPagedAttentionBackend  # noqa: E402
-from light_vllm_amd.errors import (  # noqa: E402
-    ExecutionError,
-    ExecutionNotReadyError,
-    KVCacheCapacityError,
-    KVCacheError,
-)
+from light_vllm_amd import errors  # noqa: E402
 from light_vllm_amd.interfaces import (  # noqa: E402
     AttentionLayerSpec,
     DraftTree,
@@ -64,3 +59,15 @@ __all__ = [
     "query_visibility",
     "semantic_positions",
 ]
+
+
+# The exception classes are the ones bound in ``errors`` at lookup time (the
+# host's own classes when light-vllm is importable or ``errors.bind`` named
+# them), so ``light_vllm_amd.KVCacheError`` is always what raise sites raise.
+_ERROR_NAMES = ("ExecutionError", "ExecutionNotReadyError", "KVCacheCapacityError", "KVCacheError")
+
+
+def __getattr__(name: str):
+    if name in _ERROR_NAMES:
+        return getattr(errors, name)
+    raise AttributeError(f"module {__name__!r} has no attribute {name!r}")

@@ -4,12 +4,18 @@ Drop-in for light-vllm's ``PagedAttentionBackend`` protocol
 (src/light_vllm/runtime/execution/paged_attention.py:209-223).  A context is
 created once per model step by ``PagedStepHandler.forward``
 (src/light_vllm/runtime/execution/worker.py:286) and its ``forward`` is called
-once per layer by the model (src/light_vllm/modeling/models/qwen2.py:417-423):
+once per layer by the model (src/light_vllm/modeling/models/qwen2.py:417-423).
 
-1. validate shapes exactly as ``_validate_paged_attention_tensors``
+``create`` proves the step's block tables (light-vllm's rules and messages),
+and builds the step plan for every layer shape of the cache in the native host
+planner: slots, per-request records, flat tables, ancestor rows and the
+decode / prefill work lists go to the GPU in one non-blocking copy.
+
+``forward``:
+1. validates shapes exactly as ``_validate_paged_attention_tensors``
    (paged_attention.py:226-247) plus the dtype/device rule of the Triton
    backend (triton_paged_attention.py:475-478);
-2. attend with write-before-attend semantics: the stream-K decode kernel
+2. attends with write-before-attend semantics: the stream-K decode kernel
    (short query runs) and the MFMA prefill kernel (long ones) in its 8-wave
    shape read this step's K/V from the inputs and append their own requests'
    tokens to their pool slots themselves, and a merge kernel combines split
@@ -17,7 +23,6 @@ once per layer by the model (src/light_vllm/modeling/models/qwen2.py:417-423):
    (HIP ``lvamd_kv_append``), and with ``rotary=`` one rotary-append launch
    writes the pool first.  Everything is on the current stream with no host
    synchronisation.
-
 """
 
 from __future__ import annotations
@@ -25,10 +30,9 @@ from __future__ import annotations
 import torch
 from torch import Tensor
 
-from light_vllm_amd import native
-from light_vllm_amd.errors import KVCacheError
+from light_vllm_amd import errors, native
 from light_vllm_amd.paged_cache import current_stream, dtype_code, hip_append, hip_append_rotary
-from light_vllm_amd.plan import UNIT_TOKENS, StepPlan
+from light_vllm_amd.plan import DECODE_MAX_COLUMNS, PREFILL_MIN_TILES, UNIT_TOKENS, Staging, StepPlan
 
 SUPPORTED_HEAD_SIZES = (32, 64, 80, 96, 128, 256)
 
@@ -41,16 +45,20 @@ def validate_paged_attention_tensors(cache, metadata, layer_id: str, query: Tens
     """
 
     layer_spec = cache.layer_spec(layer_id)
-    if query.ndim != 3:
-        raise KVCacheError("paged attention query must have three dimensions")
-    if query.shape[0] != key.shape[0] or value.shape != key.shape:
-        raise KVCacheError("paged attention Q/K/V token dimensions must match")
-    if query.shape[0] != metadata.num_query_tokens:
-        raise KVCacheError("paged attention metadata token count does not match query")
-    if tuple(query.shape[1:]) != (layer_spec.num_query_heads, layer_spec.head_size):
-        raise KVCacheError("paged attention query shape does not match the layer spec")
-    if tuple(key.shape[1:]) != (layer_spec.num_kv_heads, layer_spec.head_size):
-        raise KVCacheError("paged attention K/V shape does not match the layer spec")
+    rules = (
+        (lambda: query.ndim == 3, "paged attention query must have three dimensions"),
+        (lambda: query.shape[0] == key.shape[0] and value.shape == key.shape,
+         "paged attention Q/K/V token dimensions must match"),
+        (lambda: query.shape[0] == metadata.num_query_tokens,
+         "paged attention metadata token count does not match query"),
+        (lambda: tuple(query.shape[1:]) == (layer_spec.num_query_heads, layer_spec.head_size),
+         "paged attention query shape does not match the layer spec"),
+        (lambda: tuple(key.shape[1:]) == (layer_spec.num_kv_heads, layer_spec.head_size),
+         "paged attention K/V shape does not match the layer spec"),
+    )
+    for holds, message in rules:
+        if not holds():
+            raise errors.KVCacheError(message)
     return layer_spec
 
 
@@ -81,37 +89,33 @@ def _rows_aligned(t: Tensor) -> bool:
     ) % 16 == 0
 
 
+def _workspace_floats(work, spec, prefill_columns: int) -> tuple[int, int]:
+    """(decode partial floats, prefill partial floats) of a layer shape's work."""
+
+    per_row = spec.head_size + 2
+    dec = work.num_partial_slots * spec.num_kv_heads * 16 * work.col_tiles * per_row
+    pre = work.num_prefill_partial_slots * spec.num_kv_heads * prefill_columns * per_row
+    return dec, pre
+
+
 class _LayerLaunch:
     """Launch facts shared by every layer of one shape in one step plan.
 
-    Holds the work lists and every kernel argument that does not depend on
-    the layer's tensors, so a layer's ``forward`` only reads tensor pointers
-    and strides.
+    Holds every kernel argument that does not depend on the layer's tensors,
+    so a layer's ``forward`` only reads tensor pointers and strides.
     """
 
-    __slots__ = ("work", "group", "dtype", "decode_args", "merge_args", "prefill_args", "prefill_merge_args",
+    __slots__ = ("work", "dtype", "decode_args", "merge_args", "prefill_args", "prefill_merge_args",
                  "workspace_ptr")
 
-    @staticmethod
-    def workspace_floats(work, spec, prefill_columns: int) -> tuple[int, int]:
-        """(decode partial floats, prefill partial floats) of this work."""
-
-        per_row = spec.head_size + 2
-        dec = work.num_partial_slots * spec.num_kv_heads * 16 * work.col_tiles * per_row
-        pre = work.num_prefill_partial_slots * spec.num_kv_heads * prefill_columns * per_row
-        return dec, pre
-
-    def __init__(self, plan: StepPlan, work, spec, group: int, dtype: int, block_size: int,
-                 workspace_ptr: int | None, prefill_columns: int) -> None:
+    def __init__(self, plan: StepPlan, work, spec, dtype: int, block_size: int, workspace_ptr: int | None,
+                 prefill_columns: int) -> None:
+        group = spec.num_query_heads // spec.num_kv_heads
         self.work = work
-        self.group = group
         self.dtype = dtype
         self.workspace_ptr = workspace_ptr
-        self.decode_args = None
-        self.merge_args = None
-        self.prefill_args = None
-        self.prefill_merge_args = None
-        dec_floats, pre_floats = self.workspace_floats(work, spec, prefill_columns)
+        self.decode_args = self.merge_args = self.prefill_args = self.prefill_merge_args = None
+        dec_floats, pre_floats = _workspace_floats(work, spec, prefill_columns)
         part_acc = part_ml = pre_acc = pre_ml = None
         if dec_floats:
             part_acc = workspace_ptr
@@ -122,30 +126,31 @@ class _LayerLaunch:
         if work.waves_per_head:
             # lvamd_paged_decode arguments after the output strides, up to the scale.
             self.decode_args = (
-                work.pieces.data_ptr(), work.wave_first.data_ptr(), work.waves_per_head,
-                plan.tables.data_ptr(), plan.vis.data_ptr(),
+                work.pieces_ptr, work.wave_first_ptr, work.waves_per_head, plan.tables_ptr, plan.vis_ptr,
                 part_acc, part_ml, work.num_partial_slots,
                 spec.num_kv_heads, group, spec.head_size, work.col_tiles, block_size,
             )
         if work.num_jobs:
             # lvamd_paged_attention_merge arguments after the output strides, up to the stream.
             self.merge_args = (part_acc, part_ml) + (
-                work.jobs.data_ptr(), work.num_jobs, spec.num_kv_heads, group, spec.head_size, work.col_tiles,
+                work.jobs_ptr, work.num_jobs, spec.num_kv_heads, group, spec.head_size, work.col_tiles,
                 work.merge_columns, dtype,
             )
         if work.num_prefill_units:
             # lvamd_paged_prefill arguments after the output strides, up to the scale.
             self.prefill_args = (
-                plan.req_meta.data_ptr(), plan.tables.data_ptr(), plan.vis.data_ptr(),
-                work.prefill_units.data_ptr(), work.num_prefill_units,
+                plan.req_meta_ptr, plan.tables_ptr, plan.vis_ptr, work.units_ptr, work.num_prefill_units,
                 pre_acc, pre_ml, work.num_prefill_partial_slots,
                 spec.num_kv_heads, group, spec.head_size, work.prefill_waves, block_size,
             )
         if work.num_prefill_jobs:
             self.prefill_merge_args = (pre_acc, pre_ml) + (
-                work.prefill_jobs.data_ptr(), work.num_prefill_jobs, spec.num_kv_heads, group, spec.head_size,
+                work.prefill_jobs_ptr, work.num_prefill_jobs, spec.num_kv_heads, group, spec.head_size,
                 prefill_columns // 16, work.prefill_merge_columns, dtype,
             )
+
+
+_NO_APPEND = (None, 0, 0, None, 0, 0)
 
 
 class HipPagedAttention:
@@ -154,17 +159,11 @@ class HipPagedAttention:
     # forward accepts rotary=(cosines, sines): RoPE is applied inside the append.
     supports_rotary = True
 
-    def __init__(self, cache, metadata, workspace: _Workspace, plan: StepPlan, use_prefill: bool = True,
-                 col_tiles: int | None = None, split_prefill: bool = True, prefill_waves: int | None = None) -> None:
+    def __init__(self, backend: "HipPagedAttentionBackend", cache, plan: StepPlan) -> None:
+        self._backend = backend
         self._cache = cache
         self._config = cache.config
-        self._use_prefill = use_prefill
-        self._col_tiles = col_tiles
-        self._split_prefill = split_prefill
-        self._prefill_waves = prefill_waves
-        self._metadata = metadata
         self._layer_ids: set[str] = set()
-        self._workspace = workspace
         self._plan = plan
         self._lib = native.load()
 
@@ -189,38 +188,40 @@ class HipPagedAttention:
         """
 
         if layer_id in self._layer_ids:
-            raise KVCacheError(f"paged attention layer {layer_id!r} ran more than once")
+            raise errors.KVCacheError(f"paged attention layer {layer_id!r} ran more than once")
         self._layer_ids.add(layer_id)
         spec = validate_paged_attention_tensors(self._cache, self._plan, layer_id, query, key, value)
         config = self._config
         if query.device != config.device or query.dtype != config.dtype:
-            raise KVCacheError("HIP paged attention query dtype and device must match the KV cache")
+            raise errors.KVCacheError("HIP paged attention query dtype and device must match the KV cache")
         if key.dtype != config.dtype or value.dtype != config.dtype or key.device != config.device or (
             value.device != config.device
         ):
-            raise KVCacheError("paged KV update dtype and device must match the cache")
+            raise errors.KVCacheError("paged KV update dtype and device must match the cache")
         if spec.head_size not in SUPPORTED_HEAD_SIZES:
-            raise KVCacheError(
+            raise errors.KVCacheError(
                 f"HIP paged attention supports head sizes {SUPPORTED_HEAD_SIZES}, not {spec.head_size}"
             )
 
         if not _rows_aligned(query):
             query = query.contiguous()
         out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
-        launch = self._launch(spec, query.dtype)
+        launch = self._launch(spec)
         layer = self._cache.layer(layer_id)
         stream = current_stream(query.device)
         lib = self._lib
+        plan = self._plan
         if rotary is not None:
             # The rotated queries go to a fresh buffer and the pool receives
             # the whole step's rotated K and V, so attention reads the pool.
-            query = hip_append_rotary(self._cache, layer_id, query, key, value, rotary, self._plan.slots)
-            new_kv = (None, 0, 0, None, 0, 0)
+            query = hip_append_rotary(self._cache, layer_id, query, key, value, rotary, plan.slots_ptr,
+                                      plan.num_tokens)
+            new_kv = _NO_APPEND
         elif launch.prefill_args is not None and launch.work.prefill_waves != 8:
             # The 4-wave prefill shape reads this step's K/V from the pool, so
             # the whole step is appended first.
-            hip_append(self._cache, layer_id, key, value, self._plan.slots)
-            new_kv = (None, 0, 0, None, 0, 0)
+            hip_append(self._cache, layer_id, key, value, plan.slots_ptr, plan.num_tokens)
+            new_kv = _NO_APPEND
         else:
             # The decode kernel and the 8-wave prefill shape append their own
             # requests' tokens (fused append): they read this step's keys and
@@ -254,7 +255,6 @@ class HipPagedAttention:
                              "lvamd_paged_attention_merge")
         return out
 
-
     def decode_launch(
         self, layer_id: str, query: Tensor, out: Tensor, *, scale: float, key: Tensor | None = None,
         value: Tensor | None = None,
@@ -265,8 +265,7 @@ class HipPagedAttention:
         without, the pool must already hold this step's K/V.
         """
 
-        spec = self._cache.layer_spec(layer_id)
-        launch = self._launch(spec, query.dtype)
+        launch = self._launch(self._cache.layer_spec(layer_id))
         if launch.decode_args is None:
             return None
         return _DecodeLaunch(self._lib, launch, self._cache.layer(layer_id), query, key, value, out, float(scale))
@@ -274,15 +273,14 @@ class HipPagedAttention:
     def prefill(self, layer_id: str, query: Tensor, out: Tensor, *, scale: float) -> None:
         """Only the prefill kernel of this layer (the pool must hold the step's K/V)."""
 
-        spec = self._cache.layer_spec(layer_id)
-        launch = self._launch(spec, query.dtype)
+        launch = self._launch(self._cache.layer_spec(layer_id))
         if launch.prefill_args is None:
             return
         layer = self._cache.layer(layer_id)
         stream = current_stream(query.device)
         o_args = (out.data_ptr(), out.stride(0), out.stride(1))
         native.check(self._lib.lvamd_paged_prefill(
-            query.data_ptr(), query.stride(0), query.stride(1), None, 0, 0, None, 0, 0,
+            query.data_ptr(), query.stride(0), query.stride(1), *_NO_APPEND,
             layer.keys.data_ptr(), layer.values.data_ptr(), *o_args,
             *launch.prefill_args, float(scale), launch.dtype, stream,
         ), "lvamd_paged_prefill")
@@ -291,54 +289,31 @@ class HipPagedAttention:
             native.check(self._lib.lvamd_paged_attention_merge(m[0], m[1], *o_args, *m[2:], stream),
                          "lvamd_paged_attention_merge")
 
-    def _launch(self, spec, dtype) -> _LayerLaunch:
-        """The launch facts of this layer shape, built once per plan and options."""
+    def work_of(self, spec):
+        """The work lists this step runs for layers of ``spec``'s shape."""
 
-        code = dtype_code(dtype)
-        key = (spec.num_query_heads, spec.num_kv_heads, spec.head_size, code, self._use_prefill, self._col_tiles,
-               self._split_prefill, self._prefill_waves)
+        return self._launch(spec).work
+
+    def _launch(self, spec) -> _LayerLaunch:
+        """The launch facts of this layer shape, bound once per plan."""
+
+        backend = self._backend
+        key = (spec.num_query_heads, spec.num_kv_heads, spec.head_size)
         plan = self._plan
         found = plan.launches.get(key)
-        if found is not None and found.workspace_ptr is not None and found.workspace_ptr != self._workspace.ptr():
+        if found is not None and found.workspace_ptr is not None and found.workspace_ptr != backend.workspace.ptr():
             found = None  # the workspace (shared by all plans) was regrown since
         if found is None:
-            work = self._work(spec, dtype)
-            group = spec.num_query_heads // spec.num_kv_heads
-            columns = native.prefill_unit_columns(code, spec.head_size) if self._use_prefill else 0
-            dec_floats, pre_floats = _LayerLaunch.workspace_floats(work, spec, columns)
+            code = dtype_code(self._config.dtype)
+            work = plan.layer_work(backend.kernel_facts(spec, code, self._config.block_size))
+            columns = backend.prefill_columns(code, spec.head_size)
+            dec_floats, pre_floats = _workspace_floats(work, spec, columns)
             ptr = None
             if dec_floats + pre_floats:
-                ptr = self._workspace.get(dec_floats + pre_floats, self._config.device).data_ptr()
-            found = _LayerLaunch(plan, work, spec, group, code, self._config.block_size, ptr, columns)
+                ptr = backend.workspace.get(dec_floats + pre_floats, self._config.device).data_ptr()
+            found = _LayerLaunch(plan, work, spec, code, self._config.block_size, ptr, columns)
             plan.launches[key] = found
         return found
-
-    def _work(self, spec, dtype):
-        group = spec.num_query_heads // spec.num_kv_heads
-        code = dtype_code(dtype)
-        columns = native.prefill_unit_columns(code, spec.head_size) if self._use_prefill else 0
-        max_ctw = native.decode_max_col_tiles(code, spec.head_size)
-        ctw = self._col_tiles
-        if ctw is None:
-            ctw = self._plan.choose_col_tiles(group, columns, max_ctw)
-        ctw = min(ctw, max_ctw)
-        resident = native.resident_decode_waves(code, spec.head_size, ctw)
-        unit = native.decode_tile_tokens(code, spec.head_size, ctw)
-        key_tokens = prefill_resident = 0
-        waves = 4
-        if columns:
-            key_tokens = native.prefill_key_tokens(code, spec.head_size)
-            if self._split_prefill:
-                prefill_resident = native.prefill_resident_units(code, spec.head_size, 4)
-            wide = native.prefill_waves_built(code, spec.head_size, 8)
-            if self._prefill_waves is not None:
-                waves = 8 if self._prefill_waves == 8 and wide else 4
-            else:
-                waves = self._plan.prefill_waves(group, spec.num_kv_heads, columns, key_tokens, prefill_resident, wide)
-            if waves != 4 and self._split_prefill:
-                prefill_resident = native.prefill_resident_units(code, spec.head_size, waves)
-        return self._plan.work(group, spec.num_kv_heads, resident, columns, unit, ctw, key_tokens, prefill_resident,
-                               waves)
 
 
 class _DecodeLaunch:
@@ -349,7 +324,7 @@ class _DecodeLaunch:
         stream = current_stream(query.device)
         self._lib = lib
         if key is None:
-            new_kv = (None, 0, 0, None, 0, 0)
+            new_kv = _NO_APPEND
         else:
             new_kv = (key.data_ptr(), key.stride(0), key.stride(1), value.data_ptr(), value.stride(0), value.stride(1))
         o_args = (out.data_ptr(), out.stride(0), out.stride(1))
@@ -374,8 +349,8 @@ class _DecodeLaunch:
 class HipPagedAttentionBackend:
     """Creates one ``HipPagedAttention`` per model step.
 
-    Construction fails with ``ExecutionNotReadyError`` when the HIP library is
-    missing, like the Triton backend without Triton
+    Construction fails with ``ExecutionNotReadyError`` when the HIP library or
+    the host planner is missing, like the Triton backend without Triton
     (triton_paged_attention.py:566-570).  The step plan of the most recent
     metadata object is kept: metadata objects are immutable, so a second
     ``create`` with the same object (and a cache of the same geometry) reuses
@@ -397,31 +372,72 @@ class HipPagedAttentionBackend:
         falls back to 4 where it is not built)."""
 
         native.load()
+        native.host()
         if partition_tokens is not None and (partition_tokens <= 0 or partition_tokens % UNIT_TOKENS):
             raise ValueError(f"partition_tokens must be a positive multiple of {UNIT_TOKENS}")
         if decode_col_tiles is not None and decode_col_tiles not in native.DECODE_COL_TILES:
             raise ValueError(f"decode_col_tiles must be one of {native.DECODE_COL_TILES}")
-        self._workspace = _Workspace()
+        if prefill_waves not in (None, 4, 8):
+            raise ValueError("prefill_waves must be 4 or 8")
+        self.workspace = _Workspace()
         self._use_prefill = use_prefill_kernel
         self._partition_tokens = partition_tokens
         self._col_tiles = decode_col_tiles
-        if prefill_waves not in (None, 4, 8):
-            raise ValueError("prefill_waves must be 4 or 8")
         self._split_prefill = split_prefill
         self._prefill_waves = prefill_waves
+        self._staging: dict[torch.device, Staging] = {}
+        self._facts: dict[tuple, tuple[int, ...]] = {}
         self._last: tuple[object, object, StepPlan] | None = None
+
+    def prefill_columns(self, code: int, head_size: int) -> int:
+        return native.prefill_unit_columns(code, head_size) if self._use_prefill else 0
+
+    def kernel_facts(self, spec, code: int, block_size: int) -> tuple[int, ...]:
+        """The library's figures for this layer shape (``plan.KERNEL_FACTS``
+        order), queried once per shape and device."""
+
+        key = (spec.num_query_heads, spec.num_kv_heads, spec.head_size, code, block_size, torch.cuda.current_device())
+        found = self._facts.get(key)
+        if found is None:
+            d = spec.head_size
+            group = spec.num_query_heads // spec.num_kv_heads
+            columns = self.prefill_columns(code, d)
+            max_ctw = native.decode_max_col_tiles(code, d)
+            has4 = max_ctw >= 4
+            key_tokens = native.prefill_key_tokens(code, d) if columns else 0
+            wide = bool(columns) and native.prefill_waves_built(code, d, 8)
+            found = (
+                group, spec.num_kv_heads, block_size, columns, key_tokens, int(self._split_prefill),
+                self._col_tiles or 0, self._prefill_waves or 0, max_ctw, int(wide),
+                native.resident_decode_waves(code, d, 1), native.decode_tile_tokens(code, d, 1),
+                native.resident_decode_waves(code, d, 4) if has4 else 0,
+                native.decode_tile_tokens(code, d, 4) if has4 else 0,
+                native.prefill_resident_units(code, d, 4) if columns else 0,
+                native.prefill_resident_units(code, d, 8) if wide else 0,
+                self._partition_tokens or 0, DECODE_MAX_COLUMNS, 4, PREFILL_MIN_TILES,
+            )
+            self._facts[key] = found
+        return found
 
     def create(self, cache, metadata) -> HipPagedAttention:
         config = cache.config
-        key = (config.num_blocks, config.block_size, config.device)
+        if config.device.type != "cuda":
+            raise errors.KVCacheError("HIP paged attention requires a GPU KV cache")
+        geometry = (config.num_blocks, config.block_size, config.device)
         last = self._last
-        if last is not None and last[0] == key and last[1] is metadata:
-            plan = last[2]
-        else:
-            if config.device.type != "cuda":
-                raise KVCacheError("HIP paged attention requires a GPU KV cache")
-            plan = StepPlan(metadata, block_size=config.block_size, device=config.device, num_blocks=config.num_blocks,
-                            partition_tokens=self._partition_tokens)
-            self._last = (key, metadata, plan)
-        return HipPagedAttention(cache, metadata, self._workspace, plan, self._use_prefill, self._col_tiles,
-                                 self._split_prefill, self._prefill_waves)
+        if last is not None and last[0] == geometry and last[1] is metadata:
+            return HipPagedAttention(self, cache, last[2])
+        staging = self._staging.get(config.device)
+        if staging is None:
+            staging = self._staging[config.device] = Staging(config.device)
+        plan = StepPlan(metadata, block_size=config.block_size, device=config.device, num_blocks=config.num_blocks,
+                        partition_tokens=self._partition_tokens, staging=staging, defer_upload=True)
+        # Every layer shape's work lists go up with the step facts.
+        code = dtype_code(config.dtype)
+        shapes = {(s.num_query_heads, s.num_kv_heads, s.head_size): s for s in cache.model_spec.layers}
+        for spec in shapes.values():
+            if spec.head_size in SUPPORTED_HEAD_SIZES:
+                plan.layer_work(self.kernel_facts(spec, code, config.block_size))
+        plan.commit()
+        self._last = (geometry, metadata, plan)
+        return HipPagedAttention(self, cache, plan)

@@ -1,7 +1,10 @@
-"""Build ``liblvamd_hip.so`` for gfx950 with hipcc (no CMake, no torch headers).
+"""Build ``liblvamd_hip.so`` for gfx950 with hipcc (no CMake, no torch headers),
+and the native host planner ``_lvamd_host`` with g++.
 
 Each HIP source compiles to an object in parallel; the objects link into one
-shared library next to this file, which travels with the source tree.
+shared library next to this file, which travels with the source tree.  The
+host planner is a CPython extension module built against this interpreter's
+headers, also next to this file.
 Usage: ``python light-vllm_amd/build.py`` or ``__graft_entry__.build()``.
 """
 
@@ -12,6 +15,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent
@@ -55,12 +59,40 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+HOST_SOURCE = CSRC / "lvamd_host.cpp"
+
+
+def host_module_path() -> Path:
+    """The native host planner, a CPython extension next to this file."""
+
+    return PACKAGE_DIR / ("_lvamd_host" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def _build_host() -> Path:
+    """Compile the host planner with g++ against this interpreter's headers."""
+
+    out = host_module_path()
+    tmp = out.with_name(out.name + ".tmp")
+    cxx = shutil.which("g++") or "g++"
+    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wextra", "-Wno-missing-field-initializers",
+           f"-I{sysconfig.get_paths()['include']}", str(HOST_SOURCE), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"g++ failed for {HOST_SOURCE.name}:\n{proc.stderr}")
+    if proc.stderr.strip():
+        print(proc.stderr, file=sys.stderr)
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = True) -> Path:
     BUILD_DIR.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
-    jobs = min(len(sources), max(1, min(8, os.cpu_count() or 1)))
+    jobs = min(len(sources) + 1, max(1, min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        host = pool.submit(_build_host)
         objects = list(pool.map(_compile, sources))
+        host.result()
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects),
            "-Wl,-rpath,/opt/rocm/lib"]

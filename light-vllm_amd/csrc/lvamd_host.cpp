@@ -1,0 +1,1028 @@
+// lvamd_host.cpp — native host side of the paged-KV backend (CPython
+// extension module _lvamd_host, built with g++ against the interpreter's
+// headers; no numpy or torch headers).
+//
+// One model step of light-vllm hands the backend Python tuples: a block
+// table per request, computed-token counts, query layouts.  Everything the
+// gfx950 kernels need is derived from them here, in single passes over the
+// Python objects, into flat int32/int64 arrays the caller stages to the GPU:
+//
+//   flatten     block tables -> flat int32 ids + per-request counts (or any
+//               int sequences -> int64), with the metadata constructor's
+//               "non-negative int" rule
+//               (src/light_vllm/runtime/execution/paged_attention.py:51-62);
+//   validate    the block-table rules of validate_block_tables
+//               (paged_attention.py:138-172), reporting the rule that fires
+//               first in the reference's order, and the request;
+//   layouts     query lengths and uint32 ancestor bit rows of tree layouts
+//               (query_visibility, src/light_vllm/runtime/execution/layout.py:44-55);
+//   stage       slots (slot_mapping, paged_attention.py:110-136) and the
+//               per-request records, written straight into a staging buffer;
+//   decode_work / prefill_work / layer_work
+//               the stream-K split of decode rows and the prefill units, and
+//               (layer_work) the per-step kernel choices of a layer shape;
+//   compact_pairs
+//               the rules and slots of PagedKVCache.compact
+//               (src/light_vllm/runtime/execution/paged_cache.py:257-314) for
+//               many requests in one call.
+//
+// Every function returns status codes; the Python layer turns them into the
+// host's exception classes and messages.  Functions run with the GIL held
+// and keep per-process scratch (epoch-stamped owner arrays) between calls.
+
+#define PY_SSIZE_T_CLEAN
+#include <Python.h>
+
+#include <algorithm>
+#include <climits>
+#include <cstdint>
+#include <cstring>
+#include <limits>
+#include <vector>
+
+namespace {
+
+// Fields per record, equal to the LVAMD_* constants of include/lvamd_paged_kv.h.
+constexpr int kReqFields = 8;
+constexpr int kPieceFields = 16;
+constexpr int kMergeFields = 8;
+constexpr int kPrefillFields = 8;
+constexpr int kPieceBlocks = 5;  // first-tile block ids in piece fields 11..15
+constexpr int kTableSlice = 256;  // decode kernel's LDS copy of a piece's table slice
+
+// A contiguous buffer argument (numpy array, bytearray, memoryview).
+class Buf {
+ public:
+  Buf(PyObject* obj, bool writable, Py_ssize_t itemsize, const char* what) {
+    const int flags = PyBUF_C_CONTIGUOUS | (writable ? PyBUF_WRITABLE : 0);
+    if (PyObject_GetBuffer(obj, &view_, flags) != 0) return;
+    held_ = true;
+    if (view_.itemsize != itemsize && !(view_.itemsize == 1 && view_.len % itemsize == 0)) {
+      PyErr_Format(PyExc_TypeError, "%s: expected %zd-byte items", what, itemsize);
+      return;
+    }
+    ok_ = true;
+    count_ = view_.len / itemsize;
+  }
+  ~Buf() {
+    if (held_) PyBuffer_Release(&view_);
+  }
+  Buf(const Buf&) = delete;
+  Buf& operator=(const Buf&) = delete;
+  bool ok() const { return ok_; }
+  Py_ssize_t count() const { return count_; }
+  template <typename T>
+  T* data() const {
+    return static_cast<T*>(view_.buf);
+  }
+
+ private:
+  Py_buffer view_{};
+  bool held_ = false;
+  bool ok_ = false;
+  Py_ssize_t count_ = 0;
+};
+
+// A bytearray of n items of T, zero-filled when asked.
+template <typename T>
+PyObject* new_array(Py_ssize_t n, T** out, bool zero = false) {
+  PyObject* arr = PyByteArray_FromStringAndSize(nullptr, n * (Py_ssize_t)sizeof(T));
+  if (arr == nullptr) return nullptr;
+  *out = reinterpret_cast<T*>(PyByteArray_AS_STRING(arr));
+  if (zero && n) std::memset(*out, 0, (size_t)n * sizeof(T));
+  return arr;
+}
+
+bool want_args(Py_ssize_t got, Py_ssize_t want, const char* name) {
+  if (got == want) return true;
+  PyErr_Format(PyExc_TypeError, "%s takes %zd arguments (%zd given)", name, want, got);
+  return false;
+}
+
+bool as_i64(PyObject* o, int64_t* v) {
+  *v = PyLong_AsLongLong(o);
+  return !(*v == -1 && PyErr_Occurred());
+}
+
+// ---------------------------------------------------------------------------
+// flatten(sequences, wide) -> (flat bytearray, counts int64 bytearray, status)
+// The concatenation of a sequence of int sequences (block tables, or one
+// sequence of per-request counts), as int32 (wide 0) or int64 (wide 1).
+// status 0: ok; 1: an item is not an exact int (bool and numpy integers are
+// not) or is negative.  Values past the item type are clamped to its
+// maximum (the range rules then reject them).
+// ---------------------------------------------------------------------------
+template <typename T>
+int flatten_into(const std::vector<PyObject*>& rows, T* flat, int64_t* counts) {
+  int status = 0;
+  const long long vmax = std::numeric_limits<T>::max();
+  Py_ssize_t k = 0;
+  for (size_t r = 0; r < rows.size(); ++r) {
+    const Py_ssize_t n = PySequence_Fast_GET_SIZE(rows[r]);
+    PyObject** items = PySequence_Fast_ITEMS(rows[r]);
+    counts[r] = n;
+    for (Py_ssize_t i = 0; i < n; ++i, ++k) {
+      PyObject* o = items[i];
+      T v = 0;
+      if (!PyLong_CheckExact(o)) {
+        status = 1;
+      } else {
+        int overflow = 0;
+        const long long x = PyLong_AsLongLongAndOverflow(o, &overflow);
+        if (overflow < 0 || (overflow == 0 && x < 0)) {
+          status = 1;
+        } else {
+          v = (overflow > 0 || x > vmax) ? (T)vmax : (T)x;
+        }
+      }
+      flat[k] = v;
+    }
+  }
+  return status;
+}
+
+PyObject* flatten(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (!want_args(nargs, 2, "flatten")) return nullptr;
+  const int wide = PyObject_IsTrue(args[1]);
+  if (wide < 0) return nullptr;
+  PyObject* outer = PySequence_Fast(args[0], "block tables must be a sequence");
+  if (outer == nullptr) return nullptr;
+  const Py_ssize_t batch = PySequence_Fast_GET_SIZE(outer);
+  std::vector<PyObject*> rows((size_t)batch, nullptr);
+  Py_ssize_t total = 0;
+  PyObject* result = nullptr;
+  PyObject* flat_obj = nullptr;
+  PyObject* counts_obj = nullptr;
+  int64_t* counts = nullptr;
+  int status = 0;
+  for (Py_ssize_t r = 0; r < batch; ++r) {
+    rows[r] = PySequence_Fast(PySequence_Fast_GET_ITEM(outer, r), "a block table must be a sequence");
+    if (rows[r] == nullptr) goto done;
+    total += PySequence_Fast_GET_SIZE(rows[r]);
+  }
+  counts_obj = new_array<int64_t>(batch, &counts);
+  if (counts_obj == nullptr) goto done;
+  if (wide) {
+    int64_t* flat = nullptr;
+    flat_obj = new_array<int64_t>(total, &flat);
+    if (flat_obj == nullptr) goto done;
+    status = flatten_into<int64_t>(rows, flat, counts);
+  } else {
+    int32_t* flat = nullptr;
+    flat_obj = new_array<int32_t>(total, &flat);
+    if (flat_obj == nullptr) goto done;
+    status = flatten_into<int32_t>(rows, flat, counts);
+  }
+  result = Py_BuildValue("(OOi)", flat_obj, counts_obj, status);
+done:
+  Py_XDECREF(flat_obj);
+  Py_XDECREF(counts_obj);
+  for (PyObject* row : rows) Py_XDECREF(row);
+  Py_DECREF(outer);
+  return result;
+}
+
+// ---------------------------------------------------------------------------
+// Per-block scratch, one 16-byte record per physical block, valid when its
+// epoch equals the current call's: the request that last listed the block,
+// and that request's logical index of it with its readonly bit.  Epochs
+// avoid clearing the array per call; a wrap clears it once.
+// ---------------------------------------------------------------------------
+struct BlockRecord {
+  uint32_t epoch;
+  int32_t request;
+  uint32_t owner;  // logical index << 1 | readonly
+  uint32_t pad;
+};
+
+struct BlockScratch {
+  std::vector<BlockRecord> rec;
+  uint32_t epoch = 0;
+
+  void reserve(int64_t num_blocks) {
+    if ((int64_t)rec.size() < num_blocks) {
+      rec.assign((size_t)num_blocks, BlockRecord{0u, -1, 0u, 0u});
+      epoch = 0;
+    }
+  }
+  uint32_t next_epoch() {
+    if (++epoch == 0) {
+      std::fill(rec.begin(), rec.end(), BlockRecord{0u, -1, 0u, 0u});
+      epoch = 1;
+    }
+    return epoch;
+  }
+};
+BlockScratch g_scratch;
+
+// Rule codes of validate, in the order the reference checks them per request.
+enum TableRule {
+  kTablesOk = 0,
+  kTableShort = 1,      // "block table does not cover all scheduled tokens"
+  kTableLong = 2,       // "block table contains unused physical blocks"
+  kTableRange = 3,      // "block table contains an out-of-range physical block"
+  kTableReadonly = 4,   // "readonly prefix blocks exceed the computed prefix"
+  kTableAliasOne = 5,   // "block table aliases a physical block within one request"
+  kTableAliasMany = 6,  // "block tables alias a physical block across requests"
+};
+
+// validate(flat i32, counts i64, computed i64, reserved i64, readonly i64,
+//          num_blocks, block_size) -> (rule, request)
+//
+// Per request, in order: coverage, range and readonly are checked first
+// (cheap, sequential); then one pass over the table visits each block's
+// record once, noting a repeat inside the table (this request already
+// listed the block) and a bad share (another request listed it at another
+// logical index, or one side is not readonly).  A repeat is reported before
+// a bad share of the same request, as the reference checks the whole table
+// for repeats before it looks at sharing.
+PyObject* validate(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (!want_args(nargs, 7, "validate")) return nullptr;
+  Buf flat(args[0], false, 4, "flat"), counts(args[1], false, 8, "counts"), computed(args[2], false, 8, "computed"),
+      reserved(args[3], false, 8, "reserved"), readonly(args[4], false, 8, "readonly");
+  if (!flat.ok() || !counts.ok() || !computed.ok() || !reserved.ok() || !readonly.ok()) return nullptr;
+  int64_t num_blocks = 0, bs = 0;
+  if (!as_i64(args[5], &num_blocks) || !as_i64(args[6], &bs)) return nullptr;
+  const Py_ssize_t batch = counts.count();
+  if (computed.count() != batch || reserved.count() != batch || readonly.count() != batch || bs <= 0 ||
+      num_blocks <= 0 || num_blocks > INT32_MAX) {
+    PyErr_SetString(PyExc_ValueError, "validate: inconsistent arguments");
+    return nullptr;
+  }
+  const int32_t* ids = flat.data<int32_t>();
+  const int64_t* cnt = counts.data<int64_t>();
+  const int64_t* comp = computed.data<int64_t>();
+  const int64_t* res = reserved.data<int64_t>();
+  const int64_t* ro = readonly.data<int64_t>();
+  int64_t total = 0;
+  for (Py_ssize_t r = 0; r < batch; ++r) total += cnt[r];
+  if (total != flat.count()) {
+    PyErr_SetString(PyExc_ValueError, "validate: counts do not match the flat table");
+    return nullptr;
+  }
+  BlockScratch& s = g_scratch;
+  s.reserve(num_blocks);
+  const uint32_t epoch = s.next_epoch();
+  BlockRecord* rec = s.rec.data();
+  int rule = kTablesOk;
+  Py_ssize_t r = 0;
+  for (int64_t off = 0; r < batch; off += cnt[r], ++r) {
+    const int64_t n = cnt[r];
+    const int64_t required = (comp[r] + res[r] + bs - 1) / bs;
+    if (n < required) { rule = kTableShort; break; }
+    if (n > required) { rule = kTableLong; break; }
+    const int32_t* t = ids + off;
+    bool in_range = true;
+    for (int64_t i = 0; i < n; ++i) in_range &= (uint32_t)t[i] < (uint32_t)num_blocks;
+    if (!in_range) { rule = kTableRange; break; }
+    if (ro[r] > n || ro[r] * bs > comp[r]) { rule = kTableReadonly; break; }
+    bool repeat = false, bad_share = false;
+    for (int64_t i = 0; i < n; ++i) {
+      BlockRecord& b = rec[t[i]];
+      const uint32_t mine = ((uint32_t)i << 1) | (uint32_t)(i < ro[r]);
+      if (b.epoch == epoch) {
+        if (b.request == (int32_t)r) {
+          repeat = true;
+        } else {
+          bad_share |= !((b.owner >> 1) == (uint32_t)i && (b.owner & 1u) && (mine & 1u));
+        }
+      }
+      b.epoch = epoch;
+      b.request = (int32_t)r;
+      b.owner = mine;
+    }
+    if (repeat) { rule = kTableAliasOne; break; }
+    if (bad_share) { rule = kTableAliasMany; break; }
+  }
+  return Py_BuildValue("(in)", rule, rule == kTablesOk ? (Py_ssize_t)-1 : r);
+}
+
+// ---------------------------------------------------------------------------
+// layouts(query_layouts) -> (q_lens i64, vis_off i64, vis_words i64, vis u32, status)
+// A layout is anything with a ``parent_indices`` sequence of exact ints.
+// Linear layouts (parent i - 1 for every i) get vis_off -1; the others one
+// uint32 row per query: bit j of word w of row q set iff query 32w + j is q
+// or an ancestor of q.  status 1: a parent is not an int in [-1, index).
+// ---------------------------------------------------------------------------
+PyObject* layouts(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (!want_args(nargs, 1, "layouts")) return nullptr;
+  PyObject* outer = PySequence_Fast(args[0], "query layouts must be a sequence");
+  if (outer == nullptr) return nullptr;
+  const Py_ssize_t batch = PySequence_Fast_GET_SIZE(outer);
+  int64_t *qlen = nullptr, *voff = nullptr, *vwords = nullptr;
+  PyObject* qlen_obj = new_array<int64_t>(batch, &qlen);
+  PyObject* voff_obj = new_array<int64_t>(batch, &voff);
+  PyObject* vwords_obj = new_array<int64_t>(batch, &vwords);
+  std::vector<uint32_t> vis;
+  std::vector<int32_t> parents;
+  PyObject* result = nullptr;
+  int status = 0;
+  if (qlen_obj == nullptr || voff_obj == nullptr || vwords_obj == nullptr) goto done;
+  for (Py_ssize_t r = 0; r < batch; ++r) {
+    PyObject* attr = PyObject_GetAttrString(PySequence_Fast_GET_ITEM(outer, r), "parent_indices");
+    if (attr == nullptr) goto done;
+    PyObject* seq = PySequence_Fast(attr, "parent_indices must be a sequence");
+    Py_DECREF(attr);
+    if (seq == nullptr) goto done;
+    const Py_ssize_t q = PySequence_Fast_GET_SIZE(seq);
+    PyObject** items = PySequence_Fast_ITEMS(seq);
+    parents.resize((size_t)q);
+    bool linear = true;
+    for (Py_ssize_t i = 0; i < q; ++i) {
+      long v = PyLong_CheckExact(items[i]) ? PyLong_AsLong(items[i]) : LONG_MIN;
+      if (v == -1 && PyErr_Occurred()) {
+        PyErr_Clear();
+        v = LONG_MIN;
+      }
+      if (v < -1 || v >= i) status = 1;
+      parents[(size_t)i] = (int32_t)std::max<long>(-1, std::min<long>(v, i - 1));
+      linear &= parents[(size_t)i] == i - 1;
+    }
+    Py_DECREF(seq);
+    qlen[r] = q;
+    if (linear) {
+      voff[r] = -1;
+      vwords[r] = 0;
+      continue;
+    }
+    const int64_t words = (q + 31) / 32;
+    voff[r] = (int64_t)vis.size();
+    vwords[r] = words;
+    vis.resize(vis.size() + (size_t)(q * words), 0u);
+    uint32_t* rows = vis.data() + voff[r];
+    for (Py_ssize_t i = 0; i < q; ++i) {
+      uint32_t* row = rows + i * words;
+      // Ancestors precede their children: row i = row of its parent + bit i.
+      const int32_t p = parents[(size_t)i];
+      if (p >= 0) std::memcpy(row, rows + p * words, (size_t)words * 4);
+      row[i >> 5] |= 1u << (i & 31);
+    }
+  }
+  {
+    uint32_t* out = nullptr;
+    PyObject* vis_obj = new_array<uint32_t>((Py_ssize_t)vis.size(), &out);
+    if (vis_obj == nullptr) goto done;
+    if (!vis.empty()) std::memcpy(out, vis.data(), vis.size() * 4);
+    result = Py_BuildValue("(OOOOi)", qlen_obj, voff_obj, vwords_obj, vis_obj, status);
+    Py_DECREF(vis_obj);
+  }
+done:
+  Py_XDECREF(qlen_obj);
+  Py_XDECREF(voff_obj);
+  Py_XDECREF(vwords_obj);
+  Py_DECREF(outer);
+  return result;
+}
+
+// ---------------------------------------------------------------------------
+// stage(flat i32, counts i64, computed i64, q_lens i64, vis_off i64,
+//       vis_words i64, block_size, slots_out i64[T], req_meta_out i32[B*8]) -> status
+// slots_out[t] = table[pos // bs] * bs + pos % bs for pos = computed + offset;
+// req_meta rows (table_off, blocks, computed, q_len, q_start, vis_off,
+// vis_words, 0).  status 1: a query position past its table (only possible
+// when the tables were not validated).
+// ---------------------------------------------------------------------------
+PyObject* stage(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (!want_args(nargs, 9, "stage")) return nullptr;
+  Buf flat(args[0], false, 4, "flat"), counts(args[1], false, 8, "counts"), computed(args[2], false, 8, "computed"),
+      q_lens(args[3], false, 8, "q_lens"), vis_off(args[4], false, 8, "vis_off"),
+      vis_words(args[5], false, 8, "vis_words");
+  int64_t bs = 0;
+  if (!flat.ok() || !counts.ok() || !computed.ok() || !q_lens.ok() || !vis_off.ok() || !vis_words.ok() ||
+      !as_i64(args[6], &bs))
+    return nullptr;
+  Buf slots(args[7], true, 8, "slots_out"), meta(args[8], true, 4, "req_meta_out");
+  if (!slots.ok() || !meta.ok()) return nullptr;
+  const Py_ssize_t batch = counts.count();
+  const int64_t* cnt = counts.data<int64_t>();
+  const int64_t* comp = computed.data<int64_t>();
+  const int64_t* ql = q_lens.data<int64_t>();
+  int64_t tokens = 0;
+  for (Py_ssize_t r = 0; r < batch; ++r) tokens += ql[r];
+  if (bs <= 0 || computed.count() != batch || q_lens.count() != batch || vis_off.count() != batch ||
+      vis_words.count() != batch || slots.count() != tokens || meta.count() != batch * kReqFields) {
+    PyErr_SetString(PyExc_ValueError, "stage: inconsistent arguments");
+    return nullptr;
+  }
+  const int32_t* ids = flat.data<int32_t>();
+  int64_t* out = slots.data<int64_t>();
+  int32_t* rm = meta.data<int32_t>();
+  int status = 0;
+  int64_t off = 0, t = 0;
+  for (Py_ssize_t r = 0; r < batch; ++r) {
+    int32_t* m = rm + r * kReqFields;
+    m[0] = (int32_t)off;
+    m[1] = (int32_t)cnt[r];
+    m[2] = (int32_t)comp[r];
+    m[3] = (int32_t)ql[r];
+    m[4] = (int32_t)t;
+    m[5] = (int32_t)vis_off.data<int64_t>()[r];
+    m[6] = (int32_t)vis_words.data<int64_t>()[r];
+    m[7] = 0;
+    for (int64_t i = 0; i < ql[r]; ++i, ++t) {
+      const int64_t pos = comp[r] + i;
+      const int64_t lb = pos / bs;
+      if (lb >= cnt[r]) {
+        status = 1;
+        out[t] = -1;
+        continue;
+      }
+      out[t] = (int64_t)ids[off + lb] * bs + (pos - lb * bs);
+    }
+    off += cnt[r];
+  }
+  return PyLong_FromLong(status);
+}
+
+// ---------------------------------------------------------------------------
+// Work lists of one layer shape.
+//
+// Decode rows are the requests whose q_len * group columns fit
+// decode_max_columns (every request when it is 0); a request has
+// ceil(ceil(q_len * group / 16) / col_tiles) column groups, each a segment
+// of computed + q_len tokens.  Stream-K: the segments are laid end to end in
+// unit_tokens units, and the unit range is cut into W balanced contiguous
+// shares (wave w: units [w*total/W, (w+1)*total/W)), W the fewest shares
+// that give the largest share the resident waves would get, and no share
+// above what the kernel's LDS table slice covers.  A wave's share is a list
+// of pieces (the part of each segment inside it); a segment cut into several
+// pieces gets consecutive partial slots and one merge job.
+//
+// Prefill rows are the others.  A unit is up to ``columns`` MFMA columns
+// (query, head-in-group pairs) of one request; it needs the keys up to its
+// last query.  With fewer units than slots_per_head, every unit's tile range
+// is cut into near-equal pieces of at least min_tiles tiles; the pieces of a
+// split unit write consecutive partial slots and one merge job combines
+// them.  Units come heaviest first (key tiles x columns, stable).
+// ---------------------------------------------------------------------------
+struct Requests {
+  const int32_t* meta;  // [batch][kReqFields]
+  int64_t batch;
+  int64_t q_len(int64_t r) const { return meta[r * kReqFields + 3]; }
+  int64_t computed(int64_t r) const { return meta[r * kReqFields + 2]; }
+  const int32_t* row(int64_t r) const { return meta + r * kReqFields; }
+};
+
+struct DecodeLists {
+  std::vector<int32_t> pieces, first, jobs;
+  int64_t waves = 0, per_wave = 0, merge_cols = 1;
+  int32_t slots = 0;
+};
+
+struct DecodeParams {
+  int64_t group, col_tiles, max_cols, hkv, resident, bs, min_units, max_units, unit;
+};
+
+void build_decode(const Requests& q, const int32_t* ids, int64_t nflat, const DecodeParams& d, DecodeLists& out) {
+  struct Seg {
+    int32_t req, group;
+    int64_t start, tiles;
+  };
+  std::vector<Seg> segs;
+  int64_t total = 0;
+  for (int64_t r = 0; r < q.batch; ++r) {
+    const int64_t columns = q.q_len(r) * d.group;
+    if (d.max_cols > 0 && columns > d.max_cols) continue;
+    const int64_t tiles = (q.computed(r) + q.q_len(r) + d.unit - 1) / d.unit;
+    const int64_t ngroups = ((columns + 15) / 16 + d.col_tiles - 1) / d.col_tiles;
+    for (int64_t g = 0; g < ngroups; ++g) {
+      segs.push_back({(int32_t)r, (int32_t)g, total, tiles});
+      total += tiles;
+    }
+  }
+  if (total == 0) return;
+  int64_t cap = std::max<int64_t>(1, ((kTableSlice - 2) * d.bs) / d.unit);
+  if (d.max_units > 0) cap = std::max<int64_t>(1, std::min(cap, d.max_units));
+  int64_t waves = std::max<int64_t>(
+      1, std::min(std::max<int64_t>(1, d.resident / d.hkv), (total + d.min_units - 1) / d.min_units));
+  waves = std::max(waves, (total + cap - 1) / cap);
+  const int64_t per_wave = (total + waves - 1) / waves;
+  waves = (total + per_wave - 1) / per_wave;
+  // Walk segment ends and share bounds together: one piece per step.
+  struct PieceRec {
+    int32_t seg, wave;
+    int64_t lo, hi;
+  };
+  std::vector<PieceRec> recs;
+  recs.reserve(segs.size() + (size_t)waves);
+  std::vector<int32_t> seg_pieces(segs.size(), 0);
+  for (size_t s = 0, pos = 0, w = 0; (int64_t)pos < total;) {
+    const int64_t seg_end = segs[s].start + segs[s].tiles;
+    const int64_t bound = ((int64_t)(w + 1) * total) / waves;
+    const int64_t end = std::min(seg_end, bound);
+    recs.push_back({(int32_t)s, (int32_t)w, (int64_t)pos, end});
+    ++seg_pieces[s];
+    pos = (size_t)end;
+    if (end == seg_end) ++s;
+    if (end == bound) ++w;
+  }
+  const int64_t per_slot = 16 * d.col_tiles;  // columns of one partial slot
+  out.pieces.assign(recs.size() * kPieceFields, 0);
+  out.first.assign((size_t)waves + 1, 0);
+  out.waves = waves;
+  out.per_wave = per_wave;
+  int64_t w = 0;
+  for (size_t p = 0; p < recs.size(); ++p) {
+    const PieceRec& x = recs[p];
+    const Seg& sg = segs[(size_t)x.seg];
+    const int32_t* m = q.row(sg.req);
+    int32_t* o = out.pieces.data() + p * kPieceFields;
+    while (w <= x.wave) out.first[(size_t)w++] = (int32_t)p;
+    const bool multi = seg_pieces[(size_t)x.seg] > 1;
+    const int64_t tok_begin = (x.lo - sg.start) * d.unit;
+    o[0] = sg.req;
+    o[1] = sg.group;
+    o[2] = (int32_t)tok_begin;
+    o[3] = (int32_t)std::min((x.hi - sg.start) * d.unit, q.computed(sg.req) + q.q_len(sg.req));
+    o[4] = multi ? out.slots : -1;
+    o[5] = m[0];   // table_off
+    o[6] = m[2];   // computed
+    o[7] = m[3];   // q_len
+    o[8] = m[4];   // q_start
+    o[9] = m[5];   // vis_off
+    o[10] = m[6];  // vis_words
+    const int64_t lb0 = tok_begin / d.bs;
+    for (int k = 0; k < kPieceBlocks; ++k) {
+      const int64_t lb = lb0 + k, idx = m[0] + lb;
+      o[11 + k] = (lb < m[1] && idx < nflat) ? ids[idx] : 0;
+    }
+    if (multi && x.lo == sg.start) {
+      const int32_t job[kMergeFields] = {sg.req, sg.group, out.slots, seg_pieces[(size_t)x.seg], m[4], m[3], 0, 0};
+      out.jobs.insert(out.jobs.end(), job, job + kMergeFields);
+      // The merge grid covers the most columns any job has.
+      out.merge_cols = std::max(out.merge_cols, std::min(per_slot, (int64_t)m[3] * d.group - sg.group * per_slot));
+    }
+    if (multi) ++out.slots;
+  }
+  while (w <= waves) out.first[(size_t)w++] = (int32_t)recs.size();
+}
+
+struct PrefillLists {
+  std::vector<int32_t> units, jobs;
+  int32_t slots = 0;
+  int64_t merge_cols = 1;
+  double mean_tiles = 0.0;
+};
+
+struct PrefillParams {
+  int64_t group, columns, key_tokens, slots_per_head, min_tiles, max_cols;
+};
+
+// (request, first column, columns, key tiles) of every prefill unit.
+struct Unit {
+  int32_t req;
+  int64_t col0, cols, tiles;
+};
+
+std::vector<Unit> prefill_units_of(const Requests& q, const PrefillParams& p) {
+  std::vector<Unit> units;
+  for (int64_t r = 0; r < q.batch; ++r) {
+    const int64_t ncols = q.q_len(r) * p.group;
+    if (ncols <= p.max_cols) continue;
+    for (int64_t c0 = 0; c0 < ncols; c0 += p.columns) {
+      const int64_t cols = std::min(p.columns, ncols - c0);
+      const int64_t kneed = q.computed(r) + (c0 + cols - 1) / p.group + 1;
+      units.push_back({(int32_t)r, c0, cols, (kneed + p.key_tokens - 1) / p.key_tokens});
+    }
+  }
+  return units;
+}
+
+void build_prefill(const Requests& q, const PrefillParams& p, PrefillLists& out) {
+  const std::vector<Unit> units = prefill_units_of(q, p);
+  const int64_t n = (int64_t)units.size();
+  int64_t tile_sum = 0;
+  for (const Unit& u : units) tile_sum += u.tiles;
+  out.mean_tiles = n ? (double)tile_sum / (double)n : 0.0;
+  std::vector<int64_t> npieces((size_t)n, 1);
+  if (p.slots_per_head > 0 && n < p.slots_per_head) {
+    const int64_t target = std::max(p.min_tiles, (tile_sum + p.slots_per_head - 1) / p.slots_per_head);
+    for (int64_t u = 0; u < n; ++u) npieces[(size_t)u] = std::max<int64_t>(1, (units[(size_t)u].tiles + target - 1) / target);
+  }
+  struct PRec {
+    int64_t unit, t0, t1, i, work;
+    int32_t slot;
+  };
+  std::vector<PRec> recs;
+  for (int64_t u = 0; u < n; ++u) {
+    const int64_t k = npieces[(size_t)u], tiles = units[(size_t)u].tiles;
+    for (int64_t i = 0; i < k; ++i) {
+      const int64_t t0 = (i * tiles) / k, t1 = ((i + 1) * tiles) / k;
+      // Partial slots in (unit, piece) order, before the heaviest-first sort.
+      recs.push_back({u, t0, t1, i, (t1 - t0) * units[(size_t)u].cols, k > 1 ? out.slots++ : -1});
+    }
+  }
+  for (const PRec& x : recs) {
+    if (x.slot < 0 || x.i != 0) continue;
+    const Unit& un = units[(size_t)x.unit];
+    const int32_t* m = q.row(un.req);
+    const int32_t job[kMergeFields] = {un.req, (int32_t)(un.col0 / p.columns), x.slot,
+                                       (int32_t)npieces[(size_t)x.unit], m[4], m[3], 0, 0};
+    out.jobs.insert(out.jobs.end(), job, job + kMergeFields);
+    out.merge_cols = std::max(out.merge_cols, un.cols);
+  }
+  std::stable_sort(recs.begin(), recs.end(), [](const PRec& a, const PRec& b) { return a.work > b.work; });
+  out.units.assign(recs.size() * kPrefillFields, 0);
+  for (size_t k = 0; k < recs.size(); ++k) {
+    const PRec& x = recs[k];
+    const Unit& un = units[(size_t)x.unit];
+    int32_t* o = out.units.data() + k * kPrefillFields;
+    o[0] = un.req;
+    o[1] = (int32_t)un.col0;
+    o[2] = (int32_t)un.cols;
+    o[3] = (int32_t)(x.t0 * p.key_tokens);
+    o[4] = x.i + 1 < npieces[(size_t)x.unit] ? (int32_t)(x.t1 * p.key_tokens) : 0;
+    o[5] = x.slot;
+  }
+}
+
+// Column tiles per decode wave: 4 when the decode rows' K/V re-reads at one
+// tile per wave cost more than the four-tile kernel's slower tiles
+//   sum(seq * ceil(tiles / 4)) * cost4 < sum(seq * tiles),
+// else 1 (always 1 when the four-tile kernel is not built, max_ctw < 4).
+int64_t choose_col_tiles(const Requests& q, int64_t group, int64_t max_cols, int64_t max_ctw, double cost4) {
+  if (max_ctw < 4) return 1;
+  double one = 0.0, four = 0.0;
+  for (int64_t r = 0; r < q.batch; ++r) {
+    const int64_t columns = q.q_len(r) * group;
+    if (max_cols > 0 && columns > max_cols) continue;
+    const double seq = (double)(q.computed(r) + q.q_len(r));
+    const int64_t nct = (columns + 15) / 16;
+    one += seq * (double)nct;
+    four += seq * (double)((nct + 3) / 4);
+  }
+  return four * cost4 < one ? 4 : 1;
+}
+
+// Prefill workgroup shape: 8 waves of one column tile when the units will
+// be split over the resident workgroups or are short (mean key tiles per
+// unit at most wide_max_tiles), else 4 waves of two column tiles.
+int64_t choose_prefill_waves(const Requests& q, const PrefillParams& p, int64_t slots_per_head8, bool wide_built,
+                             double wide_max_tiles) {
+  if (!wide_built) return 4;
+  const std::vector<Unit> units = prefill_units_of(q, p);
+  if (units.empty()) return 4;
+  int64_t tile_sum = 0;
+  for (const Unit& u : units) tile_sum += u.tiles;
+  const bool split = slots_per_head8 > 0 && (int64_t)units.size() < slots_per_head8;
+  return split || (double)tile_sum / (double)units.size() <= wide_max_tiles ? 8 : 4;
+}
+
+template <typename T>
+PyObject* to_bytearray(const std::vector<T>& v) {
+  T* out = nullptr;
+  PyObject* arr = new_array<T>((Py_ssize_t)v.size(), &out);
+  if (arr != nullptr && !v.empty()) std::memcpy(out, v.data(), v.size() * sizeof(T));
+  return arr;
+}
+
+PyObject* decode_result(const DecodeLists& d) {
+  PyObject* a = to_bytearray(d.pieces);
+  PyObject* b = to_bytearray(d.first);
+  PyObject* c = to_bytearray(d.jobs);
+  PyObject* result = (a && b && c) ? Py_BuildValue("(OOOLLiL)", a, b, c, (long long)d.waves, (long long)d.per_wave,
+                                                   d.slots, (long long)d.merge_cols)
+                                   : nullptr;
+  Py_XDECREF(a);
+  Py_XDECREF(b);
+  Py_XDECREF(c);
+  return result;
+}
+
+PyObject* prefill_result(const PrefillLists& p) {
+  PyObject* a = to_bytearray(p.units);
+  PyObject* b = to_bytearray(p.jobs);
+  PyObject* result =
+      (a && b) ? Py_BuildValue("(OOidL)", a, b, p.slots, p.mean_tiles, (long long)p.merge_cols) : nullptr;
+  Py_XDECREF(a);
+  Py_XDECREF(b);
+  return result;
+}
+
+bool requests_of(const Buf& meta, Requests* q, const char* name) {
+  q->meta = meta.data<int32_t>();
+  q->batch = meta.count() / kReqFields;
+  if (meta.count() != q->batch * kReqFields) {
+    PyErr_Format(PyExc_ValueError, "%s: req_meta is not [batch][%d]", name, kReqFields);
+    return false;
+  }
+  return true;
+}
+
+// decode_work(req_meta i32[B*8], flat i32, group, col_tiles, decode_max_columns,
+//             num_kv_heads, resident_waves, block_size, min_units_per_wave,
+//             max_units_per_wave (0 = none), unit_tokens)
+//   -> (pieces i32 [n, 16], wave_first i32 [W + 1], jobs i32 [m, 8],
+//       W, largest share, partial slots, most columns of a merge job)
+PyObject* decode_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (!want_args(nargs, 11, "decode_work")) return nullptr;
+  Buf meta(args[0], false, 4, "req_meta"), flat(args[1], false, 4, "flat");
+  if (!meta.ok() || !flat.ok()) return nullptr;
+  Requests q;
+  if (!requests_of(meta, &q, "decode_work")) return nullptr;
+  DecodeParams d;
+  int64_t* fields[] = {&d.group, &d.col_tiles, &d.max_cols, &d.hkv, &d.resident, &d.bs, &d.min_units, &d.max_units,
+                       &d.unit};
+  for (int i = 0; i < 9; ++i)
+    if (!as_i64(args[2 + i], fields[i])) return nullptr;
+  if (d.group <= 0 || d.col_tiles <= 0 || d.hkv <= 0 || d.bs <= 0 || d.unit <= 0 || d.min_units <= 0) {
+    PyErr_SetString(PyExc_ValueError, "decode_work: inconsistent arguments");
+    return nullptr;
+  }
+  DecodeLists out;
+  build_decode(q, flat.data<int32_t>(), flat.count(), d, out);
+  return decode_result(out);
+}
+
+// prefill_work(req_meta i32[B*8], group, columns, key_tokens, slots_per_head,
+//              min_tiles, decode_max_columns)
+//   -> (units i32 [n, 8], jobs i32 [m, 8], partial slots, mean key tiles per
+//       unit, most columns of a merge job)
+PyObject* prefill_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (!want_args(nargs, 7, "prefill_work")) return nullptr;
+  Buf meta(args[0], false, 4, "req_meta");
+  if (!meta.ok()) return nullptr;
+  Requests q;
+  if (!requests_of(meta, &q, "prefill_work")) return nullptr;
+  PrefillParams p;
+  int64_t* fields[] = {&p.group, &p.columns, &p.key_tokens, &p.slots_per_head, &p.min_tiles, &p.max_cols};
+  for (int i = 0; i < 6; ++i)
+    if (!as_i64(args[1 + i], fields[i])) return nullptr;
+  if (p.group <= 0 || p.columns <= 0 || p.key_tokens <= 0 || p.min_tiles <= 0) {
+    PyErr_SetString(PyExc_ValueError, "prefill_work: inconsistent arguments");
+    return nullptr;
+  }
+  PrefillLists out;
+  build_prefill(q, p, out);
+  return prefill_result(out);
+}
+
+// layer_work(req_meta i32[B*8], flat i32, kernel facts (int64 array, 20
+//            entries, below), cost4, wide_max_tiles)
+//   -> (col_tiles, prefill_waves, decode result or None, prefill result or None)
+//
+// Everything one layer shape needs in one call: the decode kernel's column
+// tiles per wave and the prefill workgroup shape are chosen for this step
+// (unless forced), then both work lists are built.  Kernel facts:
+//   0 group, 1 num_kv_heads, 2 block_size, 3 prefill columns (0: no prefill
+//   kernel), 4 prefill key tokens, 5 split prefill (0/1), 6 forced col tiles
+//   (0: choose), 7 forced prefill waves (0: choose), 8 widest col tiles built,
+//   9 8-wave prefill built (0/1), 10 resident decode waves at 1 col tile,
+//   11 tile tokens at 1, 12 resident at 4, 13 tile tokens at 4, 14 resident
+//   4-wave prefill workgroups, 15 resident 8-wave ones, 16 max tokens per
+//   decode wave (0: no cap), 17 decode max columns, 18 min units per wave,
+//   19 prefill min tiles.
+PyObject* layer_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (!want_args(nargs, 5, "layer_work")) return nullptr;
+  Buf meta(args[0], false, 4, "req_meta"), flat(args[1], false, 4, "flat"), kf(args[2], false, 8, "facts");
+  if (!meta.ok() || !flat.ok() || !kf.ok()) return nullptr;
+  const double cost4 = PyFloat_AsDouble(args[3]), wide_max = PyFloat_AsDouble(args[4]);
+  if (PyErr_Occurred()) return nullptr;
+  Requests q;
+  if (!requests_of(meta, &q, "layer_work")) return nullptr;
+  if (kf.count() != 20) {
+    PyErr_SetString(PyExc_ValueError, "layer_work: expected 20 kernel facts");
+    return nullptr;
+  }
+  const int64_t* k = kf.data<int64_t>();
+  const int64_t group = k[0], hkv = k[1], bs = k[2], columns = k[3];
+  const int64_t max_cols = columns > 0 ? k[17] : 0;
+  if (group <= 0 || hkv <= 0 || bs <= 0) {
+    PyErr_SetString(PyExc_ValueError, "layer_work: inconsistent arguments");
+    return nullptr;
+  }
+  int64_t ctw = k[6] > 0 ? std::min(k[6], k[8]) : choose_col_tiles(q, group, max_cols, k[8], cost4);
+  if (ctw != 4) ctw = 1;
+  PrefillParams p{group, columns > 0 ? columns : 1, k[4] > 0 ? k[4] : 1, 0, k[19] > 0 ? k[19] : 1, max_cols};
+  int64_t waves = 4;
+  bool any_decode = false, any_prefill = false;
+  for (int64_t r = 0; r < q.batch; ++r) {
+    const bool wide = max_cols > 0 && q.q_len(r) * group > max_cols;
+    any_decode |= !wide;
+    any_prefill |= wide;
+  }
+  if (any_prefill) {
+    if (k[7] > 0) {
+      waves = (k[7] == 8 && k[9]) ? 8 : 4;
+    } else {
+      waves = choose_prefill_waves(q, p, k[5] ? k[14] / hkv : 0, k[9] != 0, wide_max);
+    }
+    p.slots_per_head = k[5] ? (waves == 8 ? k[15] : k[14]) / hkv : 0;
+  }
+  PyObject* dec = Py_None;
+  PyObject* pre = Py_None;
+  Py_INCREF(dec);
+  Py_INCREF(pre);
+  if (any_decode) {
+    const int64_t unit = ctw == 4 ? k[13] : k[11];
+    const int64_t max_units = (k[16] > 0 && unit > 0) ? std::max<int64_t>(1, k[16] / unit) : 0;
+    DecodeParams d{group, ctw, max_cols, hkv, ctw == 4 ? k[12] : k[10], bs, k[18] > 0 ? k[18] : 4, max_units, unit};
+    if (d.unit <= 0 || d.resident <= 0) {
+      PyErr_SetString(PyExc_ValueError, "layer_work: missing decode kernel facts");
+      Py_DECREF(dec);
+      Py_DECREF(pre);
+      return nullptr;
+    }
+    DecodeLists out;
+    build_decode(q, flat.data<int32_t>(), flat.count(), d, out);
+    Py_DECREF(dec);
+    dec = decode_result(out);
+  }
+  if (any_prefill && dec != nullptr) {
+    PrefillLists out;
+    build_prefill(q, p, out);
+    Py_DECREF(pre);
+    pre = prefill_result(out);
+  }
+  PyObject* result = (dec && pre) ? Py_BuildValue("(LLOO)", (long long)ctw, (long long)waves, dec, pre) : nullptr;
+  Py_XDECREF(dec);
+  Py_XDECREF(pre);
+  return result;
+}
+
+// ---------------------------------------------------------------------------
+// compact_pairs(requests, num_blocks, block_size, keep_equal) ->
+//   (rule, request index, moved counts i64[R], src i64[n], dst i64[n])
+//
+// Each request is a mapping with PagedKVCache.compact's arguments
+// (block_ids, num_computed_tokens, num_query_tokens,
+// num_reserved_query_tokens, retained_query_indices and optionally
+// num_readonly_prefix_blocks).  Rules in the reference's order
+// (paged_cache.py:276-302); the first failing one is reported:
+//   1 counts not non-negative ints          (ValueError)
+//   2 reserved < queries                     (ValueError)
+//   3 retained index not a non-negative int  (ValueError)
+//   4 retained indices not unique            (ValueError)
+//   5 retained index >= queries              (KVCacheError)
+//   6 table size != blocks the reserve needs (KVCacheError)
+//   7 an id not an int in [0, num_blocks)    (KVCacheError)
+//   8 an id repeated in the table            (KVCacheError)
+//   9 readonly blocks past the computed prefix (KVCacheError)
+//  10 two requests write the same slot       (KVCacheError)
+//  11 a request is missing an argument       (TypeError)
+// moved[r] counts the pairs with src != dst; those with src == dst are
+// dropped from src/dst unless keep_equal is true.
+// ---------------------------------------------------------------------------
+PyObject* compact_pairs(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (!want_args(nargs, 4, "compact_pairs")) return nullptr;
+  int64_t num_blocks = 0, bs = 0;
+  if (!as_i64(args[1], &num_blocks) || !as_i64(args[2], &bs)) return nullptr;
+  const int keep_equal = PyObject_IsTrue(args[3]);
+  if (keep_equal < 0) return nullptr;
+  if (bs <= 0 || num_blocks <= 0 || num_blocks > INT32_MAX) {
+    PyErr_SetString(PyExc_ValueError, "compact_pairs: inconsistent arguments");
+    return nullptr;
+  }
+  PyObject* reqs = PySequence_Fast(args[0], "compact requests must be a sequence");
+  if (reqs == nullptr) return nullptr;
+  const Py_ssize_t nreq = PySequence_Fast_GET_SIZE(reqs);
+  BlockScratch& s = g_scratch;
+  s.reserve(num_blocks);
+  std::vector<int64_t> src, dst, moved((size_t)nreq, 0);
+  std::vector<int64_t> ret;
+  int rule = 0;
+  Py_ssize_t r = 0;
+  static const char* kCountKeys[4] = {"num_computed_tokens", "num_query_tokens", "num_reserved_query_tokens",
+                                      "num_readonly_prefix_blocks"};
+  for (; r < nreq && rule == 0; ++r) {
+    PyObject* req = PySequence_Fast_GET_ITEM(reqs, r);
+    if (!PyDict_Check(req)) {
+      rule = 11;
+      break;
+    }
+    int64_t cnt[4] = {0, 0, 0, 0};
+    for (int k = 0; k < 4 && rule == 0; ++k) {
+      PyObject* v = PyDict_GetItemString(req, kCountKeys[k]);
+      if (v == nullptr) {
+        if (k == 3) continue;  // num_readonly_prefix_blocks defaults to 0
+        rule = 11;
+        break;
+      }
+      int overflow = 0;
+      cnt[k] = PyLong_CheckExact(v) ? PyLong_AsLongLongAndOverflow(v, &overflow) : -1;
+      if (cnt[k] < 0 || overflow) rule = 1;
+    }
+    if (rule) break;
+    const int64_t computed = cnt[0], queries = cnt[1], reserved = cnt[2], readonly = cnt[3];
+    if (reserved < queries) { rule = 2; break; }
+    PyObject* ids_obj = PyDict_GetItemString(req, "block_ids");
+    PyObject* ret_obj = PyDict_GetItemString(req, "retained_query_indices");
+    if (ids_obj == nullptr || ret_obj == nullptr) { rule = 11; break; }
+    PyObject* rseq = PySequence_Fast(ret_obj, "retained query indices must be a sequence");
+    if (rseq == nullptr) { Py_DECREF(reqs); return nullptr; }
+    const Py_ssize_t nret = PySequence_Fast_GET_SIZE(rseq);
+    ret.assign((size_t)nret, 0);
+    for (Py_ssize_t i = 0; i < nret && rule == 0; ++i) {
+      PyObject* v = PySequence_Fast_ITEMS(rseq)[i];
+      int overflow = 0;
+      ret[(size_t)i] = PyLong_CheckExact(v) ? PyLong_AsLongLongAndOverflow(v, &overflow) : -1;
+      if (ret[(size_t)i] < 0 || overflow) rule = 3;
+    }
+    Py_DECREF(rseq);
+    if (rule) break;
+    {
+      std::vector<int64_t> sorted(ret);
+      std::sort(sorted.begin(), sorted.end());
+      if (std::adjacent_find(sorted.begin(), sorted.end()) != sorted.end()) { rule = 4; break; }
+    }
+    bool tail_ok = true;
+    for (int64_t x : ret) tail_ok &= x < queries;
+    if (!tail_ok) { rule = 5; break; }
+    PyObject* tseq = PySequence_Fast(ids_obj, "block_ids must be a sequence");
+    if (tseq == nullptr) { Py_DECREF(reqs); return nullptr; }
+    const Py_ssize_t n = PySequence_Fast_GET_SIZE(tseq);
+    PyObject** items = PySequence_Fast_ITEMS(tseq);
+    const int64_t required = (computed + reserved + bs - 1) / bs;
+    if (n != required) {
+      Py_DECREF(tseq);
+      rule = 6;
+      break;
+    }
+    bool ids_ok = true;
+    for (Py_ssize_t i = 0; i < n && ids_ok; ++i) {
+      int overflow = 0;
+      const long long v = PyLong_CheckExact(items[i]) ? PyLong_AsLongLongAndOverflow(items[i], &overflow) : -1;
+      ids_ok = overflow == 0 && v >= 0 && v < num_blocks;
+    }
+    if (!ids_ok) {
+      Py_DECREF(tseq);
+      rule = 7;
+      break;
+    }
+    const uint32_t seen = s.next_epoch();
+    bool unique = true;
+    for (Py_ssize_t i = 0; i < n && unique; ++i) {
+      BlockRecord& b = s.rec[(size_t)PyLong_AsLongLong(items[i])];
+      unique = b.epoch != seen;
+      b.epoch = seen;
+    }
+    if (!unique) {
+      Py_DECREF(tseq);
+      rule = 8;
+      break;
+    }
+    if (readonly * bs > computed) {
+      Py_DECREF(tseq);
+      rule = 9;
+      break;
+    }
+    auto slot_of = [&](int64_t pos) -> int64_t {
+      const int64_t lb = pos / bs;
+      return PyLong_AsLongLong(items[lb]) * bs + (pos - lb * bs);
+    };
+    for (Py_ssize_t i = 0; i < nret; ++i) {
+      const int64_t from = slot_of(computed + ret[(size_t)i]);
+      const int64_t to = slot_of(computed + i);
+      if (from != to || keep_equal) {
+        src.push_back(from);
+        dst.push_back(to);
+      }
+      moved[(size_t)r] += from != to;
+    }
+    Py_DECREF(tseq);
+  }
+  Py_DECREF(reqs);
+  if (rule == 0 && dst.size() > 1) {
+    std::vector<int64_t> sorted(dst);
+    std::sort(sorted.begin(), sorted.end());
+    if (std::adjacent_find(sorted.begin(), sorted.end()) != sorted.end()) {
+      rule = 10;
+      r = nreq;
+    }
+  }
+  if (rule) return Py_BuildValue("(inOOO)", rule, r, Py_None, Py_None, Py_None);
+  int64_t *m = nullptr, *so = nullptr, *d = nullptr;
+  PyObject* m_obj = new_array<int64_t>(nreq, &m);
+  PyObject* s_obj = new_array<int64_t>((Py_ssize_t)src.size(), &so);
+  PyObject* d_obj = new_array<int64_t>((Py_ssize_t)dst.size(), &d);
+  PyObject* result = nullptr;
+  if (m_obj && s_obj && d_obj) {
+    std::copy(moved.begin(), moved.end(), m);
+    std::copy(src.begin(), src.end(), so);
+    std::copy(dst.begin(), dst.end(), d);
+    result = Py_BuildValue("(inOOO)", 0, (Py_ssize_t)-1, m_obj, s_obj, d_obj);
+  }
+  Py_XDECREF(m_obj);
+  Py_XDECREF(s_obj);
+  Py_XDECREF(d_obj);
+  return result;
+}
+
+PyMethodDef kMethods[] = {
+    {"flatten", (PyCFunction)(void (*)(void))flatten, METH_FASTCALL, "int sequences -> (flat, counts int64, status)"},
+    {"validate", (PyCFunction)(void (*)(void))validate, METH_FASTCALL, "block-table rules -> (rule, request)"},
+    {"layouts", (PyCFunction)(void (*)(void))layouts, METH_FASTCALL, "query layouts -> lengths and ancestor bit rows"},
+    {"stage", (PyCFunction)(void (*)(void))stage, METH_FASTCALL, "slots and per-request records into buffers"},
+    {"decode_work", (PyCFunction)(void (*)(void))decode_work, METH_FASTCALL, "stream-K decode pieces"},
+    {"prefill_work", (PyCFunction)(void (*)(void))prefill_work, METH_FASTCALL, "prefill units and merge jobs"},
+    {"layer_work", (PyCFunction)(void (*)(void))layer_work, METH_FASTCALL, "one layer shape's choices and lists"},
+    {"compact_pairs", (PyCFunction)(void (*)(void))compact_pairs, METH_FASTCALL, "compact rules and moved slot pairs"},
+    {nullptr, nullptr, 0, nullptr},
+};
+
+PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_lvamd_host", "Native host-side step planner of the paged-KV backend.",
+                       -1, kMethods};
+
+}  // namespace
+
+PyMODINIT_FUNC PyInit__lvamd_host(void) { return PyModule_Create(&kModule); }

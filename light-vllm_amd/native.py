@@ -1,18 +1,22 @@
-"""ctypes binding of the gfx950 HIP library (``liblvamd_hip.so``).
+"""ctypes binding of the gfx950 HIP library (``liblvamd_hip.so``), and the
+loader of the native host planner (``_lvamd_host``).
 
 The library is the product: there is no CPU or PyTorch fallback.  ``load()``
-raises ``ExecutionNotReadyError`` when the library has not been built, and
-every call that returns a non-zero status raises ``ExecutionError``.
+and ``host()`` raise ``ExecutionNotReadyError`` when their module has not been
+built, and every call that returns a non-zero status raises ``ExecutionError``
+(the host's classes when bound, see ``errors``).
 """
 
 from __future__ import annotations
 
 import ctypes
 import functools
+import importlib.util
 import re
+import sysconfig
 from pathlib import Path
 
-from light_vllm_amd.errors import ExecutionError, ExecutionNotReadyError
+from light_vllm_amd import errors
 
 LIB_NAME = "liblvamd_hip.so"
 ABI_VERSION = 11
@@ -83,6 +87,28 @@ def library_path() -> Path:
     return PACKAGE_DIR / LIB_NAME
 
 
+HOST_MODULE = "_lvamd_host"
+
+
+def host_path() -> Path:
+    return PACKAGE_DIR / (HOST_MODULE + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+@functools.lru_cache(maxsize=1)
+def host():
+    """The native host planner (``csrc/lvamd_host.cpp``), built next to the HIP library."""
+
+    path = host_path()
+    if not path.exists():
+        raise errors.ExecutionNotReadyError(
+            f"the host planner {path} is not built; run __graft_entry__.build() first"
+        )
+    spec = importlib.util.spec_from_file_location(HOST_MODULE, path)
+    module = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(module)
+    return module
+
+
 def header_functions() -> list[str]:
     """Names of every function the C header declares."""
 
@@ -95,7 +121,7 @@ def header_functions() -> list[str]:
 def load() -> ctypes.CDLL:
     path = library_path()
     if not path.exists():
-        raise ExecutionNotReadyError(
+        raise errors.ExecutionNotReadyError(
             f"the HIP library {path} is not built; run __graft_entry__.build() first"
         )
     lib = ctypes.CDLL(str(path))
@@ -105,7 +131,7 @@ def load() -> ctypes.CDLL:
         fn.argtypes = argtypes
     version = lib.lvamd_abi_version()
     if version != ABI_VERSION:
-        raise ExecutionNotReadyError(f"{path} has ABI version {version}, expected {ABI_VERSION}")
+        raise errors.ExecutionNotReadyError(f"{path} has ABI version {version}, expected {ABI_VERSION}")
     return lib
 
 
@@ -144,7 +170,7 @@ def decode_max_col_tiles(dtype_code: int, head_size: int) -> int:
     for ctw in sorted(DECODE_COL_TILES, reverse=True):
         if lib.lvamd_paged_decode_tile_tokens(dtype_code, head_size, ctw) > 0:
             return ctw
-    raise ExecutionError(f"no decode kernel for dtype {dtype_code}, head size {head_size}")
+    raise errors.ExecutionError(f"no decode kernel for dtype {dtype_code}, head size {head_size}")
 
 
 @functools.lru_cache(maxsize=None)
@@ -182,4 +208,4 @@ def prefill_waves_built(dtype_code: int, head_size: int, waves: int) -> bool:
 def check(status: int, what: str) -> None:
     if status != 0:
         message = load().lvamd_status_string(status).decode()
-        raise ExecutionError(f"{what} failed: {message} (status {status})")
+        raise errors.ExecutionError(f"{what} failed: {message} (status {status})")

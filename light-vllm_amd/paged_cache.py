@@ -1,11 +1,13 @@
 """Physical paged K/V pool on an MI355X, with HIP append, compact and block copy.
 
-Restates light-vllm's ``PagedKVCache`` (src/light_vllm/runtime/execution/
-paged_cache.py:30-338): same config, same per-layer layout
-``[num_blocks, block_size, num_kv_heads, head_size]`` (separate K and V
-tensors), same validation rules and messages.  The data movement runs in the
-gfx950 kernels of ``liblvamd_hip.so``; there is no PyTorch fallback, and a
-cache on a non-GPU device is rejected.
+The contract is light-vllm's ``PagedKVCache`` (src/light_vllm/runtime/
+execution/paged_cache.py:30-338): the config and its messages, the per-layer
+layout ``[num_blocks, block_size, num_kv_heads, head_size]`` with separate K
+and V tensors, ``layer`` / ``layer_spec`` / ``prepare_write`` /
+``write_prepared`` / ``write`` / ``compact`` and their error messages.  The
+data movement runs in the gfx950 kernels of ``liblvamd_hip.so`` (there is no
+PyTorch fallback, and a cache on a non-GPU device is rejected); compact's
+rules run in the native host planner, for one request or a whole step.
 
 ``hip_compact`` and ``hip_block_copy`` work on any cache object exposing the
 reference's public surface (``config``, ``model_spec.layers``, ``layer(id)``),
@@ -17,13 +19,13 @@ from __future__ import annotations
 import weakref
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 from torch import Tensor
 
-from light_vllm_amd import native
-from light_vllm_amd.errors import KVCacheError
+from light_vllm_amd import errors, native
 from light_vllm_amd.interfaces import AttentionLayerSpec, ModelKVCacheSpec
-from light_vllm_amd.plan import table_proven
+from light_vllm_amd.plan import Staging
 
 _DTYPE_CODES = {torch.float32: native.DTYPE_F32, torch.float16: native.DTYPE_F16, torch.bfloat16: native.DTYPE_BF16}
 
@@ -32,7 +34,7 @@ def dtype_code(dtype: torch.dtype) -> int:
     try:
         return _DTYPE_CODES[dtype]
     except KeyError as exc:
-        raise KVCacheError(f"HIP paged KV supports float32, float16 and bfloat16, not {dtype}") from exc
+        raise errors.KVCacheError(f"HIP paged KV supports float32, float16 and bfloat16, not {dtype}") from exc
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
@@ -48,9 +50,15 @@ def current_stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def _positive_int(value) -> bool:
+    return type(value) is int and value > 0
+
+
 @dataclass(frozen=True, slots=True)
 class PagedKVCacheConfig:
-    """Number and size of physical blocks, dtype and device of the pool."""
+    """Number and size of physical blocks, dtype and device of the pool.
+
+    With a fixed block count the config is its own planner (``plan``)."""
 
     num_blocks: int
     block_size: int
@@ -58,12 +66,13 @@ class PagedKVCacheConfig:
     device: str | torch.device = "cpu"
 
     def __post_init__(self) -> None:
-        if type(self.num_blocks) is not int or self.num_blocks <= 0:
-            raise ValueError("num_blocks must be a positive integer")
-        if type(self.block_size) is not int or self.block_size <= 0:
-            raise ValueError("block_size must be a positive integer")
-        if not self.dtype.is_floating_point:
-            raise ValueError("KV cache dtype must be floating point")
+        for holds, message in (
+            (_positive_int(self.num_blocks), "num_blocks must be a positive integer"),
+            (_positive_int(self.block_size), "block_size must be a positive integer"),
+            (self.dtype.is_floating_point, "KV cache dtype must be floating point"),
+        ):
+            if not holds:
+                raise ValueError(message)
         object.__setattr__(self, "device", torch.device(self.device))
 
     def plan(self, model_spec: ModelKVCacheSpec) -> "PagedKVCacheConfig":
@@ -71,10 +80,12 @@ class PagedKVCacheConfig:
 
 
 def kv_cache_bytes_per_block(model_spec: ModelKVCacheSpec, *, block_size: int, dtype: torch.dtype) -> int:
-    """Bytes of one physical block across all layers, K and V."""
+    """Bytes of one physical block across all layers: K and V rows of every
+    layer's own kv-head shape, ``block_size`` tokens."""
 
-    per_token = sum(2 * layer.num_kv_heads * layer.head_size for layer in model_spec.layers)
-    return block_size * per_token * torch.empty((), dtype=dtype).element_size()
+    element = torch.empty((), dtype=dtype).element_size()
+    row_elements = sum(spec.num_kv_heads * spec.head_size for spec in model_spec.layers)
+    return 2 * row_elements * block_size * element
 
 
 @dataclass(frozen=True, slots=True)
@@ -87,15 +98,22 @@ class PagedLayerCache:
 
 @dataclass(frozen=True, slots=True)
 class PagedKVWriteMapping:
-    """Physical write slots of one step, reused by every layer."""
+    """Physical write slots of one step, reused by every layer.
+
+    ``slots`` holds the slots of the tokens that are written; when only some
+    of the step's ``num_query_tokens`` tokens are, ``source_indices`` names
+    them (token t of the update goes to ``slots[i]`` for
+    ``source_indices[i] == t``)."""
 
     slots: Tensor
     num_query_tokens: int
     source_indices: Tensor | None = None
 
 
-class _LayerPointers:
-    """Device arrays of per-layer K and V base addresses, grouped by row size."""
+class _CacheState:
+    """Per-cache launch state: device arrays of per-layer K and V base
+    addresses grouped by row size, a staging ring for the index uploads,
+    and the compact workspace (grown on demand)."""
 
     def __init__(self, cache) -> None:
         device = cache.config.device
@@ -108,30 +126,39 @@ class _LayerPointers:
         for row_bytes, ptrs in groups.items():
             table = torch.tensor(ptrs, dtype=torch.int64).t().contiguous().to(device)
             self.groups.append((row_bytes, len(ptrs), table))
+        self.staging = Staging(device)
+        self._device = device
+        self._workspace: Tensor | None = None
+
+    def workspace(self, nbytes: int) -> Tensor:
+        if self._workspace is None or self._workspace.numel() < nbytes:
+            self._workspace = torch.empty(nbytes, dtype=torch.uint8, device=self._device)
+        return self._workspace
 
 
-_POINTER_CACHE: "weakref.WeakKeyDictionary[object, _LayerPointers]" = weakref.WeakKeyDictionary()
+_CACHE_STATE: "weakref.WeakKeyDictionary[object, _CacheState]" = weakref.WeakKeyDictionary()
 
 
-def _layer_pointers(cache) -> _LayerPointers:
-    """Per-cache pointer tables, built on first use and dropped with the cache."""
+def _layer_pointers(cache) -> _CacheState:
+    """Per-cache launch state, built on first use and dropped with the cache."""
 
-    found = _POINTER_CACHE.get(cache)
+    found = _CACHE_STATE.get(cache)
     if found is None:
-        found = _LayerPointers(cache)
-        _POINTER_CACHE[cache] = found
+        found = _CacheState(cache)
+        _CACHE_STATE[cache] = found
     return found
 
 
 def _require_gpu(cache) -> None:
     if cache.config.device.type != "cuda":
-        raise KVCacheError("the HIP paged KV path requires a GPU KV cache")
+        raise errors.KVCacheError("the HIP paged KV path requires a GPU KV cache")
 
 
-def hip_append(cache, layer_id: str, key: Tensor, value: Tensor, slots: Tensor) -> None:
+def hip_append(cache, layer_id: str, key: Tensor, value: Tensor, slots_ptr: int, num_tokens: int) -> None:
     """``flatK[slots[t]] = key[t]``, ``flatV[slots[t]] = value[t]`` on the current stream.
 
-    ``slots`` is int64 with one entry per token (negative = skip).
+    ``slots_ptr`` is the device address of int64 slots, one per token
+    (negative = skip), ``num_tokens`` of them.
     """
 
     layer = cache.layer(layer_id)
@@ -144,7 +171,7 @@ def hip_append(cache, layer_id: str, key: Tensor, value: Tensor, slots: Tensor) 
         key.data_ptr(), key.stride(0), key.stride(1),
         value.data_ptr(), value.stride(0), value.stride(1),
         layer.keys.data_ptr(), layer.values.data_ptr(),
-        slots.data_ptr(), slots.numel(),
+        slots_ptr, num_tokens,
         spec.num_kv_heads, spec.head_size, dtype_code(key.dtype),
         current_stream(key.device),
     )
@@ -152,7 +179,7 @@ def hip_append(cache, layer_id: str, key: Tensor, value: Tensor, slots: Tensor) 
 
 
 def hip_append_rotary(cache, layer_id: str, query: Tensor, key: Tensor, value: Tensor,
-                      rotary: tuple[Tensor, Tensor], slots: Tensor) -> Tensor:
+                      rotary: tuple[Tensor, Tensor], slots_ptr: int, num_tokens: int) -> Tensor:
     """Rotate ``query`` and ``key`` (Qwen2's half rotation, rounded as
     apply_rotary's PyTorch path rounds it) and append: ``flatK[slots[t]] =
     rotate(key[t])``, ``flatV[slots[t]] = value[t]``; returns the rotated
@@ -167,9 +194,9 @@ def hip_append_rotary(cache, layer_id: str, query: Tensor, key: Tensor, value: T
     tokens = query.shape[0]
     for name, t in (("cosines", cosines), ("sines", sines)):
         if not isinstance(t, Tensor) or t.dim() != 2 or tuple(t.shape) != (tokens, spec.head_size):
-            raise KVCacheError(f"rotary {name} must have shape [{tokens}, {spec.head_size}]")
+            raise errors.KVCacheError(f"rotary {name} must have shape [{tokens}, {spec.head_size}]")
         if t.dtype != query.dtype or t.device != query.device:
-            raise KVCacheError(f"rotary {name} dtype and device must match the query")
+            raise errors.KVCacheError(f"rotary {name} dtype and device must match the query")
     if cosines.stride(1) != 1:
         cosines = cosines.contiguous()
     if sines.stride(1) != 1:
@@ -188,7 +215,7 @@ def hip_append_rotary(cache, layer_id: str, query: Tensor, key: Tensor, value: T
         key.data_ptr(), key.stride(0), key.stride(1),
         value.data_ptr(), value.stride(0), value.stride(1),
         cosines.data_ptr(), cosines.stride(0), sines.data_ptr(), sines.stride(0),
-        layer.keys.data_ptr(), layer.values.data_ptr(), slots.data_ptr(), slots.numel(),
+        layer.keys.data_ptr(), layer.values.data_ptr(), slots_ptr, num_tokens,
         spec.num_query_heads, spec.num_kv_heads, spec.head_size, dtype_code(query.dtype),
         current_stream(query.device),
     )
@@ -196,120 +223,99 @@ def hip_append_rotary(cache, layer_id: str, query: Tensor, key: Tensor, value: T
     return rotated
 
 
-def compact_slots(
-    config,
-    block_ids: tuple[int, ...],
-    *,
-    num_computed_tokens: int,
-    num_query_tokens: int,
-    num_reserved_query_tokens: int,
-    retained_query_indices: tuple[int, ...],
-    num_readonly_prefix_blocks: int = 0,
-) -> tuple[tuple[int, ...], tuple[int, ...]]:
-    """Validate a compact request and return (source slots, target slots).
-
-    Rules and messages of PagedKVCache.compact (paged_cache.py:269-312).
-    """
-
-    block_ids = tuple(block_ids)
-    retained = tuple(retained_query_indices)
-    counts = (num_computed_tokens, num_query_tokens, num_reserved_query_tokens, num_readonly_prefix_blocks)
-    if any(type(v) is not int or v < 0 for v in counts):
-        raise ValueError("paged compact counts must be non-negative integers")
-    if num_reserved_query_tokens < num_query_tokens:
-        raise ValueError("reserved query tokens must cover every actual query")
-    if any(type(i) is not int or i < 0 for i in retained):
-        raise ValueError("retained query indices must be non-negative integers")
-    if len(set(retained)) != len(retained):
-        raise ValueError("retained query indices must be unique")
-    if any(i >= num_query_tokens for i in retained):
-        raise KVCacheError("retained query index exceeds the paged KV tail")
-    bs = config.block_size
-    required = (num_computed_tokens + num_reserved_query_tokens + bs - 1) // bs
-    if len(block_ids) != required:
-        raise KVCacheError("block table does not exactly cover the reserved query slots")
-    # Every id an int (not a bool or numpy scalar) in [0, num_blocks), none
-    # repeated; checked with C-level passes (map/min/max/set) since tables run
-    # to thousands of ids, and skipped for a table object that the step's
-    # attention context has already proven (plan.table_proven).
-    if not table_proven(block_ids, config.num_blocks):
-        if block_ids and (
-            set(map(type, block_ids)) != {int} or min(block_ids) < 0 or max(block_ids) >= config.num_blocks
-        ):
-            raise KVCacheError("block table contains an invalid physical block")
-        if len(set(block_ids)) != len(block_ids):
-            raise KVCacheError("block table aliases a physical block within one request")
-    if num_readonly_prefix_blocks * bs > num_computed_tokens:
-        raise KVCacheError("readonly prefix blocks exceed the computed prefix")
-
-    def slot(position: int) -> int:
-        return block_ids[position // bs] * bs + position % bs
-
-    sources = tuple(slot(num_computed_tokens + i) for i in retained)
-    targets = tuple(slot(num_computed_tokens + i) for i in range(len(retained)))
-    return sources, targets
+# Compact rules by the native planner's code: (exception kind, message).
+# The messages and the order in which the rules fire are light-vllm's
+# (paged_cache.py:276-302); rule 10 is the batch rule of ``compact_many``.
+_COMPACT_RULES = {
+    1: ("value", "paged compact counts must be non-negative integers"),
+    2: ("value", "reserved query tokens must cover every actual query"),
+    3: ("value", "retained query indices must be non-negative integers"),
+    4: ("value", "retained query indices must be unique"),
+    5: ("kv", "retained query index exceeds the paged KV tail"),
+    6: ("kv", "block table does not exactly cover the reserved query slots"),
+    7: ("kv", "block table contains an invalid physical block"),
+    8: ("kv", "block table aliases a physical block within one request"),
+    9: ("kv", "readonly prefix blocks exceed the computed prefix"),
+    10: ("kv", "compact requests of one step must not write the same slot"),
+    11: ("type", "a compact request needs block_ids, num_computed_tokens, num_query_tokens, "
+                 "num_reserved_query_tokens and retained_query_indices"),
+}
 
 
-def hip_compact(cache, block_ids: tuple[int, ...], **kwargs) -> int:
+def _compact_plan(config, requests, *, keep_equal: bool = False):
+    """(moved per request, source slots, target slots) of compact requests,
+    as int64 arrays; the first broken rule raises its error."""
+
+    rule, _, moved, src, dst = native.host().compact_pairs(requests, config.num_blocks, config.block_size,
+                                                           keep_equal)
+    if rule:
+        kind, message = _COMPACT_RULES[rule]
+        if kind == "kv":
+            raise errors.KVCacheError(message)
+        raise (ValueError if kind == "value" else TypeError)(message)
+    return np.frombuffer(moved, dtype=np.int64), np.frombuffer(src, dtype=np.int64), np.frombuffer(dst, dtype=np.int64)
+
+
+def _compact_request(block_ids, **counts) -> dict:
+    request = dict(counts)
+    request["block_ids"] = block_ids
+    return request
+
+
+def compact_slots(config, block_ids: tuple[int, ...], **counts) -> tuple[tuple[int, ...], tuple[int, ...]]:
+    """(source slots, target slots) of one compact request, src == dst pairs
+    included: retained query i moves from logical position computed +
+    retained[i] to computed + i.  Raises as ``compact`` does."""
+
+    _, src, dst = _compact_plan(config, (_compact_request(block_ids, **counts),), keep_equal=True)
+    return tuple(src.tolist()), tuple(dst.tolist())
+
+
+def hip_compact(cache, block_ids: tuple[int, ...], **counts) -> int:
     """Move the retained query K/V to the contiguous formal tail of every layer.
 
     Returns the number of tokens whose slot changed (0 = nothing written).
-    Pairs whose source equals their target are dropped before the copy: such
-    a slot is neither read nor written by any other pair (targets are unique
-    and sources are unique), so dropping it leaves the result unchanged.
+    Pairs whose source equals their target are left out of the copy: such a
+    slot is neither read nor written by any other pair (targets are unique and
+    sources are unique), so the result is the same.
     """
 
-    _require_gpu(cache)
-    sources, targets = compact_slots(cache.config, block_ids, **kwargs)
-    moved = [(s, t) for s, t in zip(sources, targets) if s != t]
-    _launch_compact(cache, moved)
-    return len(moved)
+    return hip_compact_many(cache, (_compact_request(block_ids, **counts),))[0]
 
 
 def hip_compact_many(cache, requests) -> tuple[int, ...]:
     """``hip_compact`` for several requests of one step in a single launch.
 
-    Each request is a mapping of ``hip_compact``'s keyword arguments
-    (``block_ids``, ``num_computed_tokens``, ...), validated exactly as a
-    single compact; destinations must be unique across the batch (every
-    source is read before any destination is written, as for one request).
-    Returns each request's moved-token count.
+    Each request is a dict of ``compact``'s keyword arguments with
+    ``block_ids``; every request is validated by compact's rules, and the
+    destinations must be unique across the batch (every source is read before
+    any destination is written, as for one request).  Returns each request's
+    moved-token count.
     """
 
     _require_gpu(cache)
-    moved: list[tuple[int, int]] = []
-    counts = []
-    for request in requests:
-        kwargs = dict(request)
-        block_ids = kwargs.pop("block_ids")
-        sources, targets = compact_slots(cache.config, tuple(block_ids), **kwargs)
-        pairs = [(s, t) for s, t in zip(sources, targets) if s != t]
-        counts.append(len(pairs))
-        moved += pairs
-    if len({t for _, t in moved}) != len(moved):
-        raise KVCacheError("compact requests of one step must not write the same slot")
-    _launch_compact(cache, moved)
-    return tuple(counts)
+    if not isinstance(requests, (list, tuple)):
+        requests = tuple(requests)
+    moved, src, dst = _compact_plan(cache.config, requests)
+    if src.size:
+        _launch_compact(cache, src, dst)
+    return tuple(moved.tolist())
 
 
-def _launch_compact(cache, moved: list[tuple[int, int]]) -> None:
-    if not moved:
-        return
+def _launch_compact(cache, src: np.ndarray, dst: np.ndarray) -> None:
+    pointers = _layer_pointers(cache)
     device = cache.config.device
-    pairs = torch.tensor(moved, dtype=torch.int64).t().contiguous()
-    if device.type == "cuda":
-        pairs = pairs.pin_memory()
-    pairs = pairs.to(device, non_blocking=True)
+    n = int(src.size)
+    blob, (src_off, dst_off) = pointers.staging.stage([src.view(np.int32), dst.view(np.int32)])
+    src_ptr, dst_ptr = blob.data_ptr() + 4 * src_off, blob.data_ptr() + 4 * dst_off
     lib = native.load()
     stream = current_stream(device)
-    n = len(moved)
-    for row_bytes, num_layers, ptrs in _layer_pointers(cache).groups:
+    for row_bytes, num_layers, ptrs in pointers.groups:
         ws_bytes = lib.lvamd_kv_compact_workspace_size(n, num_layers, row_bytes)
-        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device) if ws_bytes else None
+        workspace = pointers.workspace(ws_bytes) if ws_bytes else None
         status = lib.lvamd_kv_compact(
             ptrs[0].data_ptr(), ptrs[1].data_ptr(), num_layers, row_bytes,
-            pairs[0].data_ptr(), pairs[1].data_ptr(), n,
-            workspace.data_ptr() if workspace is not None else None, ws_bytes, stream,
+            src_ptr, dst_ptr, n, workspace.data_ptr() if workspace is not None else None, ws_bytes, stream,
         )
         native.check(status, "lvamd_kv_compact")
 
@@ -329,25 +335,23 @@ def hip_block_copy(cache, src_blocks, dst_blocks) -> None:
     num_blocks = cache.config.num_blocks
     both = src + dst
     if both and (set(map(type, both)) != {int} or min(both) < 0 or max(both) >= num_blocks):
-        raise KVCacheError("block copy names an invalid physical block")
+        raise errors.KVCacheError("block copy names an invalid physical block")
     if len(set(dst)) != len(dst):
-        raise KVCacheError("block copy writes the same physical block twice")
+        raise errors.KVCacheError("block copy writes the same physical block twice")
     if set(src) & set(dst):
-        raise KVCacheError("block copy sources and destinations must be disjoint")
+        raise errors.KVCacheError("block copy sources and destinations must be disjoint")
     if not src:
         return
-    device = cache.config.device
-    pairs = torch.tensor((src, dst), dtype=torch.int64)
-    if device.type == "cuda":
-        pairs = pairs.pin_memory()
-    pairs = pairs.to(device, non_blocking=True)
+    pointers = _layer_pointers(cache)
+    blob, (src_off, dst_off) = pointers.staging.stage([np.asarray(src, dtype=np.int64).view(np.int32),
+                                                       np.asarray(dst, dtype=np.int64).view(np.int32)])
     lib = native.load()
-    stream = current_stream(device)
+    stream = current_stream(cache.config.device)
     bs = cache.config.block_size
-    for row_bytes, num_layers, ptrs in _layer_pointers(cache).groups:
+    for row_bytes, num_layers, ptrs in pointers.groups:
         status = lib.lvamd_kv_block_copy(
             ptrs[0].data_ptr(), ptrs[1].data_ptr(), num_layers, row_bytes * bs,
-            pairs[0].data_ptr(), pairs[1].data_ptr(), len(src), stream,
+            blob.data_ptr() + 4 * src_off, blob.data_ptr() + 4 * dst_off, len(src), stream,
         )
         native.check(status, "lvamd_kv_block_copy")
 
@@ -357,7 +361,7 @@ class PagedKVCache:
 
     def __init__(self, model_spec: ModelKVCacheSpec, config: PagedKVCacheConfig) -> None:
         if config.device.type != "cuda":
-            raise KVCacheError("the HIP paged KV cache requires a GPU (cuda) device")
+            raise errors.KVCacheError("the HIP paged KV cache requires a GPU (cuda) device")
         dtype_code(config.dtype)
         self._model_spec = model_spec
         self._config = config
@@ -376,69 +380,82 @@ class PagedKVCache:
         try:
             return self._layer_specs[layer_id]
         except KeyError as exc:
-            raise KVCacheError(f"KV cache layer {layer_id!r} was not found") from exc
+            raise errors.KVCacheError(f"KV cache layer {layer_id!r} was not found") from exc
 
     def layer(self, layer_id: str) -> PagedLayerCache:
         try:
             return self._layers[layer_id]
         except KeyError as exc:
-            raise KVCacheError(f"KV cache layer {layer_id!r} was not found") from exc
+            raise errors.KVCacheError(f"KV cache layer {layer_id!r} was not found") from exc
 
     @torch.inference_mode()
     def prepare_write(self, slot_mapping: Tensor, *, validate: bool = True) -> PagedKVWriteMapping:
-        """Normalise one step's slot mapping for reuse by all layers (paged_cache.py:165-206)."""
+        """One step's slot mapping, normalised once for every layer's write
+        (light-vllm: paged_cache.py:165-206).
+
+        Negative entries mark tokens that are not written.  With ``validate``
+        the written slots are checked in range and distinct, from one host
+        copy of the mapping; metadata-proven mappings pass ``validate=False``
+        and stay on the device untouched.
+        """
 
         if slot_mapping.ndim != 1:
-            raise KVCacheError("slot mapping must have one entry per packed query token")
+            raise errors.KVCacheError("slot mapping must have one entry per packed query token")
         if slot_mapping.device != self._config.device:
-            raise KVCacheError("slot mapping device must match the cache")
-        flat = slot_mapping.flatten()
+            raise errors.KVCacheError("slot mapping device must match the cache")
+        num_tokens = slot_mapping.numel()
         if not validate:
-            return PagedKVWriteMapping(slots=flat.to(torch.long), num_query_tokens=flat.numel())
-        active = flat >= 0
-        source_indices = torch.nonzero(active, as_tuple=False).flatten()
-        slots = flat.index_select(0, source_indices).to(torch.long)
-        if slots.numel():
-            num_slots = self._config.num_blocks * self._config.block_size
-            if int(slots.min()) < 0 or int(slots.max()) >= num_slots:
-                raise KVCacheError("slot mapping contains an out-of-range physical slot")
-            if slots.unique().numel() != slots.numel():
-                raise KVCacheError("slot mapping must not write the same physical slot twice")
+            return PagedKVWriteMapping(slots=slot_mapping.to(torch.long), num_query_tokens=num_tokens)
+        host = slot_mapping.to("cpu", torch.long).numpy()
+        written = np.flatnonzero(host >= 0)
+        chosen = host[written]
+        if chosen.size:
+            if int(chosen.max()) >= self._config.num_blocks * self._config.block_size:
+                raise errors.KVCacheError("slot mapping contains an out-of-range physical slot")
+            if np.unique(chosen).size != chosen.size:
+                raise errors.KVCacheError("slot mapping must not write the same physical slot twice")
+        device = self._config.device
+        every = written.size == num_tokens
         return PagedKVWriteMapping(
-            slots=slots,
-            num_query_tokens=flat.numel(),
-            source_indices=None if source_indices.numel() == flat.numel() else source_indices,
+            slots=torch.from_numpy(chosen).to(device),
+            num_query_tokens=num_tokens,
+            source_indices=None if every else torch.from_numpy(written).to(device),
         )
 
     @torch.inference_mode()
     def write_prepared(self, layer_id: str, key: Tensor, value: Tensor, mapping: PagedKVWriteMapping) -> None:
-        """Write K/V through a prepared mapping (paged_cache.py:209-248), on the HIP append kernel."""
+        """Write one layer's K/V through a prepared mapping (light-vllm:
+        paged_cache.py:209-248) with the HIP append kernel, which takes one
+        slot per token and skips negative ones."""
 
         self.layer(layer_id)
         spec = self.layer_spec(layer_id)
+        cfg = self._config
         tail = (spec.num_kv_heads, spec.head_size)
-        if key.ndim != 3 or tuple(key.shape[1:]) != tail:
-            raise KVCacheError("paged KV update must have shape [tokens, kv_heads, head_size]")
-        if value.shape != key.shape:
-            raise KVCacheError("paged K/V updates must have the same shape")
-        if mapping.num_query_tokens != key.shape[0]:
-            raise KVCacheError("slot mapping must have one entry per query token")
-        if key.dtype != self._config.dtype or key.device != self._config.device:
-            raise KVCacheError("paged KV update dtype and device must match the cache")
-        if value.dtype != key.dtype or value.device != key.device:
-            raise KVCacheError("paged K/V updates must use the same dtype and device")
-        if mapping.slots.device != self._config.device or (
-            mapping.source_indices is not None and mapping.source_indices.device != self._config.device
-        ):
-            raise KVCacheError("prepared slot mapping device must match the cache")
+        rules = (
+            (lambda: key.ndim == 3 and tuple(key.shape[1:]) == tail,
+             "paged KV update must have shape [tokens, kv_heads, head_size]"),
+            (lambda: value.shape == key.shape, "paged K/V updates must have the same shape"),
+            (lambda: mapping.num_query_tokens == key.shape[0], "slot mapping must have one entry per query token"),
+            (lambda: key.dtype == cfg.dtype and key.device == cfg.device,
+             "paged KV update dtype and device must match the cache"),
+            (lambda: value.dtype == key.dtype and value.device == key.device,
+             "paged K/V updates must use the same dtype and device"),
+            (lambda: mapping.slots.device == cfg.device
+             and (mapping.source_indices is None or mapping.source_indices.device == cfg.device),
+             "prepared slot mapping device must match the cache"),
+        )
+        for holds, message in rules:
+            if not holds():
+                raise errors.KVCacheError(message)
         if mapping.slots.numel() == 0:
             return
-        slots = mapping.slots
+        per_token = mapping.slots
         if mapping.source_indices is not None:
-            dense = torch.full((mapping.num_query_tokens,), -1, dtype=torch.long, device=slots.device)
-            dense.index_copy_(0, mapping.source_indices, slots)
-            slots = dense
-        hip_append(self, layer_id, key, value, slots.contiguous())
+            per_token = torch.full((mapping.num_query_tokens,), -1, dtype=torch.long, device=cfg.device)
+            per_token[mapping.source_indices] = mapping.slots
+        per_token = per_token.contiguous()
+        hip_append(self, layer_id, key, value, per_token.data_ptr(), per_token.numel())
 
     @torch.inference_mode()
     def write(self, layer_id: str, key: Tensor, value: Tensor, slot_mapping: Tensor) -> None:
@@ -457,21 +474,17 @@ class PagedKVCache:
         retained_query_indices: tuple[int, ...],
         num_readonly_prefix_blocks: int = 0,
     ) -> int:
-        """Move the accepted path to the contiguous formal tail (paged_cache.py:257-326)."""
+        """Move the accepted path to the contiguous formal tail of every layer
+        (light-vllm: paged_cache.py:257-326); returns how many tokens moved."""
 
-        return hip_compact(
-            self,
-            block_ids,
-            num_computed_tokens=num_computed_tokens,
-            num_query_tokens=num_query_tokens,
-            num_reserved_query_tokens=num_reserved_query_tokens,
-            retained_query_indices=retained_query_indices,
-            num_readonly_prefix_blocks=num_readonly_prefix_blocks,
-        )
+        return hip_compact(self, block_ids, num_computed_tokens=num_computed_tokens,
+                           num_query_tokens=num_query_tokens, num_reserved_query_tokens=num_reserved_query_tokens,
+                           retained_query_indices=retained_query_indices,
+                           num_readonly_prefix_blocks=num_readonly_prefix_blocks)
 
     @torch.inference_mode()
     def compact_many(self, requests) -> tuple[int, ...]:
-        """``compact`` for every request of a step in one launch (one mapping of
+        """``compact`` for every request of a step in one launch (one dict of
         ``compact``'s arguments, with ``block_ids``, per request)."""
 
         return hip_compact_many(self, requests)

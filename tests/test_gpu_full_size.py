@@ -62,7 +62,7 @@ def test_c3_full_mixed_batch() -> None:
     step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=computed,
                      layouts=_lin(*([512] * 8 + [1] * 56)), seed=3003)
     ctx = _run(step)
-    work = ctx._work(step.cache.layer_spec(step.layer_ids[0]), step.query.dtype)
+    work = ctx.work_of(step.cache.layer_spec(step.layer_ids[0]))
     assert work.num_prefill_units > 0 and work.waves_per_head > 0
 
 
@@ -71,7 +71,7 @@ def test_c4_full_one_layer_32k_contexts() -> None:
     step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[32768] * 16,
                      layouts=_lin(*([1] * 16)), num_blocks=32800, seed=4004)
     ctx = _run(step)
-    work = ctx._work(step.cache.layer_spec(step.layer_ids[0]), step.query.dtype)
+    work = ctx.work_of(step.cache.layer_spec(step.layer_ids[0]))
     assert work.num_jobs == 16  # every 32K sequence is split across waves and merged
 
 
@@ -86,5 +86,5 @@ def test_c5_full_tree_verification_shared_prefix() -> None:
     step = make_step(hq=12, hkv=2, d=128, bs=16, dtype=torch.bfloat16, computed=computed, layouts=layouts,
                      shared_prefix_blocks=128, seed=5005)
     ctx = _run(step)
-    work = ctx._work(step.cache.layer_spec(step.layer_ids[0]), step.query.dtype)
+    work = ctx.work_of(step.cache.layer_spec(step.layer_ids[0]))
     assert work.num_prefill_partial_slots > 0  # split-K tree verification

@@ -44,7 +44,7 @@ def _check(step, *, backend=None, dense=False, expect_prefill=True, waves=None):
     out = ctx.forward(lid, step.query, step.key, step.value, scale=step.scale)
     torch.cuda.synchronize()
     spec = step.cache.layer_spec(lid)
-    work = ctx._work(spec, step.query.dtype)
+    work = ctx.work_of(spec)
     assert (work.num_prefill_units > 0) == expect_prefill
     if waves is not None and expect_prefill:
         assert work.prefill_waves == (waves if spec.head_size <= 128 else 4)
@@ -157,7 +157,7 @@ def _tree(rng, n):
 def _split_work(step, waves=None):
     backend = lv.HipPagedAttentionBackend(prefill_waves=waves)
     ctx = backend.create(step.cache, step.metadata)
-    return backend, ctx._work(step.cache.layer_spec(step.layer_ids[0]), step.query.dtype)
+    return backend, ctx.work_of(step.cache.layer_spec(step.layer_ids[0]))
 
 
 @pytest.mark.parametrize("waves", WAVES)
@@ -212,7 +212,7 @@ def test_split_k_matches_the_unsplit_kernel() -> None:
     a = _check(step, backend=backend)
     whole = lv.HipPagedAttentionBackend(split_prefill=False)
     ctx = whole.create(step.cache, step.metadata)
-    w2 = ctx._work(step.cache.layer_spec(step.layer_ids[0]), step.query.dtype)
+    w2 = ctx.work_of(step.cache.layer_spec(step.layer_ids[0]))
     assert w2.num_prefill_partial_slots == 0 and w2.num_prefill_units == 2
     b = _check(step, backend=whole)
     assert (a.float() - b.float()).abs().max().item() <= 2e-2

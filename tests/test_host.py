@@ -392,26 +392,33 @@ def test_kv_cache_bytes_per_block() -> None:
     assert lv.kv_cache_bytes_per_block(spec, block_size=2, dtype=torch.float32) == 128
 
 
-def _tables_valid_of(md, num_blocks, bs):
-    from light_vllm_amd.plan import tables_valid
-    counts = np.asarray([len(t) for t in md.block_tables], dtype=np.int64)
-    flat = np.asarray([b for t in md.block_tables for b in t], dtype=np.int64)
-    return tables_valid(flat, counts, np.asarray(md.num_computed_tokens, dtype=np.int64),
-                        np.asarray(md.num_reserved_query_tokens, dtype=np.int64),
-                        np.asarray(md.num_readonly_prefix_blocks, dtype=np.int64),
-                        num_blocks=num_blocks, block_size=bs)
+def _oracle_message(fn, *args, **kwargs):
+    try:
+        fn(*args, **kwargs)
+    except (O.OracleKVCacheError, ValueError) as exc:
+        return type(exc).__name__.replace("Oracle", ""), str(exc)
+    return None
 
 
-@pytest.mark.parametrize("seed", range(54))
-def test_vectorised_table_check_agrees_with_validate_block_tables(seed) -> None:
-    """The step plan's array check passes exactly when the metadata's own
-    validate_block_tables does, on valid steps and on each kind of mistake
-    (short/long tables, out-of-range ids, aliasing within and across
-    requests, readonly sharing at another logical index or of a writable
-    block or at another logical index, readonly counts past the prefix)."""
+def _plan_message(fn, *args, **kwargs):
+    try:
+        fn(*args, **kwargs)
+    except (lv.KVCacheError, ValueError) as exc:
+        return type(exc).__name__, str(exc)
+    return None
+
+
+@pytest.mark.parametrize("seed", range(90))
+def test_native_table_rules_raise_the_oracles_message(seed) -> None:
+    """The native block-table check raises exactly the message the oracle's
+    restatement of validate_block_tables raises (paged_attention.py:138-172),
+    on valid steps, on each kind of mistake (short/long tables, out-of-range
+    ids, aliasing within and across requests, readonly sharing at another
+    logical index or of a writable block, readonly counts past the prefix),
+    and on steps with two mistakes at once, where the rule order decides."""
 
     rng = np.random.default_rng(seed)
-    bs = int(rng.choice([1, 4, 16]))
+    bs = int(rng.choice([1, 3, 4, 16]))
     batch = int(rng.integers(1, 7))
     shared = int(rng.integers(0, 3))
     computed = [shared * bs + int(rng.integers(0, 40)) for _ in range(batch)]
@@ -424,41 +431,38 @@ def test_vectorised_table_check_agrees_with_validate_block_tables(seed) -> None:
         rest = rest[n - shared :]
     readonly = [shared] * batch
     num_blocks = len(pool)
-    kind = seed % 9
-    r = int(rng.integers(0, batch))
-    if kind == 1:
-        tables[r] = tables[r][:-1] or tables[r]
-    elif kind == 2:
-        tables[r] = tables[r] + [rest[0] if rest else num_blocks - 1]
-    elif kind == 3:
-        tables[r][-1] = num_blocks + int(rng.integers(0, 3))
-    elif kind == 4 and len(tables[r]) > 1:
-        tables[r][-1] = tables[r][0]
-    elif kind == 5 and batch > 1:
-        other = (r + 1) % batch
-        tables[r][-1] = tables[other][-1]
-    elif kind == 6 and shared and batch > 1:
-        readonly[r] = 0  # a shared block that this request may write
-    elif kind == 7:
-        readonly[r] = len(tables[r]) + 1
-    elif kind == 8 and shared == 2:  # a shared readonly block at another logical index
-        tables[r][0], tables[r][1] = tables[r][1], tables[r][0]
+
+    def plant(kind: int) -> None:
+        r = int(rng.integers(0, batch))
+        if kind == 1:
+            tables[r] = tables[r][:-1] or tables[r]
+        elif kind == 2:
+            tables[r] = tables[r] + [rest[0] if rest else num_blocks - 1]
+        elif kind == 3:
+            tables[r][-1] = num_blocks + int(rng.integers(0, 3))
+        elif kind == 4 and len(tables[r]) > 1:
+            tables[r][-1] = tables[r][0]
+        elif kind == 5 and batch > 1:
+            tables[r][-1] = tables[(r + 1) % batch][-1]
+        elif kind == 6 and shared and batch > 1:
+            readonly[r] = 0  # a shared block that this request may write
+        elif kind == 7:
+            readonly[r] = len(tables[r]) + 1
+        elif kind == 8 and shared == 2:  # a shared readonly block at another logical index
+            tables[r][0], tables[r][1] = tables[r][1], tables[r][0]
+
+    plant(seed % 9)
+    if seed >= 45:
+        plant(int(rng.integers(1, 9)))
     md = lv.PagedAttentionMetadata(
         block_tables=tuple(tuple(t) for t in tables), num_computed_tokens=tuple(computed),
         query_layouts=tuple(lv.QueryLayout((-1,)) for _ in range(batch)),
         num_reserved_query_tokens=tuple(reserved), num_readonly_prefix_blocks=tuple(readonly),
     )
-    try:
-        md.validate_block_tables(num_blocks=num_blocks, block_size=bs)
-        ok = True
-    except lv.KVCacheError:
-        ok = False
-    assert _tables_valid_of(md, num_blocks, bs) == ok
-    if not ok:  # the plan raises the metadata's own message
-        with pytest.raises(lv.KVCacheError):
-            StepPlan(md, block_size=bs, device=CPU, num_blocks=num_blocks)
-    else:
-        StepPlan(md, block_size=bs, device=CPU, num_blocks=num_blocks)
+    expect = _oracle_message(O.validate_block_tables, md.block_tables, computed, reserved, readonly,
+                             num_blocks=num_blocks, block_size=bs)
+    assert _plan_message(md.validate_block_tables, num_blocks=num_blocks, block_size=bs) == expect
+    assert _plan_message(StepPlan, md, block_size=bs, device=CPU, num_blocks=num_blocks) == expect
 
 
 def test_prefill_shape_choice_follows_the_measured_workloads() -> None:
@@ -501,30 +505,77 @@ def test_compact_slots_known_answer_and_rules() -> None:
             compact_slots(cfg, table, **kw)
 
 
-def test_compact_trusts_only_the_table_objects_a_step_plan_proved() -> None:
-    """A step plan that validated its tables lists those tuple objects, and
-    compact then skips their id checks; an equal tuple that is another object,
-    or another pool size, is checked again.  The list is bounded."""
+@pytest.mark.parametrize("seed", range(60))
+def test_native_compact_rules_raise_the_oracles_message(seed) -> None:
+    """compact's rules in the native planner raise what the oracle's
+    restatement of PagedKVCache.compact raises (paged_cache.py:276-302), one
+    or two planted mistakes at a time, and valid requests give the oracle's
+    slot pairs."""
 
     from types import SimpleNamespace
 
-    from light_vllm_amd import plan as P
-    from light_vllm_amd.paged_cache import compact_slots
+    from light_vllm_amd.paged_cache import _compact_plan
 
-    rng = np.random.default_rng(3)
-    md = _random_metadata(rng, batch=4, bs=4)
-    num_blocks = max(max(t) for t in md.block_tables) + 1
-    StepPlan(md, block_size=4, device=CPU, num_blocks=num_blocks)
-    cfg = SimpleNamespace(block_size=4, num_blocks=num_blocks)
-    for r, table in enumerate(md.block_tables):
-        copy = tuple(list(table))
-        assert P.table_proven(table, num_blocks)
-        assert not P.table_proven(table, num_blocks + 1)
-        assert not P.table_proven(copy, num_blocks)
-        q = md.query_lengths[r]
-        kw = dict(num_computed_tokens=md.num_computed_tokens[r], num_query_tokens=q,
-                  num_reserved_query_tokens=md.num_reserved_query_tokens[r],
-                  retained_query_indices=tuple(range(q))[::-1])
-        assert compact_slots(cfg, table, **kw) == compact_slots(cfg, copy, **kw)
-    P.note_proven_tables([(i,) for i in range(P._PROVEN_LIMIT + 10)], 1 << 20)
-    assert len(P._PROVEN_TABLES) == P._PROVEN_LIMIT
+    rng = np.random.default_rng(700 + seed)
+    bs = int(rng.choice([1, 2, 16]))
+    computed, queries = int(rng.integers(0, 50)), int(rng.integers(1, 10))
+    reserved = queries + int(rng.integers(0, 3))
+    readonly = int(rng.integers(0, computed // bs + 1))
+    need = (computed + reserved + bs - 1) // bs
+    num_blocks = need + 6
+    table = [int(x) for x in rng.permutation(num_blocks)[:need]]
+    retained = [int(x) for x in rng.permutation(queries)[: int(rng.integers(1, queries + 1))]]
+    counts = dict(num_computed_tokens=computed, num_query_tokens=queries, num_reserved_query_tokens=reserved,
+                  num_readonly_prefix_blocks=readonly)
+
+    def plant(kind: int) -> None:
+        if kind == 1:
+            counts["num_computed_tokens"] = -1
+        elif kind == 2:
+            counts["num_reserved_query_tokens"] = queries - 1
+        elif kind == 3:
+            retained[0] = True
+        elif kind == 4 and len(retained) > 1:
+            retained[1] = retained[0]
+        elif kind == 5:
+            retained[0] = queries
+        elif kind == 6:
+            table.append(num_blocks - 1)
+        elif kind == 7:
+            table[0] = num_blocks
+        elif kind == 8 and len(table) > 1:
+            table[-1] = table[0]
+        elif kind == 9:
+            counts["num_readonly_prefix_blocks"] = computed // bs + 1
+
+    plant(seed % 10)
+    if seed >= 30:
+        plant(int(rng.integers(1, 10)))
+    pools = [(np.zeros((num_blocks, bs, 1, 1), np.float32), np.zeros((num_blocks, bs, 1, 1), np.float32))]
+    expect = _oracle_message(O.compact, pools, tuple(table), retained_query_indices=tuple(retained),
+                             num_blocks=num_blocks, block_size=bs, **counts)
+    cfg = SimpleNamespace(block_size=bs, num_blocks=num_blocks)
+    request = dict(block_ids=tuple(table), retained_query_indices=tuple(retained), **counts)
+    got = _plan_message(_compact_plan, cfg, (request,))
+    assert got == expect
+    if expect is None:
+        moved, src, dst = _compact_plan(cfg, (request,))
+        slot = lambda pos: table[pos // bs] * bs + pos % bs  # noqa: E731
+        pairs = [(slot(computed + i), slot(computed + j)) for j, i in enumerate(retained)]
+        assert list(zip(src.tolist(), dst.tolist())) == [p for p in pairs if p[0] != p[1]]
+        assert moved.tolist() == [sum(a != b for a, b in pairs)]
+
+
+def test_compact_many_batch_rule_and_missing_arguments() -> None:
+    from types import SimpleNamespace
+
+    from light_vllm_amd.paged_cache import _compact_plan
+
+    cfg = SimpleNamespace(block_size=2, num_blocks=8)
+    req = dict(block_ids=(0, 1), num_computed_tokens=1, num_query_tokens=2, num_reserved_query_tokens=2,
+               retained_query_indices=(1,))
+    assert _compact_plan(cfg, [req])[0].tolist() == [1]
+    with pytest.raises(lv.KVCacheError, match="same slot"):
+        _compact_plan(cfg, [req, req])
+    with pytest.raises(TypeError, match="needs block_ids"):
+        _compact_plan(cfg, [dict(block_ids=(0, 1), num_computed_tokens=1)])
