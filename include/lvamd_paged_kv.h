@@ -31,7 +31,8 @@ enum lvamd_status {
   LVAMD_ERR_INVALID_ARGUMENT = -1,  /* null pointer, negative size, misaligned row  */
   LVAMD_ERR_UNSUPPORTED = -2,       /* dtype / head_size / group size not built     */
   LVAMD_ERR_WORKSPACE = -3,         /* missing or undersized workspace              */
-  LVAMD_ERR_LAUNCH = -4             /* hipLaunchKernel / hipGetLastError failed     */
+  LVAMD_ERR_LAUNCH = -4,            /* hipLaunchKernel / hipGetLastError failed     */
+  LVAMD_ERR_SCRATCH_LIMIT = -5      /* input needs more than the static scratch     */
 };
 
 enum lvamd_dtype { LVAMD_F32 = 0, LVAMD_F16 = 1, LVAMD_BF16 = 2 };
@@ -254,6 +255,27 @@ int lvamd_kv_compact(const uint64_t* layer_key_ptrs, const uint64_t* layer_value
                      const int64_t* src_slots, const int64_t* dst_slots, int64_t num_pairs,
                      void* workspace, int64_t workspace_bytes, lvamd_stream_t stream);
 int64_t lvamd_kv_compact_inline_pairs(void);
+
+/*
+ * Allocation-free variant of lvamd_kv_compact: the same kernels and result,
+ * but calls with more than lvamd_kv_compact_inline_pairs() pairs stage their
+ * rows in a device array the library holds (LVAMD_COMPACT_STATIC_SCRATCH_BYTES
+ * per GPU, for the life of the process) instead of a caller workspace, so the
+ * call itself allocates nothing (no hipMalloc, no library allocation).
+ * Returns LVAMD_ERR_SCRATCH_LIMIT, without launching, when
+ * num_pairs * num_layers * 2 * row_bytes exceeds that size.  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams, other threads) race and must be serialised by the caller.
+ *
+ * No counterpart in the reference.  It is for callers that cannot allocate:
+ * code under HIP graph capture, tight serving loops, and harnesses that
+ * forbid hipMalloc.
+ */
+#define LVAMD_COMPACT_STATIC_SCRATCH_BYTES (16LL << 20)
+int lvamd_kv_compact_static(const uint64_t* layer_key_ptrs, const uint64_t* layer_value_ptrs,
+                            int32_t num_layers, int64_t row_bytes,
+                            const int64_t* src_slots, const int64_t* dst_slots, int64_t num_pairs,
+                            lvamd_stream_t stream);
 int64_t lvamd_kv_compact_workspace_size(int64_t num_pairs, int32_t num_layers, int64_t row_bytes);
 
 /*

@@ -8,7 +8,9 @@
 //   compact - PagedKVCache.compact        (src/light_vllm/runtime/execution/paged_cache.py:257-326)
 //   block copy has no reference counterpart (copy-on-write of a whole block).
 
+#include <atomic>
 #include <initializer_list>
+#include <mutex>
 #include <type_traits>
 
 #include "lvamd_common.h"
@@ -269,6 +271,43 @@ __global__ __launch_bounds__(256) void kv_compact_phase_kernel(const CompactArgs
 }
 
 // ---------------------------------------------------------------------------
+// Allocation-free compact (lvamd_kv_compact_static): the two-phase kernels
+// stage their rows in this file-scope array instead of a caller workspace.
+// Each GPU holds its own copy for the life of the process; its device
+// address is looked up once per device (hipGetSymbolAddress, with that device
+// current) and kept, and only that address is handed to kernels.  Every call
+// on a GPU shares the array: calls that overlap on one GPU race.  Nothing in
+// it needs clearing (the gather phase writes every staged byte before the
+// scatter phase reads it).
+// ---------------------------------------------------------------------------
+constexpr int64_t kStaticScratchBytes = LVAMD_COMPACT_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<char*> g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mutex;
+
+// The current device's address of ``scratch``.
+static int static_scratch(char** out) {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return LVAMD_ERR_LAUNCH;
+  if (device < 0 || device >= kMaxDevices) return LVAMD_ERR_UNSUPPORTED;
+  char* ptr = g_scratch_ptr[device].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    ptr = g_scratch_ptr[device].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      void* addr = nullptr;
+      if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || addr == nullptr) return LVAMD_ERR_LAUNCH;
+      ptr = static_cast<char*>(addr);
+      g_scratch_ptr[device].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return LVAMD_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Block copy: grid over (pair, layer, K|V); threads stride over the block.
 // ---------------------------------------------------------------------------
 struct BlockCopyArgs {
@@ -319,11 +358,12 @@ const char* lvamd_status_string(int status) {
     case LVAMD_ERR_UNSUPPORTED: return "unsupported dtype, head size or group size";
     case LVAMD_ERR_WORKSPACE: return "workspace missing or too small";
     case LVAMD_ERR_LAUNCH: return "kernel launch failed";
+    case LVAMD_ERR_SCRATCH_LIMIT: return "call needs more than the library's static scratch holds";
     default: return "unknown status";
   }
 }
 
-int lvamd_abi_version(void) { return 11; }
+int lvamd_abi_version(void) { return 12; }
 
 int lvamd_kv_append(const void* key, int64_t key_token_stride, int64_t key_head_stride,
                     const void* value, int64_t value_token_stride, int64_t value_head_stride,
@@ -480,6 +520,23 @@ int lvamd_kv_compact(const uint64_t* layer_key_ptrs, const uint64_t* layer_value
       break;
   }
   return launch_status();
+}
+
+int lvamd_kv_compact_static(const uint64_t* layer_key_ptrs, const uint64_t* layer_value_ptrs,
+                            int32_t num_layers, int64_t row_bytes,
+                            const int64_t* src_slots, const int64_t* dst_slots, int64_t num_pairs,
+                            lvamd_stream_t stream) {
+  if (num_pairs < 0 || num_layers <= 0 || row_bytes <= 0) return LVAMD_ERR_INVALID_ARGUMENT;
+  char* ws = nullptr;
+  if (num_pairs > kCompactInline) {
+    // Staged rows: num_pairs * num_layers * 2 * row_bytes, without overflow.
+    const int64_t per_pair = (int64_t)num_layers * 2 * row_bytes;
+    if (per_pair > kStaticScratchBytes || num_pairs > kStaticScratchBytes / per_pair) return LVAMD_ERR_SCRATCH_LIMIT;
+    const int status = static_scratch(&ws);
+    if (status != LVAMD_OK) return status;
+  }
+  return lvamd_kv_compact(layer_key_ptrs, layer_value_ptrs, num_layers, row_bytes, src_slots, dst_slots, num_pairs,
+                          ws, ws ? kStaticScratchBytes : 0, stream);
 }
 
 int lvamd_kv_block_copy(const uint64_t* layer_key_ptrs, const uint64_t* layer_value_ptrs,

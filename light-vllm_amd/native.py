@@ -19,7 +19,7 @@ from pathlib import Path
 from light_vllm_amd import errors
 
 LIB_NAME = "liblvamd_hip.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
@@ -72,6 +72,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lvamd_kv_compact": (
         ctypes.c_int,
         [_p, _p, _i32, _i64, _p, _p, _i64, _p, _i64, _p],
+    ),
+    "lvamd_kv_compact_static": (
+        ctypes.c_int,
+        [_p, _p, _i32, _i64, _p, _p, _i64, _p],
     ),
     "lvamd_kv_compact_inline_pairs": (_i64, []),
     "lvamd_kv_compact_workspace_size": (_i64, [_i64, _i32, _i64]),
