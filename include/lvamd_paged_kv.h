@@ -161,8 +161,8 @@ int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_str
  * dtype, head size and col_tiles: the planner's stream-K width.  Needs a GPU. */
 int lvamd_paged_decode_resident_waves(int32_t dtype, int32_t head_size, int32_t col_tiles);
 
-/* Tokens per decode-kernel tile for this dtype, head size and col_tiles (64
- * for one column tile, 32 for four; 16 for rows above 256 bytes): the planner
+/* Tokens per decode-kernel tile for this dtype, head size and col_tiles (32
+ * for one column tile, 16 for four; 16 for rows above 256 bytes): the planner
  * cuts pieces on multiples of it.  A piece may start anywhere; tile-aligned
  * pieces avoid partial tiles. */
 int lvamd_paged_decode_tile_tokens(int32_t dtype, int32_t head_size, int32_t col_tiles);

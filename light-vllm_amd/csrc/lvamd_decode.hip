@@ -29,7 +29,7 @@
 //     misses cost more than a separate launch.)
 //   * Fused append: this step's tokens are read from the input K/V and
 //     written to their pool slots by the piece that covers them.
-//   * Per tile (64 tokens for one column tile, 16 for four or for wide
+//   * Per tile (32 tokens for one column tile, 16 for four or for wide
 //     rows), lane (g = l/16, l%16) loads 16-byte chunks 4kk+g of token rows
 //     16s + l%16 of K and V: the K chunks land in VGPRs already in the
 //     A-operand layout of S^T = K Q^T (MFMA 16x16x32 bf16/fp16, 16x16x4
@@ -99,15 +99,17 @@ __device__ __forceinline__ int vslot(int r, int c) {
 }
 
 // Decode tile shape: a tile is TT tokens of one kv head.  With one column
-// tile per wave, TT = 64 when a head's row slice is at most 256 bytes
-// (bf16/fp16 up to D = 128, fp32 up to D = 64), else 16, so one tile's K (and
-// V) take at most 64 VGPRs per lane; with four column tiles TT = 16, which
-// leaves registers for their Q operands and accumulators (at TT = 32 the
-// bf16 D = 128 kernel spills).
+// tile per wave, TT = 32 when a head's row slice is at most 256 bytes
+// (bf16/fp16 up to D = 128, fp32 up to D = 64), else 16; with four column
+// tiles TT = 16, which leaves registers for their Q operands and accumulators
+// (at TT = 32 the bf16 D = 128 kernel spills).  32-token tiles beat 64 on the
+// Qwen2.5-7B decode (62.8 against 65.3 us in one process): the stream-K
+// shares, cut on whole tiles, then differ by a half tile instead of a whole
+// one, and the memory system stays saturated with 16 KiB per wave in flight.
 template <typename T, int D, int CTW>
 struct DecodeTile {
   static constexpr int ROW = (int)sizeof(T) * D;
-  static constexpr int TT1 = ROW <= 256 ? 64 : 16;
+  static constexpr int TT1 = ROW <= 256 ? 32 : 16;
   static constexpr int TT = CTW == 1 ? TT1 : 16;
   static constexpr int SUB = TT / 16;                                // 16-row groups per tile
   static constexpr int VSLOTS = SUB * TileShape<T, D>::NCH * 64;     // 16-byte LDS slots per V tile

@@ -371,7 +371,7 @@ def test_library_loads_and_exports_every_header_function() -> None:
     assert lib.lvamd_paged_prefill_key_tokens(2, 128) == 64 and lib.lvamd_paged_prefill_key_tokens(2, 256) == 32
     assert lib.lvamd_paged_prefill_key_tokens(0, 128) == -2  # no fp32 prefill kernel
     # Tile sizes per kernel; four column tiles only for rows of at most 256 bytes.
-    assert lib.lvamd_paged_decode_tile_tokens(2, 128, 1) == 64
+    assert lib.lvamd_paged_decode_tile_tokens(2, 128, 1) == 32
     assert lib.lvamd_paged_decode_tile_tokens(2, 128, 4) == 16
     assert lib.lvamd_paged_decode_tile_tokens(2, 256, 1) == 16
     assert lib.lvamd_paged_decode_tile_tokens(2, 256, 4) == -2
