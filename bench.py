@@ -281,7 +281,10 @@ def serving_steps(device: torch.device, steps: int, warmup: int) -> dict:
     stream = torch.cuda.current_stream(device)
     times = {"metadata": [], "plan": [], "submit": [], "gpu": [], "wall": []}
     kv_bytes = []
+    host = lv.native.host()
     for s in range(warmup + steps):
+        if s == warmup:
+            counts0 = host.counts()
         for r in range(cfg.batch):  # one more computed token; a new block when the last one filled
             computed[r] += 1
             if (computed[r] + 1 + cfg.bs - 1) // cfg.bs > len(blocks[r]):
@@ -307,9 +310,13 @@ def serving_steps(device: torch.device, steps: int, warmup: int) -> dict:
             kv_bytes.append(NUM_LAYERS * algorithmic_bytes(np.asarray(computed))["step"])
     assert torch.isfinite(out.float()).all()
     mean = {name: float(np.mean(vals)) for name, vals in times.items()}
+    proofs, checks, reused, read = (b - a for a, b in zip(counts0, host.counts()))
     return {
         "steps": steps,
         "layers": NUM_LAYERS,
+        "incremental_table_proofs": proofs,
+        "full_table_checks": checks,
+        "block_ids_reused_pct": round(100.0 * reused / max(1, reused + read), 1),
         "host_metadata_us": round(mean["metadata"] * 1e3, 1),
         "host_plan_us": round(mean["plan"] * 1e3, 1),
         "host_plan_us_p90": round(float(np.percentile(times["plan"], 90)) * 1e3, 1),

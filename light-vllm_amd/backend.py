@@ -27,6 +27,8 @@ decode / prefill work lists go to the GPU in one non-blocking copy.
 
 from __future__ import annotations
 
+import weakref
+
 import torch
 from torch import Tensor
 
@@ -387,6 +389,8 @@ class HipPagedAttentionBackend:
         self._prefill_waves = prefill_waves
         self._staging: dict[torch.device, Staging] = {}
         self._facts: dict[tuple, tuple[int, ...]] = {}
+        # cache -> kernel facts of its layer shapes (dropped with the cache).
+        self._shapes: "weakref.WeakKeyDictionary[object, tuple[tuple[int, ...], ...]]" = weakref.WeakKeyDictionary()
         self._last: tuple[object, object, StepPlan] | None = None
 
     def prefill_columns(self, code: int, head_size: int) -> int:
@@ -419,6 +423,20 @@ class HipPagedAttentionBackend:
             self._facts[key] = found
         return found
 
+    def _cache_facts(self, cache) -> tuple[tuple[int, ...], ...]:
+        """Kernel facts of each distinct supported layer shape of ``cache``
+        (looked up once per cache object)."""
+
+        found = self._shapes.get(cache)
+        if found is None:
+            config = cache.config
+            code = dtype_code(config.dtype)
+            shapes = {(s.num_query_heads, s.num_kv_heads, s.head_size): s for s in cache.model_spec.layers}
+            found = self._shapes[cache] = tuple(
+                self.kernel_facts(spec, code, config.block_size) for spec in shapes.values()
+                if spec.head_size in SUPPORTED_HEAD_SIZES)
+        return found
+
     def create(self, cache, metadata) -> HipPagedAttention:
         config = cache.config
         if config.device.type != "cuda":
@@ -433,11 +451,8 @@ class HipPagedAttentionBackend:
         plan = StepPlan(metadata, block_size=config.block_size, device=config.device, num_blocks=config.num_blocks,
                         partition_tokens=self._partition_tokens, staging=staging, defer_upload=True)
         # Every layer shape's work lists go up with the step facts.
-        code = dtype_code(config.dtype)
-        shapes = {(s.num_query_heads, s.num_kv_heads, s.head_size): s for s in cache.model_spec.layers}
-        for spec in shapes.values():
-            if spec.head_size in SUPPORTED_HEAD_SIZES:
-                plan.layer_work(self.kernel_facts(spec, code, config.block_size))
+        for facts in self._cache_facts(cache):
+            plan.layer_work(facts)
         plan.commit()
         self._last = (geometry, metadata, plan)
         return HipPagedAttention(self, cache, plan)

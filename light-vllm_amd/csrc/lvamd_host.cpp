@@ -104,6 +104,14 @@ bool as_i64(PyObject* o, int64_t* v) {
   return !(*v == -1 && PyErr_Occurred());
 }
 
+// Counts of how calls were served: incremental table proofs, full table
+// checks, and block ids taken from the previous flatten without reading
+// their int objects (against ids read).
+struct PlannerCounts {
+  long long incremental_proofs = 0, full_checks = 0, reused_ids = 0, read_ids = 0;
+};
+PlannerCounts g_counts;
+
 // ---------------------------------------------------------------------------
 // flatten(sequences, wide) -> (flat bytearray, counts int64 bytearray, status)
 // The concatenation of a sequence of int sequences (block tables, or one
@@ -141,6 +149,82 @@ int flatten_into(const std::vector<PyObject*>& rows, T* flat, int64_t* counts) {
   return status;
 }
 
+// The block tables of the previous int32 flatten.  Only tuple rows are kept,
+// with a reference each: a tuple cannot change and keeps its items alive, so
+// an item pointer equal to the previous row's is the same int object, of
+// the same value.  light-vllm builds every step's tables as
+// ``tuple(allocation.block_ids)`` over the same int objects, so a decode
+// step's rows repeat the previous step's items and add at most a block.
+struct PrevFlatten {
+  std::vector<PyObject*> rows;  // owned references (tuples), or nullptr
+  std::vector<int64_t> offsets;
+  std::vector<int32_t> values;
+
+  void reset() {
+    for (PyObject* row : rows) Py_XDECREF(row);
+    rows.clear();
+    offsets.clear();
+    values.clear();
+  }
+};
+PrevFlatten g_prev_flatten;
+
+// flatten_into for block tables, reusing the values of the leading items a
+// row shares (by identity) with the same row of the previous call.
+int flatten_tables_into(const std::vector<PyObject*>& rows, int32_t* flat, int64_t* counts) {
+  PrevFlatten& prev = g_prev_flatten;
+  int status = 0;
+  Py_ssize_t k = 0;
+  for (size_t r = 0; r < rows.size(); ++r) {
+    PyObject* row = rows[r];
+    const Py_ssize_t n = PySequence_Fast_GET_SIZE(row);
+    PyObject** items = PySequence_Fast_ITEMS(row);
+    counts[r] = n;
+    Py_ssize_t same = 0;
+    if (r < prev.rows.size() && prev.rows[r] != nullptr && PyTuple_CheckExact(row)) {
+      PyObject** old = PySequence_Fast_ITEMS(prev.rows[r]);
+      const Py_ssize_t limit = std::min(n, PyTuple_GET_SIZE(prev.rows[r]));
+      while (same < limit && items[same] == old[same]) ++same;
+      if (same) std::memcpy(flat + k, prev.values.data() + prev.offsets[r], (size_t)same * sizeof(int32_t));
+    }
+    g_counts.reused_ids += same;
+    g_counts.read_ids += n - same;
+    for (Py_ssize_t i = same; i < n; ++i) {
+      PyObject* o = items[i];
+      int32_t v = 0;
+      if (!PyLong_CheckExact(o)) {
+        status = 1;
+      } else {
+        int overflow = 0;
+        const long long x = PyLong_AsLongLongAndOverflow(o, &overflow);
+        if (overflow < 0 || (overflow == 0 && x < 0)) {
+          status = 1;
+        } else {
+          v = (overflow > 0 || x > INT32_MAX) ? INT32_MAX : (int32_t)x;
+        }
+      }
+      flat[k + i] = v;
+    }
+    k += n;
+  }
+  // Keep this call's tuple rows for the next one (only a fully valid call).
+  prev.reset();
+  if (status == 0) {
+    prev.rows.resize(rows.size(), nullptr);
+    prev.offsets.resize(rows.size(), 0);
+    prev.values.assign(flat, flat + k);
+    for (size_t r = 0, off = 0; r < rows.size(); ++r) {
+      prev.offsets[r] = (int64_t)off;
+      off += (size_t)PySequence_Fast_GET_SIZE(rows[r]);
+      if (PyTuple_CheckExact(rows[r])) {
+        Py_INCREF(rows[r]);
+        prev.rows[r] = rows[r];
+      }
+    }
+  }
+  return status;
+}
+
 PyObject* flatten(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   if (!want_args(nargs, 2, "flatten")) return nullptr;
   const int wide = PyObject_IsTrue(args[1]);
@@ -171,7 +255,7 @@ PyObject* flatten(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     int32_t* flat = nullptr;
     flat_obj = new_array<int32_t>(total, &flat);
     if (flat_obj == nullptr) goto done;
-    status = flatten_into<int32_t>(rows, flat, counts);
+    status = flatten_tables_into(rows, flat, counts);
   }
   result = Py_BuildValue("(OOi)", flat_obj, counts_obj, status);
 done:
@@ -213,7 +297,8 @@ struct BlockScratch {
     return epoch;
   }
 };
-BlockScratch g_scratch;
+BlockScratch g_scratch;          // validate's block owners
+BlockScratch g_compact_scratch;  // compact_pairs' per-table repeat check
 
 // Rule codes of validate, in the order the reference checks them per request.
 enum TableRule {
@@ -226,8 +311,83 @@ enum TableRule {
   kTableAliasMany = 6,  // "block tables alias a physical block across requests"
 };
 
+// The tables of the last call of validate that passed, with the epoch whose
+// block records they own.
+struct PrevTables {
+  std::vector<int32_t> flat;
+  std::vector<int64_t> counts, readonly;
+  int64_t num_blocks = -1, block_size = -1;
+  uint32_t epoch = 0;
+  bool valid = false;
+
+  void save(const int32_t* ids, const int64_t* cnt, const int64_t* ro, int64_t batch, int64_t nb, int64_t bs,
+            uint32_t ep) {
+    int64_t total = 0;
+    for (int64_t r = 0; r < batch; ++r) total += cnt[r];
+    flat.assign(ids, ids + total);
+    counts.assign(cnt, cnt + batch);
+    readonly.assign(ro, ro + batch);
+    num_blocks = nb;
+    block_size = bs;
+    epoch = ep;
+    valid = true;
+  }
+};
+PrevTables g_prev_tables;
+
+// The incremental proof of a decode step: every table of the last passing
+// call is a prefix of the same request's table now (same batch, same
+// readonly counts), and the block records of that call are still current.
+// Then the old blocks keep their proof; coverage and the readonly bound are
+// re-checked per request, and each appended block is checked for range and
+// for being listed nowhere else (an appended block lies past the readonly
+// prefix, so any other listing breaks a rule).  Returns true when the step
+// is proven; false sends it to the full check, which also names the first
+// broken rule.
+bool validate_appended(const int32_t* ids, const int64_t* cnt, const int64_t* comp, const int64_t* res,
+                       const int64_t* ro, int64_t batch, int64_t num_blocks, int64_t bs) {
+  PrevTables& prev = g_prev_tables;
+  BlockScratch& s = g_scratch;
+  if (!prev.valid || prev.num_blocks != num_blocks || prev.block_size != bs || prev.epoch != s.epoch ||
+      (int64_t)prev.counts.size() != batch)
+    return false;
+  for (int64_t r = 0, off = 0, old_off = 0; r < batch; off += cnt[r], old_off += prev.counts[r], ++r) {
+    const int64_t n = cnt[r], old_n = prev.counts[r];
+    if (n < old_n || ro[r] != prev.readonly[r]) return false;
+    if (n != (comp[r] + res[r] + bs - 1) / bs || ro[r] > n || ro[r] * bs > comp[r]) return false;
+    if (std::memcmp(ids + off, prev.flat.data() + old_off, (size_t)old_n * sizeof(int32_t)) != 0) return false;
+  }
+  // Appended blocks: stamped into the current epoch's records as they pass,
+  // so one appended twice is caught too.  A failure leaves stamps behind; the
+  // full check starts a new epoch, which voids them.
+  BlockRecord* rec = s.rec.data();
+  for (int64_t r = 0, off = 0; r < batch; off += cnt[r], ++r) {
+    for (int64_t i = prev.counts[r]; i < cnt[r]; ++i) {
+      const int32_t b = ids[off + i];
+      if ((uint32_t)b >= (uint32_t)num_blocks || rec[b].epoch == s.epoch) return false;
+      rec[b].epoch = s.epoch;
+      rec[b].request = (int32_t)r;
+      rec[b].owner = ((uint32_t)i << 1) | (uint32_t)(i < ro[r]);
+    }
+  }
+  prev.save(ids, cnt, ro, batch, num_blocks, bs, s.epoch);
+  ++g_counts.incremental_proofs;
+  return true;
+}
+
+// counts() -> (incremental table proofs, full table checks, reused ids, read ids)
+PyObject* counts(PyObject*, PyObject* const*, Py_ssize_t nargs) {
+  if (!want_args(nargs, 0, "counts")) return nullptr;
+  const PlannerCounts& c = g_counts;
+  return Py_BuildValue("(LLLL)", c.incremental_proofs, c.full_checks, c.reused_ids, c.read_ids);
+}
+
 // validate(flat i32, counts i64, computed i64, reserved i64, readonly i64,
 //          num_blocks, block_size) -> (rule, request)
+//
+// A decode step that only appends blocks to the last proven tables takes the
+// incremental proof (validate_appended); any other step, and any step it
+// cannot prove, takes the full check below.
 //
 // Per request, in order: coverage, range and readonly are checked first
 // (cheap, sequential); then one pass over the table visits each block's
@@ -262,6 +422,8 @@ PyObject* validate(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   }
   BlockScratch& s = g_scratch;
   s.reserve(num_blocks);
+  if (validate_appended(ids, cnt, comp, res, ro, batch, num_blocks, bs)) return Py_BuildValue("(in)", 0, (Py_ssize_t)-1);
+  ++g_counts.full_checks;
   const uint32_t epoch = s.next_epoch();
   BlockRecord* rec = s.rec.data();
   int rule = kTablesOk;
@@ -293,6 +455,11 @@ PyObject* validate(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     }
     if (repeat) { rule = kTableAliasOne; break; }
     if (bad_share) { rule = kTableAliasMany; break; }
+  }
+  if (rule == kTablesOk) {
+    g_prev_tables.save(ids, cnt, ro, batch, num_blocks, bs, epoch);
+  } else {
+    g_prev_tables.valid = false;
   }
   return Py_BuildValue("(in)", rule, rule == kTablesOk ? (Py_ssize_t)-1 : r);
 }
@@ -876,7 +1043,7 @@ PyObject* compact_pairs(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   PyObject* reqs = PySequence_Fast(args[0], "compact requests must be a sequence");
   if (reqs == nullptr) return nullptr;
   const Py_ssize_t nreq = PySequence_Fast_GET_SIZE(reqs);
-  BlockScratch& s = g_scratch;
+  BlockScratch& s = g_compact_scratch;
   s.reserve(num_blocks);
   std::vector<int64_t> src, dst, moved((size_t)nreq, 0);
   std::vector<int64_t> ret;
@@ -1016,6 +1183,7 @@ PyMethodDef kMethods[] = {
     {"decode_work", (PyCFunction)(void (*)(void))decode_work, METH_FASTCALL, "stream-K decode pieces"},
     {"prefill_work", (PyCFunction)(void (*)(void))prefill_work, METH_FASTCALL, "prefill units and merge jobs"},
     {"layer_work", (PyCFunction)(void (*)(void))layer_work, METH_FASTCALL, "one layer shape's choices and lists"},
+    {"counts", (PyCFunction)(void (*)(void))counts, METH_FASTCALL, "how the planner's calls were served"},
     {"compact_pairs", (PyCFunction)(void (*)(void))compact_pairs, METH_FASTCALL, "compact rules and moved slot pairs"},
     {nullptr, nullptr, 0, nullptr},
 };

@@ -584,3 +584,88 @@ def test_compact_many_batch_rule_and_missing_arguments() -> None:
         _compact_plan(cfg, [req, req])
     with pytest.raises(TypeError, match="needs block_ids"):
         _compact_plan(cfg, [dict(block_ids=(0, 1), num_computed_tokens=1)])
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_incremental_planner_paths_agree_with_a_fresh_check_every_step(seed) -> None:
+    """Decode-like steps: contexts grow, tables take new blocks, some steps
+    swap a request, mutate a list row in place, or plant a mistake (an
+    appended block already listed elsewhere or twice, one out of range, a
+    readonly change, a shrinking table).  Every step, the native flatten
+    (which reuses the previous step's values for identical int objects) must
+    equal a fresh conversion, and the native table check (which proves an
+    append-only step incrementally) must raise exactly the oracle's message."""
+
+    host = native.host()
+    proofs0, checks0, reused0, _ = host.counts()
+    rng = np.random.default_rng(900 + seed)
+    bs, batch = int(rng.choice([1, 4, 16])), 6
+    num_blocks = 400
+    free = [int(b) for b in rng.permutation(num_blocks)]
+    ints = {b: int(str(b)) for b in range(num_blocks + 8)}  # one int object per id, reused every step
+    computed = [int(rng.integers(0, 30)) for _ in range(batch)]
+    tables = []
+    for c in computed:
+        tables.append([ints[free.pop()] for _ in range((c + 1 + bs - 1) // bs)])
+    readonly = [0] * batch
+    for step in range(60):
+        for r in range(batch):
+            computed[r] += 1
+            while len(tables[r]) < (computed[r] + 1 + bs - 1) // bs:
+                tables[r].append(ints[free.pop()])
+        kind = int(rng.integers(0, 12)) if step % 3 == 2 else 0
+        r = int(rng.integers(0, batch))
+        rows = [tuple(t) for t in tables]
+        if kind == 1:  # an appended block already in another table
+            rows[r] = rows[r] + (rows[(r + 1) % batch][-1],)
+            computed_step = list(computed)
+            computed_step[r] += bs
+        elif kind == 2:  # an appended block out of range
+            rows[r] = rows[r] + (ints[num_blocks + 3],)
+            computed_step = list(computed)
+            computed_step[r] += bs
+        elif kind == 3:  # an appended block listed twice in its own table
+            rows[r] = rows[r] + (rows[r][0],)
+            computed_step = list(computed)
+            computed_step[r] += bs
+        elif kind == 4:  # a readonly prefix appears
+            computed_step = list(computed)
+            readonly_step = list(readonly)
+        elif kind == 5:  # a row given as a list that is mutated in place afterwards
+            rows[r] = list(rows[r])
+            computed_step = list(computed)
+        else:
+            computed_step = list(computed)
+        readonly_step = list(readonly)
+        if kind == 4:
+            readonly_step[r] = min(1, computed_step[r] // bs)
+        if kind == 6 and len(rows[r]) > 1:  # a shrinking table (coverage breaks)
+            rows[r] = rows[r][:-1]
+        if kind == 7:  # a request replaced by a fresh one
+            fresh = [ints[free.pop()] for _ in range((3 + 1 + bs - 1) // bs)]
+            tables[r] = fresh
+            computed[r] = computed_step[r] = 3
+            rows[r] = tuple(fresh)
+        reserved = [1] * batch
+        flat, counts, status = host.flatten(rows, False)
+        assert status == 0
+        expect_flat = [b for row in rows for b in row]
+        assert np.frombuffer(flat, dtype=np.int32).tolist() == expect_flat
+        assert np.frombuffer(counts, dtype=np.int64).tolist() == [len(row) for row in rows]
+        if kind == 5:
+            rows[r].append(ints[num_blocks + 1])  # in place: the next flatten must not trust it
+            again, _, _ = host.flatten(rows, False)
+            assert np.frombuffer(again, dtype=np.int32).tolist() == [b for row in rows for b in row]
+            rows[r].pop()
+            host.flatten(rows, False)
+        expect = _oracle_message(O.validate_block_tables, rows, computed_step, reserved, readonly_step,
+                                 num_blocks=num_blocks, block_size=bs)
+        rule, _ = host.validate(np.frombuffer(flat, dtype=np.int32), np.frombuffer(counts, dtype=np.int64),
+                                np.asarray(computed_step, dtype=np.int64), np.asarray(reserved, dtype=np.int64),
+                                np.asarray(readonly_step, dtype=np.int64), num_blocks, bs)
+        from light_vllm_amd.facts import TABLE_RULES
+        got = None if rule == 0 else ("KVCacheError", TABLE_RULES[rule])
+        assert got == expect, f"step {step} kind {kind}"
+    proofs, checks, reused, _ = host.counts()
+    assert proofs - proofs0 >= 20 and checks - checks0 >= 5, "both table paths must be exercised"
+    assert reused - reused0 > 0, "the flatten must have reused the previous step's values"
