@@ -34,7 +34,7 @@ from torch import Tensor
 
 from light_vllm_amd import errors, native
 from light_vllm_amd.paged_cache import current_stream, dtype_code, hip_append, hip_append_rotary
-from light_vllm_amd.plan import DECODE_MAX_COLUMNS, PREFILL_MIN_TILES, UNIT_TOKENS, Staging, StepPlan
+from light_vllm_amd.plan import DECODE_MAX_COLUMNS, PREFILL_MIN_TILES, UNIT_TOKENS, LayerShapes, Staging, StepPlan
 
 SUPPORTED_HEAD_SIZES = (32, 64, 80, 96, 128, 256)
 
@@ -390,7 +390,7 @@ class HipPagedAttentionBackend:
         self._staging: dict[torch.device, Staging] = {}
         self._facts: dict[tuple, tuple[int, ...]] = {}
         # cache -> kernel facts of its layer shapes (dropped with the cache).
-        self._shapes: "weakref.WeakKeyDictionary[object, tuple[tuple[int, ...], ...]]" = weakref.WeakKeyDictionary()
+        self._shapes: "weakref.WeakKeyDictionary[object, LayerShapes]" = weakref.WeakKeyDictionary()
         self._last: tuple[object, object, StepPlan] | None = None
 
     def prefill_columns(self, code: int, head_size: int) -> int:
@@ -423,7 +423,7 @@ class HipPagedAttentionBackend:
             self._facts[key] = found
         return found
 
-    def _cache_facts(self, cache) -> tuple[tuple[int, ...], ...]:
+    def _cache_shapes(self, cache) -> LayerShapes:
         """Kernel facts of each distinct supported layer shape of ``cache``
         (looked up once per cache object)."""
 
@@ -432,7 +432,7 @@ class HipPagedAttentionBackend:
             config = cache.config
             code = dtype_code(config.dtype)
             shapes = {(s.num_query_heads, s.num_kv_heads, s.head_size): s for s in cache.model_spec.layers}
-            found = self._shapes[cache] = tuple(
+            found = self._shapes[cache] = LayerShapes(
                 self.kernel_facts(spec, code, config.block_size) for spec in shapes.values()
                 if spec.head_size in SUPPORTED_HEAD_SIZES)
         return found
@@ -448,11 +448,9 @@ class HipPagedAttentionBackend:
         staging = self._staging.get(config.device)
         if staging is None:
             staging = self._staging[config.device] = Staging(config.device)
+        # One native call validates, plans every layer shape of the cache and
+        # stages it all; one copy uploads it.
         plan = StepPlan(metadata, block_size=config.block_size, device=config.device, num_blocks=config.num_blocks,
-                        partition_tokens=self._partition_tokens, staging=staging, defer_upload=True)
-        # Every layer shape's work lists go up with the step facts.
-        for facts in self._cache_facts(cache):
-            plan.layer_work(facts)
-        plan.commit()
+                        partition_tokens=self._partition_tokens, staging=staging, shapes=self._cache_shapes(cache))
         self._last = (geometry, metadata, plan)
         return HipPagedAttention(self, cache, plan)

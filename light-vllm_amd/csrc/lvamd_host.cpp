@@ -16,11 +16,15 @@
 //               first in the reference's order, and the request;
 //   layouts     query lengths and uint32 ancestor bit rows of tree layouts
 //               (query_visibility, src/light_vllm/runtime/execution/layout.py:44-55);
+//   metadata    the metadata constructor's field rules and defaults
+//               (paged_attention.py:29-62) plus flatten and layouts, in one call;
 //   stage       slots (slot_mapping, paged_attention.py:110-136) and the
 //               per-request records, written straight into a staging buffer;
 //   decode_work / prefill_work / layer_work
 //               the stream-K split of decode rows and the prefill units, and
 //               (layer_work) the per-step kernel choices of a layer shape;
+//   plan_step   validate + stage + layer_work for every layer shape, written
+//               into one pinned staging buffer (the backend's per-step call);
 //   compact_pairs
 //               the rules and slots of PagedKVCache.compact
 //               (src/light_vllm/runtime/execution/paged_cache.py:257-314) for
@@ -184,7 +188,11 @@ int flatten_tables_into(const std::vector<PyObject*>& rows, int32_t* flat, int64
     if (r < prev.rows.size() && prev.rows[r] != nullptr && PyTuple_CheckExact(row)) {
       PyObject** old = PySequence_Fast_ITEMS(prev.rows[r]);
       const Py_ssize_t limit = std::min(n, PyTuple_GET_SIZE(prev.rows[r]));
-      while (same < limit && items[same] == old[same]) ++same;
+      if (std::memcmp(items, old, (size_t)limit * sizeof(PyObject*)) == 0) {
+        same = limit;  // the usual decode step: the whole old row, maybe a block more
+      } else {
+        while (same < limit && items[same] == old[same]) ++same;
+      }
       if (same) std::memcpy(flat + k, prev.values.data() + prev.offsets[r], (size_t)same * sizeof(int32_t));
     }
     g_counts.reused_ids += same;
@@ -382,6 +390,9 @@ PyObject* counts(PyObject*, PyObject* const*, Py_ssize_t nargs) {
   return Py_BuildValue("(LLLL)", c.incremental_proofs, c.full_checks, c.reused_ids, c.read_ids);
 }
 
+int check_tables(const int32_t* ids, const int64_t* cnt, const int64_t* comp, const int64_t* res, const int64_t* ro,
+                 int64_t batch, int64_t num_blocks, int64_t bs, int64_t* bad);
+
 // validate(flat i32, counts i64, computed i64, reserved i64, readonly i64,
 //          num_blocks, block_size) -> (rule, request)
 //
@@ -420,14 +431,25 @@ PyObject* validate(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     PyErr_SetString(PyExc_ValueError, "validate: counts do not match the flat table");
     return nullptr;
   }
+  int64_t bad = -1;
+  const int rule = check_tables(ids, cnt, comp, res, ro, batch, num_blocks, bs, &bad);
+  return Py_BuildValue("(in)", rule, (Py_ssize_t)bad);
+}
+
+// The rule check behind validate (arguments already consistent): the
+// incremental proof when it applies, else the full check.  Returns the
+// first broken rule (kTablesOk if none) and sets *bad to its request.
+int check_tables(const int32_t* ids, const int64_t* cnt, const int64_t* comp, const int64_t* res, const int64_t* ro,
+                 int64_t batch, int64_t num_blocks, int64_t bs, int64_t* bad) {
   BlockScratch& s = g_scratch;
   s.reserve(num_blocks);
-  if (validate_appended(ids, cnt, comp, res, ro, batch, num_blocks, bs)) return Py_BuildValue("(in)", 0, (Py_ssize_t)-1);
+  *bad = -1;
+  if (validate_appended(ids, cnt, comp, res, ro, batch, num_blocks, bs)) return kTablesOk;
   ++g_counts.full_checks;
   const uint32_t epoch = s.next_epoch();
   BlockRecord* rec = s.rec.data();
   int rule = kTablesOk;
-  Py_ssize_t r = 0;
+  int64_t r = 0;
   for (int64_t off = 0; r < batch; off += cnt[r], ++r) {
     const int64_t n = cnt[r];
     const int64_t required = (comp[r] + res[r] + bs - 1) / bs;
@@ -460,8 +482,9 @@ PyObject* validate(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     g_prev_tables.save(ids, cnt, ro, batch, num_blocks, bs, epoch);
   } else {
     g_prev_tables.valid = false;
+    *bad = r;
   }
-  return Py_BuildValue("(in)", rule, rule == kTablesOk ? (Py_ssize_t)-1 : r);
+  return rule;
 }
 
 // ---------------------------------------------------------------------------
@@ -471,26 +494,21 @@ PyObject* validate(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
 // uint32 row per query: bit j of word w of row q set iff query 32w + j is q
 // or an ancestor of q.  status 1: a parent is not an int in [-1, index).
 // ---------------------------------------------------------------------------
-PyObject* layouts(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
-  if (!want_args(nargs, 1, "layouts")) return nullptr;
-  PyObject* outer = PySequence_Fast(args[0], "query layouts must be a sequence");
-  if (outer == nullptr) return nullptr;
-  const Py_ssize_t batch = PySequence_Fast_GET_SIZE(outer);
-  int64_t *qlen = nullptr, *voff = nullptr, *vwords = nullptr;
-  PyObject* qlen_obj = new_array<int64_t>(batch, &qlen);
-  PyObject* voff_obj = new_array<int64_t>(batch, &voff);
-  PyObject* vwords_obj = new_array<int64_t>(batch, &vwords);
-  std::vector<uint32_t> vis;
-  std::vector<int32_t> parents;
-  PyObject* result = nullptr;
+PyObject* g_parent_indices = nullptr;  // interned "parent_indices"
+
+// layouts' body over ``batch`` layout objects: fills the per-request arrays
+// and appends the ancestor rows to ``vis``.  Returns the status, or -1 with
+// a Python error set (no parent_indices, not a sequence).
+int parse_layouts(PyObject* const* layouts, Py_ssize_t batch, int64_t* qlen, int64_t* voff, int64_t* vwords,
+                  std::vector<uint32_t>& vis) {
+  static std::vector<int32_t> parents;
   int status = 0;
-  if (qlen_obj == nullptr || voff_obj == nullptr || vwords_obj == nullptr) goto done;
   for (Py_ssize_t r = 0; r < batch; ++r) {
-    PyObject* attr = PyObject_GetAttrString(PySequence_Fast_GET_ITEM(outer, r), "parent_indices");
-    if (attr == nullptr) goto done;
+    PyObject* attr = PyObject_GetAttr(layouts[r], g_parent_indices);
+    if (attr == nullptr) return -1;
     PyObject* seq = PySequence_Fast(attr, "parent_indices must be a sequence");
     Py_DECREF(attr);
-    if (seq == nullptr) goto done;
+    if (seq == nullptr) return -1;
     const Py_ssize_t q = PySequence_Fast_GET_SIZE(seq);
     PyObject** items = PySequence_Fast_ITEMS(seq);
     parents.resize((size_t)q);
@@ -525,6 +543,24 @@ PyObject* layouts(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
       row[i >> 5] |= 1u << (i & 31);
     }
   }
+  return status;
+}
+
+PyObject* layouts(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (!want_args(nargs, 1, "layouts")) return nullptr;
+  PyObject* outer = PySequence_Fast(args[0], "query layouts must be a sequence");
+  if (outer == nullptr) return nullptr;
+  const Py_ssize_t batch = PySequence_Fast_GET_SIZE(outer);
+  int64_t *qlen = nullptr, *voff = nullptr, *vwords = nullptr;
+  PyObject* qlen_obj = new_array<int64_t>(batch, &qlen);
+  PyObject* voff_obj = new_array<int64_t>(batch, &voff);
+  PyObject* vwords_obj = new_array<int64_t>(batch, &vwords);
+  std::vector<uint32_t> vis;
+  PyObject* result = nullptr;
+  int status = 0;
+  if (qlen_obj == nullptr || voff_obj == nullptr || vwords_obj == nullptr) goto done;
+  status = parse_layouts(PySequence_Fast_ITEMS(outer), batch, qlen, voff, vwords, vis);
+  if (status < 0) goto done;
   {
     uint32_t* out = nullptr;
     PyObject* vis_obj = new_array<uint32_t>((Py_ssize_t)vis.size(), &out);
@@ -542,6 +578,227 @@ done:
 }
 
 // ---------------------------------------------------------------------------
+// metadata(block_tables, num_computed_tokens, query_layouts,
+//          num_reserved_query_tokens, num_readonly_prefix_blocks)
+//   -> rule (int 1..9) when a field rule fails, or
+//      ((tables, computed, layouts, reserved, readonly),
+//       (flat i32, counts i64, computed i64, reserved i64, readonly i64,
+//        q_lens i64, vis_off i64, vis_words i64, vis u32), tokens, linear)
+//
+// The construction of PagedAttentionMetadata in one pass
+// (src/light_vllm/runtime/execution/paged_attention.py:29-62): the fields
+// as tuples (every block table a tuple), the empty reserved field defaulting
+// to each layout's query count and the empty readonly field to zeros, and
+// the field rules in the reference's order:
+//   1 no request; 2 computed or layouts batch differs from the tables';
+//   3 reserved batch; 4 readonly batch; 5 a computed count not a
+//   non-negative exact int; 6 a reserved count not an exact int covering its
+//   layout's queries; 7 a readonly count not a non-negative exact int;
+//   8 a block id not a non-negative exact int; 9 a parent not -1 or an
+//   earlier query (checked by QueryLayout itself in the reference).
+// Then the step facts: flatten, the int fields as int64, layouts' rows.
+// A layout's query count is the length of its parent_indices.
+// ---------------------------------------------------------------------------
+enum MetadataRule {
+  kMdEmpty = 1,
+  kMdBatch = 2,
+  kMdReservedBatch = 3,
+  kMdReadonlyBatch = 4,
+  kMdComputed = 5,
+  kMdReserved = 6,
+  kMdReadonly = 7,
+  kMdBlockIds = 8,
+  kMdParents = 9,
+};
+
+// Exact non-negative ints of a tuple into int64 (clamped at INT64_MAX);
+// false when an item is not one.
+bool counts_of(PyObject* tuple, int64_t* out) {
+  const Py_ssize_t n = PyTuple_GET_SIZE(tuple);
+  bool ok = true;
+  for (Py_ssize_t i = 0; i < n; ++i) {
+    PyObject* o = PyTuple_GET_ITEM(tuple, i);
+    int64_t v = -1;
+    if (PyLong_CheckExact(o)) {
+      int overflow = 0;
+      const long long x = PyLong_AsLongLongAndOverflow(o, &overflow);
+      v = overflow > 0 ? INT64_MAX : (overflow < 0 ? -1 : x);
+    }
+    ok &= v >= 0;
+    out[i] = v;
+  }
+  return ok;
+}
+
+PyObject* metadata(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (!want_args(nargs, 5, "metadata")) return nullptr;
+  PyObject* fields[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};  // the five fields as tuples
+  PyObject* arrays[9] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  PyObject* result = nullptr;
+  int rule = 0;
+  Py_ssize_t batch = 0, total = 0;
+  int64_t *counts = nullptr, *computed = nullptr, *reserved = nullptr, *readonly = nullptr, *qlen = nullptr,
+          *voff = nullptr, *vwords = nullptr;
+  int32_t* flat = nullptr;
+  static std::vector<uint32_t> vis;
+  static std::vector<PyObject*> rows;
+  vis.clear();
+  int64_t tokens = 0;
+  bool linear = true;
+  for (int i = 0; i < 5; ++i) {
+    fields[i] = PySequence_Tuple(args[i]);
+    if (fields[i] == nullptr) goto done;
+  }
+  {
+    // Every block table as a tuple (a new outer tuple only if a row changes).
+    PyObject* tables = fields[0];
+    batch = PyTuple_GET_SIZE(tables);
+    PyObject* rebuilt = nullptr;
+    for (Py_ssize_t r = 0; r < batch; ++r) {
+      PyObject* row = PyTuple_GET_ITEM(tables, r);
+      if (PyTuple_CheckExact(row) && rebuilt == nullptr) continue;
+      if (rebuilt == nullptr) {
+        rebuilt = PyTuple_New(batch);
+        if (rebuilt == nullptr) goto done;
+        for (Py_ssize_t k = 0; k < r; ++k) PyTuple_SET_ITEM(rebuilt, k, Py_NewRef(PyTuple_GET_ITEM(tables, k)));
+      }
+      PyObject* as_tuple = PySequence_Tuple(row);
+      if (as_tuple == nullptr) {
+        Py_DECREF(rebuilt);
+        goto done;
+      }
+      PyTuple_SET_ITEM(rebuilt, r, as_tuple);
+    }
+    if (rebuilt != nullptr) {
+      Py_DECREF(fields[0]);
+      fields[0] = rebuilt;
+    }
+  }
+  if (batch == 0) {
+    rule = kMdEmpty;
+    goto done;
+  }
+  if (PyTuple_GET_SIZE(fields[1]) != batch || PyTuple_GET_SIZE(fields[2]) != batch) {
+    rule = kMdBatch;
+    goto done;
+  }
+  arrays[5] = new_array<int64_t>(batch, &qlen);
+  arrays[6] = new_array<int64_t>(batch, &voff);
+  arrays[7] = new_array<int64_t>(batch, &vwords);
+  if (arrays[5] == nullptr || arrays[6] == nullptr || arrays[7] == nullptr) goto done;
+  {
+    // Query counts (len of parent_indices; len(layout) where there is none).
+    PyObject** layouts = &PyTuple_GET_ITEM(fields[2], 0);
+    for (Py_ssize_t r = 0; r < batch; ++r) {
+      PyObject* attr = PyObject_GetAttr(layouts[r], g_parent_indices);
+      Py_ssize_t q;
+      if (attr != nullptr) {
+        q = PyObject_Size(attr);
+        Py_DECREF(attr);
+      } else {
+        PyErr_Clear();
+        q = PyObject_Size(layouts[r]);
+      }
+      if (q < 0) goto done;
+      qlen[r] = q;
+      tokens += q;
+    }
+  }
+  if (PyTuple_GET_SIZE(fields[3]) == 0) {
+    PyObject* filled = PyTuple_New(batch);
+    if (filled == nullptr) goto done;
+    for (Py_ssize_t r = 0; r < batch; ++r) {
+      PyObject* n = PyLong_FromLongLong(qlen[r]);
+      if (n == nullptr) {
+        Py_DECREF(filled);
+        goto done;
+      }
+      PyTuple_SET_ITEM(filled, r, n);
+    }
+    Py_SETREF(fields[3], filled);
+  }
+  if (PyTuple_GET_SIZE(fields[3]) != batch) {
+    rule = kMdReservedBatch;
+    goto done;
+  }
+  if (PyTuple_GET_SIZE(fields[4]) == 0) {
+    PyObject* zeros = PyTuple_New(batch);
+    if (zeros == nullptr) goto done;
+    for (Py_ssize_t r = 0; r < batch; ++r) PyTuple_SET_ITEM(zeros, r, PyLong_FromLong(0));
+    Py_SETREF(fields[4], zeros);
+  }
+  if (PyTuple_GET_SIZE(fields[4]) != batch) {
+    rule = kMdReadonlyBatch;
+    goto done;
+  }
+  arrays[2] = new_array<int64_t>(batch, &computed);
+  arrays[3] = new_array<int64_t>(batch, &reserved);
+  arrays[4] = new_array<int64_t>(batch, &readonly);
+  if (arrays[2] == nullptr || arrays[3] == nullptr || arrays[4] == nullptr) goto done;
+  if (!counts_of(fields[1], computed)) {
+    rule = kMdComputed;
+    goto done;
+  }
+  {
+    bool ok = counts_of(fields[3], reserved);
+    for (Py_ssize_t r = 0; r < batch; ++r) ok &= reserved[r] >= qlen[r];
+    if (!ok) {
+      rule = kMdReserved;
+      goto done;
+    }
+  }
+  if (!counts_of(fields[4], readonly)) {
+    rule = kMdReadonly;
+    goto done;
+  }
+  rows.assign(&PyTuple_GET_ITEM(fields[0], 0), &PyTuple_GET_ITEM(fields[0], 0) + batch);
+  for (PyObject* row : rows) total += PyTuple_GET_SIZE(row);
+  arrays[0] = new_array<int32_t>(total, &flat);
+  arrays[1] = new_array<int64_t>(batch, &counts);
+  if (arrays[0] == nullptr || arrays[1] == nullptr) goto done;
+  if (flatten_tables_into(rows, flat, counts) != 0) {
+    rule = kMdBlockIds;
+    goto done;
+  }
+  {
+    const int status = parse_layouts(&PyTuple_GET_ITEM(fields[2], 0), batch, qlen, voff, vwords, vis);
+    if (status < 0) goto done;
+    if (status > 0) {
+      rule = kMdParents;
+      goto done;
+    }
+    for (Py_ssize_t r = 0; r < batch; ++r) linear &= voff[r] < 0;
+  }
+  {
+    uint32_t* out = nullptr;
+    arrays[8] = new_array<uint32_t>((Py_ssize_t)vis.size(), &out);
+    if (arrays[8] == nullptr) goto done;
+    if (!vis.empty()) std::memcpy(out, vis.data(), vis.size() * 4);
+    PyObject* norm = PyTuple_New(5);
+    PyObject* facts = PyTuple_New(9);
+    if (norm == nullptr || facts == nullptr) {
+      Py_XDECREF(norm);
+      Py_XDECREF(facts);
+      goto done;
+    }
+    for (int i = 0; i < 5; ++i) {
+      PyTuple_SET_ITEM(norm, i, fields[i]);
+      fields[i] = nullptr;
+    }
+    for (int i = 0; i < 9; ++i) {
+      PyTuple_SET_ITEM(facts, i, arrays[i]);
+      arrays[i] = nullptr;
+    }
+    result = Py_BuildValue("(NNLO)", norm, facts, (long long)tokens, linear ? Py_True : Py_False);
+  }
+done:
+  for (PyObject* f : fields) Py_XDECREF(f);
+  for (PyObject* a : arrays) Py_XDECREF(a);
+  if (result == nullptr && rule != 0 && !PyErr_Occurred()) return PyLong_FromLong(rule);
+  return result;
+}
+
+// ---------------------------------------------------------------------------
 // stage(flat i32, counts i64, computed i64, q_lens i64, vis_off i64,
 //       vis_words i64, block_size, slots_out i64[T], req_meta_out i32[B*8]) -> status
 // slots_out[t] = table[pos // bs] * bs + pos % bs for pos = computed + offset;
@@ -549,6 +806,9 @@ done:
 // vis_words, 0).  status 1: a query position past its table (only possible
 // when the tables were not validated).
 // ---------------------------------------------------------------------------
+int stage_rows(const int32_t* ids, const int64_t* cnt, const int64_t* comp, const int64_t* ql, const int64_t* voff,
+               const int64_t* vwords, int64_t batch, int64_t bs, int64_t* out, int32_t* rm);
+
 PyObject* stage(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   if (!want_args(nargs, 9, "stage")) return nullptr;
   Buf flat(args[0], false, 4, "flat"), counts(args[1], false, 8, "counts"), computed(args[2], false, 8, "computed"),
@@ -571,20 +831,26 @@ PyObject* stage(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     PyErr_SetString(PyExc_ValueError, "stage: inconsistent arguments");
     return nullptr;
   }
-  const int32_t* ids = flat.data<int32_t>();
-  int64_t* out = slots.data<int64_t>();
-  int32_t* rm = meta.data<int32_t>();
+  const int status = stage_rows(flat.data<int32_t>(), cnt, comp, ql, vis_off.data<int64_t>(),
+                                vis_words.data<int64_t>(), batch, bs, slots.data<int64_t>(), meta.data<int32_t>());
+  return PyLong_FromLong(status);
+}
+
+// stage's body: slots and req_meta rows; returns 1 when a query position
+// lies past its table (its slot is -1), else 0.
+int stage_rows(const int32_t* ids, const int64_t* cnt, const int64_t* comp, const int64_t* ql, const int64_t* voff,
+               const int64_t* vwords, int64_t batch, int64_t bs, int64_t* out, int32_t* rm) {
   int status = 0;
   int64_t off = 0, t = 0;
-  for (Py_ssize_t r = 0; r < batch; ++r) {
+  for (int64_t r = 0; r < batch; ++r) {
     int32_t* m = rm + r * kReqFields;
     m[0] = (int32_t)off;
     m[1] = (int32_t)cnt[r];
     m[2] = (int32_t)comp[r];
     m[3] = (int32_t)ql[r];
     m[4] = (int32_t)t;
-    m[5] = (int32_t)vis_off.data<int64_t>()[r];
-    m[6] = (int32_t)vis_words.data<int64_t>()[r];
+    m[5] = (int32_t)voff[r];
+    m[6] = (int32_t)vwords[r];
     m[7] = 0;
     for (int64_t i = 0; i < ql[r]; ++i, ++t) {
       const int64_t pos = comp[r] + i;
@@ -598,7 +864,7 @@ PyObject* stage(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     }
     off += cnt[r];
   }
-  return PyLong_FromLong(status);
+  return status;
 }
 
 // ---------------------------------------------------------------------------
@@ -634,6 +900,14 @@ struct DecodeLists {
   std::vector<int32_t> pieces, first, jobs;
   int64_t waves = 0, per_wave = 0, merge_cols = 1;
   int32_t slots = 0;
+  void reset() {
+    pieces.clear();
+    first.clear();
+    jobs.clear();
+    waves = per_wave = 0;
+    merge_cols = 1;
+    slots = 0;
+  }
 };
 
 struct DecodeParams {
@@ -665,7 +939,9 @@ void build_decode(const Requests& q, const int32_t* ids, int64_t nflat, const De
   waves = std::max(waves, (total + cap - 1) / cap);
   const int64_t per_wave = (total + waves - 1) / waves;
   waves = (total + per_wave - 1) / per_wave;
-  // Walk segment ends and share bounds together: one piece per step.
+  // Walk segment ends and share bounds together: one piece per step.  The
+  // bound of share w, floor((w + 1) * total / waves), is stepped with a
+  // running remainder (no division per piece).
   struct PieceRec {
     int32_t seg, wave;
     int64_t lo, hi;
@@ -673,17 +949,33 @@ void build_decode(const Requests& q, const int32_t* ids, int64_t nflat, const De
   std::vector<PieceRec> recs;
   recs.reserve(segs.size() + (size_t)waves);
   std::vector<int32_t> seg_pieces(segs.size(), 0);
+  const int64_t share_q = total / waves, share_r = total % waves;
+  int64_t bound = share_q, rem = share_r;
+  if (rem >= waves) {
+    rem -= waves;
+    ++bound;
+  }
   for (size_t s = 0, pos = 0, w = 0; (int64_t)pos < total;) {
     const int64_t seg_end = segs[s].start + segs[s].tiles;
-    const int64_t bound = ((int64_t)(w + 1) * total) / waves;
     const int64_t end = std::min(seg_end, bound);
     recs.push_back({(int32_t)s, (int32_t)w, (int64_t)pos, end});
     ++seg_pieces[s];
     pos = (size_t)end;
     if (end == seg_end) ++s;
-    if (end == bound) ++w;
+    if (end == bound) {
+      ++w;
+      bound += share_q;
+      rem += share_r;
+      if (rem >= waves) {
+        rem -= waves;
+        ++bound;
+      }
+    }
   }
   const int64_t per_slot = 16 * d.col_tiles;  // columns of one partial slot
+  // Whole blocks per unit when units are whole blocks (the usual case), so
+  // a piece's first logical block needs no division.
+  const int64_t blocks_per_unit = d.unit % d.bs == 0 ? d.unit / d.bs : 0;
   out.pieces.assign(recs.size() * kPieceFields, 0);
   out.first.assign((size_t)waves + 1, 0);
   out.waves = waves;
@@ -708,7 +1000,7 @@ void build_decode(const Requests& q, const int32_t* ids, int64_t nflat, const De
     o[8] = m[4];   // q_start
     o[9] = m[5];   // vis_off
     o[10] = m[6];  // vis_words
-    const int64_t lb0 = tok_begin / d.bs;
+    const int64_t lb0 = blocks_per_unit ? (x.lo - sg.start) * blocks_per_unit : tok_begin / d.bs;
     for (int k = 0; k < kPieceBlocks; ++k) {
       const int64_t lb = lb0 + k, idx = m[0] + lb;
       o[11 + k] = (lb < m[1] && idx < nflat) ? ids[idx] : 0;
@@ -729,6 +1021,13 @@ struct PrefillLists {
   int32_t slots = 0;
   int64_t merge_cols = 1;
   double mean_tiles = 0.0;
+  void reset() {
+    units.clear();
+    jobs.clear();
+    slots = 0;
+    merge_cols = 1;
+    mean_tiles = 0.0;
+  }
 };
 
 struct PrefillParams {
@@ -939,6 +1238,26 @@ PyObject* prefill_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
 //   4-wave prefill workgroups, 15 resident 8-wave ones, 16 max tokens per
 //   decode wave (0: no cap), 17 decode max columns, 18 min units per wave,
 //   19 prefill min tiles.
+constexpr int kKernelFacts = 20;
+
+// One layer shape's plan: the choices and the lists of both kernels.
+struct LayerPlan {
+  int64_t ctw = 1, waves = 4;
+  bool has_dec = false, has_pre = false;
+  DecodeLists dec;
+  PrefillLists pre;
+  void reset() {
+    ctw = 1;
+    waves = 4;
+    has_dec = has_pre = false;
+    dec.reset();
+    pre.reset();
+  }
+};
+
+const char* plan_layer(const Requests& q, const int32_t* ids, int64_t nflat, const int64_t* k, double cost4,
+                       double wide_max, LayerPlan& out);
+
 PyObject* layer_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   if (!want_args(nargs, 5, "layer_work")) return nullptr;
   Buf meta(args[0], false, 4, "req_meta"), flat(args[1], false, 4, "flat"), kf(args[2], false, 8, "facts");
@@ -947,17 +1266,32 @@ PyObject* layer_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   if (PyErr_Occurred()) return nullptr;
   Requests q;
   if (!requests_of(meta, &q, "layer_work")) return nullptr;
-  if (kf.count() != 20) {
-    PyErr_SetString(PyExc_ValueError, "layer_work: expected 20 kernel facts");
+  if (kf.count() != kKernelFacts) {
+    PyErr_Format(PyExc_ValueError, "layer_work: expected %d kernel facts", kKernelFacts);
     return nullptr;
   }
-  const int64_t* k = kf.data<int64_t>();
+  LayerPlan plan;
+  if (const char* err = plan_layer(q, flat.data<int32_t>(), flat.count(), kf.data<int64_t>(), cost4, wide_max, plan)) {
+    PyErr_Format(PyExc_ValueError, "layer_work: %s", err);
+    return nullptr;
+  }
+  PyObject* dec = plan.has_dec ? decode_result(plan.dec) : Py_NewRef(Py_None);
+  PyObject* pre = plan.has_pre ? prefill_result(plan.pre) : Py_NewRef(Py_None);
+  PyObject* result =
+      (dec && pre) ? Py_BuildValue("(LLOO)", (long long)plan.ctw, (long long)plan.waves, dec, pre) : nullptr;
+  Py_XDECREF(dec);
+  Py_XDECREF(pre);
+  return result;
+}
+
+// layer_work's body: the choices for this step, then both work lists.
+// Returns an error message, or nullptr when ``out`` holds the plan.
+const char* plan_layer(const Requests& q, const int32_t* ids, int64_t nflat, const int64_t* k, double cost4,
+                       double wide_max, LayerPlan& out) {
   const int64_t group = k[0], hkv = k[1], bs = k[2], columns = k[3];
   const int64_t max_cols = columns > 0 ? k[17] : 0;
-  if (group <= 0 || hkv <= 0 || bs <= 0) {
-    PyErr_SetString(PyExc_ValueError, "layer_work: inconsistent arguments");
-    return nullptr;
-  }
+  if (group <= 0 || hkv <= 0 || bs <= 0) return "inconsistent arguments";
+  out.reset();
   int64_t ctw = k[6] > 0 ? std::min(k[6], k[8]) : choose_col_tiles(q, group, max_cols, k[8], cost4);
   if (ctw != 4) ctw = 1;
   PrefillParams p{group, columns > 0 ? columns : 1, k[4] > 0 ? k[4] : 1, 0, k[19] > 0 ? k[19] : 1, max_cols};
@@ -976,34 +1310,165 @@ PyObject* layer_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     }
     p.slots_per_head = k[5] ? (waves == 8 ? k[15] : k[14]) / hkv : 0;
   }
-  PyObject* dec = Py_None;
-  PyObject* pre = Py_None;
-  Py_INCREF(dec);
-  Py_INCREF(pre);
+  out.ctw = ctw;
+  out.waves = waves;
   if (any_decode) {
     const int64_t unit = ctw == 4 ? k[13] : k[11];
     const int64_t max_units = (k[16] > 0 && unit > 0) ? std::max<int64_t>(1, k[16] / unit) : 0;
     DecodeParams d{group, ctw, max_cols, hkv, ctw == 4 ? k[12] : k[10], bs, k[18] > 0 ? k[18] : 4, max_units, unit};
-    if (d.unit <= 0 || d.resident <= 0) {
-      PyErr_SetString(PyExc_ValueError, "layer_work: missing decode kernel facts");
-      Py_DECREF(dec);
-      Py_DECREF(pre);
+    if (d.unit <= 0 || d.resident <= 0) return "missing decode kernel facts";
+    build_decode(q, ids, nflat, d, out.dec);
+    out.has_dec = true;
+  }
+  if (any_prefill) {
+    build_prefill(q, p, out.pre);
+    out.has_pre = true;
+  }
+  return nullptr;
+}
+
+// ---------------------------------------------------------------------------
+// plan_step(flat i32, counts i64, computed i64, reserved i64, readonly i64,
+//           q_lens i64, vis_off i64, vis_words i64, vis u32, num_blocks,
+//           block_size, kernel facts i64 [n][20], cost4, wide_max_tiles,
+//           out i32 (writable))
+//   -> rule (int 1..6): a block-table rule fails (validate's codes);
+//      (needed, None, None): ``out`` holds fewer than ``needed`` entries;
+//      (used, (slots, req_meta, tables, vis offsets), shapes) otherwise.
+//
+// A whole step in one call: validate's rules, then stage's slots and
+// records, the flat tables and ancestor rows, and layer_work for each of the
+// n kernel-fact rows, all written into ``out`` (a pinned staging buffer),
+// each part starting on a 16-entry (64-byte) boundary.  Offsets are in
+// int32 entries; slots take two entries per token.  Per shape:
+//   (col_tiles, prefill_waves, decode waves per head, largest share,
+//    decode partial slots, decode merge jobs, decode merge columns,
+//    prefill units, prefill merge jobs, prefill partial slots,
+//    prefill merge columns, pieces, wave_first, jobs, units, prefill jobs,
+//    decode pieces)
+// with the five offsets -1 for an absent list.
+// ---------------------------------------------------------------------------
+std::vector<LayerPlan> g_layer_plans;
+
+int64_t align16(int64_t n) { return (n + 15) & ~int64_t(15); }
+
+PyObject* plan_step(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (!want_args(nargs, 15, "plan_step")) return nullptr;
+  Buf flat(args[0], false, 4, "flat"), counts(args[1], false, 8, "counts"), computed(args[2], false, 8, "computed"),
+      reserved(args[3], false, 8, "reserved"), readonly(args[4], false, 8, "readonly"),
+      q_lens(args[5], false, 8, "q_lens"), vis_off(args[6], false, 8, "vis_off"),
+      vis_words(args[7], false, 8, "vis_words"), vis(args[8], false, 4, "vis");
+  if (!flat.ok() || !counts.ok() || !computed.ok() || !reserved.ok() || !readonly.ok() || !q_lens.ok() ||
+      !vis_off.ok() || !vis_words.ok() || !vis.ok())
+    return nullptr;
+  int64_t num_blocks = 0, bs = 0;
+  if (!as_i64(args[9], &num_blocks) || !as_i64(args[10], &bs)) return nullptr;
+  Buf kf(args[11], false, 8, "kernel facts");
+  if (!kf.ok()) return nullptr;
+  const double cost4 = PyFloat_AsDouble(args[12]), wide_max = PyFloat_AsDouble(args[13]);
+  if (PyErr_Occurred()) return nullptr;
+  Buf out(args[14], true, 4, "out");
+  if (!out.ok()) return nullptr;
+  const int64_t batch = counts.count();
+  const int64_t* cnt = counts.data<int64_t>();
+  const int64_t* ql = q_lens.data<int64_t>();
+  int64_t total_blocks = 0, tokens = 0;
+  for (int64_t r = 0; r < batch; ++r) {
+    total_blocks += cnt[r];
+    tokens += ql[r];
+  }
+  if (batch <= 0 || computed.count() != batch || reserved.count() != batch || readonly.count() != batch ||
+      q_lens.count() != batch || vis_off.count() != batch || vis_words.count() != batch ||
+      total_blocks != flat.count() || bs <= 0 || num_blocks <= 0 || num_blocks > INT32_MAX ||
+      kf.count() % kKernelFacts != 0 || batch > INT32_MAX / kReqFields) {
+    PyErr_SetString(PyExc_ValueError, "plan_step: inconsistent arguments");
+    return nullptr;
+  }
+  const int32_t* ids = flat.data<int32_t>();
+  int64_t bad = -1;
+  const int rule = check_tables(ids, cnt, computed.data<int64_t>(), reserved.data<int64_t>(),
+                                readonly.data<int64_t>(), batch, num_blocks, bs, &bad);
+  if (rule != kTablesOk) return PyLong_FromLong(rule);
+  // Offsets of the step's facts; the requests' records are staged first
+  // into scratch (the planner reads them), then copied.
+  const int64_t o_slots = 0, o_meta = align16(2 * tokens), o_tables = o_meta + align16(batch * kReqFields),
+                o_vis = o_tables + align16(std::max<int64_t>(1, total_blocks));
+  int64_t used = o_vis + align16(std::max<Py_ssize_t>(1, vis.count()));
+  static std::vector<int32_t> meta;
+  static std::vector<int64_t> slots;
+  meta.resize((size_t)(batch * kReqFields));
+  slots.resize((size_t)tokens);
+  if (stage_rows(ids, cnt, computed.data<int64_t>(), ql, vis_off.data<int64_t>(), vis_words.data<int64_t>(), batch,
+                 bs, slots.data(), meta.data()) != 0) {
+    PyErr_SetString(PyExc_ValueError, "plan_step: a query position lies past its block table");
+    return nullptr;
+  }
+  const int64_t nshapes = kf.count() / kKernelFacts;
+  if ((int64_t)g_layer_plans.size() < nshapes) g_layer_plans.resize((size_t)nshapes);
+  Requests q{meta.data(), batch};
+  struct Offsets {
+    int64_t pieces, first, jobs, units, pjobs;
+  };
+  std::vector<Offsets> offs((size_t)nshapes);
+  for (int64_t s = 0; s < nshapes; ++s) {
+    LayerPlan& plan = g_layer_plans[(size_t)s];
+    if (const char* err = plan_layer(q, ids, total_blocks, kf.data<int64_t>() + s * kKernelFacts, cost4, wide_max,
+                                     plan)) {
+      PyErr_Format(PyExc_ValueError, "plan_step: %s", err);
       return nullptr;
     }
-    DecodeLists out;
-    build_decode(q, flat.data<int32_t>(), flat.count(), d, out);
-    Py_DECREF(dec);
-    dec = decode_result(out);
+    Offsets& o = offs[(size_t)s];
+    auto place = [&used](const std::vector<int32_t>& v, bool present) -> int64_t {
+      if (!present || v.empty()) return -1;
+      const int64_t at = used;
+      used += align16((int64_t)v.size());
+      return at;
+    };
+    o.pieces = place(plan.dec.pieces, plan.has_dec);
+    o.first = place(plan.dec.first, plan.has_dec);
+    o.jobs = place(plan.dec.jobs, plan.has_dec);
+    o.units = place(plan.pre.units, plan.has_pre);
+    o.pjobs = place(plan.pre.jobs, plan.has_pre);
   }
-  if (any_prefill && dec != nullptr) {
-    PrefillLists out;
-    build_prefill(q, p, out);
-    Py_DECREF(pre);
-    pre = prefill_result(out);
+  if (used > out.count()) return Py_BuildValue("(LOO)", (long long)used, Py_None, Py_None);
+  int32_t* dst = out.data<int32_t>();
+  std::memcpy(dst + o_slots, slots.data(), (size_t)tokens * 8);
+  std::memcpy(dst + o_meta, meta.data(), meta.size() * 4);
+  std::memcpy(dst + o_tables, ids, (size_t)total_blocks * 4);
+  std::memcpy(dst + o_vis, vis.data<int32_t>(), (size_t)vis.count() * 4);
+  PyObject* shapes = PyTuple_New((Py_ssize_t)nshapes);
+  if (shapes == nullptr) return nullptr;
+  for (int64_t s = 0; s < nshapes; ++s) {
+    const LayerPlan& plan = g_layer_plans[(size_t)s];
+    const Offsets& o = offs[(size_t)s];
+    auto put = [dst](const std::vector<int32_t>& v, int64_t at) {
+      if (at >= 0) std::memcpy(dst + at, v.data(), v.size() * 4);
+    };
+    put(plan.dec.pieces, o.pieces);
+    put(plan.dec.first, o.first);
+    put(plan.dec.jobs, o.jobs);
+    put(plan.pre.units, o.units);
+    put(plan.pre.jobs, o.pjobs);
+    const DecodeLists& d = plan.dec;
+    const PrefillLists& p = plan.pre;
+    PyObject* one = Py_BuildValue(
+        "(LLLLLLLLLLLLLLLLL)", (long long)plan.ctw, (long long)plan.waves, (long long)(plan.has_dec ? d.waves : 0),
+        (long long)(plan.has_dec ? d.per_wave : 0), (long long)(plan.has_dec ? d.slots : 0),
+        (long long)(plan.has_dec ? (int64_t)d.jobs.size() / kMergeFields : 0),
+        (long long)(plan.has_dec ? d.merge_cols : 1),
+        (long long)(plan.has_pre ? (int64_t)p.units.size() / kPrefillFields : 0),
+        (long long)(plan.has_pre ? (int64_t)p.jobs.size() / kMergeFields : 0), (long long)(plan.has_pre ? p.slots : 0),
+        (long long)(plan.has_pre ? p.merge_cols : 1), (long long)o.pieces, (long long)o.first, (long long)o.jobs,
+        (long long)o.units, (long long)o.pjobs,
+        (long long)(plan.has_dec ? (int64_t)d.pieces.size() / kPieceFields : 0));
+    if (one == nullptr) {
+      Py_DECREF(shapes);
+      return nullptr;
+    }
+    PyTuple_SET_ITEM(shapes, (Py_ssize_t)s, one);
   }
-  PyObject* result = (dec && pre) ? Py_BuildValue("(LLOO)", (long long)ctw, (long long)waves, dec, pre) : nullptr;
-  Py_XDECREF(dec);
-  Py_XDECREF(pre);
+  PyObject* result = Py_BuildValue("(L(LLLL)N)", (long long)used, (long long)o_slots, (long long)o_meta,
+                                   (long long)o_tables, (long long)o_vis, shapes);
   return result;
 }
 
@@ -1179,10 +1644,12 @@ PyMethodDef kMethods[] = {
     {"flatten", (PyCFunction)(void (*)(void))flatten, METH_FASTCALL, "int sequences -> (flat, counts int64, status)"},
     {"validate", (PyCFunction)(void (*)(void))validate, METH_FASTCALL, "block-table rules -> (rule, request)"},
     {"layouts", (PyCFunction)(void (*)(void))layouts, METH_FASTCALL, "query layouts -> lengths and ancestor bit rows"},
+    {"metadata", (PyCFunction)(void (*)(void))metadata, METH_FASTCALL, "metadata fields -> rule or (fields, facts)"},
     {"stage", (PyCFunction)(void (*)(void))stage, METH_FASTCALL, "slots and per-request records into buffers"},
     {"decode_work", (PyCFunction)(void (*)(void))decode_work, METH_FASTCALL, "stream-K decode pieces"},
     {"prefill_work", (PyCFunction)(void (*)(void))prefill_work, METH_FASTCALL, "prefill units and merge jobs"},
     {"layer_work", (PyCFunction)(void (*)(void))layer_work, METH_FASTCALL, "one layer shape's choices and lists"},
+    {"plan_step", (PyCFunction)(void (*)(void))plan_step, METH_FASTCALL, "a whole step, staged into one buffer"},
     {"counts", (PyCFunction)(void (*)(void))counts, METH_FASTCALL, "how the planner's calls were served"},
     {"compact_pairs", (PyCFunction)(void (*)(void))compact_pairs, METH_FASTCALL, "compact rules and moved slot pairs"},
     {nullptr, nullptr, 0, nullptr},
@@ -1193,4 +1660,8 @@ PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_lvamd_host", "Native host-side s
 
 }  // namespace
 
-PyMODINIT_FUNC PyInit__lvamd_host(void) { return PyModule_Create(&kModule); }
+PyMODINIT_FUNC PyInit__lvamd_host(void) {
+  g_parent_indices = PyUnicode_InternFromString("parent_indices");
+  if (g_parent_indices == nullptr) return nullptr;
+  return PyModule_Create(&kModule);
+}

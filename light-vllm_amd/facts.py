@@ -3,22 +3,21 @@
 light-vllm hands the backend Python tuples per step (block tables, computed
 counts, query layouts; src/light_vllm/runtime/execution/worker.py:275-285).
 ``StepFacts`` holds the same facts as flat arrays, produced by one native pass
-over the Python objects (``csrc/lvamd_host.cpp``): the step plan, the
-metadata's derived properties and the validation all read these arrays.
+over the Python objects (``csrc/lvamd_host.cpp``, ``metadata``): the step
+plan, the metadata's derived properties and the validation all read them.
 
 ``facts_of(metadata)`` accepts this package's ``PagedAttentionMetadata``
 (which builds its facts once, on construction) or any object with
 light-vllm's metadata attributes (parsed on the call).
 
-The block-table rules and their messages are light-vllm's
-(src/light_vllm/runtime/execution/paged_attention.py:110-172): the native
-check reports which rule fails first, in the reference's order, and
-``raise_table_rule`` raises it with the host's ``KVCacheError``.
+The field rules (paged_attention.py:29-62) and block-table rules
+(src/light_vllm/runtime/execution/paged_attention.py:110-172) and their
+messages are light-vllm's: the native checks report which rule fails first,
+in the reference's order, by code; ``FIELD_RULES`` and ``TABLE_RULES`` hold
+the messages, raised as ``ValueError`` and the host's ``KVCacheError``.
 """
 
 from __future__ import annotations
-
-from dataclasses import dataclass
 
 import numpy as np
 
@@ -35,37 +34,78 @@ TABLE_RULES = {
 }
 
 
-def _i64(data) -> np.ndarray:
-    return np.frombuffer(data, dtype=np.int64)
+# Messages of the metadata field rules, by the native planner's rule code
+# (paged_attention.py:29-62 holds them in this order).
+FIELD_RULES = {
+    1: "paged attention metadata must contain at least one request",
+    2: "paged attention metadata fields must have the same batch size",
+    3: "reserved query counts must have the same batch size",
+    4: "readonly prefix counts must have the same batch size",
+    5: "computed-token counts must be non-negative integers",
+    6: "reserved query counts must cover every actual query",
+    7: "readonly prefix counts must be non-negative integers",
+    8: "block tables must contain non-negative integers",
+    9: "each query parent must be -1 or precede its child",
+}
+
+# (name, dtype) of the native planner's buffers, in ``StepFacts.raw`` order.
+_ARRAYS = (
+    ("flat", np.int32),       # every block table, concatenated
+    ("counts", np.int64),     # blocks per table
+    ("computed", np.int64),   # num_computed_tokens
+    ("reserved", np.int64),   # num_reserved_query_tokens
+    ("readonly", np.int64),   # num_readonly_prefix_blocks
+    ("q_lens", np.int64),     # queries per request
+    ("vis_off", np.int64),    # first ancestor row in ``vis``, -1 for a linear layout
+    ("vis_words", np.int64),  # uint32 words per ancestor row
+    ("vis", np.uint32),       # ancestor bit rows of the tree layouts
+)
 
 
-@dataclass(frozen=True, slots=True, eq=False)
+def _array_property(index: int, name: str):
+    def get(self) -> np.ndarray:
+        arrays = self._arrays
+        if arrays is None:
+            arrays = self._arrays = tuple(np.frombuffer(buf, dtype=dt) for buf, (_, dt) in zip(self.raw, _ARRAYS))
+        return arrays[index]
+
+    get.__name__ = name
+    return property(get)
+
+
 class StepFacts:
-    """One step's metadata as arrays (one entry per request unless noted)."""
+    """One step's metadata as arrays (one entry per request unless noted).
 
-    flat: np.ndarray       # int32: every block table, concatenated
-    counts: np.ndarray     # int64: blocks per table
-    computed: np.ndarray   # int64: num_computed_tokens
-    reserved: np.ndarray   # int64: num_reserved_query_tokens
-    readonly: np.ndarray   # int64: num_readonly_prefix_blocks
-    q_lens: np.ndarray     # int64: queries per request
-    vis_off: np.ndarray    # int64: first ancestor row in ``vis``, -1 for a linear layout
-    vis_words: np.ndarray  # int64: uint32 words per ancestor row
-    vis: np.ndarray        # uint32: ancestor bit rows of the tree layouts
+    ``raw`` holds the native planner's buffers (``_ARRAYS`` order), which the
+    planner reads directly; the named numpy views are made on first use.
+    """
+
+    __slots__ = ("raw", "batch", "num_tokens", "linear", "_arrays")
+
+    def __init__(self, raw: tuple, num_tokens: int, linear: bool) -> None:
+        self.raw = raw
+        self.batch = len(raw[1]) // 8
+        self.num_tokens = num_tokens  # packed query tokens of the step
+        self.linear = linear  # whether every layout is the ordinary causal chain
+        self._arrays: tuple[np.ndarray, ...] | None = None
+
+    flat = _array_property(0, "flat")
+    counts = _array_property(1, "counts")
+    computed = _array_property(2, "computed")
+    reserved = _array_property(3, "reserved")
+    readonly = _array_property(4, "readonly")
+    q_lens = _array_property(5, "q_lens")
+    vis_off = _array_property(6, "vis_off")
+    vis_words = _array_property(7, "vis_words")
+    vis = _array_property(8, "vis")
 
     @property
-    def batch(self) -> int:
-        return int(self.counts.shape[0])
+    def num_blocks_listed(self) -> int:
+        return len(self.raw[0]) // 4
 
     @property
-    def num_tokens(self) -> int:
-        return int(self.q_lens.sum())
-
-    @property
-    def linear(self) -> bool:
-        """Whether every layout is the ordinary causal chain."""
-
-        return bool(np.all(self.vis_off < 0))
+    def num_vis_words(self) -> int:
+        return len(self.raw[8]) // 4
 
     @property
     def table_off(self) -> np.ndarray:
@@ -94,8 +134,7 @@ class StepFacts:
 
         if num_blocks > np.iinfo(np.int32).max:
             raise ValueError("num_blocks must fit in int32")
-        rule, _ = native.host().validate(self.flat, self.counts, self.computed, self.reserved, self.readonly,
-                                         num_blocks, block_size)
+        rule, _ = native.host().validate(*self.raw[:5], num_blocks, block_size)
         if rule:
             raise errors.KVCacheError(TABLE_RULES[rule])
 
@@ -122,30 +161,16 @@ class StepFacts:
         return bits[:, :q].astype(bool)
 
 
-def parse_ints(values, what: str) -> np.ndarray:
-    """int64 array of a sequence of exact non-negative ints; ValueError(what) otherwise."""
+def parse_fields(block_tables, computed, layouts, reserved, readonly) -> tuple[tuple, StepFacts]:
+    """The metadata constructor's work in one native call: the five fields
+    as tuples (defaults filled in) and the step's facts.  The first broken
+    field rule, in the reference's order, raises ``ValueError``."""
 
-    flat, _, status = native.host().flatten((values,), True)
-    if status:
-        raise ValueError(what)
-    return _i64(flat)
-
-
-def build_facts(block_tables, computed, layouts, reserved, readonly) -> StepFacts:
-    """Parse already-checked per-request fields into ``StepFacts``."""
-
-    host = native.host()
-    flat, counts, status = host.flatten(block_tables, False)
-    if status:
-        raise ValueError("block tables must contain non-negative integers")
-    q_lens, vis_off, vis_words, vis, bad = host.layouts(layouts)
-    if bad:
-        raise ValueError("each query parent must be -1 or precede its child")
-    return StepFacts(
-        flat=np.frombuffer(flat, dtype=np.int32), counts=_i64(counts), computed=computed, reserved=reserved,
-        readonly=readonly, q_lens=_i64(q_lens), vis_off=_i64(vis_off), vis_words=_i64(vis_words),
-        vis=np.frombuffer(vis, dtype=np.uint32),
-    )
+    found = native.host().metadata(block_tables, computed, layouts, reserved, readonly)
+    if type(found) is int:
+        raise ValueError(FIELD_RULES[found])
+    fields, raw, tokens, linear = found
+    return fields, StepFacts(raw, tokens, linear)
 
 
 def facts_of(metadata) -> StepFacts:
@@ -154,10 +179,5 @@ def facts_of(metadata) -> StepFacts:
     found = getattr(metadata, "facts", None)
     if isinstance(found, StepFacts):
         return found
-    return build_facts(
-        metadata.block_tables,
-        parse_ints(metadata.num_computed_tokens, "computed-token counts must be non-negative integers"),
-        metadata.query_layouts,
-        parse_ints(metadata.num_reserved_query_tokens, "reserved query counts must cover every actual query"),
-        parse_ints(metadata.num_readonly_prefix_blocks, "readonly prefix counts must be non-negative integers"),
-    )
+    return parse_fields(metadata.block_tables, metadata.num_computed_tokens, metadata.query_layouts,
+                        metadata.num_reserved_query_tokens, metadata.num_readonly_prefix_blocks)[1]

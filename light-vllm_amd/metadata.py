@@ -7,31 +7,25 @@ validation messages, and the same rule firing first when several are broken.
 The backend reads a metadata object only through these attributes, so
 light-vllm's own class can be passed in its place.
 
-How it is built here: construction checks the batch shape, then hands every
-integer field to the native host planner in one pass each (exact-int and
-sign checks in C), and keeps the result as ``facts`` (``StepFacts``: flat
-int32 block ids, per-request arrays, packed ancestor rows).  The derived
-properties, ``slot_mapping``, ``validate_block_tables`` and the backend's
-step plan all read those arrays, so a step's tuples are walked once.
+How it is built here: construction hands the five fields to the native host
+planner in one call, which applies the field rules (exact-int, sign, batch
+and coverage checks in C, first failure by the reference's order) and
+returns the normalized tuples and ``facts`` (``StepFacts``: flat int32 block
+ids, per-request arrays, packed ancestor rows).  The derived properties,
+``slot_mapping``, ``validate_block_tables`` and the backend's step plan all
+read those arrays, so a step's tuples are walked once.
 """
 
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from typing import Callable
 
 import numpy as np
 import torch
 from torch import Tensor
 
-from light_vllm_amd.facts import StepFacts, build_facts, parse_ints
+from light_vllm_amd.facts import StepFacts, parse_fields
 from light_vllm_amd.interfaces import QueryLayout
-
-
-def _first_failure(rules: tuple[tuple[Callable[[], bool], str], ...]) -> None:
-    for holds, message in rules:
-        if not holds():
-            raise ValueError(message)
 
 
 @dataclass(frozen=True, slots=True)
@@ -47,36 +41,18 @@ class PagedAttentionMetadata:
     facts: StepFacts = field(init=False, repr=False, compare=False)
 
     def __post_init__(self) -> None:
-        tables = tuple(map(tuple, self.block_tables))
-        computed = tuple(self.num_computed_tokens)
-        layouts = tuple(self.query_layouts)
-        batch = len(tables)
-        _first_failure((
-            (lambda: batch > 0, "paged attention metadata must contain at least one request"),
-            (lambda: len(computed) == batch == len(layouts),
-             "paged attention metadata fields must have the same batch size"),
-        ))
-        # Empty reserved / readonly fields default per request: the layout's
-        # query count, and no readonly prefix.
-        reserved = tuple(self.num_reserved_query_tokens) or tuple(len(layout) for layout in layouts)
-        readonly = tuple(self.num_readonly_prefix_blocks) or (0,) * batch
-        _first_failure((
-            (lambda: len(reserved) == batch, "reserved query counts must have the same batch size"),
-            (lambda: len(readonly) == batch, "readonly prefix counts must have the same batch size"),
-        ))
-        computed_arr = parse_ints(computed, "computed-token counts must be non-negative integers")
-        q_lens = np.fromiter(map(len, layouts), dtype=np.int64, count=batch)
-        reserved_arr = parse_ints(reserved, "reserved query counts must cover every actual query")
-        if np.any(reserved_arr < q_lens):
-            raise ValueError("reserved query counts must cover every actual query")
-        readonly_arr = parse_ints(readonly, "readonly prefix counts must be non-negative integers")
-        facts = build_facts(tables, computed_arr, layouts, reserved_arr, readonly_arr)
-        object.__setattr__(self, "block_tables", tables)
-        object.__setattr__(self, "num_computed_tokens", computed)
-        object.__setattr__(self, "query_layouts", layouts)
-        object.__setattr__(self, "num_reserved_query_tokens", reserved)
-        object.__setattr__(self, "num_readonly_prefix_blocks", readonly)
-        object.__setattr__(self, "facts", facts)
+        # One native call: the fields as tuples with their defaults (empty
+        # reserved -> each layout's query count, empty readonly -> zeros),
+        # every field rule in order, and the step facts.
+        fields, facts = parse_fields(self.block_tables, self.num_computed_tokens, self.query_layouts,
+                                     self.num_reserved_query_tokens, self.num_readonly_prefix_blocks)
+        put = object.__setattr__
+        put(self, "block_tables", fields[0])
+        put(self, "num_computed_tokens", fields[1])
+        put(self, "query_layouts", fields[2])
+        put(self, "num_reserved_query_tokens", fields[3])
+        put(self, "num_readonly_prefix_blocks", fields[4])
+        put(self, "facts", facts)
 
     @property
     def batch_size(self) -> int:

@@ -32,8 +32,8 @@ import numpy as np
 import torch
 from torch import Tensor
 
-from light_vllm_amd import native
-from light_vllm_amd.facts import StepFacts, facts_of
+from light_vllm_amd import errors, native
+from light_vllm_amd.facts import TABLE_RULES, StepFacts, facts_of
 
 # Requests whose queries x group fit one 16-column MFMA tile use the split-K
 # decode kernel; wider ones (prompt chunks, tree verification) use the MFMA
@@ -77,40 +77,61 @@ class Staging:
     """
 
     DEPTH = 4
+    MIN_ENTRIES = 1 << 16  # int32 entries of a fresh buffer (256 KiB)
 
     def __init__(self, device: torch.device) -> None:
         self.device = torch.device(device)
         self._gpu = self.device.type == "cuda"
         self._host: list[Tensor | None] = [None] * self.DEPTH
+        self._views: list[np.ndarray | None] = [None] * self.DEPTH
         self._events: list[object | None] = [None] * self.DEPTH
         self._next = 0
         self._slot = -1
 
+    def take(self, n: int = 0) -> np.ndarray:
+        """The next buffer of the ring, whole (at least ``n`` int32 entries),
+        once the copy that last read it has finished."""
+
+        if not self._gpu:
+            return np.zeros(max(n, self.MIN_ENTRIES), dtype=np.int32)
+        slot = self._next
+        self._next = (slot + 1) % self.DEPTH
+        event = self._events[slot]
+        if event is not None:
+            event.synchronize()
+        self._slot = slot
+        view = self._views[slot]
+        if view is None or view.shape[0] < n:
+            view = self.grow(n)
+        return view
+
+    def grow(self, n: int) -> np.ndarray:
+        """Replace the buffer ``take`` returned by one of at least ``n`` entries."""
+
+        if not self._gpu:
+            return np.zeros(max(n, self.MIN_ENTRIES), dtype=np.int32)
+        slot = self._slot
+        old = self._host[slot]
+        size = max(n, self.MIN_ENTRIES, 2 * old.numel() if old is not None else 0)
+        host = self._host[slot] = torch.empty(size, dtype=torch.int32, pin_memory=True)
+        view = self._views[slot] = host.numpy()
+        return view
+
     def buffer(self, n: int) -> np.ndarray:
         """A writable int32 host array of ``n`` entries for the next upload."""
 
-        if not self._gpu:
-            return np.zeros(max(n, 1), dtype=np.int32)
-        slot = self._next
-        self._next = (slot + 1) % self.DEPTH
-        if self._events[slot] is not None:
-            self._events[slot].synchronize()
-        host = self._host[slot]
-        if host is None or host.numel() < n:
-            host = torch.empty(max(n, 4096, 2 * (host.numel() if host is not None else 0)), dtype=torch.int32,
-                               pin_memory=True)
-            self._host[slot] = host
-        self._slot = slot
-        return host.numpy()[:n]
+        return self.take(n)[:n]
 
     def upload(self, array: np.ndarray) -> Tensor:
-        """The device copy of the array ``buffer`` returned (non-blocking, current stream)."""
+        """The device copy of a prefix of the buffer ``take`` returned
+        (non-blocking, on the current stream)."""
 
         if not self._gpu:
             return torch.from_numpy(array)
         slot = self._slot
-        dev = torch.empty(array.shape[0], dtype=torch.int32, device=self.device)
-        dev.copy_(self._host[slot][: array.shape[0]], non_blocking=True)
+        n = array.shape[0]
+        dev = torch.empty(n, dtype=torch.int32, device=self.device)
+        dev.copy_(self._host[slot][:n], non_blocking=True)
         event = self._events[slot]
         if event is None:
             event = self._events[slot] = torch.cuda.Event()
@@ -166,7 +187,7 @@ class DecodeWork:
                  "waves_per_head", "num_jobs", "num_partial_slots", "units_per_wave", "col_tiles",
                  "num_prefill_units", "num_prefill_jobs", "num_prefill_partial_slots", "prefill_waves",
                  "merge_columns", "prefill_merge_columns", "pieces_ptr", "wave_first_ptr", "jobs_ptr",
-                 "units_ptr", "prefill_jobs_ptr")
+                 "units_ptr", "prefill_jobs_ptr", "_staged")
 
     def __init__(self, *, col_tiles: int, prefill_waves: int) -> None:
         self.col_tiles = col_tiles  # column tiles per decode wave (partials hold 16 * col_tiles columns)
@@ -177,6 +198,35 @@ class DecodeWork:
         self.num_prefill_units = self.num_prefill_jobs = self.num_prefill_partial_slots = 0
         self.merge_columns = self.prefill_merge_columns = 1  # most columns any merge job has
         self.pieces_ptr = self.wave_first_ptr = self.jobs_ptr = self.units_ptr = self.prefill_jobs_ptr = None
+        self._staged = None  # (uploaded blob, {list name: (offset, rows, fields)}) of a fused plan
+
+    @classmethod
+    def staged(cls, row: tuple[int, ...], blob: Tensor) -> "DecodeWork":
+        """A layer shape's work as ``plan_step`` placed it in ``blob`` (the
+        uploaded step buffer): counts from ``row``, lists only on the device."""
+
+        (ctw, waves, wph, per_wave, slots, njobs, mcols, nunits, npjobs, pslots, pmcols,
+         o_pieces, o_first, o_jobs, o_units, o_pjobs, npieces) = row
+        work = cls(col_tiles=ctw, prefill_waves=waves)
+        work.waves_per_head, work.units_per_wave, work.num_partial_slots = wph, per_wave, slots
+        work.num_jobs, work.merge_columns = njobs, mcols
+        work.num_prefill_units, work.num_prefill_jobs = nunits, npjobs
+        work.num_prefill_partial_slots, work.prefill_merge_columns = pslots, pmcols
+        base = blob.data_ptr()
+        if o_pieces >= 0:
+            work.pieces_ptr, work.wave_first_ptr = base + 4 * o_pieces, base + 4 * o_first
+        if o_jobs >= 0:
+            work.jobs_ptr = base + 4 * o_jobs
+        if o_units >= 0:
+            work.units_ptr = base + 4 * o_units
+        if o_pjobs >= 0:
+            work.prefill_jobs_ptr = base + 4 * o_pjobs
+        work._staged = (blob, {
+            "pieces": (o_pieces, npieces, PIECE_FIELDS), "wave_first": (o_first, wph + 1, 1),
+            "jobs": (o_jobs, njobs, MERGE_FIELDS), "prefill_units": (o_units, nunits, PREFILL_FIELDS),
+            "prefill_jobs": (o_pjobs, npjobs, MERGE_FIELDS),
+        })
+        return work
 
     def parts(self) -> list[tuple[str, np.ndarray]]:
         """(pointer attribute, array) of every list to upload."""
@@ -186,29 +236,35 @@ class DecodeWork:
                  ("prefill_jobs_ptr", self.prefill_jobs_host)]
         return [(name, array) for name, array in found if array is not None and array.size]
 
-    @staticmethod
-    def _tensor(array):
-        return None if array is None or not array.size else torch.from_numpy(array)
+    def _tensor(self, array, name: str):
+        if self._staged is None:
+            return None if array is None or not array.size else torch.from_numpy(array)
+        blob, lists = self._staged
+        off, rows, fields = lists[name]
+        if off < 0 or not rows:
+            return None
+        flat = blob[off : off + rows * fields].cpu()
+        return flat if fields == 1 else flat.view(rows, fields)
 
     @property
     def pieces(self) -> Tensor | None:  # int32 [n_pieces, 16]
-        return self._tensor(self.pieces_host)
+        return self._tensor(self.pieces_host, "pieces")
 
     @property
     def wave_first(self) -> Tensor | None:  # int32 [waves_per_head + 1]
-        return self._tensor(self.wave_first_host)
+        return self._tensor(self.wave_first_host, "wave_first")
 
     @property
     def jobs(self) -> Tensor | None:  # int32 [n_jobs, 8]
-        return self._tensor(self.jobs_host)
+        return self._tensor(self.jobs_host, "jobs")
 
     @property
     def prefill_units(self) -> Tensor | None:  # int32 [n_prefill_units, 8]
-        return self._tensor(self.units_host)
+        return self._tensor(self.units_host, "prefill_units")
 
     @property
     def prefill_jobs(self) -> Tensor | None:  # int32 [n, 8] merge jobs of split prefill units
-        return self._tensor(self.prefill_jobs_host)
+        return self._tensor(self.prefill_jobs_host, "prefill_jobs")
 
 
 def _as_i32(data) -> np.ndarray:
@@ -234,48 +290,98 @@ class StepPlan:
         num_blocks: int | None = None,
         staging: Staging | None = None,
         defer_upload: bool = False,
+        shapes: "LayerShapes | None" = None,
     ) -> None:
         """With ``num_blocks`` the block tables are validated first, with the
         rules and messages of ``PagedAttentionMetadata.validate_block_tables``
         (paged_attention.py:138-173), in the native planner.  With
-        ``defer_upload`` nothing is copied until ``commit()``."""
+        ``defer_upload`` nothing is copied until ``commit()``.
+
+        With ``shapes`` (and ``num_blocks``) the whole step is planned in one
+        native call (``plan_step``): validation, the step facts and every
+        listed layer shape's work lists, written straight into a pinned
+        staging buffer and uploaded at once; the plan is committed."""
 
         self.block_size = block_size
         self.device = torch.device(device)
         self.partition_tokens = partition_tokens
         self._staging = staging if staging is not None else Staging(self.device)
         facts: StepFacts = facts_of(metadata)
-        if num_blocks is not None:
-            facts.check_tables(num_blocks=num_blocks, block_size=block_size)
-        batch, tokens = facts.batch, facts.num_tokens
-        nflat, nvis = max(int(facts.flat.size), 1), max(int(facts.vis.size), 1)
-        # Step facts as one int32 array: [slots as int32 pairs | req_meta | tables | vis].
-        sizes = (2 * tokens, batch * native.REQ_FIELDS, nflat, nvis)
-        self._offs = offs = np.concatenate(([0], np.cumsum(sizes))).tolist()
-        arr = np.zeros(offs[-1], dtype=np.int32)
-        req_meta = arr[offs[1] : offs[2]]
-        if native.host().stage(facts.flat, facts.counts, facts.computed, facts.q_lens, facts.vis_off,
-                               facts.vis_words, block_size, arr[offs[0] : offs[1]].view(np.int64), req_meta):
-            facts.check_coverage(block_size)
-            raise ValueError("a query position lies past its block table")
-        arr[offs[2] : offs[2] + facts.flat.size] = facts.flat
-        arr[offs[3] : offs[3] + facts.vis.size] = facts.vis.view(np.int32)
-        self._req_meta = req_meta
-        self._facts_host = arr
-        self.num_tokens = tokens
-        self.batch_size = batch
-        self.has_tree = not facts.linear
         self.facts = facts
+        self.num_tokens = tokens = facts.num_tokens
+        self.batch_size = batch = facts.batch
+        self.has_tree = not facts.linear
         self._work: dict[tuple[int, ...], DecodeWork] = {}
         self._col_tiles: dict[tuple[int, int, int], int] = {}
         self._pending: list[DecodeWork] = []
         self._late_blobs: list[Tensor] = []  # uploads of work lists asked for after commit
         self._blob: Tensor | None = None
         self._committed = False
+        self._req_meta_host: np.ndarray | None = None
         # Bound launch arguments per layer shape, filled by the backend.
         self.launches: dict[tuple, object] = {}
+        # (start, length) in int32 entries of slots, req_meta, tables and vis in the upload.
+        self._spans: tuple[tuple[int, int], ...] = ()
+        nflat, nvis = facts.num_blocks_listed, facts.num_vis_words
+        if shapes is not None:
+            if num_blocks is None:
+                raise ValueError("a step planned with layer shapes validates its tables: pass num_blocks")
+            self._plan_step(num_blocks, shapes, (2 * tokens, batch * native.REQ_FIELDS, nflat, nvis))
+            return
+        if num_blocks is not None:
+            facts.check_tables(num_blocks=num_blocks, block_size=block_size)
+        # Step facts as one int32 array: [slots as int32 pairs | req_meta | tables | vis].
+        sizes = (2 * tokens, batch * native.REQ_FIELDS, max(nflat, 1), max(nvis, 1))
+        offs = np.concatenate(([0], np.cumsum(sizes))).tolist()
+        self._spans = tuple((offs[i], sizes[i]) for i in range(4))
+        arr = np.zeros(offs[-1], dtype=np.int32)
+        req_meta = arr[offs[1] : offs[2]]
+        if native.host().stage(facts.flat, facts.counts, facts.computed, facts.q_lens, facts.vis_off,
+                               facts.vis_words, block_size, arr[offs[0] : offs[1]].view(np.int64), req_meta):
+            facts.check_coverage(block_size)
+            raise ValueError("a query position lies past its block table")
+        arr[offs[2] : offs[2] + nflat] = facts.flat
+        arr[offs[3] : offs[3] + nvis] = facts.vis.view(np.int32)
+        self._req_meta_host = req_meta
+        self._facts_host = arr
         if not defer_upload:
             self.commit()
+
+    def _plan_step(self, num_blocks: int, shapes: "LayerShapes", sizes: tuple[int, int, int, int]) -> None:
+        raw = self.facts.raw
+        host = native.host()
+        staging = self._staging
+        buf = staging.take()
+        while True:
+            found = host.plan_step(*raw, num_blocks, self.block_size, shapes.array, COL_TILES4_COST,
+                                   float(PREFILL_WIDE_MAX_TILES), buf)
+            if type(found) is int:
+                raise errors.KVCacheError(TABLE_RULES[found])
+            used, offs, rows = found
+            if offs is not None:
+                break
+            buf = staging.grow(used)
+        blob = self._blob = staging.upload(buf[:used])
+        base = blob.data_ptr()
+        self._spans = tuple(zip(offs, sizes))
+        self.slots_ptr, self.req_meta_ptr, self.tables_ptr, self.vis_ptr = (base + 4 * o for o in offs)
+        for key, row in zip(shapes.keys, rows):
+            self._work[key] = DecodeWork.staged(row, blob)
+        self._committed = True
+
+    @property
+    def _req_meta(self) -> np.ndarray:
+        """int32 [B * 8] per-request records on the host (built on first use
+        when the step was planned in one call)."""
+
+        if self._req_meta_host is None:
+            f = self.facts
+            meta = np.empty(self.batch_size * native.REQ_FIELDS, dtype=np.int32)
+            slots = np.empty(self.num_tokens, dtype=np.int64)
+            native.host().stage(f.flat, f.counts, f.computed, f.q_lens, f.vis_off, f.vis_words, self.block_size,
+                                slots, meta)
+            self._req_meta_host = meta
+        return self._req_meta_host
 
     def commit(self) -> None:
         """Upload the step facts and every work list built so far (one copy)."""
@@ -294,17 +400,18 @@ class StepPlan:
             if work is not None:
                 setattr(work, name, base + 4 * off)
         self._blob = blob
-        offs = self._offs
-        self.slots_ptr = base + 4 * offs[0]
-        self.req_meta_ptr = base + 4 * offs[1]
-        self.tables_ptr = base + 4 * offs[2]
-        self.vis_ptr = base + 4 * offs[3]
+        spans = self._spans
+        self.slots_ptr = base + 4 * spans[0][0]
+        self.req_meta_ptr = base + 4 * spans[1][0]
+        self.tables_ptr = base + 4 * spans[2][0]
+        self.vis_ptr = base + 4 * spans[3][0]
         self._pending = []
         self._committed = True
 
     def _view(self, i: int) -> Tensor:
         self.commit()
-        return self._blob[self._offs[i] : self._offs[i + 1]]
+        start, length = self._spans[i]
+        return self._blob[start : start + length]
 
     @property
     def slots(self) -> Tensor:  # int64 [T]
@@ -448,6 +555,20 @@ KERNEL_FACTS = (
     "prefill_resident_4", "prefill_resident_8", "partition_tokens", "decode_max_columns",
     "min_units_per_wave", "prefill_min_tiles",
 )
+
+
+class LayerShapes:
+    """The kernel-facts rows (``KERNEL_FACTS`` order) of every layer shape a
+    step plans for: the rows as tuples (keys of the plan's work lists) and as
+    one int64 array (the native planner's argument)."""
+
+    __slots__ = ("keys", "array")
+
+    def __init__(self, rows) -> None:
+        self.keys = tuple(tuple(int(v) for v in row) for row in rows)
+        if any(len(row) != len(KERNEL_FACTS) for row in self.keys):
+            raise ValueError(f"each layer shape needs {len(KERNEL_FACTS)} kernel facts")
+        self.array = np.asarray(self.keys, dtype=np.int64).reshape(-1)
 
 
 def _fill_work(work: DecodeWork, dec, pre) -> None:

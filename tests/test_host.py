@@ -14,7 +14,7 @@ import torch
 
 import light_vllm_amd as lv
 from light_vllm_amd import native
-from light_vllm_amd.plan import StepPlan
+from light_vllm_amd.plan import LayerShapes, Staging, StepPlan
 from oracle import paged_kv_oracle as O
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())
@@ -468,6 +468,63 @@ def test_native_table_rules_raise_the_oracles_message(seed) -> None:
                              num_blocks=num_blocks, block_size=bs)
     assert _plan_message(md.validate_block_tables, num_blocks=num_blocks, block_size=bs) == expect
     assert _plan_message(StepPlan, md, block_size=bs, device=CPU, num_blocks=num_blocks) == expect
+    assert _plan_message(StepPlan, md, block_size=bs, device=CPU, num_blocks=num_blocks,
+                         shapes=_layer_shapes(bs)) == expect
+
+
+def _layer_shapes(bs: int) -> LayerShapes:
+    """Two layer shapes in ``KERNEL_FACTS`` order: grouped queries with the
+    four-column-tile decode kernel and both prefill shapes, and a
+    one-query-per-head shape without them."""
+
+    return LayerShapes((
+        (7, 4, bs, 128, 64, 1, 0, 0, 4, 1, 2048, 32, 1024, 16, 512, 256, 0, 16, 4, 4),
+        (1, 8, bs, 256, 64, 0, 0, 0, 1, 0, 2048, 32, 0, 0, 512, 0, 0, 16, 4, 4),
+    ))
+
+
+@pytest.mark.parametrize("small_buffer", (False, True))
+@pytest.mark.parametrize("seed", range(8))
+def test_one_call_step_plan_equals_the_per_shape_plan(seed, small_buffer, monkeypatch) -> None:
+    """``plan_step`` (validation, staging and every layer shape in one native
+    call, written into one buffer) gives the same slots, records, tables,
+    ancestor rows and work lists as the step facts plus ``layer_work`` per
+    shape; with a staging buffer too small at first it grows and plans again."""
+
+    if small_buffer:
+        monkeypatch.setattr(Staging, "MIN_ENTRIES", 16)
+    rng = np.random.default_rng(500 + seed)
+    bs = int(rng.choice([1, 3, 12, 16]))
+    md = _random_metadata(rng, batch=int(rng.integers(1, 12)), bs=bs, tree=seed % 2 == 1)
+    num_blocks = sum(len(t) for t in md.block_tables) + 5
+    shapes = _layer_shapes(bs)
+    one = StepPlan(md, block_size=bs, device=CPU, num_blocks=num_blocks, shapes=shapes)
+    ref = StepPlan(md, block_size=bs, device=CPU, num_blocks=num_blocks)
+    assert one.slots.tolist() == ref.slots.tolist()
+    assert one.req_meta.tolist() == ref.req_meta.tolist()
+    assert one.tables.tolist() == ref.tables.tolist()[: one.tables.numel()]
+    assert one.vis.tolist() == ref.vis.tolist()[: one.vis.numel()]
+    counts = ("col_tiles", "prefill_waves", "waves_per_head", "units_per_wave", "num_partial_slots", "num_jobs",
+              "merge_columns", "num_prefill_units", "num_prefill_jobs", "num_prefill_partial_slots",
+              "prefill_merge_columns")
+    for key in shapes.keys:
+        a, b = one.layer_work(key), ref.layer_work(key)
+        assert [getattr(a, n) for n in counts] == [getattr(b, n) for n in counts]
+        for name in ("pieces", "wave_first", "jobs", "prefill_units", "prefill_jobs"):
+            x, y = getattr(a, name), getattr(b, name)
+            assert (x is None) == (y is None), name
+            if x is not None:
+                assert x.tolist() == y.tolist(), name
+        # Device addresses: every list present has one, inside the upload.
+        base, end = one._blob.data_ptr(), one._blob.data_ptr() + 4 * one._blob.numel()
+        for ptr, rows in ((a.pieces_ptr, a.pieces), (a.jobs_ptr, a.jobs), (a.units_ptr, a.prefill_units),
+                          (a.prefill_jobs_ptr, a.prefill_jobs)):
+            assert (ptr is None) == (rows is None)
+            if ptr is not None:
+                assert base <= ptr and ptr + 4 * rows.numel() <= end and (ptr - base) % 64 == 0
+    # A layer shape asked for later is planned on its own, from the records.
+    late = (4, 2, bs, 128, 64, 1, 0, 0, 4, 1, 2048, 32, 1024, 16, 512, 256, 0, 16, 4, 4)
+    assert one.layer_work(late).num_prefill_units == ref.layer_work(late).num_prefill_units
 
 
 def test_prefill_shape_choice_follows_the_measured_workloads() -> None:
