@@ -32,7 +32,8 @@ enum lvamd_status {
   LVAMD_ERR_UNSUPPORTED = -2,       /* dtype / head_size / group size not built     */
   LVAMD_ERR_WORKSPACE = -3,         /* missing or undersized workspace              */
   LVAMD_ERR_LAUNCH = -4,            /* hipLaunchKernel / hipGetLastError failed     */
-  LVAMD_ERR_SCRATCH_LIMIT = -5      /* input needs more than the static scratch     */
+  LVAMD_ERR_SCRATCH_LIMIT = -5,     /* input needs more than the static scratch     */
+  LVAMD_ERR_RUNTIME = -6            /* a HIP runtime call (copy, event) failed      */
 };
 
 enum lvamd_dtype { LVAMD_F32 = 0, LVAMD_F16 = 1, LVAMD_BF16 = 2 };
@@ -292,6 +293,17 @@ int lvamd_kv_block_copy(const uint64_t* layer_key_ptrs, const uint64_t* layer_va
                         int32_t num_layers, int64_t block_bytes,
                         const int64_t* src_blocks, const int64_t* dst_blocks, int64_t num_pairs,
                         lvamd_stream_t stream);
+
+/*
+ * The per-step upload of a staged plan: copies bytes from pinned host memory
+ * to device memory on stream (asynchronous), then records event (a
+ * hipEvent_t; NULL for none) on stream, so the caller can tell when the
+ * pinned buffer may be refilled.  Replaces the pinned-buffer copy of
+ * light-vllm's CudaStaging (src/light_vllm/runtime/execution/cuda_staging.py:27-49)
+ * plus its event, in one call.  LVAMD_ERR_RUNTIME if either HIP call fails.
+ */
+int lvamd_stage_upload(void* device_dst, const void* pinned_src, int64_t bytes, void* event,
+                       lvamd_stream_t stream);
 
 /*
  * Measurement only: streams bytes (a multiple of 16) of buf from HBM with

@@ -35,6 +35,17 @@ from light_vllm_amd.paged_cache import (  # noqa: E402
     kv_cache_bytes_per_block,
 )
 
+# ``from light_vllm_amd import errors`` registers the submodule under the
+# directory's name and ``import light_vllm_amd.errors`` under the alias; a
+# module found under only one of them would be loaded a second time under
+# the other, with its own state (the bound exception classes, the loaded
+# library).  Every submodule is imported by now: register each under both.
+for _name, _module in list(_sys.modules.items()):
+    for _have, _add in (("light-vllm_amd.", "light_vllm_amd."), ("light_vllm_amd.", "light-vllm_amd.")):
+        if _name.startswith(_have):
+            _sys.modules.setdefault(_add + _name[len(_have):], _module)
+del _name, _module, _have, _add
+
 __all__ = [
     "AttentionLayerSpec",
     "DraftTree",

@@ -359,11 +359,21 @@ const char* lvamd_status_string(int status) {
     case LVAMD_ERR_WORKSPACE: return "workspace missing or too small";
     case LVAMD_ERR_LAUNCH: return "kernel launch failed";
     case LVAMD_ERR_SCRATCH_LIMIT: return "call needs more than the library's static scratch holds";
+    case LVAMD_ERR_RUNTIME: return "HIP runtime call failed";
     default: return "unknown status";
   }
 }
 
-int lvamd_abi_version(void) { return 12; }
+int lvamd_abi_version(void) { return 13; }
+
+int lvamd_stage_upload(void* device_dst, const void* pinned_src, int64_t bytes, void* event, lvamd_stream_t stream) {
+  if (bytes < 0 || (bytes > 0 && (!device_dst || !pinned_src))) return LVAMD_ERR_INVALID_ARGUMENT;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (bytes > 0 && hipMemcpyAsync(device_dst, pinned_src, (size_t)bytes, hipMemcpyHostToDevice, s) != hipSuccess)
+    return LVAMD_ERR_RUNTIME;
+  if (event != nullptr && hipEventRecord(static_cast<hipEvent_t>(event), s) != hipSuccess) return LVAMD_ERR_RUNTIME;
+  return LVAMD_OK;
+}
 
 int lvamd_kv_append(const void* key, int64_t key_token_stride, int64_t key_head_stride,
                     const void* value, int64_t value_token_stride, int64_t value_head_stride,

@@ -19,7 +19,7 @@ from pathlib import Path
 from light_vllm_amd import errors
 
 LIB_NAME = "liblvamd_hip.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
@@ -83,6 +83,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_p, _p, _i32, _i64, _p, _p, _i64, _p],
     ),
+    "lvamd_stage_upload": (ctypes.c_int, [_p, _p, _i64, _p, _p]),
     "lvamd_hbm_read_probe": (ctypes.c_int, [_p, _i64, _p, _i32, _p]),
 }
 

@@ -25,7 +25,7 @@ from torch import Tensor
 
 from light_vllm_amd import errors, native
 from light_vllm_amd.interfaces import AttentionLayerSpec, ModelKVCacheSpec
-from light_vllm_amd.plan import Staging
+from light_vllm_amd.plan import Staging, current_stream
 
 _DTYPE_CODES = {torch.float32: native.DTYPE_F32, torch.float16: native.DTYPE_F16, torch.bfloat16: native.DTYPE_BF16}
 
@@ -35,19 +35,6 @@ def dtype_code(dtype: torch.dtype) -> int:
         return _DTYPE_CODES[dtype]
     except KeyError as exc:
         raise errors.KVCacheError(f"HIP paged KV supports float32, float16 and bfloat16, not {dtype}") from exc
-
-
-_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
-
-
-def current_stream(device: torch.device) -> int:
-    """The current HIP stream of ``device`` as a raw handle (torch's own
-    accessor when present: it skips building a Stream object per call)."""
-
-    if _raw_stream is not None:
-        index = device.index if device.index is not None else torch.cuda.current_device()
-        return _raw_stream(index)
-    return torch.cuda.current_stream(device).cuda_stream
 
 
 def _positive_int(value) -> bool:

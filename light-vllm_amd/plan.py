@@ -65,6 +65,18 @@ UNIT_TOKENS = 32
 COL_TILES4_COST = 3.4
 PREFILL_WIDE_MAX_TILES = 20  # mean key tiles per unit up to which 8-wave prefill workgroups win
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def current_stream(device: torch.device) -> int:
+    """The current HIP stream of ``device`` as a raw handle (torch's own
+    accessor when present: it skips building a Stream object per call)."""
+
+    if _raw_stream is not None:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(index)
+    return torch.cuda.current_stream(device).cuda_stream
+
 
 class Staging:
     """Pinned host buffers for per-step uploads, reused round-robin.
@@ -82,6 +94,7 @@ class Staging:
     def __init__(self, device: torch.device) -> None:
         self.device = torch.device(device)
         self._gpu = self.device.type == "cuda"
+        self._lib = native.load() if self._gpu else None
         self._host: list[Tensor | None] = [None] * self.DEPTH
         self._views: list[np.ndarray | None] = [None] * self.DEPTH
         self._events: list[object | None] = [None] * self.DEPTH
@@ -131,11 +144,14 @@ class Staging:
         slot = self._slot
         n = array.shape[0]
         dev = torch.empty(n, dtype=torch.int32, device=self.device)
-        dev.copy_(self._host[slot][:n], non_blocking=True)
         event = self._events[slot]
         if event is None:
             event = self._events[slot] = torch.cuda.Event()
-        event.record()
+            event.record()  # creates the HIP event behind it
+        # One library call: the async H2D copy, then the slot's event.
+        native.check(self._lib.lvamd_stage_upload(dev.data_ptr(), self._host[slot].data_ptr(), 4 * n,
+                                                  event.cuda_event, current_stream(self.device)),
+                     "lvamd_stage_upload")
         return dev
 
     def stage(self, parts: list[np.ndarray]) -> tuple[Tensor, list[int]]:

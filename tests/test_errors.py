@@ -242,3 +242,36 @@ def test_light_vllm_classes_are_bound_when_importable(tmp_path) -> None:
     out = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0, out.stderr
     assert "host class: block table contains an out-of-range physical block" in out.stdout
+
+
+def test_every_import_path_reaches_the_same_modules() -> None:
+    """``import light_vllm_amd.errors``, ``from light_vllm_amd import errors``
+    and the directory's own name give one module object each, so a binding
+    made through any of them is the one raise sites use (fresh interpreter:
+    nothing imported before the package)."""
+
+    script = textwrap.dedent(f"""
+        import importlib, sys
+        sys.path.insert(0, {str(PACKAGE.parent)!r})
+        importlib.import_module("light-vllm_amd")
+        import light_vllm_amd.errors as by_alias
+        import light_vllm_amd.native as native_alias
+        from light_vllm_amd import errors as by_attribute
+        import light_vllm_amd as lv
+        names = ("errors", "native", "facts", "plan", "backend", "metadata", "paged_cache", "interfaces", "layout")
+        for name in names:
+            assert sys.modules["light_vllm_amd." + name] is sys.modules["light-vllm_amd." + name], name
+        assert by_alias is by_attribute is lv.errors and native_alias is lv.native
+        class Host(RuntimeError):
+            pass
+        from light_vllm_amd.errors import bind
+        bind(kv_cache_error=Host)
+        try:
+            lv.PagedAttentionMetadata(block_tables=((0, 9),), num_computed_tokens=(3,),
+                query_layouts=(lv.linear_query_layout(1),)).validate_block_tables(num_blocks=8, block_size=2)
+        except Host as exc:
+            print("bound class:", exc)
+    """)
+    out = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert "bound class: block table contains an out-of-range physical block" in out.stdout
