@@ -33,6 +33,7 @@ import torch
 from torch import Tensor
 
 from light_vllm_amd import errors, native
+from light_vllm_amd.metadata import PagedAttentionMetadata
 from light_vllm_amd.paged_cache import current_stream, dtype_code, hip_append, hip_append_rotary
 from light_vllm_amd.plan import DECODE_MAX_COLUMNS, PREFILL_MIN_TILES, UNIT_TOKENS, LayerShapes, Staging, StepPlan
 
@@ -356,7 +357,8 @@ class HipPagedAttentionBackend:
     (triton_paged_attention.py:566-570).  The step plan of the most recent
     metadata object is kept: metadata objects are immutable, so a second
     ``create`` with the same object (and a cache of the same geometry) reuses
-    the validated, staged plan.
+    the validated, staged plan.  This package's metadata is recognised by its
+    facts (the metadata object itself is not kept alive).
     """
 
     def __init__(
@@ -442,8 +444,12 @@ class HipPagedAttentionBackend:
         if config.device.type != "cuda":
             raise errors.KVCacheError("HIP paged attention requires a GPU KV cache")
         geometry = (config.num_blocks, config.block_size, config.device)
+        # This package's metadata is recognised by its facts object, which the
+        # plan holds anyway: the metadata itself (a step's worth of tuples) is
+        # not kept alive, so the caller frees it, not the next create().
+        key = metadata.facts if isinstance(metadata, PagedAttentionMetadata) else metadata
         last = self._last
-        if last is not None and last[0] == geometry and last[1] is metadata:
+        if last is not None and last[1] is key and last[0] == geometry:
             return HipPagedAttention(self, cache, last[2])
         staging = self._staging.get(config.device)
         if staging is None:
@@ -452,5 +458,5 @@ class HipPagedAttentionBackend:
         # stages it all; one copy uploads it.
         plan = StepPlan(metadata, block_size=config.block_size, device=config.device, num_blocks=config.num_blocks,
                         partition_tokens=self._partition_tokens, staging=staging, shapes=self._cache_shapes(cache))
-        self._last = (geometry, metadata, plan)
+        self._last = (geometry, key, plan)
         return HipPagedAttention(self, cache, plan)
