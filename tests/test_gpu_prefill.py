@@ -188,7 +188,7 @@ def test_split_k_c5_shape_shared_prefix() -> None:
 
 
 @pytest.mark.parametrize("waves", WAVES)
-@pytest.mark.parametrize("bs", (1, 3, 16))
+@pytest.mark.parametrize("bs", (1, 3, 12, 16))
 def test_split_k_causal_chunks_and_block_sizes(bs, waves) -> None:
     # Causal chunks with long prior context: 40 x 7 = 280 columns (three units,
     # the last partial), split over keys; plus decode rows in the same step.
