@@ -412,6 +412,27 @@ def kv_move_sweep(args, device: torch.device) -> int:
         ms = _time_launches(compact, 20, 3, device, batch=5)
         moved = 2 * n * layers * 2 * row
         out["compact"].append({"rows": n, "us": round(ms * 1e3, 2), "GBps": round(moved / (ms * 1e-3) / 1e9, 1)})
+    # Append: one C2-shaped layer (4 KV heads, D 128, bf16, 1 GiB per pool),
+    # T tokens to random distinct slots; bytes = 4 * T * Hkv * D * 2.
+    out["append"] = []
+    a_hkv, a_blocks = 4, 32768
+    a_row = a_hkv * d * 2
+    pool_k = torch.empty((a_blocks * bs, a_row // 2), dtype=torch.bfloat16, device=device)
+    pool_v = torch.empty_like(pool_k)
+    for n in (64, 1024, 16384, 65536):
+        key = torch.randn((n, a_hkv, d), device=device).to(torch.bfloat16)
+        value = torch.randn((n, a_hkv, d), device=device).to(torch.bfloat16)
+        slots = torch.from_numpy(rng.permutation(a_blocks * bs)[:n].astype(np.int64)).to(device)
+
+        def append(i: int) -> None:
+            native.check(lib.lvamd_kv_append(
+                key.data_ptr(), key.stride(0), key.stride(1), value.data_ptr(), value.stride(0), value.stride(1),
+                pool_k.data_ptr(), pool_v.data_ptr(), slots.data_ptr(), n, a_hkv, d, native.DTYPE_BF16,
+                current_stream(device)), "lvamd_kv_append")
+
+        ms = _time_launches(append, 20, 3, device, batch=5)
+        moved = 4 * n * a_row
+        out["append"].append({"tokens": n, "us": round(ms * 1e3, 2), "GBps": round(moved / (ms * 1e-3) / 1e9, 1)})
     print(json.dumps(out), flush=True)
     return 0
 
@@ -878,6 +899,7 @@ def run_c5(args, device) -> int:
     cow_ms = _time_launches(lambda i: cow(), args.steps, args.warmup, device)
     attend_ms = _time_launches(lambda i: attend(), max(10, args.steps // 4), 2, device)
     compact_ms = _time_launches(lambda i: compact(), args.steps, args.warmup, device)
+    _, compact_host_ms = _time_steps(lambda i: compact(), args.steps, args.warmup)
     rotary = None
     if not args.no_rotary:
         rotary = {"fused_attention_us": _time_launches(lambda i: w.attend_rotary(), max(10, args.steps // 4), 2,
@@ -903,6 +925,7 @@ def run_c5(args, device) -> int:
                "attention_logical_gbps": round(cfg.layers * logical_kv / (attend_ms * 1e-3) / 1e9, 1),
                "cow_copy_us": round(cow_ms * 1e3, 2), "cow_copy_gbps": round(cow_bytes / (cow_ms * 1e-3) / 1e9, 1),
                "compact_us": round(compact_ms * 1e3, 2), "compact_tokens": moved,
+               "compact_host_us": round(compact_host_ms * 1e3, 2),
                "rotary": rotary,
                "host_submit_ms": round(host_ms, 5)})
     if not args.no_cpu_baseline:
@@ -930,6 +953,8 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-rotary", action="store_true",
                         help="skip the RoPE-fused step timing (keeps a kernel trace to the attention step)")
+    parser.add_argument("--no-serving", action="store_true",
+                        help="skip the serving-shaped 28-layer steps (keeps a kernel trace to the headline step)")
     parser.add_argument("--mode", choices=("full", "decode", "copy", "kv-sweep"), default="full",
                         help="decode: only the decode kernel (counter runs); copy: a plain 1 GiB device "
                              "copy of known size (counter calibration and the practical HBM ceiling); kv-sweep: "
@@ -1072,8 +1097,9 @@ def main() -> int:
             "note": "step with RoPE: lvamd_kv_append_rotary + attention, against apply_rotary's PyTorch path + "
                     "the fused-append attention step",
         }
-    print("[bench] serving-shaped C2 steps (28 layers, new metadata each step)", file=sys.stderr, flush=True)
-    record["serving"] = serving_steps(device, max(16, min(args.steps, 100)), min(args.warmup, 10))
+    if not args.no_serving:
+        print("[bench] serving-shaped C2 steps (28 layers, new metadata each step)", file=sys.stderr, flush=True)
+        record["serving"] = serving_steps(device, max(16, min(args.steps, 100)), min(args.warmup, 10))
     ceiling = read_ceiling(device)
     record["hbm_read_ceiling"] = {
         **ceiling, "decode_kernel_frac": round(achieved / ceiling["GBps"], 4),

@@ -51,13 +51,26 @@ enum lvamd_dtype { LVAMD_F32 = 0, LVAMD_F16 = 1, LVAMD_BF16 = 2 };
  * blocks, without waiting for the block table. */
 #define LVAMD_PIECE_FIELDS 16
 /* Number of int32 fields per merge job:
- * (req, column_group, first_partial_slot, num_partials, q_start, q_len, 0, 0). */
+ * (req, column_group, first_partial_slot, num_partials, q_start, q_len,
+ *  span_slot, span_columns).
+ * span_slot 0: no span.  Otherwise (prefill jobs of a request whose shared
+ * prefix was attended by span units, below) span_slot - 1 is the span's first
+ * partial slot and span_columns = the request's first column within the span
+ * | pieces per span unit << 24: the job also combines, for its column c
+ * (v = that offset + c), the partials of span unit v / unit columns at
+ * column v % unit columns, slots span_slot - 1 + (v / unit columns) * pieces
+ * + [0, pieces). */
 #define LVAMD_MERGE_FIELDS 8
 /* Number of int32 fields per prefill work unit:
- * (req, first column, columns, key_begin, key_end, partial_slot, 0, 0).
+ * (req, first column, columns, key_begin, key_end, partial_slot, table_off, q_start).
  * key_begin and key_end are multiples of lvamd_paged_prefill_key_tokens();
  * key_end 0 means up to the unit's last visible key.  A unit with partial_slot -1 covers
- * all its keys and writes out; the others write partials. */
+ * all its keys and writes out; the others write partials.  table_off and
+ * q_start are read only for a span unit (req < 0): columns of the packed
+ * queries from token q_start on (column c = token q_start + c / group, head
+ * c % group) of requests whose tables all list the blocks at table_off over
+ * keys [0, key_end), every one of those keys below every such query's
+ * computed count; it always writes partials (key_end > 0). */
 #define LVAMD_PREFILL_FIELDS 8
 
 const char* lvamd_status_string(int status);

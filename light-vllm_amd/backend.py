@@ -364,6 +364,7 @@ class HipPagedAttentionBackend:
     def __init__(
         self, *, use_prefill_kernel: bool = True, partition_tokens: int | None = None,
         decode_col_tiles: int | None = None, split_prefill: bool = True, prefill_waves: int | None = None,
+        shared_prefix: bool = True,
     ) -> None:
         """``use_prefill_kernel=False`` sends every request through the decode
         kernel; ``partition_tokens`` caps the tokens one decode wave handles (a
@@ -373,7 +374,9 @@ class HipPagedAttentionBackend:
         ``split_prefill=False`` keeps every prefill unit's keys in one
         workgroup (no split-K partials); ``prefill_waves`` (4 or 8) fixes the
         prefill workgroup shape instead of the planner's per-step choice (8
-        falls back to 4 where it is not built)."""
+        falls back to 4 where it is not built); ``shared_prefix=False`` turns
+        off the shared-prefix spans (every prefill request then streams its
+        whole prefix itself)."""
 
         native.load()
         native.host()
@@ -388,6 +391,7 @@ class HipPagedAttentionBackend:
         self._partition_tokens = partition_tokens
         self._col_tiles = decode_col_tiles
         self._split_prefill = split_prefill
+        self._shared_prefix = shared_prefix
         self._prefill_waves = prefill_waves
         self._staging: dict[torch.device, Staging] = {}
         self._facts: dict[tuple, tuple[int, ...]] = {}
@@ -420,7 +424,7 @@ class HipPagedAttentionBackend:
                 native.decode_tile_tokens(code, d, 4) if has4 else 0,
                 native.prefill_resident_units(code, d, 4) if columns else 0,
                 native.prefill_resident_units(code, d, 8) if wide else 0,
-                self._partition_tokens or 0, DECODE_MAX_COLUMNS, 4, PREFILL_MIN_TILES,
+                self._partition_tokens or 0, DECODE_MAX_COLUMNS, 4, PREFILL_MIN_TILES, int(self._shared_prefix),
             )
             self._facts[key] = found
         return found

@@ -727,14 +727,25 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_merge_kernel(const Mer
   const int qhead = kvh * G + (col - qi * G);
   const int e0 = lane * EPL;
   const bool act = e0 < D;
+  // A request whose shared prefix was attended by span units (prefill jobs
+  // only): fields 6 = first span partial slot + 1, 7 = the request's first
+  // column within the span | pieces per span unit << 24.  Column v of the
+  // span lies in span unit v / cols at column v % cols, and that unit's
+  // pieces are consecutive slots.
+  const int span_slot = jb[6] - 1;
+  const int span_pieces = span_slot >= 0 ? (int)((uint32_t)jb[7] >> 24) : 0;
+  const int sv = (jb[7] & 0xffffff) + col;
+  const int sunit = sv / cols;
+  const int scol = sv - sunit * cols;
+  const int ntot = np + span_pieces;
 
   float mrun = -INFINITY;
   float lsum = 0.f;
   float o[EPL];
 #pragma unroll
   for (int k = 0; k < EPL; ++k) o[k] = 0.f;
-  for (int p0 = 0; p0 < np; p0 += MCP) {
-    const int n = np - p0 < MCP ? np - p0 : MCP;
+  for (int p0 = 0; p0 < ntot; p0 += MCP) {
+    const int n = ntot - p0 < MCP ? ntot - p0 : MCP;
     float2 ml[MCP];
     float pa[MCP][EPL];
 #pragma unroll
@@ -743,7 +754,9 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_merge_kernel(const Mer
 #pragma unroll
       for (int k = 0; k < EPL; ++k) pa[i][k] = 0.f;
       if (i < n) {
-        const int64_t r = ((int64_t)(slot0 + p0 + i) * Hkv + kvh) * cols + c;
+        const int p = p0 + i;
+        const int64_t r = p < np ? ((int64_t)(slot0 + p) * Hkv + kvh) * cols + c
+                                 : ((int64_t)(span_slot + sunit * span_pieces + (p - np)) * Hkv + kvh) * cols + scol;
         ml[i] = *reinterpret_cast<const float2*>(a.part_ml + r * 2);
         if (act) load_acc<EPL>(a.part_acc + r * D + e0, pa[i]);
       }

@@ -163,12 +163,32 @@ struct PrevFlatten {
   std::vector<PyObject*> rows;  // owned references (tuples), or nullptr
   std::vector<int64_t> offsets;
   std::vector<int32_t> values;
+  // Set when the table check passed on exactly these tables (for a pool of
+  // proven_blocks blocks): every id of every row is then in range and
+  // appears once in its row, which compact_pairs relies on for a row it
+  // receives as the same tuple object.
+  int64_t proven_blocks = -1;
 
   void reset() {
     for (PyObject* row : rows) Py_XDECREF(row);
     rows.clear();
     offsets.clear();
     values.clear();
+    proven_blocks = -1;
+  }
+
+  // Marks the rows proven when the checked tables (ids, cnt) are these.
+  void note_proven(const int32_t* ids, const int64_t* cnt, int64_t batch, int64_t num_blocks) {
+    proven_blocks = -1;
+    if ((int64_t)rows.size() != batch) return;
+    int64_t total = 0;
+    for (int64_t r = 0; r < batch; ++r) {
+      if (offsets[(size_t)r] != total) return;
+      total += cnt[r];
+    }
+    if (total != (int64_t)values.size() || std::memcmp(ids, values.data(), (size_t)total * sizeof(int32_t)) != 0)
+      return;
+    proven_blocks = num_blocks;
   }
 };
 PrevFlatten g_prev_flatten;
@@ -379,6 +399,7 @@ bool validate_appended(const int32_t* ids, const int64_t* cnt, const int64_t* co
     }
   }
   prev.save(ids, cnt, ro, batch, num_blocks, bs, s.epoch);
+  g_prev_flatten.note_proven(ids, cnt, batch, num_blocks);
   ++g_counts.incremental_proofs;
   return true;
 }
@@ -480,8 +501,10 @@ int check_tables(const int32_t* ids, const int64_t* cnt, const int64_t* comp, co
   }
   if (rule == kTablesOk) {
     g_prev_tables.save(ids, cnt, ro, batch, num_blocks, bs, epoch);
+    g_prev_flatten.note_proven(ids, cnt, batch, num_blocks);
   } else {
     g_prev_tables.valid = false;
+    g_prev_flatten.proven_blocks = -1;
     *bad = r;
   }
   return rule;
@@ -495,6 +518,10 @@ int check_tables(const int32_t* ids, const int64_t* cnt, const int64_t* comp, co
 // or an ancestor of q.  status 1: a parent is not an int in [-1, index).
 // ---------------------------------------------------------------------------
 PyObject* g_parent_indices = nullptr;  // interned "parent_indices"
+// Interned keys of a compact request: block_ids, num_computed_tokens,
+// num_query_tokens, num_reserved_query_tokens, num_readonly_prefix_blocks,
+// retained_query_indices.
+PyObject* g_compact_keys[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
 
 // layouts' body over ``batch`` layout objects: fills the per-request arrays
 // and appends the ancestor rows to ``vis``.  Returns the status, or -1 with
@@ -1032,30 +1059,117 @@ struct PrefillLists {
 
 struct PrefillParams {
   int64_t group, columns, key_tokens, slots_per_head, min_tiles, max_cols;
+  const int32_t* ids = nullptr;  // flat block tables, for shared-prefix spans (null: no spans)
+  int64_t block_size = 0;
+  bool spans = false;
 };
 
-// (request, first column, columns, key tiles) of every prefill unit.
+// A prefill unit: columns [col0, col0 + cols) of request req over key tiles
+// [first, first + tiles).  A span unit covers columns of a span (below): its
+// columns are the (token, head) pairs of the span's packed queries.
 struct Unit {
   int32_t req;
-  int64_t col0, cols, tiles;
+  int64_t col0, cols, tiles, first;
+  int32_t span;    // the span of a span unit or of a member's unit, else -1
+  bool span_unit;
 };
 
-std::vector<Unit> prefill_units_of(const Requests& q, const PrefillParams& p) {
+// Shared-prefix decomposition.  A span is a run of consecutive prefill rows
+// [r0, r1) whose block tables list the same block ids over the key tokens
+// [0, prefix), with prefix a whole number of key tiles and at most every
+// member's computed count: those keys are the same K/V rows for every
+// member, visible to every query, and not written this step.  They are
+// attended once per 128 columns of the span's packed queries (span units),
+// and each member's own units cover only keys [prefix, end); every member
+// unit writes partials, and its merge job adds the span units' partials of
+// its columns (merge fields 6 and 7).  light-vllm's prefix cache produces
+// such runs: sequences sharing a prompt prefix hold the same readonly blocks
+// at the same logical indices (paged_attention.py:138-172 allows sharing
+// only there).
+struct Span {
+  int64_t r0, r1, prefix, t0, ntok, table_off;
+  int64_t pieces = 1;  // pieces per span unit
+  int32_t base = -1;   // partial slot of the first span unit's first piece
+};
+
+constexpr int64_t kSpanMaxPieces = 127;         // merge field 7 holds pieces << 24
+constexpr int64_t kSpanMaxColumns = 1 << 24;    // ... and the column offset below it
+
+std::vector<Span> find_spans(const Requests& q, const PrefillParams& p) {
+  std::vector<Span> spans;
+  if (!p.spans || p.ids == nullptr || p.block_size <= 0) return spans;
+  const int64_t KT = p.key_tokens, G = p.group, bs = p.block_size;
+  auto wide = [&](int64_t r) { return q.q_len(r) * G > p.max_cols; };
+  auto units_of = [&](int64_t cols) { return (cols + p.columns - 1) / p.columns; };
+  for (int64_t r = 0; r < q.batch;) {
+    if (!wide(r) || q.row(r)[1] == 0) {
+      ++r;
+      continue;
+    }
+    const int32_t* first = p.ids + q.row(r)[0];
+    int64_t lcp = q.row(r)[1], min_comp = q.computed(r);
+    int64_t prefix = std::min(lcp * bs, min_comp) / KT * KT;
+    int64_t end = r + 1, cols = q.q_len(r) * G, member_units = units_of(q.q_len(r) * G);
+    while (end < q.batch && wide(end)) {
+      const int32_t* t = p.ids + q.row(end)[0];
+      const int64_t n = std::min<int64_t>(lcp, q.row(end)[1]);
+      int64_t l = 0;
+      while (l < n && t[l] == first[l]) ++l;
+      const int64_t mc = std::min(min_comp, q.computed(end));
+      const int64_t pre = std::min(l * bs, mc) / KT * KT;
+      // A member that would halve the prefix the run already shares ends it.
+      if (pre < 2 * KT || (end - r >= 2 && 2 * pre < prefix)) break;
+      lcp = l;
+      min_comp = mc;
+      prefix = pre;
+      cols += q.q_len(end) * G;
+      member_units += units_of(q.q_len(end) * G);
+      ++end;
+    }
+    // Worth it when the span's columns pack into fewer units than the
+    // members' own (each unit streams the prefix once).
+    if (end - r >= 2 && prefix >= 2 * KT && units_of(cols) < member_units && cols < kSpanMaxColumns) {
+      Span s;
+      s.r0 = r;
+      s.r1 = end;
+      s.prefix = prefix;
+      s.t0 = q.row(r)[4];
+      s.ntok = cols / G;
+      s.table_off = q.row(r)[0];
+      spans.push_back(s);
+    }
+    r = end;
+  }
+  return spans;
+}
+
+std::vector<Unit> prefill_units_of(const Requests& q, const PrefillParams& p, const std::vector<Span>& spans) {
   std::vector<Unit> units;
+  const int64_t KT = p.key_tokens;
+  size_t s = 0;
   for (int64_t r = 0; r < q.batch; ++r) {
     const int64_t ncols = q.q_len(r) * p.group;
     if (ncols <= p.max_cols) continue;
+    const Span* sp = (s < spans.size() && spans[s].r0 <= r && r < spans[s].r1) ? &spans[s] : nullptr;
+    const int64_t first = sp ? sp->prefix / KT : 0;
+    if (sp && r == sp->r0) {
+      const int64_t scols = sp->ntok * p.group;
+      for (int64_t c0 = 0; c0 < scols; c0 += p.columns)
+        units.push_back({-1 - (int32_t)s, c0, std::min(p.columns, scols - c0), first, 0, (int32_t)s, true});
+    }
     for (int64_t c0 = 0; c0 < ncols; c0 += p.columns) {
       const int64_t cols = std::min(p.columns, ncols - c0);
       const int64_t kneed = q.computed(r) + (c0 + cols - 1) / p.group + 1;
-      units.push_back({(int32_t)r, c0, cols, (kneed + p.key_tokens - 1) / p.key_tokens});
+      units.push_back({(int32_t)r, c0, cols, (kneed + KT - 1) / KT - first, first, sp ? (int32_t)s : -1, false});
     }
+    if (sp && r + 1 == sp->r1) ++s;
   }
   return units;
 }
 
 void build_prefill(const Requests& q, const PrefillParams& p, PrefillLists& out) {
-  const std::vector<Unit> units = prefill_units_of(q, p);
+  std::vector<Span> spans = find_spans(q, p);
+  const std::vector<Unit> units = prefill_units_of(q, p, spans);
   const int64_t n = (int64_t)units.size();
   int64_t tile_sum = 0;
   for (const Unit& u : units) tile_sum += u.tiles;
@@ -1063,7 +1177,11 @@ void build_prefill(const Requests& q, const PrefillParams& p, PrefillLists& out)
   std::vector<int64_t> npieces((size_t)n, 1);
   if (p.slots_per_head > 0 && n < p.slots_per_head) {
     const int64_t target = std::max(p.min_tiles, (tile_sum + p.slots_per_head - 1) / p.slots_per_head);
-    for (int64_t u = 0; u < n; ++u) npieces[(size_t)u] = std::max<int64_t>(1, (units[(size_t)u].tiles + target - 1) / target);
+    for (int64_t u = 0; u < n; ++u) {
+      const Unit& un = units[(size_t)u];
+      const int64_t k = std::max<int64_t>(1, (un.tiles + target - 1) / target);
+      npieces[(size_t)u] = un.span_unit ? std::min(k, kSpanMaxPieces) : k;
+    }
   }
   struct PRec {
     int64_t unit, t0, t1, i, work;
@@ -1071,19 +1189,34 @@ void build_prefill(const Requests& q, const PrefillParams& p, PrefillLists& out)
   };
   std::vector<PRec> recs;
   for (int64_t u = 0; u < n; ++u) {
-    const int64_t k = npieces[(size_t)u], tiles = units[(size_t)u].tiles;
+    const Unit& un = units[(size_t)u];
+    const int64_t k = npieces[(size_t)u], tiles = un.tiles;
+    // Partial slots in (unit, piece) order, before the heaviest-first sort:
+    // a span's units are consecutive, so piece i of its span unit j is slot
+    // base + j * pieces + i.  Span units and members' units always write
+    // partials (their merge job combines both parts).
+    if (un.span_unit && spans[(size_t)un.span].base < 0) {
+      spans[(size_t)un.span].base = out.slots;
+      spans[(size_t)un.span].pieces = k;
+    }
     for (int64_t i = 0; i < k; ++i) {
       const int64_t t0 = (i * tiles) / k, t1 = ((i + 1) * tiles) / k;
-      // Partial slots in (unit, piece) order, before the heaviest-first sort.
-      recs.push_back({u, t0, t1, i, (t1 - t0) * units[(size_t)u].cols, k > 1 ? out.slots++ : -1});
+      const bool partial = k > 1 || un.span >= 0;
+      recs.push_back({u, t0, t1, i, (t1 - t0) * un.cols, partial ? out.slots++ : -1});
     }
   }
   for (const PRec& x : recs) {
-    if (x.slot < 0 || x.i != 0) continue;
     const Unit& un = units[(size_t)x.unit];
+    if (x.slot < 0 || x.i != 0 || un.span_unit) continue;
     const int32_t* m = q.row(un.req);
+    int32_t span_slot = 0, span_cols = 0;
+    if (un.span >= 0) {
+      const Span& sp = spans[(size_t)un.span];
+      span_slot = sp.base + 1;
+      span_cols = (int32_t)(((int64_t)m[4] - sp.t0) * p.group | (sp.pieces << 24));
+    }
     const int32_t job[kMergeFields] = {un.req, (int32_t)(un.col0 / p.columns), x.slot,
-                                       (int32_t)npieces[(size_t)x.unit], m[4], m[3], 0, 0};
+                                       (int32_t)npieces[(size_t)x.unit], m[4], m[3], span_slot, span_cols};
     out.jobs.insert(out.jobs.end(), job, job + kMergeFields);
     out.merge_cols = std::max(out.merge_cols, un.cols);
   }
@@ -1093,12 +1226,20 @@ void build_prefill(const Requests& q, const PrefillParams& p, PrefillLists& out)
     const PRec& x = recs[k];
     const Unit& un = units[(size_t)x.unit];
     int32_t* o = out.units.data() + k * kPrefillFields;
+    const bool last = x.i + 1 == npieces[(size_t)x.unit];
     o[0] = un.req;
     o[1] = (int32_t)un.col0;
     o[2] = (int32_t)un.cols;
-    o[3] = (int32_t)(x.t0 * p.key_tokens);
-    o[4] = x.i + 1 < npieces[(size_t)x.unit] ? (int32_t)(x.t1 * p.key_tokens) : 0;
+    o[3] = (int32_t)((un.first + x.t0) * p.key_tokens);
+    // A request's last piece runs to its queries' keys (0: no bound); a
+    // span unit's pieces always end at a tile boundary within the prefix.
+    o[4] = (last && !un.span_unit) ? 0 : (int32_t)((un.first + x.t1) * p.key_tokens);
     o[5] = x.slot;
+    if (un.span_unit) {
+      const Span& sp = spans[(size_t)un.span];
+      o[6] = (int32_t)sp.table_off;
+      o[7] = (int32_t)sp.t0;
+    }
   }
 }
 
@@ -1126,7 +1267,7 @@ int64_t choose_col_tiles(const Requests& q, int64_t group, int64_t max_cols, int
 int64_t choose_prefill_waves(const Requests& q, const PrefillParams& p, int64_t slots_per_head8, bool wide_built,
                              double wide_max_tiles) {
   if (!wide_built) return 4;
-  const std::vector<Unit> units = prefill_units_of(q, p);
+  const std::vector<Unit> units = prefill_units_of(q, p, find_spans(q, p));
   if (units.empty()) return 4;
   int64_t tile_sum = 0;
   for (const Unit& u : units) tile_sum += u.tiles;
@@ -1165,6 +1306,16 @@ PyObject* prefill_result(const PrefillLists& p) {
   return result;
 }
 
+// Whether every request's table (table_off, blocks) lies inside the flat
+// array of nflat ids (req_meta handed in from Python is not trusted).
+bool tables_fit(const Requests& q, int64_t nflat) {
+  for (int64_t r = 0; r < q.batch; ++r) {
+    const int64_t off = q.row(r)[0], n = q.row(r)[1];
+    if (off < 0 || n < 0 || off + n > nflat) return false;
+  }
+  return true;
+}
+
 bool requests_of(const Buf& meta, Requests* q, const char* name) {
   q->meta = meta.data<int32_t>();
   q->batch = meta.count() / kReqFields;
@@ -1200,30 +1351,40 @@ PyObject* decode_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   return decode_result(out);
 }
 
-// prefill_work(req_meta i32[B*8], group, columns, key_tokens, slots_per_head,
-//              min_tiles, decode_max_columns)
+// prefill_work(req_meta i32[B*8], flat i32, group, columns, key_tokens,
+//              slots_per_head, min_tiles, decode_max_columns, block_size,
+//              shared_prefix)
 //   -> (units i32 [n, 8], jobs i32 [m, 8], partial slots, mean key tiles per
 //       unit, most columns of a merge job)
+// shared_prefix (0/1) enables the shared-prefix spans.
 PyObject* prefill_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
-  if (!want_args(nargs, 7, "prefill_work")) return nullptr;
-  Buf meta(args[0], false, 4, "req_meta");
-  if (!meta.ok()) return nullptr;
+  if (!want_args(nargs, 10, "prefill_work")) return nullptr;
+  Buf meta(args[0], false, 4, "req_meta"), flat(args[1], false, 4, "flat");
+  if (!meta.ok() || !flat.ok()) return nullptr;
   Requests q;
   if (!requests_of(meta, &q, "prefill_work")) return nullptr;
   PrefillParams p;
-  int64_t* fields[] = {&p.group, &p.columns, &p.key_tokens, &p.slots_per_head, &p.min_tiles, &p.max_cols};
-  for (int i = 0; i < 6; ++i)
-    if (!as_i64(args[1 + i], fields[i])) return nullptr;
-  if (p.group <= 0 || p.columns <= 0 || p.key_tokens <= 0 || p.min_tiles <= 0) {
+  int64_t spans = 0;
+  int64_t* fields[] = {&p.group, &p.columns, &p.key_tokens, &p.slots_per_head, &p.min_tiles, &p.max_cols,
+                       &p.block_size, &spans};
+  for (int i = 0; i < 8; ++i)
+    if (!as_i64(args[2 + i], fields[i])) return nullptr;
+  if (p.group <= 0 || p.columns <= 0 || p.key_tokens <= 0 || p.min_tiles <= 0 || p.block_size <= 0) {
     PyErr_SetString(PyExc_ValueError, "prefill_work: inconsistent arguments");
     return nullptr;
   }
+  if (!tables_fit(q, flat.count())) {
+    PyErr_SetString(PyExc_ValueError, "prefill_work: req_meta names tables past the flat array");
+    return nullptr;
+  }
+  p.ids = flat.data<int32_t>();
+  p.spans = spans != 0;
   PrefillLists out;
   build_prefill(q, p, out);
   return prefill_result(out);
 }
 
-// layer_work(req_meta i32[B*8], flat i32, kernel facts (int64 array, 20
+// layer_work(req_meta i32[B*8], flat i32, kernel facts (int64 array, 21
 //            entries, below), cost4, wide_max_tiles)
 //   -> (col_tiles, prefill_waves, decode result or None, prefill result or None)
 //
@@ -1237,8 +1398,8 @@ PyObject* prefill_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
 //   11 tile tokens at 1, 12 resident at 4, 13 tile tokens at 4, 14 resident
 //   4-wave prefill workgroups, 15 resident 8-wave ones, 16 max tokens per
 //   decode wave (0: no cap), 17 decode max columns, 18 min units per wave,
-//   19 prefill min tiles.
-constexpr int kKernelFacts = 20;
+//   19 prefill min tiles, 20 shared-prefix spans (0/1).
+constexpr int kKernelFacts = 21;
 
 // One layer shape's plan: the choices and the lists of both kernels.
 struct LayerPlan {
@@ -1270,6 +1431,10 @@ PyObject* layer_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     PyErr_Format(PyExc_ValueError, "layer_work: expected %d kernel facts", kKernelFacts);
     return nullptr;
   }
+  if (!tables_fit(q, flat.count())) {
+    PyErr_SetString(PyExc_ValueError, "layer_work: req_meta names tables past the flat array");
+    return nullptr;
+  }
   LayerPlan plan;
   if (const char* err = plan_layer(q, flat.data<int32_t>(), flat.count(), kf.data<int64_t>(), cost4, wide_max, plan)) {
     PyErr_Format(PyExc_ValueError, "layer_work: %s", err);
@@ -1295,6 +1460,9 @@ const char* plan_layer(const Requests& q, const int32_t* ids, int64_t nflat, con
   int64_t ctw = k[6] > 0 ? std::min(k[6], k[8]) : choose_col_tiles(q, group, max_cols, k[8], cost4);
   if (ctw != 4) ctw = 1;
   PrefillParams p{group, columns > 0 ? columns : 1, k[4] > 0 ? k[4] : 1, 0, k[19] > 0 ? k[19] : 1, max_cols};
+  p.ids = ids;
+  p.block_size = bs;
+  p.spans = k[20] != 0;
   int64_t waves = 4;
   bool any_decode = false, any_prefill = false;
   for (int64_t r = 0; r < q.batch; ++r) {
@@ -1512,10 +1680,10 @@ PyObject* compact_pairs(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   s.reserve(num_blocks);
   std::vector<int64_t> src, dst, moved((size_t)nreq, 0);
   std::vector<int64_t> ret;
+  static std::vector<int32_t> vals;  // one request's block ids
+  const PrevFlatten& proven = g_prev_flatten;
   int rule = 0;
   Py_ssize_t r = 0;
-  static const char* kCountKeys[4] = {"num_computed_tokens", "num_query_tokens", "num_reserved_query_tokens",
-                                      "num_readonly_prefix_blocks"};
   for (; r < nreq && rule == 0; ++r) {
     PyObject* req = PySequence_Fast_GET_ITEM(reqs, r);
     if (!PyDict_Check(req)) {
@@ -1524,7 +1692,7 @@ PyObject* compact_pairs(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     }
     int64_t cnt[4] = {0, 0, 0, 0};
     for (int k = 0; k < 4 && rule == 0; ++k) {
-      PyObject* v = PyDict_GetItemString(req, kCountKeys[k]);
+      PyObject* v = PyDict_GetItem(req, g_compact_keys[1 + k]);
       if (v == nullptr) {
         if (k == 3) continue;  // num_readonly_prefix_blocks defaults to 0
         rule = 11;
@@ -1537,8 +1705,8 @@ PyObject* compact_pairs(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     if (rule) break;
     const int64_t computed = cnt[0], queries = cnt[1], reserved = cnt[2], readonly = cnt[3];
     if (reserved < queries) { rule = 2; break; }
-    PyObject* ids_obj = PyDict_GetItemString(req, "block_ids");
-    PyObject* ret_obj = PyDict_GetItemString(req, "retained_query_indices");
+    PyObject* ids_obj = PyDict_GetItem(req, g_compact_keys[0]);
+    PyObject* ret_obj = PyDict_GetItem(req, g_compact_keys[5]);
     if (ids_obj == nullptr || ret_obj == nullptr) { rule = 11; break; }
     PyObject* rseq = PySequence_Fast(ret_obj, "retained query indices must be a sequence");
     if (rseq == nullptr) { Py_DECREF(reqs); return nullptr; }
@@ -1560,47 +1728,49 @@ PyObject* compact_pairs(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     bool tail_ok = true;
     for (int64_t x : ret) tail_ok &= x < queries;
     if (!tail_ok) { rule = 5; break; }
-    PyObject* tseq = PySequence_Fast(ids_obj, "block_ids must be a sequence");
-    if (tseq == nullptr) { Py_DECREF(reqs); return nullptr; }
-    const Py_ssize_t n = PySequence_Fast_GET_SIZE(tseq);
-    PyObject** items = PySequence_Fast_ITEMS(tseq);
     const int64_t required = (computed + reserved + bs - 1) / bs;
-    if (n != required) {
+    const int32_t* ids = nullptr;
+    Py_ssize_t n = 0;
+    if (proven.proven_blocks == num_blocks && r < (Py_ssize_t)proven.rows.size() && proven.rows[(size_t)r] == ids_obj) {
+      // The very tuple this step's metadata listed for this request, whose
+      // ids the step's table check proved in range and unique in the row.
+      n = PyTuple_GET_SIZE(ids_obj);
+      ids = proven.values.data() + proven.offsets[(size_t)r];
+      if (n != required) { rule = 6; break; }
+    } else {
+      PyObject* tseq = PySequence_Fast(ids_obj, "block_ids must be a sequence");
+      if (tseq == nullptr) { Py_DECREF(reqs); return nullptr; }
+      n = PySequence_Fast_GET_SIZE(tseq);
+      PyObject** items = PySequence_Fast_ITEMS(tseq);
+      if (n != required) {
+        Py_DECREF(tseq);
+        rule = 6;
+        break;
+      }
+      vals.resize((size_t)n);
+      bool ids_ok = true;
+      for (Py_ssize_t i = 0; i < n && ids_ok; ++i) {
+        int overflow = 0;
+        const long long v = PyLong_CheckExact(items[i]) ? PyLong_AsLongLongAndOverflow(items[i], &overflow) : -1;
+        ids_ok = overflow == 0 && v >= 0 && v < num_blocks;
+        vals[(size_t)i] = (int32_t)v;
+      }
       Py_DECREF(tseq);
-      rule = 6;
-      break;
+      if (!ids_ok) { rule = 7; break; }
+      const uint32_t seen = s.next_epoch();
+      bool unique = true;
+      for (Py_ssize_t i = 0; i < n && unique; ++i) {
+        BlockRecord& b = s.rec[(size_t)vals[(size_t)i]];
+        unique = b.epoch != seen;
+        b.epoch = seen;
+      }
+      if (!unique) { rule = 8; break; }
+      ids = vals.data();
     }
-    bool ids_ok = true;
-    for (Py_ssize_t i = 0; i < n && ids_ok; ++i) {
-      int overflow = 0;
-      const long long v = PyLong_CheckExact(items[i]) ? PyLong_AsLongLongAndOverflow(items[i], &overflow) : -1;
-      ids_ok = overflow == 0 && v >= 0 && v < num_blocks;
-    }
-    if (!ids_ok) {
-      Py_DECREF(tseq);
-      rule = 7;
-      break;
-    }
-    const uint32_t seen = s.next_epoch();
-    bool unique = true;
-    for (Py_ssize_t i = 0; i < n && unique; ++i) {
-      BlockRecord& b = s.rec[(size_t)PyLong_AsLongLong(items[i])];
-      unique = b.epoch != seen;
-      b.epoch = seen;
-    }
-    if (!unique) {
-      Py_DECREF(tseq);
-      rule = 8;
-      break;
-    }
-    if (readonly * bs > computed) {
-      Py_DECREF(tseq);
-      rule = 9;
-      break;
-    }
+    if (readonly * bs > computed) { rule = 9; break; }
     auto slot_of = [&](int64_t pos) -> int64_t {
       const int64_t lb = pos / bs;
-      return PyLong_AsLongLong(items[lb]) * bs + (pos - lb * bs);
+      return (int64_t)ids[lb] * bs + (pos - lb * bs);
     };
     for (Py_ssize_t i = 0; i < nret; ++i) {
       const int64_t from = slot_of(computed + ret[(size_t)i]);
@@ -1611,7 +1781,6 @@ PyObject* compact_pairs(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
       }
       moved[(size_t)r] += from != to;
     }
-    Py_DECREF(tseq);
   }
   Py_DECREF(reqs);
   if (rule == 0 && dst.size() > 1) {
@@ -1663,5 +1832,12 @@ PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_lvamd_host", "Native host-side s
 PyMODINIT_FUNC PyInit__lvamd_host(void) {
   g_parent_indices = PyUnicode_InternFromString("parent_indices");
   if (g_parent_indices == nullptr) return nullptr;
+  static const char* kCompactKeys[6] = {"block_ids", "num_computed_tokens", "num_query_tokens",
+                                        "num_reserved_query_tokens", "num_readonly_prefix_blocks",
+                                        "retained_query_indices"};
+  for (int i = 0; i < 6; ++i) {
+    g_compact_keys[i] = PyUnicode_InternFromString(kCompactKeys[i]);
+    if (g_compact_keys[i] == nullptr) return nullptr;
+  }
   return PyModule_Create(&kModule);
 }

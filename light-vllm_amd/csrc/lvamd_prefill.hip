@@ -127,9 +127,19 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
   const int kvh = blockIdx.x - unit * Hkv;
   const int32_t* u = a.units + (int64_t)unit * LVAMD_PREFILL_FIELDS;
   const int req = u[0], col0 = u[1], ncols = u[2], key_begin = u[3], key_end = u[4], slot = u[5];
-  const int32_t* rm = a.req_meta + (int64_t)req * LVAMD_REQ_FIELDS;
-  const int table_off = rm[0], computed = rm[2], q_len = rm[3], q_start = rm[4], vis_off = rm[5],
-            vis_words = rm[6];
+  // A span unit (req < 0) attends the packed queries of requests sharing a
+  // prefix to its keys [key_begin, key_end): its record carries the shared
+  // table's offset and the first query token.  Every key it reads lies below
+  // every query's computed count, so it is treated as a linear request whose
+  // computed count is key_end: no tile is masked, nothing is appended.
+  const bool span = req < 0;
+  const int32_t* rm = a.req_meta + (int64_t)(span ? 0 : req) * LVAMD_REQ_FIELDS;
+  const int table_off = span ? u[6] : rm[0];
+  const int computed = span ? key_end : rm[2];
+  const int q_len = span ? 0 : rm[3];
+  const int q_start = span ? u[7] : rm[4];
+  const int vis_off = span ? -1 : rm[5];
+  const int vis_words = span ? 0 : rm[6];
   const int col_end = col0 + ncols;  // exclusive, <= q_len * G
   // Keys the unit needs: up to its last query's position, within the piece's
   // key range [key_begin, key_end) (key_begin a multiple of KT; key_end 0 =

@@ -293,8 +293,13 @@ def _launch_compact(cache, src: np.ndarray, dst: np.ndarray) -> None:
     pointers = _layer_pointers(cache)
     device = cache.config.device
     n = int(src.size)
-    blob, (src_off, dst_off) = pointers.staging.stage([src.view(np.int32), dst.view(np.int32)])
-    src_ptr, dst_ptr = blob.data_ptr() + 4 * src_off, blob.data_ptr() + 4 * dst_off
+    # [src | dst] as int64 pairs of int32 words, in one pinned buffer and copy.
+    buf = pointers.staging.take(4 * n)
+    buf[: 2 * n] = src.view(np.int32)
+    buf[2 * n : 4 * n] = dst.view(np.int32)
+    blob = pointers.staging.upload(buf[: 4 * n])
+    src_ptr = blob.data_ptr()
+    dst_ptr = src_ptr + 8 * n
     lib = native.load()
     stream = current_stream(device)
     for row_bytes, num_layers, ptrs in pointers.groups:

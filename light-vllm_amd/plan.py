@@ -490,7 +490,7 @@ class StepPlan:
     def work(
         self, group: int, num_kv_heads: int, resident_waves: int = 8 * NUM_CUS, prefill_columns: int = 0,
         unit_tokens: int = UNIT_TOKENS, col_tiles: int = 1, prefill_key_tokens: int = 64,
-        prefill_resident: int = 0, prefill_waves: int = 4,
+        prefill_resident: int = 0, prefill_waves: int = 4, shared_prefix: bool = False,
     ) -> DecodeWork:
         """Work lists for layers of this (group, kv heads) shape.
 
@@ -500,12 +500,13 @@ class StepPlan:
         tile and ``col_tiles`` its column tiles per wave; ``prefill_key_tokens``
         is the prefill kernel's key tile and ``prefill_resident`` how many
         prefill workgroups of shape ``prefill_waves`` the GPU holds (0: never
-        split prefill units).  The library reports the kernel figures per
-        dtype and head size.
+        split prefill units); ``shared_prefix`` attends prefixes that runs of
+        prefill requests share once per span (the backend's default).  The
+        library reports the kernel figures per dtype and head size.
         """
 
         key = (group, num_kv_heads, resident_waves, prefill_columns, unit_tokens, col_tiles, prefill_key_tokens,
-               prefill_resident, prefill_waves)
+               prefill_resident, prefill_waves, bool(shared_prefix))
         found = self._work.get(key)
         if found is None:
             found = self._build_work(*key)
@@ -522,7 +523,7 @@ class StepPlan:
         found = self._work.get(kernel_facts)
         if found is None:
             ctw, waves, dec, pre = native.host().layer_work(
-                self._req_meta, self.facts.flat, np.asarray(kernel_facts, dtype=np.int64), COL_TILES4_COST,
+                self._req_meta, self.facts.raw[0], np.asarray(kernel_facts, dtype=np.int64), COL_TILES4_COST,
                 float(PREFILL_WIDE_MAX_TILES),
             )
             found = DecodeWork(col_tiles=int(ctw), prefill_waves=int(waves))
@@ -544,7 +545,7 @@ class StepPlan:
 
     def _build_work(
         self, group: int, num_kv_heads: int, resident_waves: int, prefill_columns: int, unit_tokens: int,
-        col_tiles: int, prefill_key_tokens: int, prefill_resident: int, prefill_waves: int,
+        col_tiles: int, prefill_key_tokens: int, prefill_resident: int, prefill_waves: int, shared_prefix: bool,
     ) -> DecodeWork:
         host = native.host()
         work = DecodeWork(col_tiles=col_tiles, prefill_waves=prefill_waves)
@@ -557,8 +558,9 @@ class StepPlan:
                                    resident_waves, self.block_size, 4, max_units, unit_tokens)
         if max_cols and bool(np.any(q_cols > max_cols)):
             slots_per_head = prefill_resident // num_kv_heads if prefill_resident else 0
-            pre = host.prefill_work(self._req_meta, group, prefill_columns, prefill_key_tokens, slots_per_head,
-                                    PREFILL_MIN_TILES, max_cols)
+            pre = host.prefill_work(self._req_meta, self.facts.raw[0], group, prefill_columns, prefill_key_tokens,
+                                    slots_per_head, PREFILL_MIN_TILES, max_cols, self.block_size,
+                                    int(shared_prefix))
         _fill_work(work, dec, pre)
         return work
 
@@ -569,7 +571,7 @@ KERNEL_FACTS = (
     "forced_col_tiles", "forced_prefill_waves", "max_col_tiles", "wide_prefill_built",
     "resident_waves_1", "tile_tokens_1", "resident_waves_4", "tile_tokens_4",
     "prefill_resident_4", "prefill_resident_8", "partition_tokens", "decode_max_columns",
-    "min_units_per_wave", "prefill_min_tiles",
+    "min_units_per_wave", "prefill_min_tiles", "shared_prefix",
 )
 
 

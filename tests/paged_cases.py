@@ -46,7 +46,13 @@ def make_step(
     shared_prefix_blocks: int = 0,
     num_layers: int = 1,
     device: str = "cuda:0",
+    prefix_groups=None,
+    group_prefix_blocks=(),
 ) -> Step:
+    """A step of requests with random history.  Every request shares the first
+    ``shared_prefix_blocks`` blocks (readonly); or, with ``prefix_groups`` (per
+    request: an index into ``group_prefix_blocks``, or -1), each group of
+    requests shares its own readonly prefix of that many blocks."""
     rng = np.random.default_rng(seed)
     gen = torch.Generator(device="cpu").manual_seed(seed)
     computed = [int(c) for c in computed]
@@ -54,16 +60,25 @@ def make_step(
     q_lens = [len(l) for l in layouts]
     reserved = [int(r) for r in (reserved or q_lens)]
     need = [(c + r + bs - 1) // bs for c, r in zip(computed, reserved)]
-    total = shared_prefix_blocks + sum(n - shared_prefix_blocks for n in need)
+    if prefix_groups is None:
+        prefix_groups = [0] * len(need)
+        group_prefix_blocks = (shared_prefix_blocks,)
+    own = [len(group_prefix_blocks) and group_prefix_blocks[g] if g >= 0 else 0 for g in prefix_groups]
+    total = sum(group_prefix_blocks) + sum(n - o for n, o in zip(need, own))
     nb = num_blocks or total + 7
     assert nb >= total
     perm = [int(x) for x in rng.permutation(nb)]
-    shared, rest = perm[:shared_prefix_blocks], perm[shared_prefix_blocks:]
+    prefixes, off = [], 0
+    for blocks in group_prefix_blocks:
+        prefixes.append(perm[off : off + blocks])
+        off += blocks
+    rest = perm[off:]
     tables = []
-    for n in need:
-        tables.append(tuple(shared + rest[: n - shared_prefix_blocks]))
-        rest = rest[n - shared_prefix_blocks :]
-    readonly = tuple(shared_prefix_blocks for _ in need)
+    for n, g in zip(need, prefix_groups):
+        shared = prefixes[g] if g >= 0 else []
+        tables.append(tuple(shared + rest[: n - len(shared)]))
+        rest = rest[n - len(shared) :]
+    readonly = tuple(group_prefix_blocks[g] if g >= 0 else 0 for g in prefix_groups)
     layer_ids = tuple(f"layer{i}" for i in range(num_layers))
     spec = lv.ModelKVCacheSpec(tuple(lv.AttentionLayerSpec(i, hq, hkv, d) for i in layer_ids))
     cache = lv.PagedKVCache(spec, lv.PagedKVCacheConfig(num_blocks=nb, block_size=bs, dtype=dtype, device=device))
@@ -89,7 +104,7 @@ def make_step(
         num_computed_tokens=tuple(computed),
         query_layouts=tuple(layouts),
         num_reserved_query_tokens=tuple(reserved),
-        num_readonly_prefix_blocks=readonly if shared_prefix_blocks else (),
+        num_readonly_prefix_blocks=readonly if any(readonly) else (),
     )
     return Step(cache, metadata, query, key, value, layer_ids, 1.0 / math.sqrt(d))
 

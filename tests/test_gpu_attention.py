@@ -209,13 +209,19 @@ def test_shape_and_dtype_validation() -> None:
 
 @pytest.mark.parametrize("partition", (32, 512, 2048))
 @pytest.mark.parametrize("bs", (1, 16))
-def test_partition_sizes_including_global_table_fallback(partition, bs) -> None:
-    # bs=1 with 512/2048-token partitions needs more table entries than the LDS
-    # slice holds, so the kernel reads the table from global memory.
+def test_partition_caps_within_the_lds_table_slice(partition, bs) -> None:
+    # A wave's table slice lives in LDS (256 entries).  At bs=1 a 512- or
+    # 2048-token partition would need more entries, so the planner cuts the
+    # shares at the slice instead (254 blocks after alignment): every share,
+    # whatever the partition asks for, must fit, and the result must hold.
     _announce(f"partition {partition} bs {bs}")
     step = make_step(hq=28, hkv=4, d=128, bs=bs, dtype=torch.bfloat16, computed=[1200, 37, 2600],
                      layouts=_lin(1, 2, 1), seed=partition + bs)
-    _run_and_check(step, backend=lv.HipPagedAttentionBackend(partition_tokens=partition))
+    backend = lv.HipPagedAttentionBackend(partition_tokens=partition)
+    work = backend.create(step.cache, step.metadata).work_of(step.cache.layer_spec(step.layer_ids[0]))
+    unit = lv.native.decode_tile_tokens(lv.native.DTYPE_BF16, 128, work.col_tiles)
+    assert work.units_per_wave * unit <= min(partition, 254 * bs)
+    _run_and_check(step, backend=backend)
 
 
 

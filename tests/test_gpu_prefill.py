@@ -174,6 +174,51 @@ def test_split_k_tree_verification_head_sizes(dtype, head_size, waves) -> None:
     _check(step, backend=backend)
 
 
+SPAN_CASES = {
+    # name: (hq, hkv, d, bs, dtype, group prefix blocks, requests per group, decode rows between)
+    "c5_bf16": (12, 2, 128, 16, "bf16", (128,), 12, False),
+    "two_groups_bs12": (12, 2, 128, 12, "bf16", (60, 25), 6, True),
+    "fp16_d64": (16, 2, 64, 16, "fp16", (40, 9), 5, True),
+    "d256": (8, 2, 256, 16, "bf16", (33,), 6, False),
+    "d80_group4": (16, 4, 80, 16, "fp16", (20,), 7, True),
+}
+
+
+@pytest.mark.parametrize("waves", WAVES)
+@pytest.mark.parametrize("name", sorted(SPAN_CASES))
+def test_shared_prefix_spans_match_the_oracle(name, waves) -> None:
+    """Requests in groups sharing readonly prefixes (draft trees, causal
+    chunks, decode rows between the groups): the spans' prefix attention plus
+    each member's own keys, merged, equals the oracle, and equals the step
+    planned without spans."""
+
+    hq, hkv, d, bs, dtype, prefixes, per_group, decode_between = SPAN_CASES[name]
+    _announce(f"shared-prefix spans {name} waves={waves}")
+    rng = np.random.default_rng(len(name) * 31 + waves)
+    layouts, computed, groups = [], [], []
+    for g, blocks in enumerate(prefixes):
+        for i in range(per_group):
+            layouts.append(_tree(rng, 9) if i % 3 else _lin(int(rng.integers(3, 20)))[0])
+            computed.append(blocks * bs + int(rng.integers(0, 300)))
+            groups.append(g)
+        if decode_between:
+            layouts.append((-1,))
+            computed.append(int(rng.integers(1, 900)))
+            groups.append(-1)
+    step = make_step(hq=hq, hkv=hkv, d=d, bs=bs, dtype=DTYPES[dtype], computed=computed, layouts=layouts,
+                     prefix_groups=groups, group_prefix_blocks=prefixes, seed=len(name) + 900)
+    backend = lv.HipPagedAttentionBackend(prefill_waves=waves)
+    _, work = backend, backend.create(step.cache, step.metadata).work_of(step.cache.layer_spec(step.layer_ids[0]))
+    assert (work.prefill_units.numpy()[:, 0] < 0).any(), "the step must use shared-prefix spans"
+    out = _check(step, backend=lv.HipPagedAttentionBackend(prefill_waves=waves))
+    plain = lv.HipPagedAttentionBackend(prefill_waves=waves, shared_prefix=False)
+    ref = plain.create(step.cache, step.metadata).forward(step.layer_ids[0], step.query, step.key, step.value,
+                                                          scale=step.scale)
+    torch.cuda.synchronize()
+    max_tol, _ = tolerances(step.query.dtype)
+    assert (out.float() - ref.float()).abs().max().item() <= max_tol
+
+
 def test_split_k_c5_shape_shared_prefix() -> None:
     # BASELINE C5 at reduced batch: 8 requests share a 2048-token prefix,
     # private suffixes, 9-token trees (1 input + 8 drafts) at group 6.

@@ -297,6 +297,155 @@ def test_prefill_pieces_cover_every_wide_request_once(group, columns, resident, 
     assert plan.work(group, 4, 2048, 0).num_prefill_units == 0
 
 
+def _prefix_metadata(rng, groups, *, bs, decode_between=False):
+    """Requests in groups sharing a readonly prefix of ``shared`` blocks each
+    (one (n, shared, q_range) per group), draft trees of q queries; with
+    ``decode_between`` a one-query request follows every group."""
+
+    tables, computed, layouts, readonly = [], [], [], []
+    nxt = 0
+    for n, shared, (qlo, qhi) in groups:
+        prefix = list(range(nxt, nxt + shared))
+        nxt += shared
+        for _ in range(n):
+            c = shared * bs + int(rng.integers(0, 200))
+            q = int(rng.integers(qlo, qhi + 1))
+            parents = tuple([-1] + [int(rng.integers(0, i)) for i in range(1, q)])
+            need = -(-(c + q) // bs)
+            tables.append(tuple(prefix + list(range(nxt, nxt + need - shared))))
+            nxt += need - shared
+            computed.append(c)
+            layouts.append(lv.QueryLayout(parents))
+            readonly.append(shared)
+        if decode_between:
+            c = int(rng.integers(1, 300))
+            need = -(-(c + 1) // bs)
+            tables.append(tuple(range(nxt, nxt + need)))
+            nxt += need
+            computed.append(c)
+            layouts.append(lv.QueryLayout((-1,)))
+            readonly.append(0)
+    md = lv.PagedAttentionMetadata(block_tables=tuple(tables), num_computed_tokens=tuple(computed),
+                                   query_layouts=tuple(layouts), num_readonly_prefix_blocks=tuple(readonly))
+    return md, nxt
+
+
+def _check_prefill_coverage(md, work, *, group, columns, key_tokens, bs):
+    """Every (column, key) pair of every wide request is covered exactly once:
+    by its own units' pieces, or, below a span's prefix, by the pieces of the
+    span unit holding the column; every merge job names exactly those pieces'
+    partial slots; spans only cover blocks all their members list at the same
+    logical index, below every member's computed count.  Returns the spans
+    found (first token -> prefix tokens)."""
+
+    computed = np.asarray(md.num_computed_tokens)
+    q_start = np.asarray(md.query_start_loc)
+    flat = [b for t in md.block_tables for b in t]
+    units = work.prefill_units.numpy() if work.num_prefill_units else np.zeros((0, 8), np.int32)
+    jobs = work.prefill_jobs.numpy() if work.num_prefill_jobs else np.zeros((0, 8), np.int32)
+    own: dict[tuple[int, int], list] = {}
+    span_units: dict[int, list] = {}  # first token -> [(col0, n, kb, ke, slot)]
+    for req, c0, n, kb, ke, slot, table_off, t0 in units.tolist():
+        assert 0 < n <= columns and c0 % columns == 0 and kb % key_tokens == 0
+        if req < 0:
+            assert ke > kb and ke % key_tokens == 0 and slot >= 0
+            span_units.setdefault(t0, []).append((c0, n, kb, ke, slot, table_off))
+        else:
+            assert table_off == t0 == 0
+            kneed = computed[req] + (c0 + n - 1) // group + 1
+            own.setdefault((req, c0), []).append((kb, ke if ke else kneed, slot, n, kneed))
+    used_slots = [u[5] for u in units.tolist() if u[5] >= 0]
+    assert sorted(used_slots) == list(range(work.num_prefill_partial_slots))
+    job_of = {(int(j[0]), int(j[1])): j for j in jobs}
+    spans = {}
+    for (req, c0), pieces in own.items():
+        pieces.sort()
+        kneed = pieces[0][4]
+        assert pieces[-1][1] == kneed and all(a[1] == b[0] for a, b in zip(pieces, pieces[1:]))
+        job = job_of.get((req, c0 // columns))
+        start = pieces[0][0]
+        if start == 0 and len(pieces) == 1 and pieces[0][2] == -1:
+            assert job is None
+            continue
+        assert job is not None and list(job[2:4]) == [pieces[0][2], len(pieces)]
+        assert [p[2] for p in pieces] == list(range(job[2], job[2] + job[3]))
+        assert job[4] == q_start[req] and job[5] == md.query_lengths[req]
+        if start == 0:
+            assert job[6] == 0
+            continue
+        # Keys [0, start) come from the request's span.
+        k = int(job[7]) >> 24
+        v0 = int(job[7]) & 0xFFFFFF
+        t0 = int(q_start[req]) - v0 // group
+        assert v0 % group == 0 and t0 in span_units and k >= 1
+        su = sorted(span_units[t0])
+        assert start == max(x[3] for x in su) and start % key_tokens == 0 and start <= computed[req]
+        spans[t0] = start
+        assert len({x[5] for x in su}) == 1
+        table_off, blocks = su[0][5], -(-start // bs)
+        assert md.block_tables[req][:blocks] == tuple(flat[table_off : table_off + blocks])
+        base = int(job[6]) - 1
+        for c in range(c0, c0 + pieces[0][3]):
+            v = v0 + c
+            mine = sorted((x[2], x[3], x[4]) for x in su if x[0] <= v < x[0] + x[1])
+            assert mine[0][0] == 0 and mine[-1][1] == start and all(a[1] == b[0] for a, b in zip(mine, mine[1:]))
+            assert [x[2] for x in mine] == list(range(base + (v // columns) * k, base + (v // columns) * k + k))
+    for r, q in enumerate(md.query_lengths):
+        if q * group > 16:
+            cols = sorted(c for (rr, c0), p in own.items() if rr == r for c in range(c0, c0 + p[0][3]))
+            assert cols == list(range(q * group))
+    return spans
+
+
+@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("bs", (1, 12, 16))
+def test_shared_prefix_spans_cover_every_key_once(seed, bs) -> None:
+    """Shared-prefix spans (C5's shape and mixtures): coverage, merge slots,
+    and the span's blocks, against the metadata itself."""
+
+    rng = np.random.default_rng(700 + seed)
+    groups = [(int(rng.integers(1, 9)), int(rng.integers(0, 700 // bs + 2)), (3, 12)) for _ in range(3)]
+    md, nb = _prefix_metadata(rng, groups, bs=bs, decode_between=seed % 2 == 1)
+    plan = StepPlan(md, block_size=bs, device=CPU, num_blocks=nb)
+    for resident in (0, 256):
+        work = plan.work(6, 2, 2048, 128, 64, 1, 64, resident, 8, shared_prefix=True)
+        spans = _check_prefill_coverage(md, work, group=6, columns=128, key_tokens=64, bs=bs)
+        ref = plan.work(6, 2, 2048, 128, 64, 1, 64, resident, 8, shared_prefix=False)
+        assert _check_prefill_coverage(md, ref, group=6, columns=128, key_tokens=64, bs=bs) == {}
+        # A group over a prefix of two or more key tiles whose trees pack into
+        # fewer 128-column units than they take one by one forms a span.
+        r = 0
+        for n, shared, _ in groups:
+            cols = sum(md.query_lengths[i] * 6 for i in range(r, r + n))
+            if n >= 2 and shared * bs >= 2 * 64 and -(-cols // 128) < n:
+                assert spans.get(md.query_start_loc[r]) == shared * bs // 64 * 64
+            r += n + (seed % 2)
+
+
+def test_shared_prefix_span_shapes() -> None:
+    """C5's step: 32 trees of 9 queries at group 6 over a 2,032-token readonly
+    prefix form one span of 1,728 columns: 14 span units over the prefix's
+    1,984 tile-aligned tokens, each member's own units from there.  Requests
+    of a full unit each, or prefixes under two key tiles, form none."""
+
+    rng = np.random.default_rng(5)
+    md, nb = _prefix_metadata(rng, [(32, 127, (9, 9))], bs=16)
+    plan = StepPlan(md, block_size=16, device=CPU, num_blocks=nb)
+    work = plan.work(6, 2, 2048, 128, 64, 1, 64, 256, 8, shared_prefix=True)
+    spans = _check_prefill_coverage(md, work, group=6, columns=128, key_tokens=64, bs=16)
+    assert spans == {0: 1984}
+    units = work.prefill_units.numpy()
+    assert len({tuple(u[1:3]) for u in units if u[0] < 0}) == 14
+    md, nb = _prefix_metadata(rng, [(4, 127, (16, 16))], bs=16)  # 16 x 8 = 128 columns each
+    work = StepPlan(md, block_size=16, device=CPU, num_blocks=nb).work(8, 1, 2048, 128, 64, 1, 64, 256, 8,
+                                                                       shared_prefix=True)
+    assert not (work.prefill_units.numpy()[:, 0] < 0).any()
+    md, nb = _prefix_metadata(rng, [(8, 7, (9, 9))], bs=16)  # 112 shared tokens: under two tiles
+    work = StepPlan(md, block_size=16, device=CPU, num_blocks=nb).work(6, 2, 2048, 128, 64, 1, 64, 256, 8,
+                                                                       shared_prefix=True)
+    assert not (work.prefill_units.numpy()[:, 0] < 0).any()
+
+
 def test_prefill_split_fills_the_resident_workgroups() -> None:
     # C5-like: tree verification of 9 queries at group 6 = 54 columns, one
     # unit per request; 4 requests x 32 key tiles over 16 slots per kv head.
@@ -478,8 +627,8 @@ def _layer_shapes(bs: int) -> LayerShapes:
     one-query-per-head shape without them."""
 
     return LayerShapes((
-        (7, 4, bs, 128, 64, 1, 0, 0, 4, 1, 2048, 32, 1024, 16, 512, 256, 0, 16, 4, 4),
-        (1, 8, bs, 256, 64, 0, 0, 0, 1, 0, 2048, 32, 0, 0, 512, 0, 0, 16, 4, 4),
+        (7, 4, bs, 128, 64, 1, 0, 0, 4, 1, 2048, 32, 1024, 16, 512, 256, 0, 16, 4, 4, 1),
+        (1, 8, bs, 256, 64, 0, 0, 0, 1, 0, 2048, 32, 0, 0, 512, 0, 0, 16, 4, 4, 0),
     ))
 
 
@@ -523,7 +672,7 @@ def test_one_call_step_plan_equals_the_per_shape_plan(seed, small_buffer, monkey
             if ptr is not None:
                 assert base <= ptr and ptr + 4 * rows.numel() <= end and (ptr - base) % 64 == 0
     # A layer shape asked for later is planned on its own, from the records.
-    late = (4, 2, bs, 128, 64, 1, 0, 0, 4, 1, 2048, 32, 1024, 16, 512, 256, 0, 16, 4, 4)
+    late = (4, 2, bs, 128, 64, 1, 0, 0, 4, 1, 2048, 32, 1024, 16, 512, 256, 0, 16, 4, 4, 1)
     assert one.layer_work(late).num_prefill_units == ref.layer_work(late).num_prefill_units
 
 
