@@ -62,16 +62,22 @@ enum lvamd_dtype { LVAMD_F32 = 0, LVAMD_F16 = 1, LVAMD_BF16 = 2 };
  * + [0, pieces). */
 #define LVAMD_MERGE_FIELDS 8
 /* Number of int32 fields per prefill work unit:
- * (req, first column, columns, key_begin, key_end, partial_slot, table_off, q_start).
+ * (req, first column, columns, key_begin, key_end, partial_slot,
+ *  table_off, q_start, computed, q_len, vis_off, vis_words, b0, b1, b2, b3).
  * key_begin and key_end are multiples of lvamd_paged_prefill_key_tokens();
- * key_end 0 means up to the unit's last visible key.  A unit with partial_slot -1 covers
- * all its keys and writes out; the others write partials.  table_off and
- * q_start are read only for a span unit (req < 0): columns of the packed
- * queries from token q_start on (column c = token q_start + c / group, head
- * c % group) of requests whose tables all list the blocks at table_off over
- * keys [0, key_end), every one of those keys below every such query's
- * computed count; it always writes partials (key_end > 0). */
-#define LVAMD_PREFILL_FIELDS 8
+ * key_end 0 means up to the unit's last visible key.  A unit with
+ * partial_slot -1 covers all its keys and writes out; the others write
+ * partials.  Fields 6-11 are the request's (as in its row of the
+ * attention metadata), so the kernel reads nothing else per unit; b0..b3 are the physical ids of the logical
+ * blocks key_begin / block_size onwards when the unit's first key tile spans
+ * at most four blocks (0 past the table), else b0 = -1 (read from tables).
+ * A span unit (req < 0): columns of the packed queries from token q_start on
+ * (column c = token q_start + c / group, head c % group) of requests whose
+ * tables all list the blocks at table_off over keys [0, key_end), each of
+ * those keys below every such query's computed count; its fields read as a
+ * linear request with computed = key_end and q_len 0, and it always writes
+ * partials (key_end > 0). */
+#define LVAMD_PREFILL_FIELDS 16
 
 const char* lvamd_status_string(int status);
 
@@ -217,16 +223,16 @@ int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
  * computed are read from them, and each such token's row is written to its
  * pool slot by the unit that holds the token's own query (bit-exact copy).
  * When they are NULL the pool must already hold this step's K/V
- * (lvamd_kv_append).  req_meta is
- * [batch][LVAMD_REQ_FIELDS].  Replaces the prefill half of the same reference
- * functions as lvamd_paged_decode.
+ * (lvamd_kv_append).  Each unit record carries its request's fields
+ * (LVAMD_PREFILL_FIELDS), so no per-request table is passed.  Replaces the
+ * prefill half of the same reference functions as lvamd_paged_decode.
  */
 int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stride,
                         const void* new_key, int64_t new_key_token_stride, int64_t new_key_head_stride,
                         const void* new_value, int64_t new_value_token_stride, int64_t new_value_head_stride,
                         void* key_pool, void* value_pool,
                         void* out, int64_t out_token_stride, int64_t out_head_stride,
-                        const int32_t* req_meta, const int32_t* tables, const uint32_t* vis,
+                        const int32_t* tables, const uint32_t* vis,
                         const int32_t* units, int32_t num_units,
                         float* part_acc, float* part_ml, int64_t num_partial_slots,
                         int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t waves,

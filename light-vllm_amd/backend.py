@@ -142,7 +142,7 @@ class _LayerLaunch:
         if work.num_prefill_units:
             # lvamd_paged_prefill arguments after the output strides, up to the scale.
             self.prefill_args = (
-                plan.req_meta_ptr, plan.tables_ptr, plan.vis_ptr, work.units_ptr, work.num_prefill_units,
+                plan.tables_ptr, plan.vis_ptr, work.units_ptr, work.num_prefill_units,
                 pre_acc, pre_ml, work.num_prefill_partial_slots,
                 spec.num_kv_heads, group, spec.head_size, work.prefill_waves, block_size,
             )

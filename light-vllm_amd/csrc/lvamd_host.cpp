@@ -50,7 +50,7 @@ namespace {
 constexpr int kReqFields = 8;
 constexpr int kPieceFields = 16;
 constexpr int kMergeFields = 8;
-constexpr int kPrefillFields = 8;
+constexpr int kPrefillFields = 16;
 constexpr int kPieceBlocks = 5;  // first-tile block ids in piece fields 11..15
 constexpr int kTableSlice = 256;  // decode kernel's LDS copy of a piece's table slice
 
@@ -1235,10 +1235,36 @@ void build_prefill(const Requests& q, const PrefillParams& p, PrefillLists& out)
     // span unit's pieces always end at a tile boundary within the prefix.
     o[4] = (last && !un.span_unit) ? 0 : (int32_t)((un.first + x.t1) * p.key_tokens);
     o[5] = x.slot;
+    // The request's fields (a span unit reads as a linear request whose
+    // computed count is its key_end), then the first tile's block ids.
+    int64_t table_off, table_len;
     if (un.span_unit) {
       const Span& sp = spans[(size_t)un.span];
+      table_off = sp.table_off;
+      table_len = (sp.prefix + p.block_size - 1) / std::max<int64_t>(1, p.block_size);
       o[6] = (int32_t)sp.table_off;
       o[7] = (int32_t)sp.t0;
+      o[8] = o[4];
+      o[9] = 0;
+      o[10] = -1;
+      o[11] = 0;
+    } else {
+      const int32_t* m = q.row(un.req);
+      table_off = m[0];
+      table_len = m[1];
+      o[6] = m[0];
+      o[7] = m[4];
+      o[8] = m[2];
+      o[9] = m[3];
+      o[10] = m[5];
+      o[11] = m[6];
+    }
+    o[12] = -1;
+    if (p.ids != nullptr && p.block_size > 0) {
+      const int64_t k0 = o[3], lb0 = k0 / p.block_size, lb1 = (k0 + p.key_tokens - 1) / p.block_size;
+      if (lb1 - lb0 < 4) {
+        for (int b = 0; b < 4; ++b) o[12 + b] = lb0 + b < table_len ? p.ids[table_off + lb0 + b] : 0;
+      }
     }
   }
 }

@@ -364,7 +364,7 @@ const char* lvamd_status_string(int status) {
   }
 }
 
-int lvamd_abi_version(void) { return 14; }
+int lvamd_abi_version(void) { return 15; }
 
 int lvamd_stage_upload(void* device_dst, const void* pinned_src, int64_t bytes, void* event, lvamd_stream_t stream) {
   if (bytes < 0 || (bytes > 0 && (!device_dst || !pinned_src))) return LVAMD_ERR_INVALID_ARGUMENT;

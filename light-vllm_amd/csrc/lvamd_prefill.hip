@@ -93,7 +93,6 @@ struct PrefillArgs {
   void* v_pool;
   void* out;
   int64_t out_tok_stride, out_head_stride;
-  const int32_t* __restrict__ req_meta;  // [B][LVAMD_REQ_FIELDS]
   const int32_t* __restrict__ tables;
   const uint32_t* __restrict__ vis;
   const int32_t* __restrict__ units;     // [n][LVAMD_PREFILL_FIELDS]
@@ -125,22 +124,16 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
   const int G = a.group;
   const int unit = blockIdx.x / Hkv;
   const int kvh = blockIdx.x - unit * Hkv;
+  // The unit record carries everything the unit needs, so the first tile's
+  // loads depend on one load (the record) only: its request's fields (a span
+  // unit, over keys every query of the span sees, reads as a linear request
+  // whose computed count is its key_end: no tile masked, nothing appended)
+  // and, when the piece's first tile spans at most four blocks, their ids.
   const int32_t* u = a.units + (int64_t)unit * LVAMD_PREFILL_FIELDS;
-  const int req = u[0], col0 = u[1], ncols = u[2], key_begin = u[3], key_end = u[4], slot = u[5];
-  // A span unit (req < 0) attends the packed queries of requests sharing a
-  // prefix to its keys [key_begin, key_end): its record carries the shared
-  // table's offset and the first query token.  Every key it reads lies below
-  // every query's computed count, so it is treated as a linear request whose
-  // computed count is key_end: no tile is masked, nothing is appended.
-  const bool span = req < 0;
-  const int32_t* rm = a.req_meta + (int64_t)(span ? 0 : req) * LVAMD_REQ_FIELDS;
-  const int table_off = span ? u[6] : rm[0];
-  const int computed = span ? key_end : rm[2];
-  const int q_len = span ? 0 : rm[3];
-  const int q_start = span ? u[7] : rm[4];
-  const int vis_off = span ? -1 : rm[5];
-  const int vis_words = span ? 0 : rm[6];
-  const int col_end = col0 + ncols;  // exclusive, <= q_len * G
+  const int col0 = u[1], ncols = u[2], key_begin = u[3], key_end = u[4], slot = u[5];
+  const int table_off = u[6], q_start = u[7], computed = u[8], q_len = u[9], vis_off = u[10], vis_words = u[11];
+  const int first_blocks[4] = {u[12], u[13], u[14], u[15]};  // -1: take them from the table
+  const int col_end = col0 + ncols;  // exclusive: <= q_len * G (a span unit: its packed columns)
   // Keys the unit needs: up to its last query's position, within the piece's
   // key range [key_begin, key_end) (key_begin a multiple of KT; key_end 0 =
   // no bound).  Tiles are numbered from position 0.
@@ -180,6 +173,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
   };
   auto logical_block = [&](int pos) -> int { return a.bs_shift >= 0 ? (pos >> a.bs_shift) : (pos / bs); };
   auto load_entry = [&](int t) -> int { return table[logical_block(key_pos(t))]; };
+  // Tile 0's entry from the record (its rows lie in the tile's blocks, the
+  // first of which is logical block key_begin / block_size).
+  auto first_entry = [&]() -> int {
+    if (first_blocks[0] < 0) return load_entry(0);
+    const int k = logical_block(key_pos(0)) - logical_block(key_begin);
+    return k == 0 ? first_blocks[0] : k == 1 ? first_blocks[1] : k == 2 ? first_blocks[2] : first_blocks[3];
+  };
   // Loads tile t's row; returns the row's pool slot when this thread must
   // append it, else -1.
   auto load_tile = [&](int t, int te, uint4 (&kr)[LPT], uint4 (&vr)[LPT]) -> int {
@@ -254,6 +254,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
   const int full_tiles = (vis_off >= 0 ? computed : computed + col0 / G + 1) / KT;
   const bool tree = vis_off >= 0;
   const float c_log2 = a.scale_log2;
+  // A tree of at most 32 queries has one ancestor word per query: each
+  // column's word is loaded once here instead of per score in the masks.
+  const bool tree_word = tree && vis_words == 1;
+  uint32_t vrow[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) vrow[ct] = tree_word ? a.vis[vis_off + qi[ct]] : 0u;
 
   float m_run[CT], l_run[CT];  // m_run in the scaled log2 domain
   f32x4 acc[CT][NT];
@@ -312,7 +318,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
               vis = pos <= computed + qi[ct];
             } else {
               const int j = pos - computed;
-              vis = j < 0 || (j < q_len && ((a.vis[vis_off + qi[ct] * vis_words + (j >> 5)] >> (j & 31)) & 1u));
+              const uint32_t word =
+                  tree_word ? vrow[ct] : (j >= 0 && j < q_len ? a.vis[vis_off + qi[ct] * vis_words + (j >> 5)] : 0u);
+              vis = j < 0 || (j < q_len && ((word >> (j & 31)) & 1u));
             }
             if (!vis) st[ct][s][r] = -INFINITY;
           }
@@ -375,12 +383,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
   // (stored to the other LDS buffer after the compute), tile t+2's loads are
   // in flight and tile t+3's table entries are being fetched.  Two register
   // sets alternate statically (a run-time swap would force waits).
-  // Prologue in two round trips: the table entries of tiles 0 and 1, then
-  // both tiles' loads (and tile 2's entries); tile 0 goes to LDS.
+  // Prologue: tile 0's loads issue as soon as the record is in (its block
+  // ids come with it, or one table round trip when they do not), tile 1's
+  // after its table entries; tile 2's entries follow; tile 0 goes to LDS.
   int ea = 0, eb = 0;
   int wa = -1, wb = -1;  // pool slots to append the staged rows at (-1: none)
   uint4 ka[LPT], va[LPT], kb[LPT], vb[LPT];
-  eb = load_entry(0);
+  eb = first_entry();
   if (ntiles > 1) ea = load_entry(1);
   wb = load_tile(0, eb, kb, vb);
   if (ntiles > 1) wa = load_tile(1, ea, ka, va);
@@ -516,7 +525,7 @@ extern "C" int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_
                                    const void* new_value, int64_t new_value_token_stride,
                                    int64_t new_value_head_stride, void* key_pool, void* value_pool,
                                    void* out, int64_t out_token_stride, int64_t out_head_stride,
-                                   const int32_t* req_meta, const int32_t* tables, const uint32_t* vis,
+                                   const int32_t* tables, const uint32_t* vis,
                                    const int32_t* units, int32_t num_units,
                                    float* part_acc, float* part_ml, int64_t num_partial_slots,
                                    int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t waves,
@@ -526,7 +535,7 @@ extern "C" int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_
   if (waves != 4 && waves != 8) return LVAMD_ERR_INVALID_ARGUMENT;
   if (num_units == 0) return LVAMD_OK;
   if (!prefill_supported(dtype, head_size)) return LVAMD_ERR_UNSUPPORTED;
-  if (!q || !key_pool || !value_pool || !out || !req_meta || !tables || !vis || !units)
+  if (!q || !key_pool || !value_pool || !out || !tables || !vis || !units)
     return LVAMD_ERR_INVALID_ARGUMENT;
   if (num_partial_slots > 0 && (!part_acc || !part_ml)) return LVAMD_ERR_WORKSPACE;
   const int es = dtype_size(dtype);
@@ -555,7 +564,6 @@ extern "C" int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_
   a.out = out;
   a.out_tok_stride = out_token_stride;
   a.out_head_stride = out_head_stride;
-  a.req_meta = req_meta;
   a.tables = tables;
   a.vis = vis;
   a.units = units;

@@ -19,7 +19,7 @@ from pathlib import Path
 from light_vllm_amd import errors
 
 LIB_NAME = "liblvamd_hip.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
@@ -28,7 +28,7 @@ DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 REQ_FIELDS = 8
 PIECE_FIELDS = 16
 MERGE_FIELDS = 8
-PREFILL_FIELDS = 8
+PREFILL_FIELDS = 16
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -62,7 +62,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "lvamd_paged_prefill": (
         ctypes.c_int,
-        [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i32, _p, _p, _i64,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _i32, _p, _p, _i64,
          _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p],
     ),
     "lvamd_paged_prefill_unit_columns": (ctypes.c_int, [_i32, _i32]),

@@ -257,8 +257,13 @@ def test_prefill_pieces_cover_every_wide_request_once(group, columns, resident, 
     units = work.prefill_units.numpy() if work.num_prefill_units else np.zeros((0, 8), np.int32)
     spans: dict[tuple[int, int], list] = {}
     work_prev = None
-    for req, c0, n, kb, ke, slot, z0, z1 in units:
-        assert 0 < n <= columns and c0 % columns == 0 and z0 == z1 == 0
+    table_off = np.concatenate(([0], np.cumsum([len(t) for t in md.block_tables])))
+    for req, c0, n, kb, ke, slot, toff, qs, comp, ql, voff, vwords, *first in units:
+        assert 0 < n <= columns and c0 % columns == 0
+        assert (toff, qs, comp, ql, vwords) == (table_off[req], md.query_start_loc[req], computed[req],
+                                                md.query_lengths[req], 0) and voff == -1
+        lb0, table = kb // 16, md.block_tables[req]
+        assert first == [table[lb0 + b] if lb0 + b < len(table) else 0 for b in range(4)]
         kneed = computed[req] + (c0 + n - 1) // group + 1
         end = ke if ke else kneed
         assert kb % key_tokens == 0 and kb < end <= kneed and (ke == 0 or ke % key_tokens == 0)
@@ -345,13 +350,24 @@ def _check_prefill_coverage(md, work, *, group, columns, key_tokens, bs):
     jobs = work.prefill_jobs.numpy() if work.num_prefill_jobs else np.zeros((0, 8), np.int32)
     own: dict[tuple[int, int], list] = {}
     span_units: dict[int, list] = {}  # first token -> [(col0, n, kb, ke, slot)]
-    for req, c0, n, kb, ke, slot, table_off, t0 in units.tolist():
+    starts = np.concatenate(([0], np.cumsum([len(t) for t in md.block_tables])))
+    for req, c0, n, kb, ke, slot, table_off, t0, comp, ql, voff, vwords, *first in units.tolist():
         assert 0 < n <= columns and c0 % columns == 0 and kb % key_tokens == 0
+        lb0, lb1 = kb // bs, (kb + key_tokens - 1) // bs
+        if lb1 - lb0 >= 4:  # else the first tile's block ids ride in the record
+            assert first[0] == -1
         if req < 0:
             assert ke > kb and ke % key_tokens == 0 and slot >= 0
+            assert (comp, ql, voff, vwords) == (ke, 0, -1, 0)
+            if lb1 - lb0 < 4:  # the blocks the piece's first tile reads
+                used = range(lb0, min(lb1, (ke - 1) // bs) + 1)
+                assert [first[b - lb0] for b in used] == [flat[table_off + b] for b in used]
             span_units.setdefault(t0, []).append((c0, n, kb, ke, slot, table_off))
         else:
-            assert table_off == t0 == 0
+            assert (table_off, t0, comp, ql) == (starts[req], q_start[req], computed[req], md.query_lengths[req])
+            if lb1 - lb0 < 4:
+                table = md.block_tables[req]
+                assert first == [table[lb0 + b] if lb0 + b < len(table) else 0 for b in range(4)]
             kneed = computed[req] + (c0 + n - 1) // group + 1
             own.setdefault((req, c0), []).append((kb, ke if ke else kneed, slot, n, kneed))
     used_slots = [u[5] for u in units.tolist() if u[5] >= 0]
@@ -507,7 +523,7 @@ def test_library_loads_and_exports_every_header_function() -> None:
     # shape takes this step's K/V (fused append); K without V is refused.
     x = ctypes.c_void_p(16)  # (never dereferenced: the checks run first)
     prefill = lambda nk, nv, waves: lib.lvamd_paged_prefill(  # noqa: E731
-        x, 0, 0, nk, 0, 0, nv, 0, 0, x, x, x, 0, 0, x, x, x, x, 1, None, None, 0, 2, 7, 128, waves, 16,
+        x, 0, 0, nk, 0, 0, nv, 0, 0, x, x, x, 0, 0, x, x, x, 1, None, None, 0, 2, 7, 128, waves, 16,
         ctypes.c_float(0.1), 2, None)
     assert prefill(None, None, 5) == -1
     assert prefill(x, None, 8) == -1
