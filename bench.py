@@ -483,8 +483,9 @@ def measured_traffic(summary_path: Path = TRAFFIC_SUMMARY) -> dict | None:
     """HBM bytes per launch of a kernel from the committed rocprofv3 counter runs.
 
     FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the kernel, each scaled
-    by what the same counter reads for a plain copy of known size (the
-    summary file records both runs and the factors).
+    by what the same counter reads for kernels of known byte counts (the HBM
+    read probe, which reads exactly 2 GiB, and a plain 1 GiB copy; the
+    summary file records the runs and the factors).
     """
 
     if not summary_path.exists():
