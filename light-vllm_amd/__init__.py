@@ -25,6 +25,7 @@ from light_vllm_amd.layout import (  # noqa: E402
     semantic_positions,
 )
 from light_vllm_amd.metadata import PagedAttentionMetadata  # noqa: E402
+from light_vllm_amd.prefix_cow import SharedPrefix, copy_commands, share_prefix  # noqa: E402
 from light_vllm_amd.paged_cache import (  # noqa: E402
     PagedKVCache,
     PagedKVCacheConfig,
@@ -62,13 +63,16 @@ __all__ = [
     "PagedKVWriteMapping",
     "PagedLayerCache",
     "QueryLayout",
+    "SharedPrefix",
     "append_draft_layout",
+    "copy_commands",
     "hip_block_copy",
     "hip_compact",
     "kv_cache_bytes_per_block",
     "linear_query_layout",
     "query_visibility",
     "semantic_positions",
+    "share_prefix",
 ]
 
 
