@@ -1757,11 +1757,21 @@ PyObject* compact_pairs(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     const int64_t required = (computed + reserved + bs - 1) / bs;
     const int32_t* ids = nullptr;
     Py_ssize_t n = 0;
-    if (proven.proven_blocks == num_blocks && r < (Py_ssize_t)proven.rows.size() && proven.rows[(size_t)r] == ids_obj) {
-      // The very tuple this step's metadata listed for this request, whose
-      // ids the step's table check proved in range and unique in the row.
+    // The very tuple this step's metadata listed for some request (looked
+    // for from this request's index on: a step's compacts usually come in
+    // table order), whose ids the step's table check proved in range and
+    // unique in the row.
+    int64_t row = -1;
+    if (proven.proven_blocks == num_blocks && PyTuple_CheckExact(ids_obj)) {
+      const size_t nrows = proven.rows.size();
+      for (size_t k = 0; k < nrows && row < 0; ++k) {
+        const size_t i = ((size_t)r + k) % nrows;
+        if (proven.rows[i] == ids_obj) row = (int64_t)i;
+      }
+    }
+    if (row >= 0) {
       n = PyTuple_GET_SIZE(ids_obj);
-      ids = proven.values.data() + proven.offsets[(size_t)r];
+      ids = proven.values.data() + proven.offsets[(size_t)row];
       if (n != required) { rule = 6; break; }
     } else {
       PyObject* tseq = PySequence_Fast(ids_obj, "block_ids must be a sequence");

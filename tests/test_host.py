@@ -793,6 +793,37 @@ def test_native_compact_rules_raise_the_oracles_message(seed) -> None:
         assert moved.tolist() == [sum(a != b for a, b in pairs)]
 
 
+def test_compact_reuses_only_tables_the_step_proved() -> None:
+    """A compact request whose block table is the very tuple the step's
+    metadata listed, after the step's table check passed, skips the id
+    checks (in any request order); a tuple the metadata listed but no table
+    check proved is checked in full."""
+
+    from light_vllm_amd.paged_cache import PagedKVCacheConfig, _compact_plan
+
+    bs, nb = 4, 64
+    tables = ((0, 1, 2), (3, 4, 5), (6, 7, 8, 9))
+    computed = (6, 7, 10)
+    layouts = tuple(lv.QueryLayout((-1, 0, 0)) for _ in tables)
+    md = lv.PagedAttentionMetadata(block_tables=tables, num_computed_tokens=computed, query_layouts=layouts)
+    config = PagedKVCacheConfig(num_blocks=nb, block_size=bs, device=CPU)
+    requests = [dict(block_ids=t, num_computed_tokens=c, num_query_tokens=3, num_reserved_query_tokens=3,
+                     retained_query_indices=(0, 2)) for t, c in zip(md.block_tables, computed)]
+    plain = _compact_plan(config, [dict(r, block_ids=list(r["block_ids"])) for r in requests])
+    StepPlan(md, block_size=bs, device=CPU, num_blocks=nb)  # the step's table check
+    for order in (requests, requests[::-1], requests[1:2]):
+        got = _compact_plan(config, order)
+        want = _compact_plan(config, [dict(r, block_ids=list(r["block_ids"])) for r in order])
+        assert all((a == b).all() for a, b in zip(got, want))
+    assert all((a == b).all() for a, b in zip(_compact_plan(config, requests), plain))
+    # Flattened by a new metadata object but never proven: an id past the
+    # pool must still be caught.
+    bad = ((0, 1, 2), (3, 4, 99), (6, 7, 8, 9))
+    lv.PagedAttentionMetadata(block_tables=bad, num_computed_tokens=computed, query_layouts=layouts)
+    with pytest.raises(lv.KVCacheError, match="invalid physical block"):
+        _compact_plan(config, [dict(requests[1], block_ids=bad[1])])
+
+
 def test_compact_many_batch_rule_and_missing_arguments() -> None:
     from types import SimpleNamespace
 
