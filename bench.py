@@ -671,7 +671,7 @@ def run_c3(args, device) -> int:
     k = torch.randn((t, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
     v = torch.randn((t, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
     scale = 1.0 / math.sqrt(cfg.d)
-    backend = lv.HipPagedAttentionBackend(decode_col_tiles=args.col_tiles)
+    backend = lv.HipPagedAttentionBackend(decode_col_tiles=args.col_tiles, prefill_order=args.prefill_order)
     print(f"[bench] C3: {cfg.n_prefill} x {cfg.chunk} prefill + {cfg.n_decode} decode, T={t}", file=sys.stderr, flush=True)
     ms, host_ms = _time_steps(
         lambda i: backend.create(caches[i % len(caches)], md).forward("layer0", q, k, v, scale=scale),
@@ -804,7 +804,7 @@ class C5:
     seed = 5005
 
 
-def build_c5(device, col_tiles=None):
+def build_c5(device, col_tiles=None, prefill_order="auto"):
     """The C5 workload: pools, metadata, step inputs and the step's three parts."""
 
     cfg = C5
@@ -848,7 +848,7 @@ def build_c5(device, col_tiles=None):
     k = torch.randn((t, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
     v = torch.randn((t, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
     scale = 1.0 / math.sqrt(cfg.d)
-    backend = lv.HipPagedAttentionBackend(decode_col_tiles=col_tiles)
+    backend = lv.HipPagedAttentionBackend(decode_col_tiles=col_tiles, prefill_order=prefill_order)
     compacts = [dict(block_ids=tables[r], num_computed_tokens=computed[r], num_query_tokens=q_len,
                      num_reserved_query_tokens=q_len, retained_query_indices=accepted[r],
                      num_readonly_prefix_blocks=shared_blocks - 1) for r in range(cfg.batch)]
@@ -886,7 +886,7 @@ def build_c5(device, col_tiles=None):
 
 
 def run_c5(args, device) -> int:
-    w = build_c5(device, args.col_tiles)
+    w = build_c5(device, args.col_tiles, args.prefill_order)
     cfg, cache, q, tables, computed, layouts = w.cfg, w.cache, w.q, w.tables, w.computed, w.layouts
     suffix, q_len, accepted, scale = w.suffix, w.q_len, w.accepted, w.scale
     cow, attend, compact = w.cow, w.attend, w.compact
@@ -964,6 +964,8 @@ def main() -> int:
                         help="cap on the tokens one decode wave handles (default: spread over all resident waves)")
     parser.add_argument("--col-tiles", type=int, choices=(1, 4), default=None,
                         help="fix the decode kernel's column tiles per wave (default: the planner's choice)")
+    parser.add_argument("--prefill-order", choices=("auto", "grouped", "plain"), default="auto",
+                        help="per-XCD order of the prefill grid (C3, C5; default: the planner's choice)")
     parser.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5"), default="c2",
                         help="BASELINE config (default c2, the headline metric); the others report their own metric")
     args = parser.parse_args()

@@ -84,6 +84,12 @@ const char* lvamd_status_string(int status);
 /* Library version, for the Python loader's compatibility check. */
 int lvamd_abi_version(void);
 
+/* XCDs (accelerator complex dies, each with its own L2) of the current
+ * device, or LVAMD_ERR_RUNTIME.  The planner orders the prefill grid per XCD
+ * (workgroup b runs on XCD b % count).  A device query with no counterpart in
+ * the reference. */
+int lvamd_xcd_count(void);
+
 /*
  * Slot-mapped KV append:  key_pool[slots[t]] = key[t], value_pool[slots[t]] = value[t]
  * for every token t with slots[t] >= 0 (a negative slot marks an inactive token
@@ -206,19 +212,21 @@ int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
 /*
  * Chunked-prefill paged attention for query runs of more than one column
  * tile (prompt chunks, tree verification; bf16 / fp16, head sizes 64, 80, 96,
- * 128, 256): one 256-thread workgroup per (unit, kv head); a unit
+ * 128, 256): one workgroup per (unit, kv head); a unit
  * (units [num_units][LVAMD_PREFILL_FIELDS]) is a run of MFMA columns of one
  * request over a key range, a column being a (query, head-in-group) pair,
  * column c = query (c / group), head (c % group).  K/V tiles (64 tokens up to
- * head size 128, else 32) are gathered through the block table into LDS and
- * shared by the workgroup's waves; QK^T and PV on MFMA 16x16x32, fp32 online
+ * head size 128, else 32) are copied through the block table straight into
+ * LDS (direct loads, double-buffered) and shared by the workgroup's waves; QK^T and PV on MFMA 16x16x32, fp32 online
  * softmax.  waves (4 or 8) picks the workgroup shape for the same unit: four
  * waves of two 16-column tiles or eight waves of one (8 only where
  * lvamd_paged_prefill_waves_built says so).  Units with a partial slot write fp32 partials to part_acc
  * [slots][num_kv_heads][unit columns][head_size] and part_ml
  * [slots][num_kv_heads][unit columns][2]; lvamd_paged_attention_merge with
  * col_tiles = unit columns / 16 combines them.
- * Append (waves == 8 only): when new_key / new_value are given
+ * A record with zero columns (field 2) is padding and does nothing (the
+ * planner orders units per XCD).
+ * Append: when new_key / new_value are given
  * ([tokens][num_kv_heads][D] with the given strides), keys at positions >=
  * computed are read from them, and each such token's row is written to its
  * pool slot by the unit that holds the token's own query (bit-exact copy).

@@ -16,12 +16,10 @@ decode / prefill work lists go to the GPU in one non-blocking copy.
    (paged_attention.py:226-247) plus the dtype/device rule of the Triton
    backend (triton_paged_attention.py:475-478);
 2. attends with write-before-attend semantics: the stream-K decode kernel
-   (short query runs) and the MFMA prefill kernel (long ones) in its 8-wave
-   shape read this step's K/V from the inputs and append their own requests'
-   tokens to their pool slots themselves, and a merge kernel combines split
-   partials; a step whose prefill rows take the 4-wave shape appends first
-   (HIP ``lvamd_kv_append``), and with ``rotary=`` one rotary-append launch
-   writes the pool first.  Everything is on the current stream with no host
+   (short query runs) and the MFMA prefill kernel (long ones) read this
+   step's K/V from the inputs and append their own requests' tokens to their
+   pool slots themselves, and a merge kernel combines split partials; with
+   ``rotary=`` one rotary-append launch writes the pool first.  Everything is on the current stream with no host
    synchronisation.
 """
 
@@ -34,7 +32,7 @@ from torch import Tensor
 
 from light_vllm_amd import errors, native
 from light_vllm_amd.metadata import PagedAttentionMetadata
-from light_vllm_amd.paged_cache import current_stream, dtype_code, hip_append, hip_append_rotary
+from light_vllm_amd.paged_cache import current_stream, dtype_code, hip_append_rotary
 from light_vllm_amd.plan import DECODE_MAX_COLUMNS, PREFILL_MIN_TILES, UNIT_TOKENS, LayerShapes, Staging, StepPlan
 
 SUPPORTED_HEAD_SIZES = (32, 64, 80, 96, 128, 256)
@@ -154,6 +152,8 @@ class _LayerLaunch:
 
 
 _NO_APPEND = (None, 0, 0, None, 0, 0)
+# Per-XCD prefill order policies (the planner's kernel fact).
+PREFILL_ORDERS = {"auto": 0, "grouped": 1, "plain": 2}
 
 
 class HipPagedAttention:
@@ -220,15 +220,10 @@ class HipPagedAttention:
             query = hip_append_rotary(self._cache, layer_id, query, key, value, rotary, plan.slots_ptr,
                                       plan.num_tokens)
             new_kv = _NO_APPEND
-        elif launch.prefill_args is not None and launch.work.prefill_waves != 8:
-            # The 4-wave prefill shape reads this step's K/V from the pool, so
-            # the whole step is appended first.
-            hip_append(self._cache, layer_id, key, value, plan.slots_ptr, plan.num_tokens)
-            new_kv = _NO_APPEND
         else:
-            # The decode kernel and the 8-wave prefill shape append their own
-            # requests' tokens (fused append): they read this step's keys and
-            # values from the inputs and write each token's row to its slot.
+            # The decode and prefill kernels append their own requests'
+            # tokens (fused append): they read this step's keys and values
+            # from the inputs and write each token's row to its slot.
             if not _rows_aligned(key):
                 key = key.contiguous()
             if not _rows_aligned(value):
@@ -364,7 +359,7 @@ class HipPagedAttentionBackend:
     def __init__(
         self, *, use_prefill_kernel: bool = True, partition_tokens: int | None = None,
         decode_col_tiles: int | None = None, split_prefill: bool = True, prefill_waves: int | None = None,
-        shared_prefix: bool = True,
+        shared_prefix: bool = True, prefill_order: str = "auto",
     ) -> None:
         """``use_prefill_kernel=False`` sends every request through the decode
         kernel; ``partition_tokens`` caps the tokens one decode wave handles (a
@@ -376,7 +371,10 @@ class HipPagedAttentionBackend:
         prefill workgroup shape instead of the planner's per-step choice (8
         falls back to 4 where it is not built); ``shared_prefix=False`` turns
         off the shared-prefix spans (every prefill request then streams its
-        whole prefix itself)."""
+        whole prefix itself); ``prefill_order`` places each request's prefill
+        units on one XCD (so they share its L2): ``"auto"`` when the
+        planner's simulated packing of the resident workgroups is no slower,
+        ``"grouped"`` always, ``"plain"`` never (heaviest first only)."""
 
         native.load()
         native.host()
@@ -386,6 +384,8 @@ class HipPagedAttentionBackend:
             raise ValueError(f"decode_col_tiles must be one of {native.DECODE_COL_TILES}")
         if prefill_waves not in (None, 4, 8):
             raise ValueError("prefill_waves must be 4 or 8")
+        if prefill_order not in PREFILL_ORDERS:
+            raise ValueError(f"prefill_order must be one of {tuple(PREFILL_ORDERS)}")
         self.workspace = _Workspace()
         self._use_prefill = use_prefill_kernel
         self._partition_tokens = partition_tokens
@@ -393,6 +393,7 @@ class HipPagedAttentionBackend:
         self._split_prefill = split_prefill
         self._shared_prefix = shared_prefix
         self._prefill_waves = prefill_waves
+        self._prefill_order = PREFILL_ORDERS[prefill_order]
         self._staging: dict[torch.device, Staging] = {}
         self._facts: dict[tuple, tuple[int, ...]] = {}
         # cache -> kernel facts of its layer shapes (dropped with the cache).
@@ -425,6 +426,7 @@ class HipPagedAttentionBackend:
                 native.prefill_resident_units(code, d, 4) if columns else 0,
                 native.prefill_resident_units(code, d, 8) if wide else 0,
                 self._partition_tokens or 0, DECODE_MAX_COLUMNS, 4, PREFILL_MIN_TILES, int(self._shared_prefix),
+                native.xcd_count() if columns else 0, self._prefill_order,
             )
             self._facts[key] = found
         return found

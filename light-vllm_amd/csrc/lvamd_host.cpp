@@ -41,7 +41,10 @@
 #include <climits>
 #include <cstdint>
 #include <cstring>
+#include <functional>
 #include <limits>
+#include <numeric>
+#include <unordered_map>
 #include <vector>
 
 namespace {
@@ -51,6 +54,9 @@ constexpr int kReqFields = 8;
 constexpr int kPieceFields = 16;
 constexpr int kMergeFields = 8;
 constexpr int kPrefillFields = 16;
+// Field 0 of a padding record of the prefill grid (its column count, field
+// 2, is zero: the kernel does nothing for it).
+constexpr int32_t kPadRecord = INT32_MAX;
 constexpr int kPieceBlocks = 5;  // first-tile block ids in piece fields 11..15
 constexpr int kTableSlice = 256;  // decode kernel's LDS copy of a piece's table slice
 
@@ -1062,6 +1068,9 @@ struct PrefillParams {
   const int32_t* ids = nullptr;  // flat block tables, for shared-prefix spans (null: no spans)
   int64_t block_size = 0;
   bool spans = false;
+  int64_t kv_heads = 1, xcds = 0;  // the device's XCDs (0 or 1: no per-XCD order)
+  int64_t resident_per_head = 0;   // resident workgroups / kv heads (0: unknown)
+  int64_t order = 0;               // per-XCD order: 0 the faster (simulated), 1 grouped, 2 plain
 };
 
 // A prefill unit: columns [col0, col0 + cols) of request req over key tiles
@@ -1167,6 +1176,74 @@ std::vector<Unit> prefill_units_of(const Requests& q, const PrefillParams& p, co
   return units;
 }
 
+// Per-XCD order of the prefill grid.  The hardware hands workgroup b to XCD
+// b % X (X XCDs, each with its own L2), and workgroup b is (unit position
+// u = b / H, kv head b % H) for H kv heads, so position u runs kv head h on
+// XCD (u H + h) % X.  That XCD depends on h and on u modulo
+// P = X / gcd(H, X) only: positions congruent modulo P form a bin whose
+// units, per kv head, all run on one XCD and share its L2.  A request's
+// units read the same keys, so the planner keeps each request (a span
+// unit's group: its span) in as few bins as the dispatch order allows.
+int64_t xcd_bins(const PrefillParams& p) {
+  if (p.xcds <= 1 || p.kv_heads <= 0) return 1;
+  return p.xcds / std::gcd(p.kv_heads, p.xcds);
+}
+
+// Bins of near-equal work: whole groups, heaviest first, each to the
+// lightest bin; then single records move from the heaviest bin to the
+// lightest while that lowers the heaviest by more than 1/32 of a bin.
+void assign_bins(const std::vector<int64_t>& group_of, const std::vector<int64_t>& work, int64_t nbins,
+                 std::vector<int64_t>& bin_of) {
+  std::unordered_map<int64_t, int64_t> gwork;
+  for (size_t k = 0; k < work.size(); ++k) gwork[group_of[k]] += work[k];
+  std::vector<std::pair<int64_t, int64_t>> groups(gwork.begin(), gwork.end());  // (group, work)
+  std::sort(groups.begin(), groups.end(), [](const auto& a, const auto& b) {
+    return a.second != b.second ? a.second > b.second : a.first < b.first;
+  });
+  std::vector<int64_t> load((size_t)nbins, 0);
+  std::unordered_map<int64_t, int64_t> gbin;
+  for (const auto& [g, w] : groups) {
+    const size_t b = (size_t)(std::min_element(load.begin(), load.end()) - load.begin());
+    gbin[g] = (int64_t)b;
+    load[b] += w;
+  }
+  for (size_t k = 0; k < work.size(); ++k) bin_of[k] = gbin[group_of[k]];
+  const int64_t total = std::accumulate(load.begin(), load.end(), (int64_t)0);
+  for (size_t iter = 0; iter < work.size(); ++iter) {
+    const size_t hi = (size_t)(std::max_element(load.begin(), load.end()) - load.begin());
+    const size_t lo = (size_t)(std::min_element(load.begin(), load.end()) - load.begin());
+    const int64_t gap = load[hi] - load[lo];
+    if (gap * 32 * nbins <= total) break;
+    int64_t best = -1;
+    for (size_t k = 0; k < work.size(); ++k)
+      if (bin_of[k] == (int64_t)hi && work[k] < gap && (best < 0 || work[k] > work[(size_t)best])) best = (int64_t)k;
+    if (best < 0) break;
+    bin_of[(size_t)best] = (int64_t)lo;
+    load[hi] -= work[(size_t)best];
+    load[lo] += work[(size_t)best];
+  }
+}
+
+// The latest finish over the bins when each bin's records (position k of
+// ``order`` in bin k % nbins; -1: padding) start in order on ``slots``
+// workgroup slots, each on the first slot to free (the dispatcher's rule).
+int64_t packed_makespan(const std::vector<int64_t>& order, const std::vector<int64_t>& work, int64_t nbins,
+                        int64_t slots) {
+  int64_t worst = 0;
+  std::vector<int64_t> heap;
+  for (int64_t b = 0; b < nbins; ++b) {
+    heap.assign((size_t)slots, 0);
+    for (size_t k = (size_t)b; k < order.size(); k += (size_t)nbins) {
+      if (order[k] < 0) continue;
+      std::pop_heap(heap.begin(), heap.end(), std::greater<int64_t>());
+      heap.back() += work[(size_t)order[k]];
+      std::push_heap(heap.begin(), heap.end(), std::greater<int64_t>());
+    }
+    worst = std::max(worst, *std::max_element(heap.begin(), heap.end()));
+  }
+  return worst;
+}
+
 void build_prefill(const Requests& q, const PrefillParams& p, PrefillLists& out) {
   std::vector<Span> spans = find_spans(q, p);
   const std::vector<Unit> units = prefill_units_of(q, p, spans);
@@ -1220,10 +1297,53 @@ void build_prefill(const Requests& q, const PrefillParams& p, PrefillLists& out)
     out.jobs.insert(out.jobs.end(), job, job + kMergeFields);
     out.merge_cols = std::max(out.merge_cols, un.cols);
   }
-  std::stable_sort(recs.begin(), recs.end(), [](const PRec& a, const PRec& b) { return a.work > b.work; });
-  out.units.assign(recs.size() * kPrefillFields, 0);
-  for (size_t k = 0; k < recs.size(); ++k) {
-    const PRec& x = recs[k];
+  // Heaviest first: the dispatch order that packs the resident workgroups
+  // best.  With several per-XCD bins the planner also builds the grouped
+  // order (each request, or span, in one bin; bins interleaved, padding in
+  // the shorter ones) and keeps it when the bins' simulated packing is no
+  // slower (within 1/64): the plain order's bins (position parity) mix
+  // every request's units, so each XCD's L2 holds all of their keys.
+  std::vector<int64_t> order(recs.size());
+  std::iota(order.begin(), order.end(), (int64_t)0);
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int64_t x, int64_t y) { return recs[(size_t)x].work > recs[(size_t)y].work; });
+  const int64_t nbins = xcd_bins(p);
+  if (nbins > 1) {
+    std::vector<int64_t> group_of(recs.size()), work(recs.size()), bin_of(recs.size());
+    for (size_t k = 0; k < recs.size(); ++k) {
+      const Unit& un = units[(size_t)recs[k].unit];
+      group_of[k] = un.span_unit ? q.batch + un.span : un.req;
+      work[k] = recs[k].work;
+    }
+    assign_bins(group_of, work, nbins, bin_of);
+    std::vector<std::vector<int64_t>> bins((size_t)nbins);
+    for (int64_t k : order) bins[(size_t)bin_of[(size_t)k]].push_back(k);  // heaviest first within a bin
+    size_t longest = 0;
+    for (const auto& b : bins) longest = std::max(longest, b.size());
+    std::vector<int64_t> grouped;
+    grouped.reserve(longest * (size_t)nbins);
+    for (size_t i = 0; i < longest; ++i)
+      for (const auto& b : bins) grouped.push_back(i < b.size() ? b[i] : -1);
+    bool keep = p.order != 2;
+    if (p.order == 0 && p.resident_per_head > 0) {
+      const int64_t slots = std::max<int64_t>(1, p.resident_per_head / nbins);
+      const int64_t mg = packed_makespan(grouped, work, nbins, slots);
+      const int64_t mp = packed_makespan(order, work, nbins, slots);
+      keep = mg * 64 <= mp * 65;
+    }
+    if (keep) order.swap(grouped);
+  }
+  out.units.assign(order.size() * kPrefillFields, 0);
+  for (size_t k = 0; k < order.size(); ++k) {
+    if (order[k] < 0) {  // padding: zero columns, nothing to do
+      int32_t* o = out.units.data() + k * kPrefillFields;
+      o[0] = kPadRecord;
+      o[5] = -1;
+      o[10] = -1;
+      o[12] = -1;
+      continue;
+    }
+    const PRec& x = recs[(size_t)order[k]];
     const Unit& un = units[(size_t)x.unit];
     int32_t* o = out.units.data() + k * kPrefillFields;
     const bool last = x.i + 1 == npieces[(size_t)x.unit];
@@ -1379,12 +1499,14 @@ PyObject* decode_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
 
 // prefill_work(req_meta i32[B*8], flat i32, group, columns, key_tokens,
 //              slots_per_head, min_tiles, decode_max_columns, block_size,
-//              shared_prefix)
+//              shared_prefix, num_kv_heads, xcds, order)
 //   -> (units i32 [n, 8], jobs i32 [m, 8], partial slots, mean key tiles per
 //       unit, most columns of a merge job)
-// shared_prefix (0/1) enables the shared-prefix spans.
+// shared_prefix (0/1) enables the shared-prefix spans; xcds > 1 orders the
+// units per XCD for num_kv_heads kv heads (padding records included) by the
+// order policy (kernel fact 22's values).
 PyObject* prefill_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
-  if (!want_args(nargs, 10, "prefill_work")) return nullptr;
+  if (!want_args(nargs, 13, "prefill_work")) return nullptr;
   Buf meta(args[0], false, 4, "req_meta"), flat(args[1], false, 4, "flat");
   if (!meta.ok() || !flat.ok()) return nullptr;
   Requests q;
@@ -1392,10 +1514,11 @@ PyObject* prefill_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   PrefillParams p;
   int64_t spans = 0;
   int64_t* fields[] = {&p.group, &p.columns, &p.key_tokens, &p.slots_per_head, &p.min_tiles, &p.max_cols,
-                       &p.block_size, &spans};
-  for (int i = 0; i < 8; ++i)
+                       &p.block_size, &spans, &p.kv_heads, &p.xcds, &p.order};
+  for (int i = 0; i < 11; ++i)
     if (!as_i64(args[2 + i], fields[i])) return nullptr;
-  if (p.group <= 0 || p.columns <= 0 || p.key_tokens <= 0 || p.min_tiles <= 0 || p.block_size <= 0) {
+  if (p.group <= 0 || p.columns <= 0 || p.key_tokens <= 0 || p.min_tiles <= 0 || p.block_size <= 0 ||
+      p.kv_heads <= 0 || p.xcds < 0 || p.order < 0 || p.order > 2) {
     PyErr_SetString(PyExc_ValueError, "prefill_work: inconsistent arguments");
     return nullptr;
   }
@@ -1405,12 +1528,13 @@ PyObject* prefill_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   }
   p.ids = flat.data<int32_t>();
   p.spans = spans != 0;
+  p.resident_per_head = p.slots_per_head;
   PrefillLists out;
   build_prefill(q, p, out);
   return prefill_result(out);
 }
 
-// layer_work(req_meta i32[B*8], flat i32, kernel facts (int64 array, 21
+// layer_work(req_meta i32[B*8], flat i32, kernel facts (int64 array, 23
 //            entries, below), cost4, wide_max_tiles)
 //   -> (col_tiles, prefill_waves, decode result or None, prefill result or None)
 //
@@ -1424,8 +1548,10 @@ PyObject* prefill_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
 //   11 tile tokens at 1, 12 resident at 4, 13 tile tokens at 4, 14 resident
 //   4-wave prefill workgroups, 15 resident 8-wave ones, 16 max tokens per
 //   decode wave (0: no cap), 17 decode max columns, 18 min units per wave,
-//   19 prefill min tiles, 20 shared-prefix spans (0/1).
-constexpr int kKernelFacts = 21;
+//   19 prefill min tiles, 20 shared-prefix spans (0/1), 21 the device's XCDs
+//   (0: no per-XCD order of the prefill grid), 22 per-XCD order (0: grouped
+//   when its simulated packing is no slower, 1: grouped, 2: plain).
+constexpr int kKernelFacts = 23;
 
 // One layer shape's plan: the choices and the lists of both kernels.
 struct LayerPlan {
@@ -1489,6 +1615,9 @@ const char* plan_layer(const Requests& q, const int32_t* ids, int64_t nflat, con
   p.ids = ids;
   p.block_size = bs;
   p.spans = k[20] != 0;
+  p.kv_heads = hkv;
+  p.xcds = k[21];
+  p.order = k[22];
   int64_t waves = 4;
   bool any_decode = false, any_prefill = false;
   for (int64_t r = 0; r < q.batch; ++r) {
@@ -1502,7 +1631,8 @@ const char* plan_layer(const Requests& q, const int32_t* ids, int64_t nflat, con
     } else {
       waves = choose_prefill_waves(q, p, k[5] ? k[14] / hkv : 0, k[9] != 0, wide_max);
     }
-    p.slots_per_head = k[5] ? (waves == 8 ? k[15] : k[14]) / hkv : 0;
+    p.resident_per_head = (waves == 8 ? k[15] : k[14]) / hkv;
+    p.slots_per_head = k[5] ? p.resident_per_head : 0;
   }
   out.ctw = ctw;
   out.waves = waves;
@@ -1524,7 +1654,7 @@ const char* plan_layer(const Requests& q, const int32_t* ids, int64_t nflat, con
 // ---------------------------------------------------------------------------
 // plan_step(flat i32, counts i64, computed i64, reserved i64, readonly i64,
 //           q_lens i64, vis_off i64, vis_words i64, vis u32, num_blocks,
-//           block_size, kernel facts i64 [n][20], cost4, wide_max_tiles,
+//           block_size, kernel facts i64 [n][23], cost4, wide_max_tiles,
 //           out i32 (writable))
 //   -> rule (int 1..6): a block-table rule fails (validate's codes);
 //      (needed, None, None): ``out`` holds fewer than ``needed`` entries;

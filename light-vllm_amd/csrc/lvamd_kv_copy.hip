@@ -364,7 +364,14 @@ const char* lvamd_status_string(int status) {
   }
 }
 
-int lvamd_abi_version(void) { return 15; }
+int lvamd_abi_version(void) { return 16; }
+
+int lvamd_xcd_count(void) {
+  int device = 0, xcds = 0;
+  if (hipGetDevice(&device) != hipSuccess) return LVAMD_ERR_RUNTIME;
+  if (hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, device) != hipSuccess) return LVAMD_ERR_RUNTIME;
+  return xcds;
+}
 
 int lvamd_stage_upload(void* device_dst, const void* pinned_src, int64_t bytes, void* event, lvamd_stream_t stream) {
   if (bytes < 0 || (bytes > 0 && (!device_dst || !pinned_src))) return LVAMD_ERR_INVALID_ARGUMENT;

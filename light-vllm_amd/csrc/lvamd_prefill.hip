@@ -12,11 +12,14 @@
 //     (query, head-in-group) pair of one kv head, so the GQA group shares
 //     every K/V byte.  One workgroup per (unit, kv head): four waves of two
 //     16-column tiles, or eight waves of one (the host picks per step).
-//   * Keys go in 64-token tiles (32 for D = 256): the workgroup gathers a tile's K and V rows
-//     through the block table (16-byte coalesced loads) into registers, then
-//     into a double-buffered LDS tile, one barrier per tile.  While tile t
-//     computes, tile t+1 waits in registers, tile t+2's loads are in flight
-//     and tile t+3's table entries are being fetched.
+//   * Keys go in 64-token tiles (32 for D = 256).  Each lane copies one
+//     16-byte chunk of one row per load straight from the pool (or this
+//     step's K/V) into LDS (global_load_lds_dwordx4: no registers, no LDS
+//     store instructions), double-buffered, one barrier per tile: tile t+1
+//     lands while tile t computes, tile t+2's table entries are in flight.
+//     The LDS layout is unpadded and XOR-swizzled (below) so that the
+//     loads, the K reads and the V transpose reads are all free of bank
+//     conflicts.
 //   * S^T = K Q^T on MFMA 16x16x32: the K A operand is read from LDS once per
 //     wave and used for all its column tiles; the accumulator layout (lane l:
 //     column l%16, keys 4*(l/16)+r) is the B operand of O^T = V^T P^T, whose
@@ -43,10 +46,6 @@ constexpr float kRescaleSlack = 8.0f;  // log2 units: probabilities stay below 2
 
 }  // namespace
 
-// LDS row padding in bytes.  32 makes every tile access conflict-free
-// (measured SQ_LDS_BANK_CONFLICT 13.8M -> 0 per C3 launch; 16 left 2.3
-// conflict cycles per LDS instruction on the transpose reads).
-constexpr int kPrefillPad = 32;
 // Keys per LDS tile up to head size 128 (32 above).
 constexpr int kPrefillKeyTile = 64;
 // Two shapes of the same 128-column unit, chosen per step by the planner:
@@ -54,31 +53,44 @@ constexpr int kPrefillKeyTile = 64;
 //   256 registers per wave, two waves per SIMD (two workgroups per CU).
 // * W = 8 waves of one column tile: half the registers (128), four waves per
 //   SIMD to hide the softmax's dependency chain, twice the LDS reads per MFMA.
-// Measured (bf16, D = 128): W = 8 is faster on split-K and short units (tree
-// verification 8K context 126 vs 142 us, 512-query chunks without history
-// 42 vs 47 us, 512-query chunks at 16K history (split) 419 vs 460 us); W = 4
-// on long unsplit units (C3: 171 vs 183 us).  Keys per LDS tile: 64 (32 for
-// D = 256, which is built for W = 4 only).
+// W = 8 is faster on split-K and short units (tree verification, chunks
+// without history), W = 4 on long unsplit units.  Keys per LDS tile: 64 (32
+// for D = 256, which is built for W = 4 only).
 constexpr int prefill_col_tiles_per_wave(int d, int w) { return w == 8 ? 1 : 2; }
 constexpr bool prefill_built(int d, int w) { return w == 4 || (w == 8 && d <= 128); }
 constexpr int prefill_key_tile(int d) { return d <= 128 ? kPrefillKeyTile : 32; }
 constexpr int prefill_unit_columns(int d) { return 16 * prefill_col_tiles_per_wave(d, 4) * 4; }
 static_assert(16 * 1 * 8 == 16 * 2 * 4, "both shapes cover the same unit columns");
 
+// LDS tile layout.  A K (or V) tile of KT rows is stored as CG column groups
+// (64 bytes = four 16-byte chunks of every row), group-major: byte
+//   cg * KT * 64 + row * 64 + 16 * (c ^ swz(row))
+// holds chunk 4 cg + c of the row.  One direct load of a wave fills 1 KB =
+// 16 rows of one group.  swz permutes the four chunk slots of a row by row
+// bits 2 and 3, which makes
+//   * the K reads (lanes 0-15 read rows 0-15 at one chunk) and
+//   * the V transpose reads (lanes 0-31 read 8 rows x 32 bytes)
+// cover every bank once, and the loads write contiguous bytes.
+// Source and LDS pointers of global_load_lds.
+typedef const __attribute__((address_space(1))) void* lds_gptr;
+typedef __attribute__((address_space(3))) void* lds_lptr;
+
+__device__ __forceinline__ constexpr int prefill_swz(int row) { return ((row >> 2) & 1) << 1 | ((row >> 3) & 1); }
+
 template <typename T, int D, int W>
 struct PrefillShape {
   static constexpr int KT = prefill_key_tile(D);               // keys per tile
   static constexpr int KS = KT / 16;                           // 16-key groups per tile
   static constexpr int CPR = D * (int)sizeof(T) / 16;          // 16-byte chunks per row
-  static constexpr int RS = D * (int)sizeof(T) + kPrefillPad;  // LDS row stride in bytes (bank spread)
+  static constexpr int CG = (CPR + 3) / 4;                     // 64-byte column groups (D = 80: the last half used)
+  static constexpr int RB = KT / 16;                           // 16-row blocks per tile
+  static constexpr int GROUP_BYTES = KT * 64;                  // one column group of a tile
+  static constexpr int TILE_BYTES = CG * GROUP_BYTES;          // a K or V tile
   static constexpr int THREADS = 64 * W;
-  static constexpr int TPR = THREADS / KT;                     // gather threads per tile row
-  static constexpr int LPT = (CPR + TPR - 1) / TPR;             // chunks per thread per tile
-  static_assert(THREADS % KT == 0, "every tile row gets the same number of gather threads");
+  static_assert(W % RB == 0, "every wave loads one row block");
   static constexpr int CT = prefill_col_tiles_per_wave(D, W);
   static constexpr int NCH = (D + 31) / 32;                    // 16x16x32 k-steps of QK^T
   static constexpr int NT = D / 16;                            // 16-row tiles of O^T
-  static constexpr int TILE_BYTES = KT * RS;
   static_assert(KT % 32 == 0, "PV steps take 32 keys");
   static_assert(sizeof(T) == 2, "the prefill kernel is built for 16-bit types");
 };
@@ -108,15 +120,19 @@ struct PrefillArgs {
 template <typename T, int D, int W>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ? 4 : (D <= 128 ? 2 : 1)))) void paged_prefill_kernel(const PrefillArgs a) {
   using P = PrefillShape<T, D, W>;
-  constexpr int CPR = P::CPR, RS = P::RS, LPT = P::LPT, TPR = P::TPR, CT = P::CT, NCH = P::NCH, NT = P::NT;
-  constexpr int KT = P::KT, KS = P::KS;
+  constexpr int CPR = P::CPR, CG = P::CG, RB = P::RB, CT = P::CT, NCH = P::NCH, NT = P::NT;
+  constexpr int KT = P::KT, KS = P::KS, GB = P::GROUP_BYTES;
   using V8 = typename std::conditional<std::is_same<T, __bf16>::value, bf16x8, f16x8>::type;
-  __shared__ __attribute__((aligned(16))) char klds[2][P::TILE_BYTES];
-  __shared__ __attribute__((aligned(16))) char vlds[2][P::TILE_BYTES];
+  // Two K and two V buffers as four objects: the compiler then sees that a
+  // load into one buffer does not alias reads of the other.
+  __shared__ __attribute__((aligned(1024))) char klds0[P::TILE_BYTES];
+  __shared__ __attribute__((aligned(1024))) char klds1[P::TILE_BYTES];
+  __shared__ __attribute__((aligned(1024))) char vlds0[P::TILE_BYTES];
+  __shared__ __attribute__((aligned(1024))) char vlds1[P::TILE_BYTES];
 
   constexpr int kThreads = P::THREADS;
   const int tid = threadIdx.x & (kThreads - 1);  // (the mask tells LLVM the thread range)
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
   const int lane = tid & 63;
   const int l16 = lane & 15;
   const int g = lane >> 4;
@@ -133,6 +149,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
   const int col0 = u[1], ncols = u[2], key_begin = u[3], key_end = u[4], slot = u[5];
   const int table_off = u[6], q_start = u[7], computed = u[8], q_len = u[9], vis_off = u[10], vis_words = u[11];
   const int first_blocks[4] = {u[12], u[13], u[14], u[15]};  // -1: take them from the table
+  if (ncols <= 0) return;  // a padding record (the host's per-XCD unit order)
   const int col_end = col0 + ncols;  // exclusive: <= q_len * G (a span unit: its packed columns)
   // Keys the unit needs: up to its last query's position, within the piece's
   // key range [key_begin, key_end) (key_begin a multiple of KT; key_end 0 =
@@ -150,25 +167,19 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
   gptr<T> const vbase = (gptr<T>)(a.v_pool);
   const int32_t* table = a.tables + table_off;
 
-  // ---- tile gather.  Thread tid owns row tid / TPR of every tile and its
-  // 16-byte chunks (tid % TPR) + TPR i: one table entry and one row address
-  // per tile, the chunk loads and LDS stores at immediate offsets.
-  const int grow = tid / TPR;
-  const int gcol = tid - grow * TPR;
-  // Fused append (8-wave shape only): keys at positions >= computed are this
-  // step's tokens, read from the input K/V; the unit that holds a token's own
-  // query (its first column) also writes the row to its pool slot, so no
-  // other launch appends.  The 4-wave shape serves long units, where the
-  // append launch is small next to the kernel and the extra registers (three
-  // more spills at D = 128) cost more: there the pool holds the step's K/V.
-  constexpr bool kAppend = W == 8;
-  gptr<const T> const knew =
-      (kAppend && a.k_new) ? (gptr<const T>)(a.k_new) + (int64_t)kvh * a.kn_head_stride : nullptr;
-  gptr<const T> const vnew =
-      (kAppend && a.v_new) ? (gptr<const T>)(a.v_new) + (int64_t)kvh * a.vn_head_stride : nullptr;
-  auto chunk_ok = [&](int i) { return gcol + TPR * i < CPR; };
+  // ---- tile loads.  Wave w loads row block w % RB of every tile, column
+  // groups w / RB, w / RB + W / RB, ...; lane l the row 16 (w % RB) + l / 4
+  // into chunk slot l % 4 of each group (chunk 4 cg + ((l % 4) ^ swz(row))):
+  // one table entry and one row address per tile.
+  const int lrow = 16 * (wave % RB) + (lane >> 2);
+  const int lchunk = (lane & 3) ^ prefill_swz(lrow);
+  // Fused append: keys at positions >= computed are this step's tokens, read
+  // from the input K/V; the unit that holds a token's own query (its first
+  // column) also writes the row to its pool slot, so no other launch appends.
+  gptr<const T> const knew = a.k_new ? (gptr<const T>)(a.k_new) + (int64_t)kvh * a.kn_head_stride : nullptr;
+  gptr<const T> const vnew = a.v_new ? (gptr<const T>)(a.v_new) + (int64_t)kvh * a.vn_head_stride : nullptr;
   auto key_pos = [&](int t) -> int {
-    const int pos = (tile0 + t) * KT + grow;
+    const int pos = (tile0 + t) * KT + lrow;
     return pos < kmax ? pos : kmax - 1;  // rows past the piece read its last key (masked)
   };
   auto logical_block = [&](int pos) -> int { return a.bs_shift >= 0 ? (pos >> a.bs_shift) : (pos / bs); };
@@ -180,48 +191,36 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
     const int k = logical_block(key_pos(0)) - logical_block(key_begin);
     return k == 0 ? first_blocks[0] : k == 1 ? first_blocks[1] : k == 2 ? first_blocks[2] : first_blocks[3];
   };
-  // Loads tile t's row; returns the row's pool slot when this thread must
-  // append it, else -1.
-  auto load_tile = [&](int t, int te, uint4 (&kr)[LPT], uint4 (&vr)[LPT]) -> int {
+  // Chunk of column group cg this lane copies (D = 80: the half-used last
+  // group's spare slots copy the row's last chunk again; nothing reads them).
+  auto chunk_of = [&](int cg) -> int {
+    const int ch = 4 * cg + lchunk;
+    if constexpr (4 * CG > CPR) return ch < CPR ? ch : CPR - 1;
+    return ch;
+  };
+  // Issues tile t's loads into (kdst, vdst); te is the row's table entry.
+  auto issue_tile = [&](int t, int te, char* kdst, char* vdst) {
     const int pos = key_pos(t);
     const uint32_t slot = (uint32_t)te * (uint32_t)bs + (uint32_t)(pos - logical_block(pos) * bs);
-    const int64_t off = (int64_t)slot * row_elems + kvh * D + gcol * 8;
+    const int64_t off = (int64_t)slot * row_elems + kvh * D;
     gptr<const T> kp = kbase + off;
     gptr<const T> vp = vbase + off;
-    int append = -1;
+    bool append = false;
     if (knew != nullptr && pos >= computed) {
       const int j = pos - computed;  // query index of the row's token
-      kp = knew + (int64_t)(q_start + j) * a.kn_tok_stride + gcol * 8;
-      vp = vnew + (int64_t)(q_start + j) * a.vn_tok_stride + gcol * 8;
-      const int raw = (tile0 + t) * KT + grow;
-      if (raw == pos && j * G >= col0) append = (int)slot;  // (j * G < col_end: pos < kmax <= kneed)
+      kp = knew + (int64_t)(q_start + j) * a.kn_tok_stride;
+      vp = vnew + (int64_t)(q_start + j) * a.vn_tok_stride;
+      const int raw = (tile0 + t) * KT + lrow;
+      append = raw == pos && j * G >= col0;  // (j * G < col_end: pos < kmax <= kneed)
     }
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      if (chunk_ok(i)) {
-        kr[i] = load16(kp + TPR * 8 * i);
-        vr[i] = load16(vp + TPR * 8 * i);
-      }
-    }
-    return append;
-  };
-  auto store_tile = [&](int b, const uint4 (&kr)[LPT], const uint4 (&vr)[LPT], int append) {
-    const int off = grow * RS + gcol * 16;
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      if (chunk_ok(i)) {
-        *reinterpret_cast<uint4*>(klds[b] + off + TPR * 16 * i) = kr[i];
-        *reinterpret_cast<uint4*>(vlds[b] + off + TPR * 16 * i) = vr[i];
-      }
-    }
-    if (append >= 0) {
-      const int64_t po = (int64_t)append * row_elems + kvh * D + gcol * 8;
-#pragma unroll
-      for (int i = 0; i < LPT; ++i) {
-        if (chunk_ok(i)) {
-          store16(kbase + po + TPR * 8 * i, kr[i]);
-          store16(vbase + po + TPR * 8 * i, vr[i]);
-        }
+    const int lds_row = (wave % RB) * 1024;
+    for (int cg = wave / RB; cg < CG; cg += W / RB) {
+      const int ch = chunk_of(cg);
+      __builtin_amdgcn_global_load_lds((lds_gptr)(kp + ch * 8), (lds_lptr)(kdst + cg * GB + lds_row), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((lds_gptr)(vp + ch * 8), (lds_lptr)(vdst + cg * GB + lds_row), 16, 0, 0);
+      if (append) {
+        store16((gptr<T>)(kbase + off + ch * 8), load16(kp + ch * 8));
+        store16((gptr<T>)(vbase + off + ch * 8), load16(vp + ch * 8));
       }
     }
   };
@@ -261,22 +260,37 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) vrow[ct] = tree_word ? a.vis[vis_off + qi[ct]] : 0u;
 
-  float m_run[CT], l_run[CT];  // m_run in the scaled log2 domain
+  // m_run in the scaled log2 domain.  The softmax denominators come from the
+  // matrix cores: l_run += ones(16 x 32) P^T puts each column's sum of its
+  // (rounded) probabilities in every row of its accumulator, so the VALU
+  // adds no probabilities and the epilogue needs no cross-lane sum.
+  float m_run[CT];
+  f32x4 l_run[CT];
   f32x4 acc[CT][NT];
+  V8 ones;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ones[i] = from_f32<T>(1.f);
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     m_run[ct] = -INFINITY;
-    l_run[ct] = 0.f;
+    l_run[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int n = 0; n < NT; ++n) acc[ct][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // ---- one tile of attention from LDS buffer b (t: tile of the piece)
-  auto compute_tile = [&](int tr, int b) {
+  // LDS read offsets of this lane: K row l16 (+16 s), chunk 4 kk + g; V^T
+  // transpose reads of row 4 g + l16 / 4 (+32 h, +16), bytes 32 n + 8 q4 of
+  // the row (chunk 2 n + q4 / 2: group n / 2, slot 2 (n % 2) + q4 / 2).
+  const int q4 = l16 & 3;
+  const int k_off = l16 * 64 + 16 * (g ^ prefill_swz(l16));
+  const int v_row = 4 * g + (l16 >> 2);
+  const int v_off0 = v_row * 64 + 16 * ((q4 >> 1) ^ prefill_swz(v_row)) + 8 * (q4 & 1);
+  const int v_off1 = v_row * 64 + 16 * ((2 + (q4 >> 1)) ^ prefill_swz(v_row)) + 8 * (q4 & 1);
+
+  // ---- one tile of attention from LDS (t: tile of the piece)
+  auto compute_tile = [&](int tr, const char* kt, const char* vt) {
     const int t = tile0 + tr;
     if (!wave_active || t * KT >= wave_kmax) return;
-    const char* kt = klds[b];
-    const char* vt = vlds[b];
     // S^T for each column tile, K chunks shared.  Each MFMA block runs at
     // raised wave priority: the SIMD's other wave then does its softmax
     // VALU work while this one feeds the matrix core, and the two phases
@@ -295,7 +309,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
 #pragma unroll
       for (int kk = 0; kk < NCH; ++kk) {
         const int ch = kk * 4 + g;
-        const uint4 kc = ch < CPR ? *reinterpret_cast<const uint4*>(kt + (16 * s + l16) * RS + ch * 16) : zero_u4();
+        const uint4 kc = ch < CPR ? *reinterpret_cast<const uint4*>(kt + kk * GB + s * 1024 + k_off) : zero_u4();
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) st[ct][s] = Mma<T>::qk(kc, qf[ct][kk], st[ct][s]);
       }
@@ -305,25 +319,44 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
     // linear request, the ancestor bits for a tree.  (A piece ends on a tile
     // boundary or at the unit's last key, so no unmasked tile reaches past
     // it; rows past kmax in a masked tile fail the visibility test.)
-    if (masked) {
+    if (masked && !tree) {
+      // Linear: key pos is visible to query qi iff pos <= computed + qi.
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
+      for (int ct = 0; ct < CT; ++ct) {
+        const int last = computed + qi[ct] - t * KT - 4 * g;  // last visible pos, tile- and lane-relative
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (16 * s + r > last) st[ct][s][r] = -INFINITY;
+      }
+    } else if (masked) {
+      // Tree: keys before computed are visible, key j = pos - computed < q_len
+      // iff bit j of the query's ancestor row.  The tile's keys span at most
+      // NW words of the row; each column loads them once per tile, always in
+      // bounds (clamped), so the loads carry no condition.
+      constexpr int NW = KT / 32 + 1;
+      const int j0 = t * KT - computed;  // j of the tile's first key
+      const int w0 = j0 >> 5;            // (arithmetic: j0 may be negative)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        uint32_t words[NW];
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+          const int w = min(max(w0 + i, 0), vis_words - 1);
+          words[i] = tree_word ? vrow[ct] : a.vis[vis_off + qi[ct] * vis_words + w];
+        }
 #pragma unroll
         for (int s = 0; s < KS; ++s)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int pos = t * KT + 16 * s + 4 * g + r;
-            bool vis;
-            if (!tree) {
-              vis = pos <= computed + qi[ct];
-            } else {
-              const int j = pos - computed;
-              const uint32_t word =
-                  tree_word ? vrow[ct] : (j >= 0 && j < q_len ? a.vis[vis_off + qi[ct] * vis_words + (j >> 5)] : 0u);
-              vis = j < 0 || (j < q_len && ((word >> (j & 31)) & 1u));
-            }
+            const int j = j0 + 16 * s + 4 * g + r;
+            const int wi = (j >> 5) - w0;  // 0 .. NW - 1
+            const uint32_t word = wi == 0 ? words[0] : wi == 1 ? words[1] : words[NW - 1];
+            const bool vis = j < 0 || (j < q_len && ((word >> (j & 31)) & 1u));
             if (!vis) st[ct][s][r] = -INFINITY;
           }
+      }
     }
     // Online softmax on raw scores: max first, scale folded into the exp.
     V8 pb[CT][KS / 2];
@@ -349,20 +382,28 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float p = fast_exp2(__builtin_fmaf(st[ct][s][r], c_log2, nbase));
-          l_run[ct] += p;
           pb[ct][s >> 1][(s & 1) * 4 + r] = from_f32<T>(p);
         }
     }
     // O^T += V^T P^T: transpose reads shared by the column tiles.
     __builtin_amdgcn_s_setprio(1);
     __builtin_amdgcn_iglp_opt(0);
-    const int q4 = l16 & 3;
+#pragma unroll
+    for (int h = 0; h < KS / 2; ++h)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        if constexpr (std::is_same<T, __bf16>::value) {
+          l_run[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[ct][h], l_run[ct], 0, 0, 0);
+        } else {
+          l_run[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[ct][h], l_run[ct], 0, 0, 0);
+        }
+      }
 #pragma unroll
     for (int h = 0; h < KS / 2; ++h)
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
-        const int lo = (32 * h + 4 * g + (l16 >> 2)) * RS + (16 * n + 4 * q4) * 2;
-        const int hi = lo + 16 * RS;
+        const int lo = (n & 1 ? v_off1 : v_off0) + (n >> 1) * GB + h * 32 * 64;
+        const int hi = lo + 16 * 64;
         const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vt + lo));
         const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vt + hi));
         const s16x4 both[2] = {v0, v1};
@@ -379,43 +420,38 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
     __builtin_amdgcn_s_setprio(0);
   };
 
-  // ---- pipeline: tile t computes from LDS while tile t+1 sits in registers
-  // (stored to the other LDS buffer after the compute), tile t+2's loads are
-  // in flight and tile t+3's table entries are being fetched.  Two register
-  // sets alternate statically (a run-time swap would force waits).
-  // Prologue: tile 0's loads issue as soon as the record is in (its block
-  // ids come with it, or one table round trip when they do not), tile 1's
-  // after its table entries; tile 2's entries follow; tile 0 goes to LDS.
-  int ea = 0, eb = 0;
-  int wa = -1, wb = -1;  // pool slots to append the staged rows at (-1: none)
-  uint4 ka[LPT], va[LPT], kb[LPT], vb[LPT];
-  eb = first_entry();
+  // ---- pipeline: tile t computes from one buffer pair while tile t+1's
+  // loads land in the other and tile t+2's table entries are fetched; then
+  // every wave waits for its own loads and the barrier publishes the tile
+  // (and frees the buffers just read).  The barrier carries no fence: the
+  // vmcnt wait is what orders the direct loads before it.
+  auto tile_done = [&]() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __builtin_amdgcn_s_barrier();
+  };
+  int ea = first_entry(), eb = 0;
+  issue_tile(0, ea, klds0, vlds0);
   if (ntiles > 1) ea = load_entry(1);
-  wb = load_tile(0, eb, kb, vb);
-  if (ntiles > 1) wa = load_tile(1, ea, ka, va);
-  if (ntiles > 2) eb = load_entry(2);
-  store_tile(0, kb, vb, wb);
-  __syncthreads();
-
-  // dc holds tile t+1, dn receives tile t+2 (entry en), ec receives tile t+3's entry.
-  auto iter = [&](int t, uint4 (&kc)[LPT], uint4 (&vc)[LPT], int& wc, uint4 (&kn)[LPT], uint4 (&vn)[LPT],
-                  int& wn, int& ec, const int en) {
-    if (t + 2 < ntiles) wn = load_tile(t + 2, en, kn, vn);
-    if (t + 3 < ntiles) ec = load_entry(t + 3);
-    compute_tile(t, t & 1);
-    if (t + 1 < ntiles) store_tile((t + 1) & 1, kc, vc, wc);
-    __syncthreads();
+  tile_done();
+  // en: tile t+1's entry (in), ef: receives tile t+2's.
+  auto step = [&](int t, const char* kc, const char* vc, char* kn, char* vn, const int en, int& ef) {
+    // The entry load goes first: a wait for it then never waits for the
+    // tile's loads (the vector memory counter retires in issue order).
+    if (t + 2 < ntiles) ef = load_entry(t + 2);
+    if (t + 1 < ntiles) issue_tile(t + 1, en, kn, vn);
+    compute_tile(t, kc, vc);
+    tile_done();
   };
   for (int t = 0; t < ntiles; t += 2) {
-    iter(t, ka, va, wa, kb, vb, wb, ea, eb);
-    if (t + 1 < ntiles) iter(t + 1, kb, vb, wb, ka, va, wa, eb, ea);
+    step(t, klds0, vlds0, klds1, vlds1, ea, eb);
+    if (t + 1 < ntiles) step(t + 1, klds1, vlds1, klds0, vlds0, eb, ea);
   }
 
   // ---- normalised output rows, or this piece's partials
   if (!wave_active) return;
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
-    const float l_tot = row_sum4(l_run[ct]);
+    const float l_tot = l_run[ct][0];
     if (!colok[ct]) continue;
     if (slot >= 0) {
       constexpr int UC = prefill_unit_columns(D);
@@ -544,7 +580,6 @@ extern "C" int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_
     return LVAMD_ERR_INVALID_ARGUMENT;
   if ((int64_t)num_units * num_kv_heads > 0x7fffffffLL) return LVAMD_ERR_INVALID_ARGUMENT;
   if ((new_key == nullptr) != (new_value == nullptr)) return LVAMD_ERR_INVALID_ARGUMENT;
-  if (new_key && waves != 8) return LVAMD_ERR_INVALID_ARGUMENT;  // only the 8-wave shape appends
   if (new_key && (((uintptr_t)new_key & 15u) || ((uintptr_t)new_value & 15u) ||
                   (new_key_token_stride * es) % 16 != 0 || (new_key_head_stride * es) % 16 != 0 ||
                   (new_value_token_stride * es) % 16 != 0 || (new_value_head_stride * es) % 16 != 0))

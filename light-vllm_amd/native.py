@@ -19,7 +19,7 @@ from pathlib import Path
 from light_vllm_amd import errors
 
 LIB_NAME = "liblvamd_hip.so"
-ABI_VERSION = 15
+ABI_VERSION = 16
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
@@ -39,6 +39,7 @@ _f32 = ctypes.c_float
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lvamd_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "lvamd_abi_version": (ctypes.c_int, []),
+    "lvamd_xcd_count": (ctypes.c_int, []),
     "lvamd_kv_append": (
         ctypes.c_int,
         [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i32, _i32, _i32, _p],
@@ -195,6 +196,14 @@ def prefill_key_tokens(dtype_code: int, head_size: int) -> int:
 
 
 @functools.lru_cache(maxsize=None)
+def xcd_count() -> int:
+    """XCDs of the current GPU (each with its own L2)."""
+
+    found = int(load().lvamd_xcd_count())
+    check(min(found, 0), "lvamd_xcd_count")
+    return found
+
+
 def prefill_resident_units(dtype_code: int, head_size: int, waves: int = 4) -> int:
     """Prefill workgroups of ``waves`` waves the current GPU holds at once."""
 

@@ -490,7 +490,8 @@ class StepPlan:
     def work(
         self, group: int, num_kv_heads: int, resident_waves: int = 8 * NUM_CUS, prefill_columns: int = 0,
         unit_tokens: int = UNIT_TOKENS, col_tiles: int = 1, prefill_key_tokens: int = 64,
-        prefill_resident: int = 0, prefill_waves: int = 4, shared_prefix: bool = False,
+        prefill_resident: int = 0, prefill_waves: int = 4, shared_prefix: bool = False, xcds: int = 0,
+        prefill_order: int = 0,
     ) -> DecodeWork:
         """Work lists for layers of this (group, kv heads) shape.
 
@@ -501,12 +502,16 @@ class StepPlan:
         is the prefill kernel's key tile and ``prefill_resident`` how many
         prefill workgroups of shape ``prefill_waves`` the GPU holds (0: never
         split prefill units); ``shared_prefix`` attends prefixes that runs of
-        prefill requests share once per span (the backend's default).  The
-        library reports the kernel figures per dtype and head size.
+        prefill requests share once per span (the backend's default);
+        ``xcds`` > 1 orders the prefill units per XCD of a device with that
+        many (the backend passes the device's count): ``prefill_order`` 0
+        keeps each request's units on one XCD when the simulated packing is
+        no slower, 1 always, 2 never.  The library reports the kernel figures
+        per dtype and head size.
         """
 
         key = (group, num_kv_heads, resident_waves, prefill_columns, unit_tokens, col_tiles, prefill_key_tokens,
-               prefill_resident, prefill_waves, bool(shared_prefix))
+               prefill_resident, prefill_waves, bool(shared_prefix), int(xcds), int(prefill_order))
         found = self._work.get(key)
         if found is None:
             found = self._build_work(*key)
@@ -546,6 +551,7 @@ class StepPlan:
     def _build_work(
         self, group: int, num_kv_heads: int, resident_waves: int, prefill_columns: int, unit_tokens: int,
         col_tiles: int, prefill_key_tokens: int, prefill_resident: int, prefill_waves: int, shared_prefix: bool,
+        xcds: int, prefill_order: int,
     ) -> DecodeWork:
         host = native.host()
         work = DecodeWork(col_tiles=col_tiles, prefill_waves=prefill_waves)
@@ -560,7 +566,7 @@ class StepPlan:
             slots_per_head = prefill_resident // num_kv_heads if prefill_resident else 0
             pre = host.prefill_work(self._req_meta, self.facts.raw[0], group, prefill_columns, prefill_key_tokens,
                                     slots_per_head, PREFILL_MIN_TILES, max_cols, self.block_size,
-                                    int(shared_prefix))
+                                    int(shared_prefix), num_kv_heads, xcds, prefill_order)
         _fill_work(work, dec, pre)
         return work
 
@@ -571,7 +577,7 @@ KERNEL_FACTS = (
     "forced_col_tiles", "forced_prefill_waves", "max_col_tiles", "wide_prefill_built",
     "resident_waves_1", "tile_tokens_1", "resident_waves_4", "tile_tokens_4",
     "prefill_resident_4", "prefill_resident_8", "partition_tokens", "decode_max_columns",
-    "min_units_per_wave", "prefill_min_tiles", "shared_prefix",
+    "min_units_per_wave", "prefill_min_tiles", "shared_prefix", "xcds", "prefill_order",
 )
 
 

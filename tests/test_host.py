@@ -4,6 +4,8 @@ metadata, and the C-ABI library's exports (loaded, no kernel launched)."""
 
 from __future__ import annotations
 
+import math
+
 import ctypes
 import json
 from pathlib import Path
@@ -346,7 +348,10 @@ def _check_prefill_coverage(md, work, *, group, columns, key_tokens, bs):
     computed = np.asarray(md.num_computed_tokens)
     q_start = np.asarray(md.query_start_loc)
     flat = [b for t in md.block_tables for b in t]
-    units = work.prefill_units.numpy() if work.num_prefill_units else np.zeros((0, 8), np.int32)
+    units = work.prefill_units.numpy() if work.num_prefill_units else np.zeros((0, 16), np.int32)
+    pads = units[:, 2] == 0  # padding records of the per-XCD order
+    assert (units[pads, 0] == PAD_RECORD).all() and (units[pads, 5] == -1).all()
+    units = units[~pads]
     jobs = work.prefill_jobs.numpy() if work.num_prefill_jobs else np.zeros((0, 8), np.int32)
     own: dict[tuple[int, int], list] = {}
     span_units: dict[int, list] = {}  # first token -> [(col0, n, kb, ke, slot)]
@@ -462,6 +467,106 @@ def test_shared_prefix_span_shapes() -> None:
     assert not (work.prefill_units.numpy()[:, 0] < 0).any()
 
 
+PAD_RECORD = 2**31 - 1
+
+
+def _record_work(u, group, key_tokens):
+    """Key tiles x columns of one prefill record (the planner's balance measure)."""
+
+    kneed = u[8] + (u[1] + u[2] - 1) // group + 1
+    kmax = u[4] if 0 < u[4] < kneed else kneed
+    return (-(-kmax // key_tokens) - u[3] // key_tokens) * u[2]
+
+
+@pytest.mark.parametrize("hkv", (1, 2, 3, 4, 8, 28))
+@pytest.mark.parametrize("seed", range(6))
+def test_prefill_grid_is_ordered_per_xcd(hkv, seed) -> None:
+    """With 8 XCDs the grid's workgroup b = (position b / H, kv head b % H)
+    runs on XCD b % 8, so positions congruent modulo P = 8 / gcd(H, 8) share
+    an XCD per kv head.  The ordered lists hold the unordered ones' records
+    plus padding, P bins interleaved, each bin heaviest first, and the bins
+    balanced to within one record (or 1/32 of a bin)."""
+
+    rng = np.random.default_rng(700 + seed)
+    group, key_tokens = 7 if hkv <= 4 else 1, 64
+    n = int(rng.integers(2, 10))
+    computed = [int(c) for c in rng.integers(0, 3000, size=n)]
+    q_lens = [int(q) for q in rng.integers(40, 600, size=n)]
+    need = [(c + q + 15) // 16 for c, q in zip(computed, q_lens)]
+    perm = [int(x) for x in rng.permutation(sum(need) + 5)]
+    tables, off = [], 0
+    for k in need:
+        tables.append(tuple(perm[off: off + k]))
+        off += k
+    md = lv.PagedAttentionMetadata(block_tables=tuple(tables), num_computed_tokens=tuple(computed),
+                                   query_layouts=tuple(lv.linear_query_layout(q) for q in q_lens))
+    plan = StepPlan(md, block_size=16, device=CPU)
+    args = (group, hkv, 2048, 128, 64, 1, key_tokens, 0)
+    flat = plan.work(*args, xcds=0).prefill_units.numpy()
+    work = plan.work(*args, xcds=8, prefill_order=1)
+    _check_prefill_coverage(md, work, group=group, columns=128, key_tokens=key_tokens, bs=16)
+    units = work.prefill_units.numpy()
+    bins = 8 // math.gcd(hkv, 8)
+    assert len(units) % bins == 0
+    real = units[units[:, 2] > 0]
+    assert sorted(map(tuple, real.tolist())) == sorted(map(tuple, flat.tolist()))
+    load = [0] * bins
+    works = [_record_work(u, group, key_tokens) for u in units.tolist()]
+    for b in range(bins):
+        seq = [w for k, w in enumerate(works) if k % bins == b and units[k, 2] > 0]
+        assert seq == sorted(seq, reverse=True)  # heaviest first
+        load[b] = sum(seq)
+    gap = max(load) - min(load)
+    assert gap * 32 * bins <= sum(load) or gap <= max(works)
+    if bins == 1:
+        assert len(real) == len(units)
+
+
+def _makespan(units, bins, slots, group, key_tokens):
+    """Latest finish over the bins when each bin's records start in order,
+    each on the first of ``slots`` slots to free (padding: nothing)."""
+
+    import heapq
+
+    worst = 0
+    for b in range(bins):
+        heap = [0] * slots
+        for u in units.tolist()[b::bins]:
+            if u[2] > 0:
+                heapq.heappush(heap, heapq.heappop(heap) + _record_work(u, group, key_tokens))
+        worst = max(worst, max(heap))
+    return worst
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_auto_prefill_order_keeps_the_faster_packing(seed) -> None:
+    """``prefill_order`` 0 (auto) returns the grouped order when its packing
+    of the resident slots is at most 1/64 slower than the plain heaviest-first
+    order's, else the plain order."""
+
+    rng = np.random.default_rng(900 + seed)
+    n = int(rng.integers(2, 12))
+    computed = [int(c) for c in rng.integers(0, 4000, size=n)]
+    q_lens = [int(q) for q in rng.integers(64, 700, size=n)]
+    need = [(c + q + 15) // 16 for c, q in zip(computed, q_lens)]
+    perm = [int(x) for x in rng.permutation(sum(need) + 5)]
+    tables, off = [], 0
+    for k in need:
+        tables.append(tuple(perm[off: off + k]))
+        off += k
+    md = lv.PagedAttentionMetadata(block_tables=tuple(tables), num_computed_tokens=tuple(computed),
+                                   query_layouts=tuple(lv.linear_query_layout(q) for q in q_lens))
+    plan = StepPlan(md, block_size=16, device=CPU)
+    hkv, slots = 4, 128  # 512 resident workgroups over 4 kv heads
+    args = (7, hkv, 2048, 128, 64, 1, 64, slots * hkv)
+    auto = plan.work(*args, xcds=8, prefill_order=0).prefill_units.numpy()
+    grouped = plan.work(*args, xcds=8, prefill_order=1).prefill_units.numpy()
+    plain = plan.work(*args, xcds=8, prefill_order=2).prefill_units.numpy()
+    assert plain.tolist() == plan.work(*args, xcds=0).prefill_units.numpy().tolist()
+    mg, mp = (_makespan(u, 2, slots // 2, 7, 64) for u in (grouped, plain))
+    assert auto.tolist() == (grouped if mg * 64 <= mp * 65 else plain).tolist()
+
+
 def test_prefill_split_fills_the_resident_workgroups() -> None:
     # C5-like: tree verification of 9 queries at group 6 = 54 columns, one
     # unit per request; 4 requests x 32 key tiles over 16 slots per kv head.
@@ -519,15 +624,15 @@ def test_library_loads_and_exports_every_header_function() -> None:
     for bad_columns in (0, 17):  # the used columns must lie within a slot's 16 * col_tiles
         assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 1, bad_columns, 2,
                                                None) == -1
-    # Prefill: the workgroup shape must be 4 or 8 waves, and only the 8-wave
-    # shape takes this step's K/V (fused append); K without V is refused.
+    # Prefill: the workgroup shape must be 4 or 8 waves; K without V and
+    # misaligned step K/V are refused.
     x = ctypes.c_void_p(16)  # (never dereferenced: the checks run first)
     prefill = lambda nk, nv, waves: lib.lvamd_paged_prefill(  # noqa: E731
         x, 0, 0, nk, 0, 0, nv, 0, 0, x, x, x, 0, 0, x, x, x, 1, None, None, 0, 2, 7, 128, waves, 16,
         ctypes.c_float(0.1), 2, None)
     assert prefill(None, None, 5) == -1
     assert prefill(x, None, 8) == -1
-    assert prefill(x, x, 4) == -1
+    assert prefill(ctypes.c_void_p(8), x, 4) == -1 and prefill(x, ctypes.c_void_p(24), 8) == -1
     assert lib.lvamd_paged_prefill_waves_built(2, 128, 8) == 1 and lib.lvamd_paged_prefill_waves_built(2, 256, 8) == 0
     assert lib.lvamd_paged_prefill_waves_built(2, 256, 4) == 1 and lib.lvamd_paged_prefill_waves_built(0, 128, 4) == 0
     assert lib.lvamd_kv_append_rotary(None, 0, 0, None, 0, 0, None, 0, 0, None, 0, 0, None, 0, None, 0, None, None,
@@ -643,8 +748,8 @@ def _layer_shapes(bs: int) -> LayerShapes:
     one-query-per-head shape without them."""
 
     return LayerShapes((
-        (7, 4, bs, 128, 64, 1, 0, 0, 4, 1, 2048, 32, 1024, 16, 512, 256, 0, 16, 4, 4, 1),
-        (1, 8, bs, 256, 64, 0, 0, 0, 1, 0, 2048, 32, 0, 0, 512, 0, 0, 16, 4, 4, 0),
+        (7, 4, bs, 128, 64, 1, 0, 0, 4, 1, 2048, 32, 1024, 16, 512, 256, 0, 16, 4, 4, 1, 8, 0),
+        (1, 8, bs, 256, 64, 0, 0, 0, 1, 0, 2048, 32, 0, 0, 512, 0, 0, 16, 4, 4, 0, 0, 0),
     ))
 
 
@@ -688,7 +793,7 @@ def test_one_call_step_plan_equals_the_per_shape_plan(seed, small_buffer, monkey
             if ptr is not None:
                 assert base <= ptr and ptr + 4 * rows.numel() <= end and (ptr - base) % 64 == 0
     # A layer shape asked for later is planned on its own, from the records.
-    late = (4, 2, bs, 128, 64, 1, 0, 0, 4, 1, 2048, 32, 1024, 16, 512, 256, 0, 16, 4, 4, 1)
+    late = (4, 2, bs, 128, 64, 1, 0, 0, 4, 1, 2048, 32, 1024, 16, 512, 256, 0, 16, 4, 4, 1, 8, 1)
     assert one.layer_work(late).num_prefill_units == ref.layer_work(late).num_prefill_units
 
 
