@@ -50,7 +50,7 @@ constexpr float kRescaleSlack = 8.0f;  // log2 units: probabilities stay below 2
 constexpr int kPrefillKeyTile = 64;
 // Two shapes of the same 128-column unit, chosen per step by the planner:
 // * W = 4 waves of two 16-column tiles: each K/V LDS read feeds two MFMAs;
-//   256 registers per wave, two waves per SIMD (two workgroups per CU).
+//   up to 256 registers per wave, two waves per SIMD (two workgroups per CU).
 // * W = 8 waves of one column tile: half the registers (128), four waves per
 //   SIMD to hide the softmax's dependency chain, twice the LDS reads per MFMA.
 // W = 8 is faster on split-K and short units (tree verification, chunks
