@@ -285,6 +285,21 @@ int lvamd_kv_compact(const uint64_t* layer_key_ptrs, const uint64_t* layer_value
 int64_t lvamd_kv_compact_inline_pairs(void);
 
 /*
+ * lvamd_kv_compact for at most lvamd_kv_compact_inline_pairs() pairs given
+ * in HOST memory: the pairs travel in the kernel's arguments (one launch, no
+ * device index buffer, no upload).  Same rules and result as
+ * lvamd_kv_compact; more pairs return LVAMD_ERR_INVALID_ARGUMENT.
+ *
+ * Replaces: the same reference loop as lvamd_kv_compact
+ *   (src/light_vllm/runtime/execution/paged_cache.py:315-326), for the
+ *   per-step compacts of speculative decoding (a few accepted tokens).
+ */
+int lvamd_kv_compact_small(const uint64_t* layer_key_ptrs, const uint64_t* layer_value_ptrs,
+                           int32_t num_layers, int64_t row_bytes,
+                           const int64_t* src_slots, const int64_t* dst_slots, int64_t num_pairs,
+                           lvamd_stream_t stream);
+
+/*
  * Allocation-free variant of lvamd_kv_compact: the same kernels and result,
  * but calls with more than lvamd_kv_compact_inline_pairs() pairs stage their
  * rows in a device array the library holds (LVAMD_COMPACT_STATIC_SCRATCH_BYTES

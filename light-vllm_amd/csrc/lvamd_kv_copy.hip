@@ -207,9 +207,11 @@ static int common_vector_bytes(std::initializer_list<uint64_t> values) {
 // (layer, K|V, 16-byte column chunk) holds the chunk of every source row in
 // registers before it writes any destination, so every source is read before
 // it can be overwritten.  Larger calls gather into a workspace first and
-// scatter in a second, stream-ordered kernel.
+// scatter in a second, stream-ordered kernel.  lvamd_kv_compact_small runs
+// the inline kernel with the pairs in its kernel arguments (the launch
+// carries them: no index buffer, no upload).
 // ---------------------------------------------------------------------------
-constexpr int kCompactInline = 16;
+constexpr int kCompactInline = 32;
 
 struct CompactArgs {
   const uint64_t* kptrs;
@@ -222,8 +224,19 @@ struct CompactArgs {
   char* ws;
 };
 
-template <typename V>
-__global__ __launch_bounds__(256) void kv_compact_inline_kernel(const CompactArgs a) {
+// The pairs of lvamd_kv_compact_small, in the kernel arguments.
+struct CompactSmallArgs {
+  const uint64_t* kptrs;
+  const uint64_t* vptrs;
+  int32_t num_layers;
+  int64_t row_bytes;
+  int64_t num_pairs;
+  int64_t src[kCompactInline];
+  int64_t dst[kCompactInline];
+};
+
+template <typename V, typename Args>
+__global__ __launch_bounds__(256) void kv_compact_inline_kernel(const Args a) {
   const int64_t cpr = a.row_bytes / (int64_t)sizeof(V);
   const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= (int64_t)a.num_layers * 2 * cpr) return;
@@ -345,6 +358,19 @@ __global__ __launch_bounds__(256) void kv_block_copy_kernel(const BlockCopyArgs 
     }                                                                                   \
   } while (0)
 
+template <typename Args>
+static int launch_compact_inline(int width, int64_t items, hipStream_t s, const Args& a) {
+  const dim3 grid((unsigned)((items + 255) / 256));
+  switch (width) {
+    case 16: hipLaunchKernelGGL((kv_compact_inline_kernel<uint4, Args>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((kv_compact_inline_kernel<uint2, Args>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((kv_compact_inline_kernel<uint32_t, Args>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((kv_compact_inline_kernel<uint16_t, Args>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((kv_compact_inline_kernel<uint8_t, Args>), grid, dim3(256), 0, s, a); break;
+  }
+  return launch_status();
+}
+
 }  // namespace lvamd
 
 using namespace lvamd;
@@ -364,7 +390,7 @@ const char* lvamd_status_string(int status) {
   }
 }
 
-int lvamd_abi_version(void) { return 16; }
+int lvamd_abi_version(void) { return 17; }
 
 int lvamd_xcd_count(void) {
   int device = 0, xcds = 0;
@@ -503,12 +529,7 @@ int lvamd_kv_compact(const uint64_t* layer_key_ptrs, const uint64_t* layer_value
   // size alone decides the access width.
   const int width = common_vector_bytes({(uint64_t)row_bytes});
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (num_pairs <= kCompactInline) {
-    const int64_t items = (int64_t)num_layers * 2 * (row_bytes / width);
-    const unsigned blocks = (unsigned)((items + 255) / 256);
-    LVAMD_LAUNCH_BY_WIDTH(kv_compact_inline_kernel, width, dim3(blocks), dim3(256), s, a);
-    return launch_status();
-  }
+  if (num_pairs <= kCompactInline) return launch_compact_inline(width, (int64_t)num_layers * 2 * (row_bytes / width), s, a);
   const int64_t need = lvamd_kv_compact_workspace_size(num_pairs, num_layers, row_bytes);
   if (!workspace || workspace_bytes < need) return LVAMD_ERR_WORKSPACE;
   const int64_t items = num_pairs * num_layers * 2 * (row_bytes / width);
@@ -537,6 +558,28 @@ int lvamd_kv_compact(const uint64_t* layer_key_ptrs, const uint64_t* layer_value
       break;
   }
   return launch_status();
+}
+
+int lvamd_kv_compact_small(const uint64_t* layer_key_ptrs, const uint64_t* layer_value_ptrs,
+                           int32_t num_layers, int64_t row_bytes,
+                           const int64_t* src_slots, const int64_t* dst_slots, int64_t num_pairs,
+                           lvamd_stream_t stream) {
+  if (num_pairs < 0 || num_pairs > kCompactInline || num_layers <= 0 || row_bytes <= 0)
+    return LVAMD_ERR_INVALID_ARGUMENT;
+  if (num_pairs == 0) return LVAMD_OK;
+  if (!layer_key_ptrs || !layer_value_ptrs || !src_slots || !dst_slots) return LVAMD_ERR_INVALID_ARGUMENT;
+  CompactSmallArgs a;
+  a.kptrs = layer_key_ptrs;
+  a.vptrs = layer_value_ptrs;
+  a.num_layers = num_layers;
+  a.row_bytes = row_bytes;
+  a.num_pairs = num_pairs;
+  for (int64_t i = 0; i < kCompactInline; ++i) {
+    a.src[i] = i < num_pairs ? src_slots[i] : 0;
+    a.dst[i] = i < num_pairs ? dst_slots[i] : 0;
+  }
+  const int width = common_vector_bytes({(uint64_t)row_bytes});
+  return launch_compact_inline(width, (int64_t)num_layers * 2 * (row_bytes / width), static_cast<hipStream_t>(stream), a);
 }
 
 int lvamd_kv_compact_static(const uint64_t* layer_key_ptrs, const uint64_t* layer_value_ptrs,

@@ -19,7 +19,7 @@ from pathlib import Path
 from light_vllm_amd import errors
 
 LIB_NAME = "liblvamd_hip.so"
-ABI_VERSION = 16
+ABI_VERSION = 17
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
@@ -75,6 +75,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_p, _p, _i32, _i64, _p, _p, _i64, _p, _i64, _p],
     ),
     "lvamd_kv_compact_static": (
+        ctypes.c_int,
+        [_p, _p, _i32, _i64, _p, _p, _i64, _p],
+    ),
+    "lvamd_kv_compact_small": (
         ctypes.c_int,
         [_p, _p, _i32, _i64, _p, _p, _i64, _p],
     ),

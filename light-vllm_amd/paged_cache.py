@@ -99,8 +99,9 @@ class PagedKVWriteMapping:
 
 class _CacheState:
     """Per-cache launch state: device arrays of per-layer K and V base
-    addresses grouped by row size, a staging ring for the index uploads,
-    and the compact workspace (grown on demand)."""
+    addresses grouped by row size (with their K and V addresses as ints),
+    a staging ring for the index uploads, the compact workspace (grown on
+    demand) and the compact kernel's inline pair limit."""
 
     def __init__(self, cache) -> None:
         device = cache.config.device
@@ -109,10 +110,13 @@ class _CacheState:
             layer = cache.layer(spec.layer_id)
             row_bytes = spec.num_kv_heads * spec.head_size * layer.keys.element_size()
             groups.setdefault(row_bytes, []).append((layer.keys.data_ptr(), layer.values.data_ptr()))
-        self.groups: list[tuple[int, int, Tensor]] = []
+        # (row bytes, layers, [K addresses | V addresses] device table, its K
+        # and V halves' addresses); the table is kept alive with its addresses.
+        self.groups: list[tuple[int, int, Tensor, int, int]] = []
         for row_bytes, ptrs in groups.items():
             table = torch.tensor(ptrs, dtype=torch.int64).t().contiguous().to(device)
-            self.groups.append((row_bytes, len(ptrs), table))
+            self.groups.append((row_bytes, len(ptrs), table, table.data_ptr(), table.data_ptr() + 8 * len(ptrs)))
+        self.inline_pairs = int(native.load().lvamd_kv_compact_inline_pairs())
         self.staging = Staging(device)
         self._device = device
         self._workspace: Tensor | None = None
@@ -293,6 +297,16 @@ def _launch_compact(cache, src: np.ndarray, dst: np.ndarray) -> None:
     pointers = _layer_pointers(cache)
     device = cache.config.device
     n = int(src.size)
+    lib = native.load()
+    stream = current_stream(device)
+    if n <= pointers.inline_pairs:
+        # A few pairs (a step's accepted tokens) ride in the kernel arguments.
+        src = np.ascontiguousarray(src, dtype=np.int64)
+        dst = np.ascontiguousarray(dst, dtype=np.int64)
+        for row_bytes, num_layers, _, kptrs, vptrs in pointers.groups:
+            native.check(lib.lvamd_kv_compact_small(kptrs, vptrs, num_layers, row_bytes, src.ctypes.data,
+                                                    dst.ctypes.data, n, stream), "lvamd_kv_compact_small")
+        return
     # [src | dst] as int64 pairs of int32 words, in one pinned buffer and copy.
     buf = pointers.staging.take(4 * n)
     buf[: 2 * n] = src.view(np.int32)
@@ -300,13 +314,11 @@ def _launch_compact(cache, src: np.ndarray, dst: np.ndarray) -> None:
     blob = pointers.staging.upload(buf[: 4 * n])
     src_ptr = blob.data_ptr()
     dst_ptr = src_ptr + 8 * n
-    lib = native.load()
-    stream = current_stream(device)
-    for row_bytes, num_layers, ptrs in pointers.groups:
+    for row_bytes, num_layers, _, kptrs, vptrs in pointers.groups:
         ws_bytes = lib.lvamd_kv_compact_workspace_size(n, num_layers, row_bytes)
         workspace = pointers.workspace(ws_bytes) if ws_bytes else None
         status = lib.lvamd_kv_compact(
-            ptrs[0].data_ptr(), ptrs[1].data_ptr(), num_layers, row_bytes,
+            kptrs, vptrs, num_layers, row_bytes,
             src_ptr, dst_ptr, n, workspace.data_ptr() if workspace is not None else None, ws_bytes, stream,
         )
         native.check(status, "lvamd_kv_compact")
@@ -340,9 +352,9 @@ def hip_block_copy(cache, src_blocks, dst_blocks) -> None:
     lib = native.load()
     stream = current_stream(cache.config.device)
     bs = cache.config.block_size
-    for row_bytes, num_layers, ptrs in pointers.groups:
+    for row_bytes, num_layers, _, kptrs, vptrs in pointers.groups:
         status = lib.lvamd_kv_block_copy(
-            ptrs[0].data_ptr(), ptrs[1].data_ptr(), num_layers, row_bytes * bs,
+            kptrs, vptrs, num_layers, row_bytes * bs,
             blob.data_ptr() + 4 * src_off, blob.data_ptr() + 4 * dst_off, len(src), stream,
         )
         native.check(status, "lvamd_kv_block_copy")

@@ -1,0 +1,66 @@
+"""GPU: ``lvamd_kv_compact_small`` (pairs in the kernel arguments) through
+the C ABI, against the closed form and against ``lvamd_kv_compact`` with the
+same pairs in device memory.
+
+Row dst[i] of every layer's K and V must hold what row src[i] held before
+the call (sources may repeat and may be destinations: every source is read
+before any destination is written); every other row is unchanged.  Row sizes
+cover each access width the kernel picks (16, 8, 4 and 2 bytes).
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from light_vllm_amd import native
+
+pytestmark = pytest.mark.gpu
+if not torch.cuda.is_available():
+    pytest.skip("needs an MI355X GPU", allow_module_level=True)
+
+DEV = torch.device("cuda:0")
+LAYERS, SLOTS = 3, 512
+
+
+def _pools(seed: int, row: int):
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    return [(torch.randint(-30000, 30000, (SLOTS, row), generator=gen, device=DEV, dtype=torch.int16),
+             torch.randint(-30000, 30000, (SLOTS, row), generator=gen, device=DEV, dtype=torch.int16))
+            for _ in range(LAYERS)]
+
+
+def _tables(pools):
+    keys = torch.tensor([k.data_ptr() for k, _ in pools], dtype=torch.int64, device=DEV)
+    values = torch.tensor([v.data_ptr() for _, v in pools], dtype=torch.int64, device=DEV)
+    return keys, values
+
+
+@pytest.mark.parametrize("row", (256, 36, 18, 9))  # int16 elements: 512, 72, 36, 18 bytes
+@pytest.mark.parametrize("n", (1, 7, 17, 32))
+def test_small_compact_matches_the_closed_form_and_the_device_pair_compact(n, row) -> None:
+    print(f"[gpu] small compact n={n} row={2 * row} bytes", file=sys.stderr, flush=True)
+    lib = native.load()
+    stream = torch.cuda.current_stream(DEV).cuda_stream
+    rng = np.random.default_rng(n * 1000 + row)
+    dst = rng.permutation(SLOTS)[:n].astype(np.int64)
+    src = rng.integers(0, SLOTS, size=n).astype(np.int64)
+    small, device_pairs = _pools(row, row), _pools(row, row)
+    before = [(k.cpu().numpy(), v.cpu().numpy()) for k, v in small]
+    sk, sv = _tables(small)
+    dk, dv = _tables(device_pairs)
+    native.check(lib.lvamd_kv_compact_small(sk.data_ptr(), sv.data_ptr(), LAYERS, 2 * row, src.ctypes.data,
+                                            dst.ctypes.data, n, stream), "lvamd_kv_compact_small")
+    src_d, dst_d = torch.tensor(src, device=DEV), torch.tensor(dst, device=DEV)
+    native.check(lib.lvamd_kv_compact(dk.data_ptr(), dv.data_ptr(), LAYERS, 2 * row, src_d.data_ptr(),
+                                      dst_d.data_ptr(), n, None, 0, stream), "lvamd_kv_compact")
+    torch.cuda.synchronize()
+    for layer, ((gk, gv), (rk, rv), (bk, bv)) in enumerate(zip(small, device_pairs, before)):
+        for got, ref, pool in ((gk, rk, bk), (gv, rv, bv)):
+            expect = pool.copy()
+            expect[dst] = pool[src]
+            np.testing.assert_array_equal(got.cpu().numpy(), expect, err_msg=f"layer {layer}: closed form")
+            np.testing.assert_array_equal(got.cpu().numpy(), ref.cpu().numpy(), err_msg=f"layer {layer}: device pairs")

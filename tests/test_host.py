@@ -603,12 +603,15 @@ def test_library_loads_and_exports_every_header_function() -> None:
         assert name in native.SIGNATURES, f"{name} has no ctypes signature"
     assert lib.lvamd_abi_version() == native.ABI_VERSION
     assert lib.lvamd_status_string(-3).decode() == "workspace missing or too small"
-    assert lib.lvamd_kv_compact_inline_pairs() == 16
-    assert lib.lvamd_kv_compact_workspace_size(17, 28, 1024) == 17 * 28 * 2 * 1024
+    assert lib.lvamd_kv_compact_inline_pairs() == 32
+    assert lib.lvamd_kv_compact_workspace_size(32, 28, 1024) == 0
+    assert lib.lvamd_kv_compact_workspace_size(33, 28, 1024) == 33 * 28 * 2 * 1024
+    # The small compact takes at most the inline pair count (refused before any HIP call).
+    assert lib.lvamd_kv_compact_small(None, None, 28, 1024, None, None, 33, None) == -1
     # The allocation-free compact refuses, before any HIP call, a call whose
     # staged rows exceed its static scratch (16 MiB): 16 MiB / (28 * 2 * 1024) = 292 pairs.
     assert lib.lvamd_kv_compact_static(None, None, 28, 1024, None, None, 293, None) == -5
-    assert lib.lvamd_kv_compact_static(None, None, 28, 1 << 40, None, None, 17, None) == -5
+    assert lib.lvamd_kv_compact_static(None, None, 28, 1 << 40, None, None, 33, None) == -5
     assert "static scratch" in lib.lvamd_status_string(-5).decode()
     # Argument checks run before any HIP call, so they are safe without a GPU.
     assert lib.lvamd_kv_append(None, 0, 0, None, 0, 0, None, None, None, 1, 2, 64, 2, None) == -1
