@@ -595,6 +595,16 @@ class C1:
     seed = 1
 
 
+def _emit(rec: dict, emit: bool):
+    """Print a config's JSON line (its own run), or hand the record back (the
+    default run's summary of every config)."""
+
+    if not emit:
+        return rec
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
 def run_c1(args, device) -> int:
     cfg = C1
     rng = np.random.default_rng(cfg.seed)
@@ -648,7 +658,7 @@ class C3:
     sets = 3
 
 
-def run_c3(args, device) -> int:
+def run_c3(args, device, emit: bool = True):
     cfg = C3
     rng = np.random.default_rng(cfg.seed)
     computed = [int(c) for c in rng.integers(cfg.prior[0], cfg.prior[1] + 1, size=cfg.n_prefill)]
@@ -730,8 +740,7 @@ def run_c3(args, device) -> int:
         sflops = 4 * cfg.hq * cfg.d * sum(c0 + j + 1 for j in range(nq))
         rec["cpu_baseline"] = {"value": round(sflops / sec / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
                                "sample": f"16 queries of the first prefill chunk (context {c0}) x{n}, numpy oracle"}
-    print(json.dumps(rec), flush=True)
-    return 0
+    return _emit(rec, emit)
 
 
 class C4:
@@ -740,7 +749,7 @@ class C4:
     seed = 4004
 
 
-def run_c4(args, device) -> int:
+def run_c4(args, device, emit: bool = True):
     cfg = C4
     rng = np.random.default_rng(cfg.seed)
     per_seq = (cfg.ctx + 1 + cfg.bs - 1) // cfg.bs
@@ -793,8 +802,7 @@ def run_c4(args, device) -> int:
         rec["cpu_baseline"] = {"value": round(L * 2 * cfg.hkv * cfg.d * 2 / sec / 1e9, 4), "unit": "GB/s",
                                "cores": 1, "kind": "port",
                                "sample": f"1 sequence x 1 layer (32769 keys) x{n}, numpy oracle"}
-    print(json.dumps(rec), flush=True)
-    return 0
+    return _emit(rec, emit)
 
 
 class C5:
@@ -885,7 +893,7 @@ def build_c5(device, col_tiles=None, prefill_order="auto"):
                            attend_torch_rotary=attend_torch_rotary)
 
 
-def run_c5(args, device) -> int:
+def run_c5(args, device, emit: bool = True):
     w = build_c5(device, args.col_tiles, args.prefill_order)
     cfg, cache, q, tables, computed, layouts = w.cfg, w.cache, w.q, w.tables, w.computed, w.layouts
     suffix, q_len, accepted, scale = w.suffix, w.q_len, w.accepted, w.scale
@@ -940,8 +948,30 @@ def run_c5(args, device) -> int:
         rec["cpu_baseline"] = {"value": round(sec * cfg.layers * 1e6, 1), "unit": "us", "cores": 1, "kind": "port",
                                "sample": f"tree attention of 1 layer (32 seqs) x{n}, numpy oracle, "
                                          f"x28 layers extrapolated (COW and compact not included)"}
-    print(json.dumps(rec), flush=True)
-    return 0
+    return _emit(rec, emit)
+
+
+def other_configs(args, device) -> dict:
+    """The C3, C4 and C5 metrics in the default run (fewer steps, no CPU
+    baselines): each config's own ``--config`` line, reduced to its metric,
+    value, roofline fraction and step time."""
+
+    sub = argparse.Namespace(**{**vars(args), "steps": min(args.steps, 50), "warmup": min(args.warmup, 5),
+                                "no_cpu_baseline": True, "no_rotary": True})
+    out = {}
+    for name, fn in (("c3", run_c3), ("c4", run_c4), ("c5", run_c5)):
+        print(f"[bench] {name} summary", file=sys.stderr, flush=True)
+        rec = fn(sub, device, emit=False)
+        keep = {k: rec[k] for k in ("metric", "value", "unit", "higher_is_better", "ms_per_step") if k in rec}
+        if "roofline" in rec:
+            keep["roofline_frac"] = rec["roofline"]["frac"]
+        for k in ("prefill_kernel_us", "pct_of_hbm_peak", "attention_us", "compact_host_us"):
+            if k in rec:
+                keep[k] = rec[k]
+        keep["steps"] = rec.get("steps", sub.steps)
+        out[name] = keep
+        torch.cuda.empty_cache()
+    return out
 
 
 def main() -> int:
@@ -966,6 +996,8 @@ def main() -> int:
                         help="fix the decode kernel's column tiles per wave (default: the planner's choice)")
     parser.add_argument("--prefill-order", choices=("auto", "grouped", "plain"), default="auto",
                         help="per-XCD order of the prefill grid (C3, C5; default: the planner's choice)")
+    parser.add_argument("--no-configs", action="store_true",
+                        help="skip the default run's summary of the C3, C4 and C5 metrics")
     parser.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5"), default="c2",
                         help="BASELINE config (default c2, the headline metric); the others report their own metric")
     args = parser.parse_args()
@@ -1112,6 +1144,8 @@ def main() -> int:
     if traffic is not None:
         record["roofline"]["traffic"] = traffic["bytes_per_launch"]
         record["roofline"]["traffic_source"] = traffic["source"]
+    if not args.no_configs:
+        record["other_configs"] = other_configs(args, device)
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
         record["cpu_baseline"] = cpu_vectorized_baseline(metadata, caches[0], q, k, v, ctx,
