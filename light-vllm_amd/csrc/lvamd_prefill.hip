@@ -25,8 +25,13 @@
 //     column l%16, keys 4*(l/16)+r) is the B operand of O^T = V^T P^T, whose
 //     V^T A operand comes from LDS by ds_read_b64_tr_b16 transpose reads, also
 //     shared by the column tiles.
-//   * Online softmax in the log2 domain with lazy rescaling (wave vote), max
-//     and sum across the four 16-lane rows with permlane swaps.
+//   * Online softmax in the log2 domain with lazy rescaling (wave vote), the
+//     max across the four 16-lane rows with permlane swaps; the sums come
+//     from the matrix cores (a ones row times P^T).
+//   * The append is fused: keys of this step's tokens are read from the
+//     step's K/V, and the unit that holds a token's own query writes its row
+//     to the pool.
+//   * A record with zero columns is padding of the planner's per-XCD order.
 //   * Split-K: a unit may cover a key range of its request (a piece); a piece
 //     that is not the whole range writes fp32 (max, sum, acc) partials that
 //     lvamd_paged_attention_merge combines.  The host splits units when there
