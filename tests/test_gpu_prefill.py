@@ -133,6 +133,26 @@ def test_c3_shape_mixed_batch(waves) -> None:
     _check(step, dense=True, waves=waves)
 
 
+@pytest.mark.parametrize("waves", WAVES)
+def test_per_xcd_orders_give_identical_outputs(waves) -> None:
+    # The per-XCD order only decides which workgroup runs which unit (and
+    # adds padding records): the grouped and plain orders give bit-identical
+    # outputs, each also checked against the oracle.
+    _announce(f"per-XCD orders waves={waves}")
+    rng = np.random.default_rng(31)
+    computed = [int(c) for c in rng.integers(0, 2000, size=5)]
+    step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=computed,
+                     layouts=_lin(*(int(q) for q in rng.integers(100, 420, size=5))), seed=31)
+    outs, units = {}, {}
+    for order in ("grouped", "plain"):
+        backend = lv.HipPagedAttentionBackend(prefill_waves=waves, prefill_order=order)
+        outs[order] = _check(step, backend=backend, waves=waves)
+        ctx = backend.create(step.cache, step.metadata)
+        units[order] = ctx.work_of(step.cache.layer_spec(step.layer_ids[0])).prefill_units.numpy()
+    assert units["grouped"].tolist() != units["plain"].tolist()
+    assert torch.equal(outs["grouped"], outs["plain"])
+
+
 def test_prefill_kernel_agrees_with_the_decode_path() -> None:
     _announce("prefill vs decode path")
     step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[200, 0],
