@@ -337,6 +337,19 @@ int lvamd_kv_block_copy(const uint64_t* layer_key_ptrs, const uint64_t* layer_va
                         lvamd_stream_t stream);
 
 /*
+ * lvamd_kv_block_copy for at most lvamd_kv_block_copy_small_pairs() pairs
+ * given in HOST memory: the pairs travel in the kernel's arguments (no device
+ * index buffer, no upload).  Same rules and result as lvamd_kv_block_copy;
+ * more pairs return LVAMD_ERR_INVALID_ARGUMENT.  No reference counterpart
+ * (as lvamd_kv_block_copy): a step's copy-on-write of a few partial pages.
+ */
+int lvamd_kv_block_copy_small(const uint64_t* layer_key_ptrs, const uint64_t* layer_value_ptrs,
+                              int32_t num_layers, int64_t block_bytes,
+                              const int64_t* src_blocks, const int64_t* dst_blocks, int64_t num_pairs,
+                              lvamd_stream_t stream);
+int64_t lvamd_kv_block_copy_small_pairs(void);
+
+/*
  * The per-step upload of a staged plan: copies bytes from pinned host memory
  * to device memory on stream (asynchronous), then records event (a
  * hipEvent_t; NULL for none) on stream, so the caller can tell when the

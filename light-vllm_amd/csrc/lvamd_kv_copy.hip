@@ -332,8 +332,19 @@ struct BlockCopyArgs {
   const int64_t* dst;
 };
 
-template <typename V>
-__global__ __launch_bounds__(256) void kv_block_copy_kernel(const BlockCopyArgs a) {
+// The pairs of lvamd_kv_block_copy_small, in the kernel arguments.
+constexpr int kBlockCopySmall = 32;
+struct BlockCopySmallArgs {
+  const uint64_t* kptrs;
+  const uint64_t* vptrs;
+  int32_t num_layers;
+  int64_t block_bytes;
+  int64_t src[kBlockCopySmall];
+  int64_t dst[kBlockCopySmall];
+};
+
+template <typename V, typename Args = BlockCopyArgs>
+__global__ __launch_bounds__(256) void kv_block_copy_kernel(const Args a) {
   const int64_t idx = blockIdx.x;
   const int64_t pair = idx / (2 * a.num_layers);
   const int64_t lk = idx - pair * 2 * a.num_layers;
@@ -390,7 +401,7 @@ const char* lvamd_status_string(int status) {
   }
 }
 
-int lvamd_abi_version(void) { return 17; }
+int lvamd_abi_version(void) { return 18; }
 
 int lvamd_xcd_count(void) {
   int device = 0, xcds = 0;
@@ -597,6 +608,37 @@ int lvamd_kv_compact_static(const uint64_t* layer_key_ptrs, const uint64_t* laye
   }
   return lvamd_kv_compact(layer_key_ptrs, layer_value_ptrs, num_layers, row_bytes, src_slots, dst_slots, num_pairs,
                           ws, ws ? kStaticScratchBytes : 0, stream);
+}
+
+int64_t lvamd_kv_block_copy_small_pairs(void) { return kBlockCopySmall; }
+
+int lvamd_kv_block_copy_small(const uint64_t* layer_key_ptrs, const uint64_t* layer_value_ptrs,
+                              int32_t num_layers, int64_t block_bytes,
+                              const int64_t* src_blocks, const int64_t* dst_blocks, int64_t num_pairs,
+                              lvamd_stream_t stream) {
+  if (num_pairs < 0 || num_pairs > kBlockCopySmall || num_layers <= 0 || block_bytes <= 0)
+    return LVAMD_ERR_INVALID_ARGUMENT;
+  if (num_pairs == 0) return LVAMD_OK;
+  if (!layer_key_ptrs || !layer_value_ptrs || !src_blocks || !dst_blocks) return LVAMD_ERR_INVALID_ARGUMENT;
+  BlockCopySmallArgs a;
+  a.kptrs = layer_key_ptrs;
+  a.vptrs = layer_value_ptrs;
+  a.num_layers = num_layers;
+  a.block_bytes = block_bytes;
+  for (int64_t i = 0; i < kBlockCopySmall; ++i) {
+    a.src[i] = i < num_pairs ? src_blocks[i] : 0;
+    a.dst[i] = i < num_pairs ? dst_blocks[i] : 0;
+  }
+  const dim3 grid((unsigned)(num_pairs * 2 * num_layers));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (common_vector_bytes({(uint64_t)block_bytes})) {
+    case 16: hipLaunchKernelGGL((kv_block_copy_kernel<uint4, BlockCopySmallArgs>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((kv_block_copy_kernel<uint2, BlockCopySmallArgs>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((kv_block_copy_kernel<uint32_t, BlockCopySmallArgs>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((kv_block_copy_kernel<uint16_t, BlockCopySmallArgs>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((kv_block_copy_kernel<uint8_t, BlockCopySmallArgs>), grid, dim3(256), 0, s, a); break;
+  }
+  return launch_status();
 }
 
 int lvamd_kv_block_copy(const uint64_t* layer_key_ptrs, const uint64_t* layer_value_ptrs,

@@ -117,6 +117,7 @@ class _CacheState:
             table = torch.tensor(ptrs, dtype=torch.int64).t().contiguous().to(device)
             self.groups.append((row_bytes, len(ptrs), table, table.data_ptr(), table.data_ptr() + 8 * len(ptrs)))
         self.inline_pairs = int(native.load().lvamd_kv_compact_inline_pairs())
+        self.small_copies = int(native.load().lvamd_kv_block_copy_small_pairs())
         self.staging = Staging(device)
         self._device = device
         self._workspace: Tensor | None = None
@@ -347,11 +348,20 @@ def hip_block_copy(cache, src_blocks, dst_blocks) -> None:
     if not src:
         return
     pointers = _layer_pointers(cache)
-    blob, (src_off, dst_off) = pointers.staging.stage([np.asarray(src, dtype=np.int64).view(np.int32),
-                                                       np.asarray(dst, dtype=np.int64).view(np.int32)])
     lib = native.load()
     stream = current_stream(cache.config.device)
     bs = cache.config.block_size
+    if len(src) <= pointers.small_copies:
+        # A step's few copies ride in the kernel arguments.
+        src_a = np.asarray(src, dtype=np.int64)
+        dst_a = np.asarray(dst, dtype=np.int64)
+        for row_bytes, num_layers, _, kptrs, vptrs in pointers.groups:
+            native.check(lib.lvamd_kv_block_copy_small(kptrs, vptrs, num_layers, row_bytes * bs, src_a.ctypes.data,
+                                                       dst_a.ctypes.data, len(src), stream),
+                         "lvamd_kv_block_copy_small")
+        return
+    blob, (src_off, dst_off) = pointers.staging.stage([np.asarray(src, dtype=np.int64).view(np.int32),
+                                                       np.asarray(dst, dtype=np.int64).view(np.int32)])
     for row_bytes, num_layers, _, kptrs, vptrs in pointers.groups:
         status = lib.lvamd_kv_block_copy(
             kptrs, vptrs, num_layers, row_bytes * bs,

@@ -1,11 +1,13 @@
-"""GPU: ``lvamd_kv_compact_small`` (pairs in the kernel arguments) through
-the C ABI, against the closed form and against ``lvamd_kv_compact`` with the
-same pairs in device memory.
+"""GPU: ``lvamd_kv_compact_small`` and ``lvamd_kv_block_copy_small`` (pairs
+in the kernel arguments) through the C ABI, against the closed form and
+against ``lvamd_kv_compact`` / ``lvamd_kv_block_copy`` with the same pairs in
+device memory.
 
-Row dst[i] of every layer's K and V must hold what row src[i] held before
-the call (sources may repeat and may be destinations: every source is read
-before any destination is written); every other row is unchanged.  Row sizes
-cover each access width the kernel picks (16, 8, 4 and 2 bytes).
+Compact: row dst[i] of every layer's K and V must hold what row src[i] held
+before the call (sources may repeat and may be destinations: every source is
+read before any destination is written); every other row is unchanged.
+Block copy: block dst[i] becomes block src[i] (disjoint sets).  Row sizes
+cover each access width the kernels pick (16, 8, 4 and 2 bytes).
 """
 
 from __future__ import annotations
@@ -57,6 +59,33 @@ def test_small_compact_matches_the_closed_form_and_the_device_pair_compact(n, ro
     src_d, dst_d = torch.tensor(src, device=DEV), torch.tensor(dst, device=DEV)
     native.check(lib.lvamd_kv_compact(dk.data_ptr(), dv.data_ptr(), LAYERS, 2 * row, src_d.data_ptr(),
                                       dst_d.data_ptr(), n, None, 0, stream), "lvamd_kv_compact")
+    torch.cuda.synchronize()
+    for layer, ((gk, gv), (rk, rv), (bk, bv)) in enumerate(zip(small, device_pairs, before)):
+        for got, ref, pool in ((gk, rk, bk), (gv, rv, bv)):
+            expect = pool.copy()
+            expect[dst] = pool[src]
+            np.testing.assert_array_equal(got.cpu().numpy(), expect, err_msg=f"layer {layer}: closed form")
+            np.testing.assert_array_equal(got.cpu().numpy(), ref.cpu().numpy(), err_msg=f"layer {layer}: device pairs")
+
+
+@pytest.mark.parametrize("row", (256, 18))  # int16 elements per block: 512 and 36 bytes
+@pytest.mark.parametrize("n", (1, 9, 32))
+def test_small_block_copy_matches_the_closed_form_and_the_device_pair_copy(n, row) -> None:
+    print(f"[gpu] small block copy n={n} block={2 * row} bytes", file=sys.stderr, flush=True)
+    lib = native.load()
+    stream = torch.cuda.current_stream(DEV).cuda_stream
+    rng = np.random.default_rng(n * 100 + row)
+    perm = rng.permutation(SLOTS)
+    src, dst = perm[:n].astype(np.int64), perm[n: 2 * n].astype(np.int64)
+    small, device_pairs = _pools(row + 1, row), _pools(row + 1, row)
+    before = [(k.cpu().numpy(), v.cpu().numpy()) for k, v in small]
+    sk, sv = _tables(small)
+    dk, dv = _tables(device_pairs)
+    native.check(lib.lvamd_kv_block_copy_small(sk.data_ptr(), sv.data_ptr(), LAYERS, 2 * row, src.ctypes.data,
+                                               dst.ctypes.data, n, stream), "lvamd_kv_block_copy_small")
+    src_d, dst_d = torch.tensor(src, device=DEV), torch.tensor(dst, device=DEV)
+    native.check(lib.lvamd_kv_block_copy(dk.data_ptr(), dv.data_ptr(), LAYERS, 2 * row, src_d.data_ptr(),
+                                         dst_d.data_ptr(), n, stream), "lvamd_kv_block_copy")
     torch.cuda.synchronize()
     for layer, ((gk, gv), (rk, rv), (bk, bv)) in enumerate(zip(small, device_pairs, before)):
         for got, ref, pool in ((gk, rk, bk), (gv, rv, bv)):

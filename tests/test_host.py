@@ -608,6 +608,8 @@ def test_library_loads_and_exports_every_header_function() -> None:
     assert lib.lvamd_kv_compact_workspace_size(33, 28, 1024) == 33 * 28 * 2 * 1024
     # The small compact takes at most the inline pair count (refused before any HIP call).
     assert lib.lvamd_kv_compact_small(None, None, 28, 1024, None, None, 33, None) == -1
+    assert lib.lvamd_kv_block_copy_small_pairs() == 32
+    assert lib.lvamd_kv_block_copy_small(None, None, 28, 8192, None, None, 33, None) == -1
     # The allocation-free compact refuses, before any HIP call, a call whose
     # staged rows exceed its static scratch (16 MiB): 16 MiB / (28 * 2 * 1024) = 292 pairs.
     assert lib.lvamd_kv_compact_static(None, None, 28, 1024, None, None, 293, None) == -5
