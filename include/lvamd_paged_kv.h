@@ -147,9 +147,10 @@ int lvamd_kv_append_rotary(const void* query, int64_t query_token_stride, int64_
  * h * waves_per_head + w, one wave64 each) processes pieces
  * [wave_first[w], wave_first[w + 1]) (LVAMD_PIECE_FIELDS int32 each).  A
  * piece with partial_slot -1 covers its whole segment and writes out; the
- * others write fp32 (max, sum, acc) partials to part_acc
- * [slots][num_kv_heads][16 * col_tiles][head_size] and part_ml
- * [slots][num_kv_heads][16 * col_tiles][2] for lvamd_paged_attention_merge.
+ * others write partials for lvamd_paged_attention_merge: each column's
+ * output row normalised by its own softmax sum, in the pool's element type,
+ * to part_acc [slots][num_kv_heads][16 * col_tiles][head_size], and its fp32
+ * (max, sum) to part_ml [slots][num_kv_heads][16 * col_tiles][2].
  *
  * Append: when new_key / new_value are given ([tokens][num_kv_heads][D] with
  * the given strides), keys and values at positions >= computed are read from
@@ -179,7 +180,7 @@ int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_str
                        void* out, int64_t out_token_stride, int64_t out_head_stride,
                        const int32_t* pieces, const int32_t* wave_first, int32_t waves_per_head,
                        const int32_t* tables, const uint32_t* vis,
-                       float* part_acc, float* part_ml, int64_t num_partial_slots,
+                       void* part_acc, float* part_ml, int64_t num_partial_slots,
                        int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t col_tiles,
                        int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream);
 
@@ -199,11 +200,13 @@ int lvamd_paged_decode_tile_tokens(int32_t dtype, int32_t head_size, int32_t col
  * 16 * col_tiles) columns of each job (the most any job has; the host knows
  * it); jobs [num_jobs][LVAMD_MERGE_FIELDS]; col_tiles (1 to 16) is
  * the number of 16-column tiles per partial slot the partials were written
- * with (the decode kernel's col_tiles, or prefill unit columns / 16).  Same reference functions as lvamd_paged_decode:
+ * with (the decode kernel's col_tiles, or prefill unit columns / 16).
+ * Partial i of a column weighs sum_i * 2^(max_i - max) (max, sum in the
+ * log2 domain); part_acc holds rows of dtype.  Same reference functions as lvamd_paged_decode:
  * the reference has no split-K, and this is the cross-partition half of that
  * computation.
  */
-int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
+int lvamd_paged_attention_merge(const void* part_acc, const float* part_ml,
                                 void* out, int64_t out_token_stride, int64_t out_head_stride,
                                 const int32_t* jobs, int32_t num_jobs,
                                 int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t col_tiles,
@@ -220,9 +223,10 @@ int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
  * LDS (direct loads, double-buffered) and shared by the workgroup's waves; QK^T and PV on MFMA 16x16x32, fp32 online
  * softmax.  waves (4 or 8) picks the workgroup shape for the same unit: four
  * waves of two 16-column tiles or eight waves of one (8 only where
- * lvamd_paged_prefill_waves_built says so).  Units with a partial slot write fp32 partials to part_acc
- * [slots][num_kv_heads][unit columns][head_size] and part_ml
- * [slots][num_kv_heads][unit columns][2]; lvamd_paged_attention_merge with
+ * lvamd_paged_prefill_waves_built says so).  Units with a partial slot write partials in the
+ * decode kernel's format (normalised rows of the pool's type to part_acc
+ * [slots][num_kv_heads][unit columns][head_size], fp32 (max, sum) to part_ml
+ * [slots][num_kv_heads][unit columns][2]); lvamd_paged_attention_merge with
  * col_tiles = unit columns / 16 combines them.
  * A record with zero columns (field 2) is padding and does nothing (the
  * planner orders units per XCD).
@@ -242,7 +246,7 @@ int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_st
                         void* out, int64_t out_token_stride, int64_t out_head_stride,
                         const int32_t* tables, const uint32_t* vis,
                         const int32_t* units, int32_t num_units,
-                        float* part_acc, float* part_ml, int64_t num_partial_slots,
+                        void* part_acc, float* part_ml, int64_t num_partial_slots,
                         int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t waves,
                         int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream);
 

@@ -72,9 +72,9 @@ class _Workspace:
     def __init__(self) -> None:
         self._buffer: Tensor | None = None
 
-    def get(self, num_floats: int, device: torch.device) -> Tensor:
-        if self._buffer is None or self._buffer.numel() < num_floats or self._buffer.device != device:
-            self._buffer = torch.empty(max(num_floats, 1), dtype=torch.float32, device=device)
+    def get(self, num_bytes: int, device: torch.device) -> Tensor:
+        if self._buffer is None or self._buffer.numel() < num_bytes or self._buffer.device != device:
+            self._buffer = torch.empty(max(num_bytes, 1), dtype=torch.uint8, device=device)
         return self._buffer
 
     def ptr(self) -> int | None:
@@ -90,13 +90,15 @@ def _rows_aligned(t: Tensor) -> bool:
     ) % 16 == 0
 
 
-def _workspace_floats(work, spec, prefill_columns: int) -> tuple[int, int]:
-    """(decode partial floats, prefill partial floats) of a layer shape's work."""
+def _partial_layout(work, spec, prefill_columns: int, element_size: int) -> tuple[int, int, int, int]:
+    """Byte sizes of a layer shape's split-K partials: (decode rows, decode
+    (max, sum) pairs, prefill rows, prefill pairs).  A row is one column's
+    normalised output in the pool's element type, a pair two fp32; every
+    size is a multiple of 16 bytes (columns come in tiles of 16)."""
 
-    per_row = spec.head_size + 2
-    dec = work.num_partial_slots * spec.num_kv_heads * 16 * work.col_tiles * per_row
-    pre = work.num_prefill_partial_slots * spec.num_kv_heads * prefill_columns * per_row
-    return dec, pre
+    dec = work.num_partial_slots * spec.num_kv_heads * 16 * work.col_tiles
+    pre = work.num_prefill_partial_slots * spec.num_kv_heads * prefill_columns
+    return dec * spec.head_size * element_size, dec * 8, pre * spec.head_size * element_size, pre * 8
 
 
 class _LayerLaunch:
@@ -110,20 +112,20 @@ class _LayerLaunch:
                  "workspace_ptr")
 
     def __init__(self, plan: StepPlan, work, spec, dtype: int, block_size: int, workspace_ptr: int | None,
-                 prefill_columns: int) -> None:
+                 prefill_columns: int, sizes: tuple[int, int, int, int]) -> None:
         group = spec.num_query_heads // spec.num_kv_heads
         self.work = work
         self.dtype = dtype
         self.workspace_ptr = workspace_ptr
         self.decode_args = self.merge_args = self.prefill_args = self.prefill_merge_args = None
-        dec_floats, pre_floats = _workspace_floats(work, spec, prefill_columns)
+        dec_rows, dec_pairs, pre_rows, pre_pairs = sizes
         part_acc = part_ml = pre_acc = pre_ml = None
-        if dec_floats:
+        if dec_rows:
             part_acc = workspace_ptr
-            part_ml = part_acc + work.num_partial_slots * spec.num_kv_heads * 16 * work.col_tiles * spec.head_size * 4
-        if pre_floats:
-            pre_acc = workspace_ptr + dec_floats * 4
-            pre_ml = pre_acc + work.num_prefill_partial_slots * spec.num_kv_heads * prefill_columns * spec.head_size * 4
+            part_ml = part_acc + dec_rows
+        if pre_rows:
+            pre_acc = workspace_ptr + dec_rows + dec_pairs
+            pre_ml = pre_acc + pre_rows
         if work.waves_per_head:
             # lvamd_paged_decode arguments after the output strides, up to the scale.
             self.decode_args = (
@@ -305,11 +307,11 @@ class HipPagedAttention:
             code = dtype_code(self._config.dtype)
             work = plan.layer_work(backend.kernel_facts(spec, code, self._config.block_size))
             columns = backend.prefill_columns(code, spec.head_size)
-            dec_floats, pre_floats = _workspace_floats(work, spec, columns)
+            sizes = _partial_layout(work, spec, columns, self._config.dtype.itemsize)
             ptr = None
-            if dec_floats + pre_floats:
-                ptr = backend.workspace.get(dec_floats + pre_floats, self._config.device).data_ptr()
-            found = _LayerLaunch(plan, work, spec, code, self._config.block_size, ptr, columns)
+            if sum(sizes):
+                ptr = backend.workspace.get(sum(sizes), self._config.device).data_ptr()
+            found = _LayerLaunch(plan, work, spec, code, self._config.block_size, ptr, columns, sizes)
             plan.launches[key] = found
         return found
 

@@ -52,6 +52,36 @@ template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float x) { return
 
 template <typename T> __device__ __forceinline__ float to_f32(T x) { return (float)x; }
 
+// Split-K partial rows are stored in the pool's element type, normalised by
+// the piece's own sum: a convex combination of V rows, so it stays within
+// the range of V's type.  Four consecutive elements per call (8 bytes for
+// 16-bit types, 16 for fp32).
+template <typename T>
+__device__ __forceinline__ void store_partial4(T* p, f32x4 v, float s) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<f32x4*>(p) = f32x4{v[0] * s, v[1] * s, v[2] * s, v[3] * s};
+  } else {
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<t4*>(p) = t4{from_f32<T>(v[0] * s), from_f32<T>(v[1] * s), from_f32<T>(v[2] * s),
+                                   from_f32<T>(v[3] * s)};
+  }
+}
+
+// N consecutive partial elements (N = 1, 2 or 4): one load, converted to
+// fp32 apart from it (partial_f32) so that a caller can issue all its loads
+// before the first conversion waits.
+template <typename T, int N> struct PartialVec { typedef T type __attribute__((ext_vector_type(N))); };
+template <typename T> struct PartialVec<T, 1> { typedef T type; };
+
+template <typename T, int N>
+__device__ __forceinline__ float partial_f32(const typename PartialVec<T, N>::type& x, int k) {
+  if constexpr (N == 1) {
+    return to_f32(x);
+  } else {
+    return to_f32<T>(x[k]);
+  }
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));

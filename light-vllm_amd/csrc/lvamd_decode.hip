@@ -80,8 +80,8 @@ struct DecodeArgs {
   const int32_t* __restrict__ wave_first;  // [waves_per_head + 1]
   const int32_t* __restrict__ tables;
   const uint32_t* __restrict__ vis;
-  float* part_acc;  // [slots][Hkv][CTW * 16][D]
-  float* part_ml;   // [slots][Hkv][CTW * 16][2]
+  void* part_acc;   // [slots][Hkv][CTW * 16][D] of T, each row normalised by its sum
+  float* part_ml;   // [slots][Hkv][CTW * 16][2]: (max, sum)
   int32_t waves_per_head;
   int32_t num_kv_heads;
   int32_t group;
@@ -578,9 +578,10 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
           for (int r = 0; r < 4; ++r) orow[16 * n + 4 * g + r] = from_f32<T>(ax[ct][n][r] * inv);
       } else {
         const int64_t cs = ((int64_t)x.slot * Hkv + kvh) * (16 * CTW) + ct * 16 + l16;
-        float* pacc = a.part_acc + cs * D;
+        T* pacc = static_cast<T*>(a.part_acc) + cs * D;
+        const float inv = sx[ct] > 0.f ? 1.f / sx[ct] : 0.f;
 #pragma unroll
-        for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(pacc + 16 * n + 4 * g) = ax[ct][n];
+        for (int n = 0; n < NT; ++n) store_partial4<T>(pacc + 16 * n + 4 * g, ax[ct][n], inv);
         if (g == 0) *reinterpret_cast<float2*>(a.part_ml + cs * 2) = make_float2(mx[ct], sx[ct]);
       }
     }
@@ -670,12 +671,13 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
 // Merge: one wave per (job, kv head, column); a workgroup holds the four
 // waves of four consecutive columns.  Lane l combines dims EPL*l..+EPL-1 of
 // its column over the job's partials, MCP partials per round trip (their
-// (max, sum) pairs and acc rows are all requested before any is used), by
-// log-sum-exp in the log2 domain.  Every lane computes the chunk's weights
-// itself from the same (max, sum) values, so no cross-lane step is needed.
+// (max, sum) pairs and normalised rows are all requested before any is
+// used), by log-sum-exp in the log2 domain: partial i weighs
+// sum_i * 2^(max_i - max).  Every lane computes the chunk's weights itself
+// from the same (max, sum) values, so no cross-lane step is needed.
 // ---------------------------------------------------------------------------
 struct MergeArgs {
-  const float* part_acc;
+  const void* part_acc;  // rows of T, normalised
   const float* part_ml;
   void* out;
   int64_t out_tok_stride, out_head_stride;
@@ -687,23 +689,6 @@ struct MergeArgs {
 };
 
 constexpr int kMergeWaves = 4;  // columns (waves) per merge workgroup
-
-template <int EPL>
-__device__ __forceinline__ void load_acc(const float* p, float (&v)[EPL]) {
-  if constexpr (EPL == 1) {
-    v[0] = *p;
-  } else if constexpr (EPL == 2) {
-    const float2 x = *reinterpret_cast<const float2*>(p);
-    v[0] = x.x;
-    v[1] = x.y;
-  } else {
-    const float4 x = *reinterpret_cast<const float4*>(p);
-    v[0] = x.x;
-    v[1] = x.y;
-    v[2] = x.z;
-    v[3] = x.w;
-  }
-}
 
 template <typename T, int D>
 __global__ __launch_bounds__(64 * kMergeWaves) void paged_merge_kernel(const MergeArgs a) {
@@ -746,21 +731,32 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_merge_kernel(const Mer
   for (int k = 0; k < EPL; ++k) o[k] = 0.f;
   for (int p0 = 0; p0 < ntot; p0 += MCP) {
     const int n = ntot - p0 < MCP ? ntot - p0 : MCP;
+    typedef typename PartialVec<T, EPL>::type Raw;
     float2 ml[MCP];
-    float pa[MCP][EPL];
+    Raw raw[MCP];
+    // Entries past the job load nothing and carry max -inf (weight 0).  No
+    // loaded value is used before the barrier, so the round trip's loads all
+    // issue before the first wait: the (max, sum) pairs are scalar loads,
+    // and a use scheduled between them (a 16-bit row's conversion) waits for
+    // every one issued so far.
 #pragma unroll
     for (int i = 0; i < MCP; ++i) {
       ml[i] = make_float2(-INFINITY, 0.f);
-#pragma unroll
-      for (int k = 0; k < EPL; ++k) pa[i][k] = 0.f;
+      raw[i] = Raw{};
       if (i < n) {
         const int p = p0 + i;
         const int64_t r = p < np ? ((int64_t)(slot0 + p) * Hkv + kvh) * cols + c
                                  : ((int64_t)(span_slot + sunit * span_pieces + (p - np)) * Hkv + kvh) * cols + scol;
         ml[i] = *reinterpret_cast<const float2*>(a.part_ml + r * 2);
-        if (act) load_acc<EPL>(a.part_acc + r * D + e0, pa[i]);
+        if (act) raw[i] = *reinterpret_cast<const Raw*>(static_cast<const T*>(a.part_acc) + r * D + e0);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    float pa[MCP][EPL];
+#pragma unroll
+    for (int i = 0; i < MCP; ++i)
+#pragma unroll
+      for (int k = 0; k < EPL; ++k) pa[i][k] = partial_f32<T, EPL>(raw[i], k);
     float mc = -INFINITY;
 #pragma unroll
     for (int i = 0; i < MCP; ++i) mc = fmaxf(mc, ml[i].x);
@@ -773,8 +769,8 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_merge_kernel(const Mer
 #pragma unroll
     for (int i = 0; i < MCP; ++i) {
       // Entries past the job and empty partials carry max -inf: weight 0.
-      const float wt = ml[i].x != -INFINITY ? fast_exp2(ml[i].x - mnew) : 0.f;
-      lsum += wt * ml[i].y;
+      const float wt = ml[i].x != -INFINITY ? fast_exp2(ml[i].x - mnew) * ml[i].y : 0.f;
+      lsum += wt;
 #pragma unroll
       for (int k = 0; k < EPL; ++k) o[k] += wt * pa[i][k];
     }
@@ -869,7 +865,7 @@ extern "C" int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t
                                   void* out, int64_t out_token_stride, int64_t out_head_stride,
                                   const int32_t* pieces, const int32_t* wave_first, int32_t waves_per_head,
                                   const int32_t* tables, const uint32_t* vis,
-                                  float* part_acc, float* part_ml, int64_t num_partial_slots,
+                                  void* part_acc, float* part_ml, int64_t num_partial_slots,
                                   int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t col_tiles,
                                   int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream) {
   const int es = dtype_size(dtype);
@@ -943,7 +939,7 @@ extern "C" int lvamd_paged_decode_resident_waves(int32_t dtype, int32_t head_siz
   });
 }
 
-extern "C" int lvamd_paged_attention_merge(const float* part_acc, const float* part_ml,
+extern "C" int lvamd_paged_attention_merge(const void* part_acc, const float* part_ml,
                                            void* out, int64_t out_token_stride, int64_t out_head_stride,
                                            const int32_t* jobs, int32_t num_jobs,
                                            int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t col_tiles,

@@ -113,8 +113,8 @@ struct PrefillArgs {
   const int32_t* __restrict__ tables;
   const uint32_t* __restrict__ vis;
   const int32_t* __restrict__ units;     // [n][LVAMD_PREFILL_FIELDS]
-  float* part_acc;                       // [slots][Hkv][unit columns][D]
-  float* part_ml;                        // [slots][Hkv][unit columns][2]
+  void* part_acc;                        // [slots][Hkv][unit columns][D] of T, rows normalised
+  float* part_ml;                        // [slots][Hkv][unit columns][2]: (max, sum)
   int32_t num_kv_heads;
   int32_t group;
   int32_t block_size;
@@ -461,9 +461,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
     if (slot >= 0) {
       constexpr int UC = prefill_unit_columns(D);
       const int64_t cs = ((int64_t)slot * Hkv + kvh) * UC + 16 * (CT * wave + ct) + l16;
-      float* pacc = a.part_acc + cs * D;
+      T* pacc = static_cast<T*>(a.part_acc) + cs * D;
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
 #pragma unroll
-      for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(pacc + 16 * n + 4 * g) = acc[ct][n];
+      for (int n = 0; n < NT; ++n) store_partial4<T>(pacc + 16 * n + 4 * g, acc[ct][n], inv);
       if (g == 0) *reinterpret_cast<float2*>(a.part_ml + cs * 2) = make_float2(m_run[ct], l_tot);
       continue;
     }
@@ -568,7 +569,7 @@ extern "C" int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_
                                    void* out, int64_t out_token_stride, int64_t out_head_stride,
                                    const int32_t* tables, const uint32_t* vis,
                                    const int32_t* units, int32_t num_units,
-                                   float* part_acc, float* part_ml, int64_t num_partial_slots,
+                                   void* part_acc, float* part_ml, int64_t num_partial_slots,
                                    int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t waves,
                                    int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream) {
   if (num_units < 0 || num_kv_heads <= 0 || group <= 0 || block_size <= 0 || num_partial_slots < 0)

@@ -19,7 +19,7 @@ from pathlib import Path
 from light_vllm_amd import errors
 
 LIB_NAME = "liblvamd_hip.so"
-ABI_VERSION = 18
+ABI_VERSION = 19
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
