@@ -33,8 +33,8 @@
 //     to the pool.
 //   * A record with zero columns is padding of the planner's per-XCD order.
 //   * Split-K: a unit may cover a key range of its request (a piece); a piece
-//     that is not the whole range writes fp32 (max, sum, acc) partials that
-//     lvamd_paged_attention_merge combines.  The host splits units when there
+//     that is not the whole range writes partials (its normalised output
+//     rows in T, fp32 max and sum) that lvamd_paged_attention_merge combines.  The host splits units when there
 //     are fewer units than resident workgroups (tree verification, short
 //     chunks), so each workgroup's waves share fewer, wider K/V tiles.
 
