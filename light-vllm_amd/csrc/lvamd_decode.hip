@@ -8,7 +8,8 @@
 // (linear layouts: i <= j); q head h reads kv head h / group; scores are
 // q.k * scale in fp32; softmax in fp32; output = (sum p v) / (sum p) in the
 // query dtype.  There is no split-K in the reference; this kernel splits each
-// sequence into partitions and merges their (max, sum, acc) partials.
+// sequence into partitions and merges their partials: each column's output
+// row normalised by its own sum (in the pool's type) and its fp32 (max, sum).
 //
 // Mapping onto CDNA4 (one wave64 per workgroup, one workgroup per SIMD):
 //   * MFMA columns are (query, head-in-group) pairs of one kv head, 16 per
@@ -562,7 +563,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   };
 
   // Results of a finished piece: the normalised output rows (a whole
-  // segment) or its (max, sum, acc) partials.
+  // segment) or its partials (normalised rows, max and sum).
   auto write_piece = [&](const Piece& x, const LaneCol (&lx)[CTW], const f32x4 (&ax)[CTW][NT],
                          const float (&mx)[CTW], const float (&sx)[CTW]) {
 #pragma unroll
