@@ -241,6 +241,47 @@ def test_two_split_k_layers_share_the_workspace() -> None:
         assert err.max() <= max_tol and err.mean() <= mean_tol
 
 
+@pytest.mark.parametrize("prefill", (False, True))
+def test_split_k_partials_hold_values_near_the_fp16_limit(prefill) -> None:
+    # Split-K partials are stored in the pool's type, normalised by their own
+    # softmax sums: a convex combination of V rows, so fp16 partials cannot
+    # overflow while |V| stays below the fp16 maximum.  V of magnitude up to
+    # about 4.5e4 (65504 is the largest fp16), split decode rows and split
+    # tree verification over a shared prefix; errors relative to the scale.
+    # (Only the pool's written history is scaled into range; slots nothing
+    # wrote may hold anything and are never read.)
+    _announce(f"fp16 partials near the limit prefill={prefill}")
+    scale_v = 8.0e3
+    rng = np.random.default_rng(77)
+    if prefill:
+        layouts = []
+        for _ in range(4):  # the input token, then an 8-node draft tree under it
+            parents = [-1] + [int(rng.integers(0, i)) for i in range(1, 8)]
+            layouts.append(tuple([-1] + [0 if q == -1 else q + 1 for q in parents]))
+        step = make_step(hq=12, hkv=2, d=128, bs=16, dtype=torch.float16,
+                         computed=[2048 + int(c) for c in rng.integers(64, 513, size=4)],
+                         layouts=layouts, shared_prefix_blocks=128, seed=77)
+    else:
+        step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.float16, computed=[3000, 1700, 2500],
+                         layouts=_lin(1, 1, 1), seed=78)
+    lid = step.layer_ids[0]
+    step.cache.layer(lid).values.mul_(scale_v)
+    step.value.mul_(scale_v)
+    assert torch.isfinite(step.value).all()
+    ctx = lv.HipPagedAttentionBackend().create(step.cache, step.metadata)
+    out = ctx.forward(lid, step.query, step.key, step.value, scale=step.scale)
+    torch.cuda.synchronize()
+    expect = oracle_attention(step, lid)  # (after the forward: the oracle reads the appended rows)
+    assert np.isfinite(expect).all()
+    work = ctx.work_of(step.cache.layer_spec(lid))
+    assert (work.num_prefill_jobs if prefill else work.num_jobs) > 0, "the step must write split-K partials"
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    err = np.abs(got - expect) / scale_v
+    max_tol, mean_tol = tolerances(torch.float16)
+    assert err.max() <= max_tol and err.mean() <= mean_tol, (err.max(), err.mean())
+
+
 # ------------------------------------------------------ four column tiles per decode wave
 @pytest.mark.parametrize("dtype", ("fp32", "fp16", "bf16"))
 @pytest.mark.parametrize("head_size", (32, 64, 80, 96, 128))
