@@ -34,6 +34,9 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
     # Packed-FP32 VALU forms are disabled (plain float code only).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Leading scalar kernel arguments (up to 16 dwords) arrive preloaded in
+    # SGPRs, so a kernel's first address does not wait for an argument load.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     f"-I{REPO_ROOT / 'include'}",
     f"-I{CSRC}",
 ]

@@ -77,13 +77,10 @@ struct DecodeArgs {
   void* v_pool;
   void* out;
   int64_t out_tok_stride, out_head_stride;
-  const int32_t* __restrict__ pieces;      // [n_pieces][LVAMD_PIECE_FIELDS]
-  const int32_t* __restrict__ wave_first;  // [waves_per_head + 1]
   const int32_t* __restrict__ tables;
   const uint32_t* __restrict__ vis;
   void* part_acc;   // [slots][Hkv][CTW * 16][D] of T, each row normalised by its sum
   float* part_ml;   // [slots][Hkv][CTW * 16][2]: (max, sum)
-  int32_t waves_per_head;
   int32_t num_kv_heads;
   int32_t group;
   int32_t block_size;
@@ -154,7 +151,13 @@ struct LaneCol {
 };
 
 template <typename T, int D, int CTW>
-__global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
+// The fields a wave needs first (its share's bounds, then its first piece)
+// are scalar kernel arguments ahead of the struct: the build preloads leading
+// scalar arguments into SGPRs, so those loads wait for no argument load.
+__global__ __launch_bounds__(64) void paged_decode_kernel(
+    const int32_t* __restrict__ wave_first,  // [waves_per_head + 1]
+    const int32_t* __restrict__ pieces,      // [n_pieces][LVAMD_PIECE_FIELDS]
+    const int32_t waves_per_head, const DecodeArgs a) {
   using S = TileShape<T, D>;
   using DT = DecodeTile<T, D, CTW>;
   constexpr int E16 = S::E16, NCH = S::NCH, NT = S::NT, CPR = S::CPR;
@@ -173,10 +176,10 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   const int Hkv = a.num_kv_heads;
   const int G = a.group;
   // Head-major grid: the waves of one kv head are consecutive workgroups.
-  const int kvh = blockIdx.x / a.waves_per_head;
-  const int w = blockIdx.x - kvh * a.waves_per_head;
-  int p = a.wave_first[w];
-  const int p_end = a.wave_first[w + 1];
+  const int kvh = blockIdx.x / waves_per_head;
+  const int w = blockIdx.x - kvh * waves_per_head;
+  int p = wave_first[w];
+  const int p_end = wave_first[w + 1];
   if (p >= p_end) return;
 
   const int64_t row_elems = (int64_t)Hkv * D;
@@ -312,7 +315,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   // piece record carries (when the tile spans at most kPieceBlocks blocks),
   // so it does not wait for the table slice; then this piece's table and Q,
   // the next piece's table (and Q).
-  Piece cur = read_piece(a.pieces, p);
+  Piece cur = read_piece(pieces, p);
   int tb = 0;
   uint4 qf[CTW][NCH];
   uint4 qn[kPrefetchQ ? CTW : 1][NCH];
@@ -324,7 +327,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   const int first_span = logical_block(min(cur.tok_begin + TT, cur.tok_end) - 1) - logical_block(cur.tok_begin);
   const bool direct = first_span < kPieceBlocks;
   if (direct) {
-    const int32_t* ids = a.pieces + (int64_t)p * LVAMD_PIECE_FIELDS + kPieceBlockField;
+    const int32_t* ids = pieces + (int64_t)p * LVAMD_PIECE_FIELDS + kPieceBlockField;
     const int b0 = ids[0], b1 = ids[1], b2 = ids[2], b3 = ids[3], b4 = ids[4];
     issue_tile_ids(
         cur, cur.tok_begin,
@@ -341,7 +344,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
   bool nxt_stored = false;  // the next piece's table slice is in tab[tb ^ 1]
   Piece nxt = cur;
   if (have_nxt) {
-    nxt = read_piece(a.pieces, p + 1);
+    nxt = read_piece(pieces, p + 1);
     load_table(nxt, tn);
     if constexpr (kPrefetchQ) load_q(nxt, qn);
   }
@@ -653,7 +656,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
     have_nxt = p + 1 < p_end;
     nxt_stored = false;
     if (have_nxt) {
-      nxt = read_piece(a.pieces, p + 1);
+      nxt = read_piece(pieces, p + 1);
       load_table(nxt, tn);
       if constexpr (kPrefetchQ) load_q(nxt, qn);
     }
@@ -677,35 +680,38 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(const DecodeArgs a) {
 // sum_i * 2^(max_i - max).  Every lane computes the chunk's weights itself
 // from the same (max, sum) values, so no cross-lane step is needed.
 // ---------------------------------------------------------------------------
+// The fields a wave needs first (its job record's address) are scalar kernel
+// arguments ahead of the rest: the build preloads leading scalar arguments
+// into SGPRs, so the job record's load does not wait for a kernel-argument
+// load; the struct's fields are loaded meanwhile.
 struct MergeArgs {
   const void* part_acc;  // rows of T, normalised
   const float* part_ml;
   void* out;
   int64_t out_tok_stride, out_head_stride;
-  const int32_t* __restrict__ jobs;  // [num_jobs][LVAMD_MERGE_FIELDS]
-  int32_t num_kv_heads;
-  int32_t group;
-  int32_t col_tiles;  // column tiles per partial slot (the decode launch's)
-  int32_t quads;      // workgroups (of kMergeWaves columns) per (job, kv head)
 };
 
 constexpr int kMergeWaves = 4;  // columns (waves) per merge workgroup
 
 template <typename T, int D>
-__global__ __launch_bounds__(64 * kMergeWaves) void paged_merge_kernel(const MergeArgs a) {
+__global__ __launch_bounds__(64 * kMergeWaves) void paged_merge_kernel(
+    const int32_t* __restrict__ jobs,  // [num_jobs][LVAMD_MERGE_FIELDS]
+    const int32_t quads,               // workgroups (of kMergeWaves columns) per (job, kv head)
+    const int32_t num_kv_heads, const int32_t group,
+    const int32_t col_tiles,           // column tiles per partial slot (the decode launch's)
+    const MergeArgs a) {
   constexpr int EPL = D <= 64 ? 1 : (D <= 128 ? 2 : 4);  // dims per lane
   constexpr int MCP = 16;
-  const int Hkv = a.num_kv_heads;
-  const int G = a.group;
-  const int cols = 16 * a.col_tiles;  // columns per partial slot
-  const int quads = a.quads;
+  const int Hkv = num_kv_heads;
+  const int G = group;
+  const int cols = 16 * col_tiles;  // columns per partial slot
   const int jh = (int)blockIdx.x / quads;
   const int c = ((int)blockIdx.x - jh * quads) * kMergeWaves +
                 __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int job = jh / Hkv;
   const int kvh = jh - job * Hkv;
   const int lane = threadIdx.x & 63;
-  const int32_t* jb = a.jobs + (int64_t)job * LVAMD_MERGE_FIELDS;
+  const int32_t* jb = jobs + (int64_t)job * LVAMD_MERGE_FIELDS;
   const int cgroup = jb[1], slot0 = jb[2], np = jb[3], q_start = jb[4], q_len = jb[5];
   const int col = cgroup * cols + c;
   if (col >= q_len * G) return;
@@ -841,14 +847,16 @@ static int dispatch_decode(int dtype, int head_size, int col_tiles, F f) {
 }
 
 template <typename T>
-static int launch_merge_t(int head_size, dim3 grid, hipStream_t s, const MergeArgs& a) {
+static int launch_merge_t(int head_size, dim3 grid, hipStream_t s, const int32_t* jobs, int32_t quads,
+                          int32_t num_kv_heads, int32_t group, int32_t col_tiles, const MergeArgs& a) {
+  const dim3 block(64 * kMergeWaves);
   switch (head_size) {
-    case 32: hipLaunchKernelGGL((paged_merge_kernel<T, 32>), grid, dim3(64 * kMergeWaves), 0, s, a); break;
-    case 64: hipLaunchKernelGGL((paged_merge_kernel<T, 64>), grid, dim3(64 * kMergeWaves), 0, s, a); break;
-    case 80: hipLaunchKernelGGL((paged_merge_kernel<T, 80>), grid, dim3(64 * kMergeWaves), 0, s, a); break;
-    case 96: hipLaunchKernelGGL((paged_merge_kernel<T, 96>), grid, dim3(64 * kMergeWaves), 0, s, a); break;
-    case 128: hipLaunchKernelGGL((paged_merge_kernel<T, 128>), grid, dim3(64 * kMergeWaves), 0, s, a); break;
-    case 256: hipLaunchKernelGGL((paged_merge_kernel<T, 256>), grid, dim3(64 * kMergeWaves), 0, s, a); break;
+    case 32: hipLaunchKernelGGL((paged_merge_kernel<T, 32>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
+    case 64: hipLaunchKernelGGL((paged_merge_kernel<T, 64>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
+    case 80: hipLaunchKernelGGL((paged_merge_kernel<T, 80>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
+    case 96: hipLaunchKernelGGL((paged_merge_kernel<T, 96>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
+    case 128: hipLaunchKernelGGL((paged_merge_kernel<T, 128>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
+    case 256: hipLaunchKernelGGL((paged_merge_kernel<T, 256>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
     default: return LVAMD_ERR_UNSUPPORTED;
   }
   return launch_status();
@@ -902,13 +910,10 @@ extern "C" int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t
   a.out = out;
   a.out_tok_stride = out_token_stride;
   a.out_head_stride = out_head_stride;
-  a.pieces = pieces;
-  a.wave_first = wave_first;
   a.tables = tables;
   a.vis = vis;
   a.part_acc = part_acc;
   a.part_ml = part_ml;
-  a.waves_per_head = waves_per_head;
   a.num_kv_heads = num_kv_heads;
   a.group = group;
   a.block_size = block_size;
@@ -917,7 +922,7 @@ extern "C" int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t
   const dim3 grid((unsigned)(waves_per_head * num_kv_heads));
   hipStream_t s = static_cast<hipStream_t>(stream);
   return dispatch_decode(dtype, head_size, col_tiles, [&]<typename T, int D, int CTW>() -> int {
-    hipLaunchKernelGGL((paged_decode_kernel<T, D, CTW>), grid, dim3(64), 0, s, a);
+    hipLaunchKernelGGL((paged_decode_kernel<T, D, CTW>), grid, dim3(64), 0, s, wave_first, pieces, waves_per_head, a);
     return launch_status();
   });
 }
@@ -959,18 +964,14 @@ extern "C" int lvamd_paged_attention_merge(const void* part_acc, const float* pa
   a.out = out;
   a.out_tok_stride = out_token_stride;
   a.out_head_stride = out_head_stride;
-  a.jobs = jobs;
-  a.num_kv_heads = num_kv_heads;
-  a.group = group;
-  a.col_tiles = col_tiles;
-  a.quads = (int32_t)quads;
   // One workgroup per (job, kv head, kMergeWaves columns), over the columns
   // the jobs use; columns past a job's own count exit at once.
   const dim3 grid((unsigned)(num_jobs * num_kv_heads * quads));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int32_t q = (int32_t)quads;
   switch (dtype) {
-    case LVAMD_BF16: return launch_merge_t<__bf16>(head_size, grid, s, a);
-    case LVAMD_F16: return launch_merge_t<_Float16>(head_size, grid, s, a);
-    default: return launch_merge_t<float>(head_size, grid, s, a);
+    case LVAMD_BF16: return launch_merge_t<__bf16>(head_size, grid, s, jobs, q, num_kv_heads, group, col_tiles, a);
+    case LVAMD_F16: return launch_merge_t<_Float16>(head_size, grid, s, jobs, q, num_kv_heads, group, col_tiles, a);
+    default: return launch_merge_t<float>(head_size, grid, s, jobs, q, num_kv_heads, group, col_tiles, a);
   }
 }

@@ -112,10 +112,8 @@ struct PrefillArgs {
   int64_t out_tok_stride, out_head_stride;
   const int32_t* __restrict__ tables;
   const uint32_t* __restrict__ vis;
-  const int32_t* __restrict__ units;     // [n][LVAMD_PREFILL_FIELDS]
   void* part_acc;                        // [slots][Hkv][unit columns][D] of T, rows normalised
   float* part_ml;                        // [slots][Hkv][unit columns][2]: (max, sum)
-  int32_t num_kv_heads;
   int32_t group;
   int32_t block_size;
   int32_t bs_shift;
@@ -123,7 +121,9 @@ struct PrefillArgs {
 };
 
 template <typename T, int D, int W>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ? 4 : (D <= 128 ? 2 : 1)))) void paged_prefill_kernel(const PrefillArgs a) {
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ? 4 : (D <= 128 ? 2 : 1)))) void paged_prefill_kernel(
+    const int32_t* __restrict__ units,  // [n][LVAMD_PREFILL_FIELDS]
+    const int32_t num_kv_heads, const PrefillArgs a) {
   using P = PrefillShape<T, D, W>;
   constexpr int CPR = P::CPR, CG = P::CG, RB = P::RB, CT = P::CT, NCH = P::NCH, NT = P::NT;
   constexpr int KT = P::KT, KS = P::KS, GB = P::GROUP_BYTES;
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
   const int lane = tid & 63;
   const int l16 = lane & 15;
   const int g = lane >> 4;
-  const int Hkv = a.num_kv_heads;
+  const int Hkv = num_kv_heads;
   const int G = a.group;
   const int unit = blockIdx.x / Hkv;
   const int kvh = blockIdx.x - unit * Hkv;
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
   // unit, over keys every query of the span sees, reads as a linear request
   // whose computed count is its key_end: no tile masked, nothing appended)
   // and, when the piece's first tile spans at most four blocks, their ids.
-  const int32_t* u = a.units + (int64_t)unit * LVAMD_PREFILL_FIELDS;
+  const int32_t* u = units + (int64_t)unit * LVAMD_PREFILL_FIELDS;
   const int col0 = u[1], ncols = u[2], key_begin = u[3], key_end = u[4], slot = u[5];
   const int table_off = u[6], q_start = u[7], computed = u[8], q_len = u[9], vis_off = u[10], vis_words = u[11];
   const int first_blocks[4] = {u[12], u[13], u[14], u[15]};  // -1: take them from the table
@@ -481,26 +481,28 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
 }
 
 template <typename T, int D>
-static int launch_prefill_d(int waves, dim3 grid, hipStream_t s, const PrefillArgs& a) {
+static int launch_prefill_d(int waves, dim3 grid, hipStream_t s, const int32_t* units, int32_t num_kv_heads,
+                            const PrefillArgs& a) {
   if (waves == 8) {
     if constexpr (prefill_built(D, 8)) {
-      hipLaunchKernelGGL((paged_prefill_kernel<T, D, 8>), grid, dim3(512), 0, s, a);
+      hipLaunchKernelGGL((paged_prefill_kernel<T, D, 8>), grid, dim3(512), 0, s, units, num_kv_heads, a);
       return launch_status();
     }
     return LVAMD_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((paged_prefill_kernel<T, D, 4>), grid, dim3(256), 0, s, a);
+  hipLaunchKernelGGL((paged_prefill_kernel<T, D, 4>), grid, dim3(256), 0, s, units, num_kv_heads, a);
   return launch_status();
 }
 
 template <typename T>
-static int launch_prefill_t(int head_size, int waves, dim3 grid, hipStream_t s, const PrefillArgs& a) {
+static int launch_prefill_t(int head_size, int waves, dim3 grid, hipStream_t s, const int32_t* units,
+                            int32_t num_kv_heads, const PrefillArgs& a) {
   switch (head_size) {
-    case 64: return launch_prefill_d<T, 64>(waves, grid, s, a);
-    case 80: return launch_prefill_d<T, 80>(waves, grid, s, a);
-    case 96: return launch_prefill_d<T, 96>(waves, grid, s, a);
-    case 128: return launch_prefill_d<T, 128>(waves, grid, s, a);
-    case 256: return launch_prefill_d<T, 256>(waves, grid, s, a);
+    case 64: return launch_prefill_d<T, 64>(waves, grid, s, units, num_kv_heads, a);
+    case 80: return launch_prefill_d<T, 80>(waves, grid, s, units, num_kv_heads, a);
+    case 96: return launch_prefill_d<T, 96>(waves, grid, s, units, num_kv_heads, a);
+    case 128: return launch_prefill_d<T, 128>(waves, grid, s, units, num_kv_heads, a);
+    case 256: return launch_prefill_d<T, 256>(waves, grid, s, units, num_kv_heads, a);
     default: return LVAMD_ERR_UNSUPPORTED;
   }
 }
@@ -607,16 +609,14 @@ extern "C" int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_
   a.out_head_stride = out_head_stride;
   a.tables = tables;
   a.vis = vis;
-  a.units = units;
   a.part_acc = part_acc;
   a.part_ml = part_ml;
-  a.num_kv_heads = num_kv_heads;
   a.group = group;
   a.block_size = block_size;
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.scale_log2 = scale * 1.4426950408889634f;
   const dim3 grid((unsigned)(num_units * num_kv_heads));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return dtype == LVAMD_BF16 ? launch_prefill_t<__bf16>(head_size, waves, grid, s, a)
-                             : launch_prefill_t<_Float16>(head_size, waves, grid, s, a);
+  return dtype == LVAMD_BF16 ? launch_prefill_t<__bf16>(head_size, waves, grid, s, units, num_kv_heads, a)
+                             : launch_prefill_t<_Float16>(head_size, waves, grid, s, units, num_kv_heads, a);
 }
