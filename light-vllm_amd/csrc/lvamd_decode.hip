@@ -585,7 +585,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
         T* pacc = static_cast<T*>(a.part_acc) + cs * D;
         const float inv = sx[ct] > 0.f ? 1.f / sx[ct] : 0.f;
 #pragma unroll
-        for (int n = 0; n < NT; ++n) store_partial4<T>(pacc + 16 * n + 4 * g, ax[ct][n], inv);
+        for (int n = 0; n < NT; ++n) store_partial4<false, T>(pacc + 16 * n + 4 * g, ax[ct][n], inv);
         if (g == 0) *reinterpret_cast<float2*>(a.part_ml + cs * 2) = make_float2(mx[ct], sx[ct]);
       }
     }
