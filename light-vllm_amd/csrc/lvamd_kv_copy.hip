@@ -235,7 +235,11 @@ struct CompactSmallArgs {
   int64_t dst[kCompactInline];
 };
 
-template <typename V, typename Args>
+// N (8, 16 or 32) is the smallest bucket holding the call's pairs.  Every
+// one of the N gathers is issued (entries past the pairs re-read pair 0),
+// so the row chunks stay in registers: conditional gathers into the array
+// made the compiler keep it in scratch memory (512 bytes per lane).
+template <typename V, typename Args, int N>
 __global__ __launch_bounds__(256) void kv_compact_inline_kernel(const Args a) {
   const int64_t cpr = a.row_bytes / (int64_t)sizeof(V);
   const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -246,15 +250,13 @@ __global__ __launch_bounds__(256) void kv_compact_inline_kernel(const Args a) {
   const int layer = (int)(rest >> 1);
   char* base = reinterpret_cast<char*>(is_v ? a.vptrs[layer] : a.kptrs[layer]);
   const int n = (int)a.num_pairs;
-  V tmp[kCompactInline];
+  V tmp[N];
 #pragma unroll
-  for (int i = 0; i < kCompactInline; ++i) {
-    if (i < n) tmp[i] = reinterpret_cast<const V*>(base + a.src[i] * a.row_bytes)[c];
-  }
+  for (int i = 0; i < N; ++i) tmp[i] = reinterpret_cast<const V*>(base + a.src[i < n ? i : 0] * a.row_bytes)[c];
   // Every gather has landed before the first scatter is issued.
   __threadfence_block();
 #pragma unroll
-  for (int i = 0; i < kCompactInline; ++i) {
+  for (int i = 0; i < N; ++i) {
     if (i < n) reinterpret_cast<V*>(base + a.dst[i] * a.row_bytes)[c] = tmp[i];
   }
 }
@@ -369,17 +371,25 @@ __global__ __launch_bounds__(256) void kv_block_copy_kernel(const Args a) {
     }                                                                                   \
   } while (0)
 
-template <typename Args>
-static int launch_compact_inline(int width, int64_t items, hipStream_t s, const Args& a) {
-  const dim3 grid((unsigned)((items + 255) / 256));
+template <typename Args, int N>
+static int launch_compact_inline_n(int width, const dim3 grid, hipStream_t s, const Args& a) {
   switch (width) {
-    case 16: hipLaunchKernelGGL((kv_compact_inline_kernel<uint4, Args>), grid, dim3(256), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((kv_compact_inline_kernel<uint2, Args>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((kv_compact_inline_kernel<uint32_t, Args>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((kv_compact_inline_kernel<uint16_t, Args>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((kv_compact_inline_kernel<uint8_t, Args>), grid, dim3(256), 0, s, a); break;
+    case 16: hipLaunchKernelGGL((kv_compact_inline_kernel<u32x4, Args, N>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((kv_compact_inline_kernel<uint2, Args, N>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((kv_compact_inline_kernel<uint32_t, Args, N>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((kv_compact_inline_kernel<uint16_t, Args, N>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((kv_compact_inline_kernel<uint8_t, Args, N>), grid, dim3(256), 0, s, a); break;
   }
   return launch_status();
+}
+
+template <typename Args>
+static int launch_compact_inline(int width, int64_t items, hipStream_t s, const Args& a) {
+  static_assert(kCompactInline == 32, "buckets of 8, 16 and 32 pairs");
+  const dim3 grid((unsigned)((items + 255) / 256));
+  if (a.num_pairs <= 8) return launch_compact_inline_n<Args, 8>(width, grid, s, a);
+  if (a.num_pairs <= 16) return launch_compact_inline_n<Args, 16>(width, grid, s, a);
+  return launch_compact_inline_n<Args, 32>(width, grid, s, a);
 }
 
 }  // namespace lvamd
