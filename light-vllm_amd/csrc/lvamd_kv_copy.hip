@@ -383,9 +383,15 @@ static int launch_compact_inline_n(int width, const dim3 grid, hipStream_t s, co
   return launch_status();
 }
 
+// One thread per row chunk of every (layer, K|V): a step's few pairs over 28
+// layers of 512-byte rows make only seven workgroups at 16-byte chunks, so
+// the chunk narrows (to 4 bytes at least) until about 32 workgroups share the
+// latency-bound gather and scatter.
 template <typename Args>
-static int launch_compact_inline(int width, int64_t items, hipStream_t s, const Args& a) {
+static int launch_compact_inline(int width, int32_t num_layers, int64_t row_bytes, hipStream_t s, const Args& a) {
   static_assert(kCompactInline == 32, "buckets of 8, 16 and 32 pairs");
+  while (width > 4 && (int64_t)num_layers * 2 * (row_bytes / width) < 32 * 256) width /= 2;
+  const int64_t items = (int64_t)num_layers * 2 * (row_bytes / width);
   const dim3 grid((unsigned)((items + 255) / 256));
   if (a.num_pairs <= 8) return launch_compact_inline_n<Args, 8>(width, grid, s, a);
   if (a.num_pairs <= 16) return launch_compact_inline_n<Args, 16>(width, grid, s, a);
@@ -550,7 +556,7 @@ int lvamd_kv_compact(const uint64_t* layer_key_ptrs, const uint64_t* layer_value
   // size alone decides the access width.
   const int width = common_vector_bytes({(uint64_t)row_bytes});
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (num_pairs <= kCompactInline) return launch_compact_inline(width, (int64_t)num_layers * 2 * (row_bytes / width), s, a);
+  if (num_pairs <= kCompactInline) return launch_compact_inline(width, num_layers, row_bytes, s, a);
   const int64_t need = lvamd_kv_compact_workspace_size(num_pairs, num_layers, row_bytes);
   if (!workspace || workspace_bytes < need) return LVAMD_ERR_WORKSPACE;
   const int64_t items = num_pairs * num_layers * 2 * (row_bytes / width);
@@ -600,7 +606,7 @@ int lvamd_kv_compact_small(const uint64_t* layer_key_ptrs, const uint64_t* layer
     a.dst[i] = i < num_pairs ? dst_slots[i] : 0;
   }
   const int width = common_vector_bytes({(uint64_t)row_bytes});
-  return launch_compact_inline(width, (int64_t)num_layers * 2 * (row_bytes / width), static_cast<hipStream_t>(stream), a);
+  return launch_compact_inline(width, num_layers, row_bytes, static_cast<hipStream_t>(stream), a);
 }
 
 int lvamd_kv_compact_static(const uint64_t* layer_key_ptrs, const uint64_t* layer_value_ptrs,
