@@ -42,7 +42,7 @@ def _tables(pools):
 
 
 @pytest.mark.parametrize("row", (256, 36, 18, 9))  # int16 elements: 512, 72, 36, 18 bytes
-@pytest.mark.parametrize("n", (1, 7, 17, 32))
+@pytest.mark.parametrize("n", (1, 7, 8, 9, 16, 17, 32))  # the kernel's 8 / 16 / 32-pair buckets
 def test_small_compact_matches_the_closed_form_and_the_device_pair_compact(n, row) -> None:
     print(f"[gpu] small compact n={n} row={2 * row} bytes", file=sys.stderr, flush=True)
     lib = native.load()
