@@ -605,7 +605,7 @@ def _emit(rec: dict, emit: bool):
     return 0
 
 
-def run_c1(args, device) -> int:
+def run_c1(args, device, emit: bool = True):
     cfg = C1
     rng = np.random.default_rng(cfg.seed)
     need = [(c + 1 + cfg.bs - 1) // cfg.bs for c in cfg.ctx]
@@ -645,8 +645,7 @@ def run_c1(args, device) -> int:
         sec, n = _time_oracle(cpu_step, args.cpu_budget)
         rec["cpu_baseline"] = {"value": round(sec * 1e6, 1), "unit": "us", "cores": 1, "kind": "port",
                                "sample": f"full C1 step x{n}, numpy oracle, single thread"}
-    print(json.dumps(rec), flush=True)
-    return 0
+    return _emit(rec, emit)
 
 
 class C3:
@@ -805,6 +804,101 @@ def run_c4(args, device, emit: bool = True):
     return _emit(rec, emit)
 
 
+class Small:
+    """The reference's only published operating point for this path: a steady
+    decode step of Qwen2.5(-Coder)-7B in bf16 at B=16, context about 256, 28
+    layers (RTX 5090: attention 0.485 ms + KV write 0.110 ms per step,
+    benchmarks/remote_5090/OPTIMIZATION_JOURNEY.md:223-231)."""
+
+    layers, hq, hkv, d, bs, batch, ctx = 28, 28, 4, 128, 16, 16, 256
+    num_blocks = 1024  # per layer pool (16 x 17 blocks in use)
+    sets = 2  # pool sets rotated step by step (2 x 28 layers of K/V > the 256 MB MALL)
+    dtype = torch.bfloat16
+    seed = 1616
+    published_us = {"attention": 485.0, "kv_write": 110.0}
+
+
+def run_small(args, device, emit: bool = True):
+    """28-layer decode step at B=16, context 256: GPU time per step (one HIP
+    graph of the step's 28 forward calls, replayed, so host submission does
+    not hide in it), the host's submission time per step and per layer
+    (create() with the step's plan reused, then 28 eager forward calls), and
+    the eager wall time per step."""
+
+    cfg = Small
+    rng = np.random.default_rng(cfg.seed)
+    per_seq = (cfg.ctx + 1 + cfg.bs - 1) // cfg.bs
+    tables = _tables(rng, [per_seq] * cfg.batch, cfg.num_blocks)
+    md = lv.PagedAttentionMetadata(block_tables=tuple(tables), num_computed_tokens=(cfg.ctx,) * cfg.batch,
+                                   query_layouts=tuple(_linear(1) for _ in range(cfg.batch)))
+    layer_ids = [f"layer{i}" for i in range(cfg.layers)]
+    spec = lv.ModelKVCacheSpec(tuple(lv.AttentionLayerSpec(lid, cfg.hq, cfg.hkv, cfg.d) for lid in layer_ids))
+    gen = torch.Generator(device=device).manual_seed(cfg.seed)
+    caches = []
+    for _ in range(cfg.sets):
+        cache = lv.PagedKVCache(spec, lv.PagedKVCacheConfig(num_blocks=cfg.num_blocks, block_size=cfg.bs,
+                                                            dtype=cfg.dtype, device=device))
+        _fill_pools(cache, layer_ids, gen, cfg.dtype)
+        caches.append(cache)
+    q = torch.randn((cfg.batch, cfg.hq, cfg.d), generator=gen, device=device).to(cfg.dtype)
+    k = torch.randn((cfg.batch, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
+    v = torch.randn((cfg.batch, cfg.hkv, cfg.d), generator=gen, device=device).to(cfg.dtype)
+    scale = 1.0 / math.sqrt(cfg.d)
+    backend = lv.HipPagedAttentionBackend(decode_col_tiles=args.col_tiles)
+
+    def step(i):
+        ctx = backend.create(caches[i % cfg.sets], md)
+        for lid in layer_ids:
+            out = ctx.forward(lid, q, k, v, scale=scale)
+        return out
+
+    steps = max(1, min(args.steps, 200))
+    ms, host_ms = _time_steps(step, steps, max(args.warmup, 2))
+    # GPU time: each pool set's 28 forwards captured once, graphs replayed in turn.
+    graphs, eager = [], []
+    for cache in caches:
+        ctx = backend.create(cache, md)
+        eager.append([ctx.forward(lid, q, k, v, scale=scale) for lid in layer_ids][-1].clone())
+        graph = torch.cuda.CUDAGraph()
+        ctx = backend.create(cache, md)
+        with torch.cuda.graph(graph):
+            graph_out = [ctx.forward(lid, q, k, v, scale=scale) for lid in layer_ids][-1]
+        graphs.append((graph, graph_out))
+    for r in range(3):  # every replay gives the eager result (the step rewrites the same slots)
+        for (graph, graph_out), ref in zip(graphs, eager):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(graph_out, ref), "graph replay differs from the eager step"
+    gpu_ms = _time_launches(lambda i: graphs[i % cfg.sets][0].replay(), max(steps, 40), 4, device, batch=10)
+    L = cfg.ctx + 1
+    per_layer = cfg.batch * L * 2 * cfg.hkv * cfg.d * 2 + 2 * cfg.batch * cfg.hq * cfg.d * 2 + \
+        cfg.batch * per_seq * 4 + 4 * cfg.batch * cfg.hkv * cfg.d * 2
+    work = backend.create(caches[0], md).work_of(spec.layers[0])
+    published = sum(cfg.published_us.values())
+    rec = _record(
+        metric="small-batch decode step (the reference's published point): GPU us per step over 28 layers, "
+               "Qwen2.5-7B shape bf16 bs16 ctx256",
+        value=gpu_ms * 1e3, unit="us", higher=False, args=args, ms=ms, dtype="bf16",
+        workload="small: 28 layers (one pool each, 2 rotating sets), batch 16, context 256, 28 Q / 4 KV heads, "
+                 "D 128, block 16; append fused into attention",
+        extra={"steps": steps, "gpu_us_per_step": round(gpu_ms * 1e3, 2),
+               "gpu_us_per_layer": round(gpu_ms * 1e3 / cfg.layers, 2),
+               "host_submit_us_per_step": round(host_ms * 1e3, 2),
+               "host_us_per_layer": round(host_ms * 1e3 / cfg.layers, 2),
+               "eager_wall_us_per_step": round(ms * 1e3, 2),
+               "gbps_gpu": round(cfg.layers * per_layer / (gpu_ms * 1e-3) / 1e9, 1),
+               "tokens_per_s_eager": round(cfg.batch / (ms * 1e-3), 1),
+               "reference_published_us": {**cfg.published_us, "hardware": "RTX 5090, GPU kernel time, 30 steady "
+                                          "steps of Qwen2.5-Coder-7B (OPTIMIZATION_JOURNEY.md:223-231)"},
+               "vs_reference_gpu_time": round(published / (gpu_ms * 1e3), 3),
+               "split_k": {"waves_per_head": work.waves_per_head, "partials": work.num_partial_slots,
+                           "merge_jobs": work.num_jobs},
+               "note": "gpu: one HIP graph per pool set holding the step's 28 forward calls, replayed (each "
+                       "replay checked equal to the eager step); host: create() with the plan reused + 28 "
+                       "eager forward calls"})
+    return _emit(rec, emit)
+
+
 class C5:
     layers, hq, hkv, d, bs, batch = 28, 12, 2, 128, 16, 32
     prefix, suffix, tree = 2048, (64, 512), 8
@@ -952,20 +1046,21 @@ def run_c5(args, device, emit: bool = True):
 
 
 def other_configs(args, device) -> dict:
-    """The C3, C4 and C5 metrics in the default run (fewer steps, no CPU
-    baselines): each config's own ``--config`` line, reduced to its metric,
-    value, roofline fraction and step time."""
+    """The C1, C3, C4, C5 and small-batch metrics in the default run (fewer
+    steps, no CPU baselines): each config's own ``--config`` line, reduced to
+    its metric, value, roofline fraction and step time."""
 
     sub = argparse.Namespace(**{**vars(args), "steps": min(args.steps, 50), "warmup": min(args.warmup, 5),
                                 "no_cpu_baseline": True, "no_rotary": True})
     out = {}
-    for name, fn in (("c3", run_c3), ("c4", run_c4), ("c5", run_c5)):
+    for name, fn in (("c1", run_c1), ("c3", run_c3), ("c4", run_c4), ("c5", run_c5), ("small", run_small)):
         print(f"[bench] {name} summary", file=sys.stderr, flush=True)
         rec = fn(sub, device, emit=False)
         keep = {k: rec[k] for k in ("metric", "value", "unit", "higher_is_better", "ms_per_step") if k in rec}
         if "roofline" in rec:
             keep["roofline_frac"] = rec["roofline"]["frac"]
-        for k in ("prefill_kernel_us", "pct_of_hbm_peak", "attention_us", "compact_host_us"):
+        for k in ("prefill_kernel_us", "pct_of_hbm_peak", "attention_us", "compact_host_us", "host_submit_ms",
+                  "gpu_us_per_layer", "host_us_per_layer", "eager_wall_us_per_step", "vs_reference_gpu_time"):
             if k in rec:
                 keep[k] = rec[k]
         keep["steps"] = rec.get("steps", sub.steps)
@@ -998,7 +1093,7 @@ def main() -> int:
                         help="per-XCD order of the prefill grid (C3, C5; default: the planner's choice)")
     parser.add_argument("--no-configs", action="store_true",
                         help="skip the default run's summary of the C3, C4 and C5 metrics")
-    parser.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5"), default="c2",
+    parser.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5", "small"), default="c2",
                         help="BASELINE config (default c2, the headline metric); the others report their own metric")
     args = parser.parse_args()
     if args.gpus != 1:
@@ -1014,7 +1109,7 @@ def main() -> int:
     if args.mode == "kv-sweep":
         return kv_move_sweep(args, device)
     if args.config != "c2":
-        return {"c1": run_c1, "c3": run_c3, "c4": run_c4, "c5": run_c5}[args.config](args, device)
+        return {"c1": run_c1, "c3": run_c3, "c4": run_c4, "c5": run_c5, "small": run_small}[args.config](args, device)
     print(f"[bench] building C2 workload, {args.sets} pool sets", file=sys.stderr, flush=True)
     metadata, caches, q, k, v, ctx = build_workload(args.sets, device)
     nbytes = algorithmic_bytes(ctx)

@@ -250,6 +250,64 @@ int lvamd_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_st
                         int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t waves,
                         int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream);
 
+/*
+ * One layer's attention in one call: the launch facts of a layer shape in one
+ * step plan, bound once per step (every layer of that shape shares them), so
+ * that a layer only adds its tensors.  Fields mirror the arguments of
+ * lvamd_paged_decode, lvamd_paged_attention_merge and lvamd_paged_prefill.
+ */
+typedef struct lvamd_attention_plan {
+  /* Decode rows (waves_per_head 0: none). */
+  const int32_t* pieces;
+  const int32_t* wave_first;
+  int32_t waves_per_head;
+  int32_t col_tiles;
+  void* part_acc;
+  float* part_ml;
+  int64_t num_partial_slots;
+  const int32_t* jobs;
+  int32_t num_jobs;
+  int32_t merge_columns;
+  /* Prefill rows (num_units 0: none). */
+  const int32_t* units;
+  int32_t num_units;
+  int32_t prefill_waves;
+  void* prefill_part_acc;
+  float* prefill_part_ml;
+  int64_t num_prefill_partial_slots;
+  const int32_t* prefill_jobs;
+  int32_t num_prefill_jobs;
+  int32_t prefill_merge_columns;
+  int32_t prefill_col_tiles; /* prefill unit columns / 16 */
+  /* Step facts and layer shape. */
+  int32_t num_kv_heads;
+  const int32_t* tables;
+  const uint32_t* vis;
+  int32_t group;
+  int32_t head_size;
+  int32_t block_size;
+  int32_t dtype;
+} lvamd_attention_plan;
+
+/*
+ * A layer's whole attention step: the decode launch and its merge launch,
+ * then the prefill launch and its merge launch, on one stream, with this
+ * step's K/V appended by the kernels (or new_key / new_value NULL when the
+ * pool already holds them).  Returns the first failing launch's status.
+ *
+ * Replaces: TorchPagedAttention.forward's write-then-attend for one layer
+ *   (src/light_vllm/runtime/execution/paged_attention.py:268-380) and the
+ *   Triton backend's per-layer launches (triton_paged_attention.py:454-560),
+ *   called from Qwen2Attention.forward (src/light_vllm/modeling/models/qwen2.py:417-423).
+ */
+int lvamd_paged_attention(const lvamd_attention_plan* plan,
+                          const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                          const void* new_key, int64_t new_key_token_stride, int64_t new_key_head_stride,
+                          const void* new_value, int64_t new_value_token_stride, int64_t new_value_head_stride,
+                          void* key_pool, void* value_pool,
+                          void* out, int64_t out_token_stride, int64_t out_head_stride,
+                          float scale, lvamd_stream_t stream);
+
 /* Columns per prefill unit for this dtype and head size (the planner's unit
  * width), or 0 when the prefill kernel does not support them. */
 int lvamd_paged_prefill_unit_columns(int32_t dtype, int32_t head_size);

@@ -25,6 +25,7 @@ decode / prefill work lists go to the GPU in one non-blocking copy.
 
 from __future__ import annotations
 
+import ctypes
 import weakref
 
 import torch
@@ -67,14 +68,21 @@ class _Workspace:
     """Split-K partials, grown on demand and reused by every layer and step.
 
     Layers run in stream order on one stream, so one buffer serves them all.
+    A buffer grows at least twofold, and the replaced ones stay allocated (a
+    context created before the growth may still launch with their
+    addresses), so together they hold less than the current one.
     """
 
     def __init__(self) -> None:
         self._buffer: Tensor | None = None
+        self._retired: list[Tensor] = []
 
     def get(self, num_bytes: int, device: torch.device) -> Tensor:
         if self._buffer is None or self._buffer.numel() < num_bytes or self._buffer.device != device:
-            self._buffer = torch.empty(max(num_bytes, 1), dtype=torch.uint8, device=device)
+            if self._buffer is not None:
+                self._retired.append(self._buffer)
+            size = max(num_bytes, 2 * self._buffer.numel() if self._buffer is not None else 0, 1)
+            self._buffer = torch.empty(size, dtype=torch.uint8, device=device)
         return self._buffer
 
     def ptr(self) -> int | None:
@@ -105,11 +113,13 @@ class _LayerLaunch:
     """Launch facts shared by every layer of one shape in one step plan.
 
     Holds every kernel argument that does not depend on the layer's tensors,
-    so a layer's ``forward`` only reads tensor pointers and strides.
+    as argument tuples of the single-kernel entry points and as one
+    ``lvamd_attention_plan`` (``plan_ptr``) for ``lvamd_paged_attention``, so
+    a layer's ``forward`` only reads tensor pointers and strides.
     """
 
     __slots__ = ("work", "dtype", "decode_args", "merge_args", "prefill_args", "prefill_merge_args",
-                 "workspace_ptr")
+                 "workspace_ptr", "plan", "plan_ptr")
 
     def __init__(self, plan: StepPlan, work, spec, dtype: int, block_size: int, workspace_ptr: int | None,
                  prefill_columns: int, sizes: tuple[int, int, int, int]) -> None:
@@ -151,8 +161,48 @@ class _LayerLaunch:
                 work.prefill_jobs_ptr, work.num_prefill_jobs, spec.num_kv_heads, group, spec.head_size,
                 prefill_columns // 16, work.prefill_merge_columns, dtype,
             )
+        p = self.plan = native.AttentionPlan(
+            pieces=work.pieces_ptr, wave_first=work.wave_first_ptr, waves_per_head=work.waves_per_head,
+            col_tiles=work.col_tiles, part_acc=part_acc, part_ml=part_ml, num_partial_slots=work.num_partial_slots,
+            jobs=work.jobs_ptr, num_jobs=work.num_jobs, merge_columns=work.merge_columns,
+            units=work.units_ptr, num_units=work.num_prefill_units, prefill_waves=work.prefill_waves,
+            prefill_part_acc=pre_acc, prefill_part_ml=pre_ml,
+            num_prefill_partial_slots=work.num_prefill_partial_slots, prefill_jobs=work.prefill_jobs_ptr,
+            num_prefill_jobs=work.num_prefill_jobs, prefill_merge_columns=work.prefill_merge_columns,
+            prefill_col_tiles=max(prefill_columns // 16, 1), num_kv_heads=spec.num_kv_heads,
+            tables=plan.tables_ptr, vis=plan.vis_ptr, group=group, head_size=spec.head_size, block_size=block_size,
+            dtype=dtype,
+        )
+        self.plan_ptr = ctypes.addressof(p)
 
 
+class _BoundLayer:
+    """One layer's facts for the fast ``forward``: the shapes its tensors must
+    have, dtype and device, pool addresses, output strides and the bound
+    ``lvamd_attention_plan`` of its shape."""
+
+    __slots__ = ("q_shape", "kv_shape", "dtype", "device", "device_index", "element_size", "k_pool", "v_pool",
+                 "out_s0", "out_s1", "plan_ptr", "launch", "attend", "fn")
+
+    def __init__(self, tokens: int, spec, config, device_index: int, launch: _LayerLaunch, layer) -> None:
+        self.q_shape = (tokens, spec.num_query_heads, spec.head_size)
+        self.kv_shape = (tokens, spec.num_kv_heads, spec.head_size)
+        self.dtype = config.dtype
+        self.device = config.device
+        self.device_index = device_index
+        self.element_size = config.dtype.itemsize
+        self.k_pool = layer.keys.data_ptr()
+        self.v_pool = layer.values.data_ptr()
+        self.out_s0 = spec.num_query_heads * spec.head_size
+        self.out_s1 = spec.head_size
+        self.launch = launch  # keeps the plan structure alive
+        self.plan_ptr = launch.plan_ptr
+        self.attend = native.host().attend
+        self.fn = native.attention_entry()
+
+
+_UNBOUND = object()
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 _NO_APPEND = (None, 0, 0, None, 0, 0)
 # Per-XCD prefill order policies (the planner's kernel fact).
 PREFILL_ORDERS = {"auto": 0, "grouped": 1, "plain": 2}
@@ -171,6 +221,9 @@ class HipPagedAttention:
         self._layer_ids: set[str] = set()
         self._plan = plan
         self._lib = native.load()
+        self._bound: dict[str, _BoundLayer | None] = {}
+        device = self._config.device
+        self._device_index = device.index if device.index is not None else torch.cuda.current_device()
 
     @property
     def layer_ids(self) -> frozenset[str]:
@@ -195,6 +248,67 @@ class HipPagedAttention:
         if layer_id in self._layer_ids:
             raise errors.KVCacheError(f"paged attention layer {layer_id!r} ran more than once")
         self._layer_ids.add(layer_id)
+        # The common case in one native call: every tensor rule holds (the
+        # layer's bound shapes, dtype and device), rows are 16-byte aligned
+        # and there is no rotary; anything else takes the general path,
+        # which raises the first broken rule's message.
+        bound = self._bound.get(layer_id, _UNBOUND)
+        if bound is _UNBOUND:
+            bound = self._bind(layer_id)
+        if bound is not None and rotary is None:
+            dt = bound.dtype
+            dev = bound.device
+            if (query.shape == bound.q_shape and key.shape == bound.kv_shape and value.shape == bound.kv_shape
+                    and query.dtype is dt and key.dtype is dt and value.dtype is dt and query.device == dev
+                    and key.device == dev and value.device == dev):
+                qs = query.stride()
+                ks = key.stride()
+                vs = value.stride()
+                qp = query.data_ptr()
+                kp = key.data_ptr()
+                vp = value.data_ptr()
+                if qs[2] == 1 and ks[2] == 1 and vs[2] == 1 and not (
+                    (qp | kp | vp | (qs[0] | qs[1] | ks[0] | ks[1] | vs[0] | vs[1]) * bound.element_size) & 15
+                ):
+                    out = torch.empty(bound.q_shape, dtype=dt, device=dev)
+                    status = bound.attend(
+                        bound.fn, bound.plan_ptr, qp, qs[0], qs[1], kp, ks[0], ks[1], vp, vs[0], vs[1],
+                        bound.k_pool, bound.v_pool, out.data_ptr(), bound.out_s0, bound.out_s1, scale,
+                        _raw_stream(bound.device_index),
+                    )
+                    if status:
+                        native.check(status, "lvamd_paged_attention")
+                    return out
+        return self._forward_general(layer_id, query, key, value, scale=scale, rotary=rotary)
+
+    def _bind(self, layer_id: str) -> "_BoundLayer | None":
+        """The fast path's facts for one layer (None when it must take the
+        general path: a cache off the GPU, an unknown layer, an unsupported
+        head size)."""
+
+        cache = self._cache
+        if _raw_stream is None or self._config.device.type != "cuda":
+            self._bound[layer_id] = None
+            return None
+        try:
+            spec = cache.layer_spec(layer_id)
+        except Exception:  # the general path raises the cache's own error
+            self._bound[layer_id] = None
+            return None
+        if spec.head_size not in SUPPORTED_HEAD_SIZES:
+            self._bound[layer_id] = None
+            return None
+        launch = self._launch(spec)
+        layer = cache.layer(layer_id)
+        bound = self._bound[layer_id] = _BoundLayer(
+            self._plan.num_tokens, spec, self._config, self._device_index, launch, layer)
+        return bound
+
+    def _forward_general(self, layer_id: str, query: Tensor, key: Tensor, value: Tensor, *, scale: float,
+                         rotary: tuple[Tensor, Tensor] | None) -> Tensor:
+        """Every rule in the reference's order, then the launches for any
+        row strides and for ``rotary``."""
+
         spec = validate_paged_attention_tensors(self._cache, self._plan, layer_id, query, key, value)
         config = self._config
         if query.device != config.device or query.dtype != config.dtype:
@@ -231,28 +345,11 @@ class HipPagedAttention:
             if not _rows_aligned(value):
                 value = value.contiguous()
             new_kv = (key.data_ptr(), key.stride(0), key.stride(1), value.data_ptr(), value.stride(0), value.stride(1))
-        scale = float(scale)
-        o_args = (out.data_ptr(), out.stride(0), out.stride(1))
-        if launch.decode_args is not None:
-            native.check(lib.lvamd_paged_decode(
-                query.data_ptr(), query.stride(0), query.stride(1), *new_kv,
-                layer.keys.data_ptr(), layer.values.data_ptr(), *o_args,
-                *launch.decode_args, scale, launch.dtype, stream,
-            ), "lvamd_paged_decode")
-            if launch.merge_args is not None:
-                m = launch.merge_args
-                native.check(lib.lvamd_paged_attention_merge(m[0], m[1], *o_args, *m[2:], stream),
-                             "lvamd_paged_attention_merge")
-        if launch.prefill_args is not None:
-            native.check(lib.lvamd_paged_prefill(
-                query.data_ptr(), query.stride(0), query.stride(1), *new_kv,
-                layer.keys.data_ptr(), layer.values.data_ptr(), *o_args,
-                *launch.prefill_args, scale, launch.dtype, stream,
-            ), "lvamd_paged_prefill")
-            if launch.prefill_merge_args is not None:
-                m = launch.prefill_merge_args
-                native.check(lib.lvamd_paged_attention_merge(m[0], m[1], *o_args, *m[2:], stream),
-                             "lvamd_paged_attention_merge")
+        native.check(lib.lvamd_paged_attention(
+            launch.plan_ptr, query.data_ptr(), query.stride(0), query.stride(1), *new_kv,
+            layer.keys.data_ptr(), layer.values.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
+            float(scale), stream,
+        ), "lvamd_paged_attention")
         return out
 
     def decode_launch(
@@ -298,13 +395,13 @@ class HipPagedAttention:
         """The launch facts of this layer shape, bound once per plan."""
 
         backend = self._backend
-        key = (spec.num_query_heads, spec.num_kv_heads, spec.head_size)
+        code = dtype_code(self._config.dtype)
+        key = (spec.num_query_heads, spec.num_kv_heads, spec.head_size, code)
         plan = self._plan
         found = plan.launches.get(key)
         if found is not None and found.workspace_ptr is not None and found.workspace_ptr != backend.workspace.ptr():
             found = None  # the workspace (shared by all plans) was regrown since
         if found is None:
-            code = dtype_code(self._config.dtype)
             work = plan.layer_work(backend.kernel_facts(spec, code, self._config.block_size))
             columns = backend.prefill_columns(code, spec.head_size)
             sizes = _partial_layout(work, spec, columns, self._config.dtype.itemsize)
@@ -451,7 +548,11 @@ class HipPagedAttentionBackend:
         config = cache.config
         if config.device.type != "cuda":
             raise errors.KVCacheError("HIP paged attention requires a GPU KV cache")
-        geometry = (config.num_blocks, config.block_size, config.device)
+        shapes = self._cache_shapes(cache)
+        # A plan is reusable by a cache of the same pool geometry, dtype and
+        # layer shapes: its work lists were built from the kernel facts of
+        # those shapes in that dtype.
+        geometry = (config.num_blocks, config.block_size, config.device, config.dtype, shapes.keys)
         # This package's metadata is recognised by its facts object, which the
         # plan holds anyway: the metadata itself (a step's worth of tuples) is
         # not kept alive, so the caller frees it, not the next create().
@@ -465,6 +566,6 @@ class HipPagedAttentionBackend:
         # One native call validates, plans every layer shape of the cache and
         # stages it all; one copy uploads it.
         plan = StepPlan(metadata, block_size=config.block_size, device=config.device, num_blocks=config.num_blocks,
-                        partition_tokens=self._partition_tokens, staging=staging, shapes=self._cache_shapes(cache))
+                        partition_tokens=self._partition_tokens, staging=staging, shapes=shapes)
         self._last = (geometry, key, plan)
         return HipPagedAttention(self, cache, plan)

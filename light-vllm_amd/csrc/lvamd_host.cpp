@@ -1975,6 +1975,38 @@ PyObject* compact_pairs(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   return result;
 }
 
+// ---------------------------------------------------------------------------
+// attend(fn, plan, q, qs0, qs1, k, ks0, ks1, v, vs0, vs1, key_pool, value_pool,
+//        out, os0, os1, scale, stream) -> status
+//
+// Calls the HIP library's lvamd_paged_attention (fn: its address, handed over
+// once by the Python loader) with plain integers: the per-layer call of the
+// backend's forward, without ctypes' per-argument conversion.  Pointers are
+// ints (0 for NULL); the status is the library's.
+// ---------------------------------------------------------------------------
+typedef int (*AttendFn)(const void*, const void*, int64_t, int64_t, const void*, int64_t, int64_t, const void*,
+                        int64_t, int64_t, void*, void*, void*, int64_t, int64_t, float, void*);
+
+PyObject* attend(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (!want_args(nargs, 18, "attend")) return nullptr;
+  int64_t v[18];
+  for (int i = 0; i < 18; ++i) {
+    if (i == 16) continue;
+    v[i] = (int64_t)PyLong_AsLongLong(args[i]);
+  }
+  const double scale = PyFloat_AsDouble(args[16]);
+  if (PyErr_Occurred()) return nullptr;
+  if (v[0] == 0 || v[1] == 0) {
+    PyErr_SetString(PyExc_ValueError, "attend: null function or plan");
+    return nullptr;
+  }
+  auto ptr = [&](int i) { return reinterpret_cast<void*>((intptr_t)v[i]); };
+  const AttendFn fn = reinterpret_cast<AttendFn>((intptr_t)v[0]);
+  const int status = fn(ptr(1), ptr(2), v[3], v[4], ptr(5), v[6], v[7], ptr(8), v[9], v[10], ptr(11), ptr(12), ptr(13),
+                        v[14], v[15], (float)scale, ptr(17));
+  return PyLong_FromLong(status);
+}
+
 PyMethodDef kMethods[] = {
     {"flatten", (PyCFunction)(void (*)(void))flatten, METH_FASTCALL, "int sequences -> (flat, counts int64, status)"},
     {"validate", (PyCFunction)(void (*)(void))validate, METH_FASTCALL, "block-table rules -> (rule, request)"},
@@ -1987,6 +2019,7 @@ PyMethodDef kMethods[] = {
     {"plan_step", (PyCFunction)(void (*)(void))plan_step, METH_FASTCALL, "a whole step, staged into one buffer"},
     {"counts", (PyCFunction)(void (*)(void))counts, METH_FASTCALL, "how the planner's calls were served"},
     {"compact_pairs", (PyCFunction)(void (*)(void))compact_pairs, METH_FASTCALL, "compact rules and moved slot pairs"},
+    {"attend", (PyCFunction)(void (*)(void))attend, METH_FASTCALL, "one layer's lvamd_paged_attention call"},
     {nullptr, nullptr, 0, nullptr},
 };
 

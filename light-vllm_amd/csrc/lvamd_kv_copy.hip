@@ -417,7 +417,7 @@ const char* lvamd_status_string(int status) {
   }
 }
 
-int lvamd_abi_version(void) { return 19; }
+int lvamd_abi_version(void) { return 20; }
 
 int lvamd_xcd_count(void) {
   int device = 0, xcds = 0;

@@ -19,7 +19,7 @@ from pathlib import Path
 from light_vllm_amd import errors
 
 LIB_NAME = "liblvamd_hip.so"
-ABI_VERSION = 19
+ABI_VERSION = 20
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 HEADER = REPO_ROOT / "include" / "lvamd_paged_kv.h"
@@ -54,6 +54,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i64,
          _p, _p, _i32, _p, _p, _p, _p, _i64,
          _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p],
+    ),
+    "lvamd_paged_attention": (
+        ctypes.c_int,
+        [_p, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _f32, _p],
     ),
     "lvamd_paged_decode_resident_waves": (ctypes.c_int, [_i32, _i32, _i32]),
     "lvamd_paged_decode_tile_tokens": (ctypes.c_int, [_i32, _i32, _i32]),
@@ -96,6 +100,21 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lvamd_stage_upload": (ctypes.c_int, [_p, _p, _i64, _p, _p]),
     "lvamd_hbm_read_probe": (ctypes.c_int, [_p, _i64, _p, _i32, _p]),
 }
+
+
+class AttentionPlan(ctypes.Structure):
+    """``lvamd_attention_plan``: one layer shape's launch facts in one step plan."""
+
+    _fields_ = [
+        ("pieces", _p), ("wave_first", _p), ("waves_per_head", _i32), ("col_tiles", _i32),
+        ("part_acc", _p), ("part_ml", _p), ("num_partial_slots", _i64),
+        ("jobs", _p), ("num_jobs", _i32), ("merge_columns", _i32),
+        ("units", _p), ("num_units", _i32), ("prefill_waves", _i32),
+        ("prefill_part_acc", _p), ("prefill_part_ml", _p), ("num_prefill_partial_slots", _i64),
+        ("prefill_jobs", _p), ("num_prefill_jobs", _i32), ("prefill_merge_columns", _i32),
+        ("prefill_col_tiles", _i32), ("num_kv_heads", _i32),
+        ("tables", _p), ("vis", _p), ("group", _i32), ("head_size", _i32), ("block_size", _i32), ("dtype", _i32),
+    ]
 
 
 def library_path() -> Path:
@@ -226,6 +245,14 @@ def prefill_waves_built(dtype_code: int, head_size: int, waves: int) -> bool:
     """Whether the prefill kernel is built with ``waves`` waves per workgroup."""
 
     return bool(load().lvamd_paged_prefill_waves_built(dtype_code, head_size, waves))
+
+
+@functools.lru_cache(maxsize=1)
+def attention_entry() -> int:
+    """Address of ``lvamd_paged_attention``, for the host module's ``attend``
+    (which calls it with plain integers)."""
+
+    return ctypes.cast(load().lvamd_paged_attention, ctypes.c_void_p).value
 
 
 def check(status: int, what: str) -> None:

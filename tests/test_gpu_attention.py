@@ -338,3 +338,65 @@ def test_auto_column_tiles_pick_four_for_trees_and_one_for_decode() -> None:
                      layouts=_lin(1, 1), seed=72)
     _, ctx = _run_and_check(step)
     assert ctx.plan.choose_col_tiles(7, 0, 4) == 1
+
+
+# ------------------------------------------------------ in-launch merge, fast path, plan reuse
+def _forward_error(step, lid, out) -> tuple[float, float]:
+    err = np.abs(out.float().cpu().numpy() - oracle_attention(step, lid))
+    return float(err.max()), float(err.mean())
+
+
+def test_fused_qkv_views_take_either_path() -> None:
+    # q, k and v as views of one fused projection row [T, (Hq + 2 Hkv) D]:
+    # aligned views go through the one-call path, a view whose rows start
+    # two bytes in goes through the general path (copied to aligned rows).
+    _announce("fused qkv views")
+    step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[900, 40, 2100],
+                     layouts=_lin(1, 1, 1), num_layers=2, seed=311)
+    t, hq, d = step.query.shape
+    hkv = step.key.shape[1]
+    width = (hq + 2 * hkv) * d
+    ctx = lv.HipPagedAttentionBackend().create(step.cache, step.metadata)
+    for lid, shift in zip(step.layer_ids, (0, 1)):
+        fused = torch.zeros((t, width + 8), dtype=step.query.dtype, device=DEV)
+        body = fused[:, shift : shift + width]
+        body[:, : hq * d] = step.query.reshape(t, -1)
+        body[:, hq * d : (hq + hkv) * d] = step.key.reshape(t, -1)
+        body[:, (hq + hkv) * d :] = step.value.reshape(t, -1)
+        q = body[:, : hq * d].view(t, hq, d)
+        k = body[:, hq * d : (hq + hkv) * d].view(t, hkv, d)
+        v = body[:, (hq + hkv) * d :].view(t, hkv, d)
+        assert not q.is_contiguous()
+        out = ctx.forward(lid, q, k, v, scale=step.scale)
+        torch.cuda.synchronize()
+        mx, mean = _forward_error(step, lid, out)
+        max_tol, mean_tol = tolerances(step.query.dtype)
+        assert mx <= max_tol and mean <= mean_tol, (lid, shift, mx, mean)
+
+
+def test_one_metadata_on_caches_of_two_dtypes() -> None:
+    # A plan is reused only by a cache of the same geometry, dtype and layer
+    # shapes: the same metadata object sent to a bf16 cache and then to an
+    # fp16 cache of equal geometry must run each cache's own kernels.
+    _announce("one metadata, two dtypes")
+    step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[1500, 33, 700],
+                     layouts=_lin(1, 9, 1), seed=321)
+    lid = step.layer_ids[0]
+    config = step.cache.config
+    spec = lv.ModelKVCacheSpec((lv.AttentionLayerSpec(lid, 28, 4, 128),))
+    cache16 = lv.PagedKVCache(spec, lv.PagedKVCacheConfig(num_blocks=config.num_blocks, block_size=config.block_size,
+                                                          dtype=torch.float16, device=DEV))
+    src = step.cache.layer(lid)
+    cache16.layer(lid).keys.copy_(src.keys.to(torch.float16))
+    cache16.layer(lid).values.copy_(src.values.to(torch.float16))
+    step16 = type(step)(cache16, step.metadata, step.query.to(torch.float16), step.key.to(torch.float16),
+                        step.value.to(torch.float16), step.layer_ids, step.scale)
+    backend = lv.HipPagedAttentionBackend()
+    for s in (step, step16):
+        ctx = backend.create(s.cache, s.metadata)
+        out = ctx.forward(lid, s.query, s.key, s.value, scale=s.scale)
+        torch.cuda.synchronize()
+        assert out.dtype == s.query.dtype
+        mx, mean = _forward_error(s, lid, out)
+        max_tol, mean_tol = tolerances(s.query.dtype)
+        assert mx <= max_tol and mean <= mean_tol, (s.query.dtype, mx, mean)

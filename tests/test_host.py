@@ -624,6 +624,15 @@ def test_library_loads_and_exports_every_header_function() -> None:
                                   None, None, 0, 4, 7, 128, 1, 16, ctypes.c_float(0.1), 2, None) == -1
     assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 1, None, None,
                                   None, None, 0, 4, 7, 128, 2, 16, ctypes.c_float(0.1), 2, None) == -2
+    x = ctypes.c_void_p(16)  # (never dereferenced: the checks run first)
+    # One layer's call: a null plan is refused; a plan without decode rows or
+    # prefill units launches nothing.
+    assert lib.lvamd_paged_attention(None, x, 0, 0, *no_append, x, x, x, 0, 0, ctypes.c_float(0.1), None) == -1
+    empty = native.AttentionPlan(num_kv_heads=4, group=7, head_size=128, block_size=16, dtype=2)
+    assert lib.lvamd_paged_attention(ctypes.byref(empty), x, 0, 0, *no_append, x, x, x, 0, 0,
+                                     ctypes.c_float(0.1), None) == 0
+    assert native.host().attend(native.attention_entry(), ctypes.addressof(empty), 16, 0, 0, 0, 0, 0, 0, 0, 0,
+                                16, 16, 16, 0, 0, 0.1, 0) == 0
     assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 1, 16, 2, None) == -1
     assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, 128, 17, 16, 2, None) == -2
     for bad_columns in (0, 17):  # the used columns must lie within a slot's 16 * col_tiles
@@ -631,7 +640,6 @@ def test_library_loads_and_exports_every_header_function() -> None:
                                                None) == -1
     # Prefill: the workgroup shape must be 4 or 8 waves; K without V and
     # misaligned step K/V are refused.
-    x = ctypes.c_void_p(16)  # (never dereferenced: the checks run first)
     prefill = lambda nk, nv, waves: lib.lvamd_paged_prefill(  # noqa: E731
         x, 0, 0, nk, 0, 0, nv, 0, 0, x, x, x, 0, 0, x, x, x, 1, None, None, 0, 2, 7, 128, waves, 16,
         ctypes.c_float(0.1), 2, None)
