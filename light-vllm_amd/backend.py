@@ -141,7 +141,7 @@ class _LayerLaunch:
             self.decode_args = (
                 work.pieces_ptr, work.wave_first_ptr, work.waves_per_head, plan.tables_ptr, plan.vis_ptr,
                 part_acc, part_ml, work.num_partial_slots,
-                spec.num_kv_heads, group, spec.head_size, work.col_tiles, block_size,
+                spec.num_kv_heads, group, spec.head_size, work.col_tiles, work.group_waves, block_size,
             )
         if work.num_jobs:
             # lvamd_paged_attention_merge arguments after the output strides, up to the stream.
@@ -165,6 +165,7 @@ class _LayerLaunch:
             pieces=work.pieces_ptr, wave_first=work.wave_first_ptr, waves_per_head=work.waves_per_head,
             col_tiles=work.col_tiles, part_acc=part_acc, part_ml=part_ml, num_partial_slots=work.num_partial_slots,
             jobs=work.jobs_ptr, num_jobs=work.num_jobs, merge_columns=work.merge_columns,
+            group_waves=work.group_waves,
             units=work.units_ptr, num_units=work.num_prefill_units, prefill_waves=work.prefill_waves,
             prefill_part_acc=pre_acc, prefill_part_ml=pre_ml,
             num_prefill_partial_slots=work.num_prefill_partial_slots, prefill_jobs=work.prefill_jobs_ptr,
@@ -458,7 +459,7 @@ class HipPagedAttentionBackend:
     def __init__(
         self, *, use_prefill_kernel: bool = True, partition_tokens: int | None = None,
         decode_col_tiles: int | None = None, split_prefill: bool = True, prefill_waves: int | None = None,
-        shared_prefix: bool = True, prefill_order: str = "auto",
+        shared_prefix: bool = True, prefill_order: str = "auto", decode_workgroups: bool = True,
     ) -> None:
         """``use_prefill_kernel=False`` sends every request through the decode
         kernel; ``partition_tokens`` caps the tokens one decode wave handles (a
@@ -473,7 +474,11 @@ class HipPagedAttentionBackend:
         whole prefix itself); ``prefill_order`` places each request's prefill
         units on one XCD (so they share its L2): ``"auto"`` when the
         planner's simulated packing of the resident workgroups is no slower,
-        ``"grouped"`` always, ``"plain"`` never (heaviest first only)."""
+        ``"grouped"`` always, ``"plain"`` never (heaviest first only);
+        ``decode_workgroups=False`` keeps every decode step on stream-K
+        shares (by default a latency-bound step, whose segments fit the
+        resident workgroups, runs one segment per workgroup of four waves
+        that combine their results in LDS, with no merge launch)."""
 
         native.load()
         native.host()
@@ -493,10 +498,12 @@ class HipPagedAttentionBackend:
         self._shared_prefix = shared_prefix
         self._prefill_waves = prefill_waves
         self._prefill_order = PREFILL_ORDERS[prefill_order]
+        self._decode_workgroups = bool(decode_workgroups)
         self._staging: dict[torch.device, Staging] = {}
         self._facts: dict[tuple, tuple[int, ...]] = {}
         # cache -> kernel facts of its layer shapes (dropped with the cache).
         self._shapes: "weakref.WeakKeyDictionary[object, LayerShapes]" = weakref.WeakKeyDictionary()
+        self._head_sizes_ok: "weakref.WeakSet[object]" = weakref.WeakSet()
         self._last: tuple[object, object, StepPlan] | None = None
 
     def prefill_columns(self, code: int, head_size: int) -> int:
@@ -526,9 +533,27 @@ class HipPagedAttentionBackend:
                 native.prefill_resident_units(code, d, 8) if wide else 0,
                 self._partition_tokens or 0, DECODE_MAX_COLUMNS, 4, PREFILL_MIN_TILES, int(self._shared_prefix),
                 native.xcd_count() if columns else 0, self._prefill_order,
+                native.decode_split_groups(code, d) if self._decode_workgroups else 0,
             )
             self._facts[key] = found
         return found
+
+    def _check_head_sizes(self, cache) -> None:
+        """A cache with a layer of an unbuilt head size is refused when the
+        step starts (KVCacheError, checked once per cache), not at that
+        layer's first forward.  The reference's Triton backend takes head
+        sizes up to 256 (triton_paged_attention.py:475-478); the kernels here
+        are built for SUPPORTED_HEAD_SIZES."""
+
+        if cache in self._head_sizes_ok:
+            return
+        for spec in cache.model_spec.layers:
+            if spec.head_size not in SUPPORTED_HEAD_SIZES:
+                raise errors.KVCacheError(
+                    f"HIP paged attention supports head sizes {SUPPORTED_HEAD_SIZES}, not {spec.head_size} "
+                    f"(layer {spec.layer_id!r})"
+                )
+        self._head_sizes_ok.add(cache)
 
     def _cache_shapes(self, cache) -> LayerShapes:
         """Kernel facts of each distinct supported layer shape of ``cache``
@@ -548,6 +573,7 @@ class HipPagedAttentionBackend:
         config = cache.config
         if config.device.type != "cuda":
             raise errors.KVCacheError("HIP paged attention requires a GPU KV cache")
+        self._check_head_sizes(cache)
         shapes = self._cache_shapes(cache)
         # A plan is reusable by a cache of the same pool geometry, dtype and
         # layer shapes: its work lists were built from the kernel facts of

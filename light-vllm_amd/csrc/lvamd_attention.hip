@@ -21,7 +21,7 @@ extern "C" int lvamd_paged_attention(const lvamd_attention_plan* plan,
                                 key_pool, value_pool, out, out_token_stride, out_head_stride, p.pieces,
                                 p.wave_first, p.waves_per_head, p.tables, p.vis, p.part_acc, p.part_ml,
                                 p.num_partial_slots, p.num_kv_heads, p.group, p.head_size,
-                                p.col_tiles, p.block_size, scale, p.dtype, stream);
+                                p.col_tiles, p.group_waves, p.block_size, scale, p.dtype, stream);
     if (status != LVAMD_OK) return status;
     if (p.num_jobs > 0) {
       status = lvamd_paged_attention_merge(p.part_acc, p.part_ml, out, out_token_stride, out_head_stride, p.jobs,
@@ -48,4 +48,4 @@ extern "C" int lvamd_paged_attention(const lvamd_attention_plan* plan,
   return status;
 }
 
-static_assert(sizeof(lvamd_attention_plan) == 160, "the Python binding (native.AttentionPlan) assumes this layout");
+static_assert(sizeof(lvamd_attention_plan) == 168, "the Python binding (native.AttentionPlan) assumes this layout");

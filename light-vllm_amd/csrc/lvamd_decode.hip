@@ -150,11 +150,60 @@ struct LaneCol {
   const uint32_t* vrow;
 };
 
-template <typename T, int D, int CTW>
+// Waves per workgroup of the workgroup split.
+constexpr int kSplitWaves = 4;
+
+// Workgroup split (WG = 4): a latency-bound step (few short segments) is
+// spread over workgroups of four waves, one segment each: each wave runs one
+// piece of its segment, the waves combine their results in LDS, and the
+// segment's output is written by the workgroup, with no partials in memory
+// and no merge launch.  WG = 1 is the stream-K kernel (one wave per
+// workgroup, split segments merged by lvamd_paged_attention_merge).
+// Wave i's result lives in its own LDS: (max, sum) of column c at ml + i *
+// ml_stride + 2c, the fp32 row at acc + i * acc_stride + c * D.
+template <typename T, int D, int CTW, int WG>
+__device__ __forceinline__ void merge_workgroup(const DecodeArgs& a, const float* ml, int ml_stride,
+                                                const float* acc, int acc_stride, int kvh, int cgroup, int q_start,
+                                                int q_len) {
+  // Thread t: column t % 16 of the segment's column tile (column group
+  // cgroup), dims [(t / 16) * D / 16, + D / 16); the waves' rows weigh
+  // sum_i * 2^(max_i - max) (each row normalised by its own sum).
+  constexpr int DPT = D / 16;
+  const int t = threadIdx.x;
+  const int c = t & 15;
+  const int d0 = (t >> 4) * DPT;
+  const int col = cgroup * 16 + c;
+  if (col >= q_len * a.group) return;
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < WG; ++i) m = fmaxf(m, ml[i * ml_stride + 2 * c]);
+  float o[DPT];
+#pragma unroll
+  for (int e = 0; e < DPT; ++e) o[e] = 0.f;
+  float lsum = 0.f;
+#pragma unroll
+  for (int i = 0; i < WG; ++i) {
+    const float mi = ml[i * ml_stride + 2 * c];
+    if (mi == -INFINITY) continue;  // an idle wave (its row holds nothing)
+    const float wt = fast_exp2(mi - m) * ml[i * ml_stride + 2 * c + 1];
+    lsum += wt;
+    const float* row = acc + i * acc_stride + c * D + d0;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) o[e] += wt * row[e];
+  }
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  const int qi = col / a.group;
+  const int qhead = kvh * a.group + (col - qi * a.group);
+  T* orow = static_cast<T*>(a.out) + (int64_t)(q_start + qi) * a.out_tok_stride + (int64_t)qhead * a.out_head_stride;
+#pragma unroll
+  for (int e = 0; e < DPT; ++e) orow[d0 + e] = from_f32<T>(o[e] * inv);
+}
+
+template <typename T, int D, int CTW, int WG>
 // The fields a wave needs first (its share's bounds, then its first piece)
 // are scalar kernel arguments ahead of the struct: the build preloads leading
 // scalar arguments into SGPRs, so those loads wait for no argument load.
-__global__ __launch_bounds__(64) void paged_decode_kernel(
+__global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
     const int32_t* __restrict__ wave_first,  // [waves_per_head + 1]
     const int32_t* __restrict__ pieces,      // [n_pieces][LVAMD_PIECE_FIELDS]
     const int32_t waves_per_head, const DecodeArgs a) {
@@ -163,24 +212,63 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
   constexpr int E16 = S::E16, NCH = S::NCH, NT = S::NT, CPR = S::CPR;
   constexpr int TT = DT::TT, SUB = DT::SUB;
   constexpr int TAB_PER_LANE = kTableSlice / 64;
+  static_assert(WG == 1 || CTW == 1, "the workgroup split runs one column tile per wave");
   // One column tile prefetches the next piece's Q; four load theirs at the
   // piece switch (their registers hold the extra accumulators instead).
   constexpr bool kPrefetchQ = CTW == 1;
-  __shared__ __attribute__((aligned(16))) uint4 vlds_a[DT::VALLOC];
-  __shared__ __attribute__((aligned(16))) uint4 vlds_b[DT::VALLOC];
-  __shared__ int32_t tab[2][kTableSlice];
+  // Per wave: two V buffers and a table slice pair; in the workgroup split
+  // the first V buffers also take the waves' results at the end (fp32 rows).
+  __shared__ __attribute__((aligned(16))) uint4 vlds_a_all[WG * DT::VALLOC];
+  __shared__ __attribute__((aligned(16))) uint4 vlds_b_all[WG * DT::VALLOC];
+  __shared__ int32_t tab_all[WG][2][kTableSlice];
+  static_assert(WG == 1 || 16 * D * 4 <= DT::VALLOC * 16, "a wave's result rows must fit its V buffer");
 
   const int lane = threadIdx.x & 63;  // (the mask tells LLVM lane < 64)
+  const int wid = WG == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  uint4* const vlds_a = vlds_a_all + wid * DT::VALLOC;
+  uint4* const vlds_b = vlds_b_all + wid * DT::VALLOC;
+  int32_t(*const tab)[kTableSlice] = tab_all[wid];
   const int l16 = lane & 15;
   const int g = lane >> 4;
   const int Hkv = a.num_kv_heads;
   const int G = a.group;
-  // Head-major grid: the waves of one kv head are consecutive workgroups.
-  const int kvh = blockIdx.x / waves_per_head;
-  const int w = blockIdx.x - kvh * waves_per_head;
+  // Head-major grid: the waves of one kv head are consecutive (in workgroups
+  // of WG waves).
+  constexpr int kWG = WG;
+  const int wg_per_head = waves_per_head / kWG;
+  const int kvh = blockIdx.x / wg_per_head;
+  const int w = (blockIdx.x - kvh * wg_per_head) * kWG + wid;
   int p = wave_first[w];
   const int p_end = wave_first[w + 1];
-  if (p >= p_end) return;
+  // Workgroup split: each wave's result rows (fp32, normalised) in its own
+  // first V buffer and its (max, sum) pairs in its own table slice, then the
+  // segment's merge once every wave has written.
+  constexpr int kAccStride = DT::VALLOC * 4;   // floats per wave's V buffer
+  constexpr int kMlStride = 2 * kTableSlice;   // floats per wave's table slices
+  float* const wg_acc = reinterpret_cast<float*>(vlds_a);
+  float* const wg_ml = reinterpret_cast<float*>(&tab[0][0]);
+  auto finish_workgroup = [&]() {
+    if constexpr (WG > 1) {
+      __syncthreads();
+      const int32_t* lead = pieces + (int64_t)wave_first[w - wid] * LVAMD_PIECE_FIELDS;
+      // A segment left whole in its first wave was written by that wave.
+      if (lead[4] >= 0)
+        merge_workgroup<T, D, CTW, WG>(a, reinterpret_cast<const float*>(&tab_all[0][0][0]), kMlStride,
+                                       reinterpret_cast<const float*>(vlds_a_all), kAccStride, kvh, lead[1],
+                                       lead[8], lead[7]);
+    }
+  };
+  if (p >= p_end) {
+    if constexpr (WG > 1) {
+      // An idle wave of a split workgroup: no result (max -inf).
+      if (lane < 16) {
+        wg_ml[2 * lane] = -INFINITY;
+        wg_ml[2 * lane + 1] = 0.f;
+      }
+      finish_workgroup();
+    }
+    return;
+  }
 
   const int64_t row_elems = (int64_t)Hkv * D;
   // Global-address-space pointers: the tile loads select between the pool
@@ -580,6 +668,19 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
         for (int n = 0; n < NT; ++n)
 #pragma unroll
           for (int r = 0; r < 4; ++r) orow[16 * n + 4 * g + r] = from_f32<T>(ax[ct][n][r] * inv);
+      } else if constexpr (WG > 1) {
+        // Workgroup split: this wave's fp32 rows and (max, sum) into LDS
+        // (the wave's own V buffer, free once its last tile is done).
+        const float inv = sx[ct] > 0.f ? 1.f / sx[ct] : 0.f;
+        float* racc = wg_acc + l16 * D;
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+          *reinterpret_cast<f32x4*>(racc + 16 * n + 4 * g) =
+              f32x4{ax[ct][n][0] * inv, ax[ct][n][1] * inv, ax[ct][n][2] * inv, ax[ct][n][3] * inv};
+        if (g == 0) {
+          wg_ml[2 * l16] = mx[ct];
+          wg_ml[2 * l16 + 1] = sx[ct];
+        }
       } else {
         const int64_t cs = ((int64_t)x.slot * Hkv + kvh) * (16 * CTW) + ct * 16 + l16;
         T* pacc = static_cast<T*>(a.part_acc) + cs * D;
@@ -669,6 +770,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
     if (step(ka, kb, vlds_a, vlds_b) && !end_piece()) break;
     if (step(kb, ka, vlds_b, vlds_a) && !end_piece()) break;
   }
+  finish_workgroup();
 }
 
 // ---------------------------------------------------------------------------
@@ -876,10 +978,13 @@ extern "C" int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t
                                   const int32_t* tables, const uint32_t* vis,
                                   void* part_acc, float* part_ml, int64_t num_partial_slots,
                                   int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t col_tiles,
-                                  int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream) {
+                                  int32_t group_waves, int32_t block_size, float scale, int32_t dtype,
+                                  lvamd_stream_t stream) {
   const int es = dtype_size(dtype);
   if (es == 0 || !head_size_supported(head_size) || !col_tiles_supported(col_tiles)) return LVAMD_ERR_UNSUPPORTED;
-  if (waves_per_head < 0 || num_kv_heads <= 0 || group <= 0 || block_size <= 0 || num_partial_slots < 0)
+  if (group_waves != 1 && !(group_waves == kSplitWaves && col_tiles == 1)) return LVAMD_ERR_UNSUPPORTED;
+  if (waves_per_head < 0 || num_kv_heads <= 0 || group <= 0 || block_size <= 0 || num_partial_slots < 0 ||
+      waves_per_head % group_waves != 0)
     return LVAMD_ERR_INVALID_ARGUMENT;
   if (waves_per_head == 0) return LVAMD_OK;
   if (!q || !key_pool || !value_pool || !out || !pieces || !wave_first || !tables)
@@ -919,11 +1024,37 @@ extern "C" int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t
   a.block_size = block_size;
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.scale_log2 = scale * 1.4426950408889634f;
-  const dim3 grid((unsigned)(waves_per_head * num_kv_heads));
+  const dim3 grid((unsigned)(waves_per_head / group_waves * num_kv_heads));
   hipStream_t s = static_cast<hipStream_t>(stream);
   return dispatch_decode(dtype, head_size, col_tiles, [&]<typename T, int D, int CTW>() -> int {
-    hipLaunchKernelGGL((paged_decode_kernel<T, D, CTW>), grid, dim3(64), 0, s, wave_first, pieces, waves_per_head, a);
+    if constexpr (CTW == 1) {
+      if (group_waves == kSplitWaves) {
+        hipLaunchKernelGGL((paged_decode_kernel<T, D, CTW, kSplitWaves>), grid, dim3(64 * kSplitWaves), 0, s,
+                           wave_first, pieces, waves_per_head, a);
+        return launch_status();
+      }
+    }
+    hipLaunchKernelGGL((paged_decode_kernel<T, D, CTW, 1>), grid, dim3(64), 0, s, wave_first, pieces,
+                       waves_per_head, a);
     return launch_status();
+  });
+}
+
+extern "C" int lvamd_paged_decode_split_groups(int32_t dtype, int32_t head_size) {
+  return dispatch_decode(dtype, head_size, 1, []<typename T, int D, int CTW>() -> int {
+    if constexpr (CTW != 1) {
+      return 0;  // (not reached: one column tile asked for)
+    } else {
+      int device = 0, cus = 0, per_cu = 0;
+      if (hipGetDevice(&device) != hipSuccess) return LVAMD_ERR_LAUNCH;
+      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+        return LVAMD_ERR_LAUNCH;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+              &per_cu, reinterpret_cast<const void*>(&paged_decode_kernel<T, D, CTW, kSplitWaves>),
+              64 * kSplitWaves, 0) != hipSuccess)
+        return LVAMD_ERR_LAUNCH;
+      return per_cu * cus;
+    }
   });
 }
 
@@ -939,7 +1070,7 @@ extern "C" int lvamd_paged_decode_resident_waves(int32_t dtype, int32_t head_siz
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
       return LVAMD_ERR_LAUNCH;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(&paged_decode_kernel<T, D, CTW>), 64, 0) != hipSuccess)
+            &per_cu, reinterpret_cast<const void*>(&paged_decode_kernel<T, D, CTW, 1>), 64, 0) != hipSuccess)
       return LVAMD_ERR_LAUNCH;
     return per_cu * cus;
   });

@@ -932,6 +932,7 @@ struct Requests {
 struct DecodeLists {
   std::vector<int32_t> pieces, first, jobs;
   int64_t waves = 0, per_wave = 0, merge_cols = 1;
+  int64_t group_waves = 1;  // 1: stream-K; kSplitWaves: workgroup split
   int32_t slots = 0;
   void reset() {
     pieces.clear();
@@ -939,13 +940,23 @@ struct DecodeLists {
     jobs.clear();
     waves = per_wave = 0;
     merge_cols = 1;
+    group_waves = 1;
     slots = 0;
   }
 };
 
 struct DecodeParams {
   int64_t group, col_tiles, max_cols, hkv, resident, bs, min_units, max_units, unit;
+  int64_t split_groups = 0;  // resident workgroups of the workgroup-split kernel (0: not built)
 };
+
+// Workgroup split of the decode kernel: workgroups of kSplitWaves waves, one
+// segment each, its pieces combined in LDS.  The planner takes it when the
+// step's segments fit the resident workgroups and its longest piece, in
+// tiles, is no longer than stream-K's largest share plus what the merge
+// launch it saves costs (kSplitMergeTiles tiles).
+constexpr int64_t kSplitWaves = 4;
+constexpr int64_t kSplitMergeTiles = 3;
 
 void build_decode(const Requests& q, const int32_t* ids, int64_t nflat, const DecodeParams& d, DecodeLists& out) {
   struct Seg {
@@ -1047,6 +1058,52 @@ void build_decode(const Requests& q, const int32_t* ids, int64_t nflat, const De
     if (multi) ++out.slots;
   }
   while (w <= waves) out.first[(size_t)w++] = (int32_t)recs.size();
+
+  // The workgroup split instead, when it is no slower (see kSplitWaves).
+  if (d.split_groups <= 0 || d.col_tiles != 1) return;
+  int64_t longest = 0;
+  for (const Seg& sg : segs) longest = std::max(longest, sg.tiles);
+  const int64_t split_share = (longest + kSplitWaves - 1) / kSplitWaves;
+  const int64_t nseg = (int64_t)segs.size();
+  if (nseg * d.hkv > d.split_groups || split_share > cap) return;
+  if (split_share > per_wave + (out.jobs.empty() ? 0 : kSplitMergeTiles)) return;
+  out.reset();
+  out.group_waves = kSplitWaves;
+  out.waves = kSplitWaves * nseg;
+  out.per_wave = split_share;
+  out.first.assign((size_t)out.waves + 1, 0);
+  int32_t np = 0;
+  for (int64_t s = 0; s < nseg; ++s) {
+    const Seg& sg = segs[(size_t)s];
+    const int32_t* m = q.row(sg.req);
+    const int64_t n = std::min(kSplitWaves, sg.tiles);
+    const int64_t seq_end = q.computed(sg.req) + q.q_len(sg.req);
+    for (int64_t i = 0; i < kSplitWaves; ++i) {
+      out.first[(size_t)(kSplitWaves * s + i)] = np;
+      if (i >= n) continue;
+      const int64_t lo = i * sg.tiles / n, hi = (i + 1) * sg.tiles / n;
+      int32_t o[kPieceFields] = {};
+      o[0] = sg.req;
+      o[1] = sg.group;
+      o[2] = (int32_t)(lo * d.unit);
+      o[3] = (int32_t)std::min(hi * d.unit, seq_end);
+      o[4] = n > 1 ? (int32_t)i : -1;
+      o[5] = m[0];
+      o[6] = m[2];
+      o[7] = m[3];
+      o[8] = m[4];
+      o[9] = m[5];
+      o[10] = m[6];
+      const int64_t lb0 = blocks_per_unit ? lo * blocks_per_unit : (lo * d.unit) / d.bs;
+      for (int k = 0; k < kPieceBlocks; ++k) {
+        const int64_t lb = lb0 + k, idx = m[0] + lb;
+        o[11 + k] = (lb < m[1] && idx < nflat) ? ids[idx] : 0;
+      }
+      out.pieces.insert(out.pieces.end(), o, o + kPieceFields);
+      ++np;
+    }
+  }
+  out.first[(size_t)out.waves] = np;
 }
 
 struct PrefillLists {
@@ -1433,8 +1490,8 @@ PyObject* decode_result(const DecodeLists& d) {
   PyObject* a = to_bytearray(d.pieces);
   PyObject* b = to_bytearray(d.first);
   PyObject* c = to_bytearray(d.jobs);
-  PyObject* result = (a && b && c) ? Py_BuildValue("(OOOLLiL)", a, b, c, (long long)d.waves, (long long)d.per_wave,
-                                                   d.slots, (long long)d.merge_cols)
+  PyObject* result = (a && b && c) ? Py_BuildValue("(OOOLLiLL)", a, b, c, (long long)d.waves, (long long)d.per_wave,
+                                                   d.slots, (long long)d.merge_cols, (long long)d.group_waves)
                                    : nullptr;
   Py_XDECREF(a);
   Py_XDECREF(b);
@@ -1474,19 +1531,22 @@ bool requests_of(const Buf& meta, Requests* q, const char* name) {
 
 // decode_work(req_meta i32[B*8], flat i32, group, col_tiles, decode_max_columns,
 //             num_kv_heads, resident_waves, block_size, min_units_per_wave,
-//             max_units_per_wave (0 = none), unit_tokens)
+//             max_units_per_wave (0 = none), unit_tokens, split_groups)
 //   -> (pieces i32 [n, 16], wave_first i32 [W + 1], jobs i32 [m, 8],
-//       W, largest share, partial slots, most columns of a merge job)
+//       W, largest share, partial slots, most columns of a merge job,
+//       waves per workgroup)
+// split_groups: resident workgroups of the workgroup-split kernel (0: never
+// split in workgroups).
 PyObject* decode_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
-  if (!want_args(nargs, 11, "decode_work")) return nullptr;
+  if (!want_args(nargs, 12, "decode_work")) return nullptr;
   Buf meta(args[0], false, 4, "req_meta"), flat(args[1], false, 4, "flat");
   if (!meta.ok() || !flat.ok()) return nullptr;
   Requests q;
   if (!requests_of(meta, &q, "decode_work")) return nullptr;
   DecodeParams d;
-  int64_t* fields[] = {&d.group, &d.col_tiles, &d.max_cols, &d.hkv, &d.resident, &d.bs, &d.min_units, &d.max_units,
-                       &d.unit};
-  for (int i = 0; i < 9; ++i)
+  int64_t* fields[] = {&d.group, &d.col_tiles, &d.max_cols, &d.hkv,       &d.resident,
+                       &d.bs,    &d.min_units, &d.max_units, &d.unit, &d.split_groups};
+  for (int i = 0; i < 10; ++i)
     if (!as_i64(args[2 + i], fields[i])) return nullptr;
   if (d.group <= 0 || d.col_tiles <= 0 || d.hkv <= 0 || d.bs <= 0 || d.unit <= 0 || d.min_units <= 0) {
     PyErr_SetString(PyExc_ValueError, "decode_work: inconsistent arguments");
@@ -1550,8 +1610,9 @@ PyObject* prefill_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
 //   decode wave (0: no cap), 17 decode max columns, 18 min units per wave,
 //   19 prefill min tiles, 20 shared-prefix spans (0/1), 21 the device's XCDs
 //   (0: no per-XCD order of the prefill grid), 22 per-XCD order (0: grouped
-//   when its simulated packing is no slower, 1: grouped, 2: plain).
-constexpr int kKernelFacts = 23;
+//   when its simulated packing is no slower, 1: grouped, 2: plain), 23
+//   resident workgroups of the workgroup-split decode kernel (0: never).
+constexpr int kKernelFacts = 24;
 
 // One layer shape's plan: the choices and the lists of both kernels.
 struct LayerPlan {
@@ -1639,7 +1700,8 @@ const char* plan_layer(const Requests& q, const int32_t* ids, int64_t nflat, con
   if (any_decode) {
     const int64_t unit = ctw == 4 ? k[13] : k[11];
     const int64_t max_units = (k[16] > 0 && unit > 0) ? std::max<int64_t>(1, k[16] / unit) : 0;
-    DecodeParams d{group, ctw, max_cols, hkv, ctw == 4 ? k[12] : k[10], bs, k[18] > 0 ? k[18] : 4, max_units, unit};
+    DecodeParams d{group, ctw, max_cols, hkv, ctw == 4 ? k[12] : k[10], bs, k[18] > 0 ? k[18] : 4, max_units, unit,
+                   k[23]};
     if (d.unit <= 0 || d.resident <= 0) return "missing decode kernel facts";
     build_decode(q, ids, nflat, d, out.dec);
     out.has_dec = true;
@@ -1654,7 +1716,7 @@ const char* plan_layer(const Requests& q, const int32_t* ids, int64_t nflat, con
 // ---------------------------------------------------------------------------
 // plan_step(flat i32, counts i64, computed i64, reserved i64, readonly i64,
 //           q_lens i64, vis_off i64, vis_words i64, vis u32, num_blocks,
-//           block_size, kernel facts i64 [n][23], cost4, wide_max_tiles,
+//           block_size, kernel facts i64 [n][24], cost4, wide_max_tiles,
 //           out i32 (writable))
 //   -> rule (int 1..6): a block-table rule fails (validate's codes);
 //      (needed, None, None): ``out`` holds fewer than ``needed`` entries;
@@ -1669,7 +1731,7 @@ const char* plan_layer(const Requests& q, const int32_t* ids, int64_t nflat, con
 //    decode partial slots, decode merge jobs, decode merge columns,
 //    prefill units, prefill merge jobs, prefill partial slots,
 //    prefill merge columns, pieces, wave_first, jobs, units, prefill jobs,
-//    decode pieces)
+//    decode pieces, decode waves per workgroup)
 // with the five offsets -1 for an absent list.
 // ---------------------------------------------------------------------------
 std::vector<LayerPlan> g_layer_plans;
@@ -1776,7 +1838,7 @@ PyObject* plan_step(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     const DecodeLists& d = plan.dec;
     const PrefillLists& p = plan.pre;
     PyObject* one = Py_BuildValue(
-        "(LLLLLLLLLLLLLLLLL)", (long long)plan.ctw, (long long)plan.waves, (long long)(plan.has_dec ? d.waves : 0),
+        "(LLLLLLLLLLLLLLLLLL)", (long long)plan.ctw, (long long)plan.waves, (long long)(plan.has_dec ? d.waves : 0),
         (long long)(plan.has_dec ? d.per_wave : 0), (long long)(plan.has_dec ? d.slots : 0),
         (long long)(plan.has_dec ? (int64_t)d.jobs.size() / kMergeFields : 0),
         (long long)(plan.has_dec ? d.merge_cols : 1),
@@ -1784,7 +1846,8 @@ PyObject* plan_step(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
         (long long)(plan.has_pre ? (int64_t)p.jobs.size() / kMergeFields : 0), (long long)(plan.has_pre ? p.slots : 0),
         (long long)(plan.has_pre ? p.merge_cols : 1), (long long)o.pieces, (long long)o.first, (long long)o.jobs,
         (long long)o.units, (long long)o.pjobs,
-        (long long)(plan.has_dec ? (int64_t)d.pieces.size() / kPieceFields : 0));
+        (long long)(plan.has_dec ? (int64_t)d.pieces.size() / kPieceFields : 0),
+        (long long)(plan.has_dec ? d.group_waves : 1));
     if (one == nullptr) {
       Py_DECREF(shapes);
       return nullptr;

@@ -53,8 +53,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i64,
          _p, _p, _i32, _p, _p, _p, _p, _i64,
-         _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p],
+         _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p],
     ),
+    "lvamd_paged_decode_split_groups": (ctypes.c_int, [_i32, _i32]),
     "lvamd_paged_attention": (
         ctypes.c_int,
         [_p, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _f32, _p],
@@ -108,7 +109,7 @@ class AttentionPlan(ctypes.Structure):
     _fields_ = [
         ("pieces", _p), ("wave_first", _p), ("waves_per_head", _i32), ("col_tiles", _i32),
         ("part_acc", _p), ("part_ml", _p), ("num_partial_slots", _i64),
-        ("jobs", _p), ("num_jobs", _i32), ("merge_columns", _i32),
+        ("jobs", _p), ("num_jobs", _i32), ("merge_columns", _i32), ("group_waves", _i32),
         ("units", _p), ("num_units", _i32), ("prefill_waves", _i32),
         ("prefill_part_acc", _p), ("prefill_part_ml", _p), ("num_prefill_partial_slots", _i64),
         ("prefill_jobs", _p), ("num_prefill_jobs", _i32), ("prefill_merge_columns", _i32),
@@ -172,7 +173,7 @@ def load() -> ctypes.CDLL:
 # Column tiles per decode wave the library builds: 1, and 4 for narrow rows.
 DECODE_COL_TILES = (1, 4)
 
-_RESIDENT: dict[tuple[int, int, int], int] = {}
+_RESIDENT: dict[tuple, int] = {}
 
 
 def resident_decode_waves(dtype_code: int, head_size: int, col_tiles: int = 1) -> int:
@@ -193,6 +194,18 @@ def decode_tile_tokens(dtype_code: int, head_size: int, col_tiles: int = 1) -> i
 
     found = int(load().lvamd_paged_decode_tile_tokens(dtype_code, head_size, col_tiles))
     check(min(found, 0), "lvamd_paged_decode_tile_tokens")
+    return found
+
+
+def decode_split_groups(dtype_code: int, head_size: int) -> int:
+    """Workgroups of the workgroup-split decode kernel the current GPU holds at once."""
+
+    key = (dtype_code, head_size, "split")
+    found = _RESIDENT.get(key)
+    if found is None:
+        found = int(load().lvamd_paged_decode_split_groups(dtype_code, head_size))
+        check(min(found, 0), "lvamd_paged_decode_split_groups")
+        _RESIDENT[key] = found
     return found
 
 

@@ -200,13 +200,16 @@ class DecodeWork:
     host arrays as CPU tensors (inspection and tests)."""
 
     __slots__ = ("pieces_host", "wave_first_host", "jobs_host", "units_host", "prefill_jobs_host",
-                 "waves_per_head", "num_jobs", "num_partial_slots", "units_per_wave", "col_tiles",
+                 "waves_per_head", "num_jobs", "num_partial_slots", "units_per_wave", "col_tiles", "group_waves",
                  "num_prefill_units", "num_prefill_jobs", "num_prefill_partial_slots", "prefill_waves",
                  "merge_columns", "prefill_merge_columns", "pieces_ptr", "wave_first_ptr", "jobs_ptr",
                  "units_ptr", "prefill_jobs_ptr", "_staged")
 
     def __init__(self, *, col_tiles: int, prefill_waves: int) -> None:
         self.col_tiles = col_tiles  # column tiles per decode wave (partials hold 16 * col_tiles columns)
+        # Decode waves per workgroup: 1 (stream-K shares, merge launch) or 4
+        # (workgroup split: one segment per workgroup, merged in LDS).
+        self.group_waves = 1
         self.prefill_waves = prefill_waves  # prefill workgroup shape: 4 waves x 2 column tiles or 8 x 1
         self.pieces_host = self.wave_first_host = self.jobs_host = None
         self.units_host = self.prefill_jobs_host = None
@@ -222,8 +225,9 @@ class DecodeWork:
         uploaded step buffer): counts from ``row``, lists only on the device."""
 
         (ctw, waves, wph, per_wave, slots, njobs, mcols, nunits, npjobs, pslots, pmcols,
-         o_pieces, o_first, o_jobs, o_units, o_pjobs, npieces) = row
+         o_pieces, o_first, o_jobs, o_units, o_pjobs, npieces, group_waves) = row
         work = cls(col_tiles=ctw, prefill_waves=waves)
+        work.group_waves = group_waves
         work.waves_per_head, work.units_per_wave, work.num_partial_slots = wph, per_wave, slots
         work.num_jobs, work.merge_columns = njobs, mcols
         work.num_prefill_units, work.num_prefill_jobs = nunits, npjobs
@@ -491,7 +495,7 @@ class StepPlan:
         self, group: int, num_kv_heads: int, resident_waves: int = 8 * NUM_CUS, prefill_columns: int = 0,
         unit_tokens: int = UNIT_TOKENS, col_tiles: int = 1, prefill_key_tokens: int = 64,
         prefill_resident: int = 0, prefill_waves: int = 4, shared_prefix: bool = False, xcds: int = 0,
-        prefill_order: int = 0,
+        prefill_order: int = 0, split_groups: int = 0,
     ) -> DecodeWork:
         """Work lists for layers of this (group, kv heads) shape.
 
@@ -506,12 +510,15 @@ class StepPlan:
         ``xcds`` > 1 orders the prefill units per XCD of a device with that
         many (the backend passes the device's count): ``prefill_order`` 0
         keeps each request's units on one XCD when the simulated packing is
-        no slower, 1 always, 2 never.  The library reports the kernel figures
-        per dtype and head size.
+        no slower, 1 always, 2 never; ``split_groups`` > 0 (the resident
+        workgroups of the workgroup-split decode kernel) lets the planner
+        give each segment a workgroup of four waves when that is no slower
+        than stream-K with its merge launch.  The library reports the kernel
+        figures per dtype and head size.
         """
 
         key = (group, num_kv_heads, resident_waves, prefill_columns, unit_tokens, col_tiles, prefill_key_tokens,
-               prefill_resident, prefill_waves, bool(shared_prefix), int(xcds), int(prefill_order))
+               prefill_resident, prefill_waves, bool(shared_prefix), int(xcds), int(prefill_order), int(split_groups))
         found = self._work.get(key)
         if found is None:
             found = self._build_work(*key)
@@ -551,7 +558,7 @@ class StepPlan:
     def _build_work(
         self, group: int, num_kv_heads: int, resident_waves: int, prefill_columns: int, unit_tokens: int,
         col_tiles: int, prefill_key_tokens: int, prefill_resident: int, prefill_waves: int, shared_prefix: bool,
-        xcds: int, prefill_order: int,
+        xcds: int, prefill_order: int, split_groups: int,
     ) -> DecodeWork:
         host = native.host()
         work = DecodeWork(col_tiles=col_tiles, prefill_waves=prefill_waves)
@@ -561,7 +568,7 @@ class StepPlan:
         if max_cols == 0 or bool(np.any(q_cols <= max_cols)):
             max_units = max(1, self.partition_tokens // unit_tokens) if self.partition_tokens else 0
             dec = host.decode_work(self._req_meta, self.facts.flat, group, col_tiles, max_cols, num_kv_heads,
-                                   resident_waves, self.block_size, 4, max_units, unit_tokens)
+                                   resident_waves, self.block_size, 4, max_units, unit_tokens, split_groups)
         if max_cols and bool(np.any(q_cols > max_cols)):
             slots_per_head = prefill_resident // num_kv_heads if prefill_resident else 0
             pre = host.prefill_work(self._req_meta, self.facts.raw[0], group, prefill_columns, prefill_key_tokens,
@@ -577,7 +584,7 @@ KERNEL_FACTS = (
     "forced_col_tiles", "forced_prefill_waves", "max_col_tiles", "wide_prefill_built",
     "resident_waves_1", "tile_tokens_1", "resident_waves_4", "tile_tokens_4",
     "prefill_resident_4", "prefill_resident_8", "partition_tokens", "decode_max_columns",
-    "min_units_per_wave", "prefill_min_tiles", "shared_prefix", "xcds", "prefill_order",
+    "min_units_per_wave", "prefill_min_tiles", "shared_prefix", "xcds", "prefill_order", "split_groups",
 )
 
 
@@ -599,7 +606,8 @@ def _fill_work(work: DecodeWork, dec, pre) -> None:
     """Store the native planner's decode and prefill results in ``work``."""
 
     if dec is not None:
-        pieces, first, jobs, waves, per_wave, slots, merge_cols = dec
+        pieces, first, jobs, waves, per_wave, slots, merge_cols, group_waves = dec
+        work.group_waves = int(group_waves)
         work.pieces_host = _as_i32(pieces).reshape(-1, PIECE_FIELDS)
         work.wave_first_host = _as_i32(first)
         work.jobs_host = _as_i32(jobs).reshape(-1, MERGE_FIELDS)

@@ -23,6 +23,9 @@ path (paths relative to light-vllm's source tree):
                                 blocks); its definition is the closed form below.
 * ``rotary_half``               src/light_vllm/modeling/models/_qwen2_kernels.py:214-224
                                 (apply_rotary's PyTorch path, with its rounding)
+* ``kv_cache_bytes_per_block`` / ``planned_num_blocks``
+                                src/light_vllm/runtime/execution/paged_cache.py:52-65, 98-114
+                                (the capacity planner's arithmetic)
 
 How each function is pinned (tests/test_oracle.py):
 * slot mapping, validation, visibility, request indices, layouts and compact:
@@ -32,6 +35,9 @@ How each function is pinned (tests/test_oracle.py):
 * rotary_half: torch's own CPU arithmetic in the tensor dtype running the
   reference expression, closed forms (cos 1 / sin 0 is the identity, cos 0 /
   sin 1 the pure half swap), norm preservation, and planted mistakes;
+* kv_cache_bytes_per_block / planned_num_blocks: known answers for the
+  Qwen2.5 shapes (bytes written out by hand from the layer shapes) and a
+  brute-force allocation count (blocks added until the budget is exceeded);
 * paged_attention: the fp64 dense softmax on random inputs (GQA, tree masks,
   multi-block, shared prefix, lookahead), plus closed forms (one visible key
   gives that key's value; identical keys give the mean of the visible values),
@@ -331,10 +337,9 @@ def dense_attention(
 
     query = np.asarray(query, dtype=np.float64)
     block_size = key_pool.shape[1]
-    num_q_heads = query.shape[1]
+    num_q_heads, head_size = query.shape[1], query.shape[2]
     num_kv_heads = key_pool.shape[2]
-    group = num_q_heads // num_kv_heads
-    kv_of_head = np.arange(num_q_heads) // group
+    group = num_q_heads // num_kv_heads  # q head h reads kv head h // group
     out = np.zeros_like(query)
     start = 0
     for table, c, parents in zip(block_tables, computed, layouts):
@@ -342,16 +347,21 @@ def dense_attention(
         length = c + q_len
         pos = np.arange(length)
         blocks = np.asarray(table)[pos // block_size]
-        keys = np.asarray(key_pool[blocks, pos % block_size], dtype=np.float64)[:, kv_of_head]
-        vals = np.asarray(value_pool[blocks, pos % block_size], dtype=np.float64)[:, kv_of_head]
+        # [kv head, key, dim]; the query heads of a kv head are its group.
+        keys = np.asarray(key_pool[blocks, pos % block_size], dtype=np.float64).transpose(1, 0, 2)
+        vals = np.asarray(value_pool[blocks, pos % block_size], dtype=np.float64).transpose(1, 0, 2)
         mask = np.ones((q_len, length), dtype=bool)
         mask[:, c:] = query_visibility(tuple(parents))
-        scores = np.einsum("qhd,thd->qht", query[start : start + q_len], keys) * float(scale)
-        scores = np.where(mask[:, None, :], scores, -np.inf)
-        scores -= scores.max(axis=2, keepdims=True)
+        q = query[start : start + q_len].reshape(q_len, num_kv_heads, group, head_size).transpose(1, 0, 2, 3)
+        q = q.reshape(num_kv_heads, q_len * group, head_size)
+        scores = np.matmul(q, keys.transpose(0, 2, 1)).reshape(num_kv_heads, q_len, group, length) * float(scale)
+        scores = np.where(mask[None, :, None, :], scores, -np.inf)
+        scores -= scores.max(axis=3, keepdims=True)
         probs = np.exp(scores)
-        probs /= probs.sum(axis=2, keepdims=True)
-        out[start : start + q_len] = np.einsum("qht,thd->qhd", probs, vals)
+        probs /= probs.sum(axis=3, keepdims=True)
+        o = np.matmul(probs.reshape(num_kv_heads, q_len * group, length), vals)  # [kv head, q x group, dim]
+        out[start : start + q_len] = o.reshape(num_kv_heads, q_len, group, head_size).transpose(1, 0, 2, 3).reshape(
+            q_len, num_q_heads, head_size)
         start += q_len
     return out
 
@@ -364,3 +374,22 @@ def visible_positions(computed: int, parents: tuple[int, ...]) -> list[list[int]
 
 def softmax_scale(head_size: int) -> float:
     return 1.0 / math.sqrt(head_size)
+
+
+def kv_cache_bytes_per_block(layers, *, block_size: int, element_size: int) -> int:
+    """Bytes of one physical block over every layer: K and V rows of each
+    layer's (num_kv_heads, head_size), ``block_size`` tokens
+    (paged_cache.py:52-65).  ``layers``: (num_kv_heads, head_size) pairs."""
+
+    per_token = sum(2 * hkv * d for hkv, d in layers)
+    return block_size * per_token * element_size
+
+
+def planned_num_blocks(free_bytes: int, memory_fraction: float, layers, *, block_size: int,
+                       element_size: int) -> int:
+    """Whole blocks in ``int(free_bytes * memory_fraction)`` bytes
+    (CudaMemoryKVCachePlanner.plan, paged_cache.py:98-114); 0 means the
+    planner raises KVCacheCapacityError."""
+
+    budget = int(free_bytes * memory_fraction)
+    return budget // kv_cache_bytes_per_block(layers, block_size=block_size, element_size=element_size)

@@ -400,3 +400,66 @@ def test_one_metadata_on_caches_of_two_dtypes() -> None:
         mx, mean = _forward_error(s, lid, out)
         max_tol, mean_tol = tolerances(s.query.dtype)
         assert mx <= max_tol and mean <= mean_tol, (s.query.dtype, mx, mean)
+
+
+# ------------------------------------------------------ workgroup split (latency-bound decode)
+@pytest.mark.parametrize("dtype", ("fp32", "fp16", "bf16"))
+@pytest.mark.parametrize("head_size", (32, 64, 80, 96, 128, 256))
+def test_workgroup_split_decode_matches_the_oracle(dtype, head_size) -> None:
+    # Short decode rows (one segment per workgroup of four waves, results
+    # combined in LDS): a 1-token context, segments of 1-3 tiles (idle
+    # waves) and of more than four, with the append fused.
+    _announce(f"workgroup split d={head_size} {dtype}")
+    hq, hkv = (28, 4) if head_size <= 128 else (16, 2)
+    step = make_step(hq=hq, hkv=hkv, d=head_size, bs=16, dtype=DTYPES[dtype],
+                     computed=[0, 31, 40, 250, 200, 130, 97, 5], layouts=_lin(*([1] * 8)), seed=400 + head_size)
+    _, ctx = _run_and_check(step)
+    work = ctx.work_of(step.cache.layer_spec(step.layer_ids[0]))
+    assert work.group_waves == 4 and work.num_jobs == 0
+
+
+@pytest.mark.parametrize("dtype", ("fp32", "bf16"))
+def test_workgroup_split_of_multi_tile_rows_without_prefill_kernel(dtype) -> None:
+    # Query runs wider than one column tile through the decode kernel (as
+    # for fp32 layers): each (request, column tile) segment takes its own
+    # workgroup, and the LDS merge writes that tile's columns.
+    _announce(f"workgroup split, column tiles 1-5 {dtype}")
+    step = make_step(hq=4, hkv=2, d=64, bs=16, dtype=DTYPES[dtype], computed=[20, 90, 3],
+                     layouts=_lin(40, 9, 17), seed=420)
+    backend = lv.HipPagedAttentionBackend(use_prefill_kernel=False, decode_col_tiles=1)
+    _, ctx = _run_and_check(step, backend=backend)
+    assert ctx.work_of(step.cache.layer_spec(step.layer_ids[0])).group_waves == 4
+
+
+@pytest.mark.parametrize("bs", (1, 3, 16))
+@pytest.mark.parametrize("hq,hkv", ((4, 4), (32, 4), (12, 2)))
+def test_workgroup_split_block_sizes_and_groups(bs, hq, hkv) -> None:
+    # Block sizes through the division path and the first-tile block ids,
+    # group sizes 1, 8 and 6, against the oracle and the stream-K plan.
+    _announce(f"workgroup split bs={bs} {hq}/{hkv}")
+    step = make_step(hq=hq, hkv=hkv, d=128, bs=bs, dtype=torch.bfloat16, computed=[250, 17, 260, 3, 129],
+                     layouts=_lin(1, 1, 1, 1, 1), num_layers=2, seed=410 + bs + hq)
+    out, ctx = _run_and_check(step)
+    assert ctx.work_of(step.cache.layer_spec(step.layer_ids[0])).group_waves == 4
+    ref = lv.HipPagedAttentionBackend(decode_workgroups=False).create(step.cache, step.metadata)
+    lid = step.layer_ids[1]
+    # (layer1's pool holds this step's K/V only after the forward below)
+    out1 = ctx.forward(lid, step.query, step.key, step.value, scale=step.scale)
+    out2 = ref.forward(lid, step.query, step.key, step.value, scale=step.scale)
+    torch.cuda.synchronize()
+    assert ref.work_of(step.cache.layer_spec(lid)).group_waves == 1
+    max_tol, _ = tolerances(step.query.dtype)
+    assert (out1.float() - out2.float()).abs().max().item() <= max_tol
+
+
+@pytest.mark.parametrize("head_size", (48, 112, 160, 192))
+def test_unbuilt_head_sizes_are_refused_when_the_step_starts(head_size) -> None:
+    # The kernels are built for head sizes 32, 64, 80, 96, 128 and 256; a
+    # cache with another layer shape fails at create() with the reference's
+    # error class, before any layer's forward.
+    spec = lv.ModelKVCacheSpec((lv.AttentionLayerSpec("a", 8, 2, 128), lv.AttentionLayerSpec("b", 8, 2, head_size)))
+    cache = lv.PagedKVCache(spec, lv.PagedKVCacheConfig(num_blocks=8, block_size=16, dtype=torch.bfloat16, device=DEV))
+    md = lv.PagedAttentionMetadata(block_tables=((0,),), num_computed_tokens=(3,),
+                                   query_layouts=(lv.linear_query_layout(1),))
+    with pytest.raises(lv.KVCacheError, match=f"not {head_size}"):
+        lv.HipPagedAttentionBackend().create(cache, md)

@@ -259,3 +259,53 @@ def test_read_probe_reads_every_chunk_once(nbytes, workgroups) -> None:
     assert got == np.bitwise_xor.reduce(words)
     # A size that is not a multiple of 16 is refused (LVAMD_ERR_INVALID_ARGUMENT).
     assert lib.lvamd_hbm_read_probe(buf.data_ptr(), 8, sink.data_ptr(), workgroups, stream) == -1
+
+
+def test_cache_built_from_the_capacity_planners_config() -> None:
+    # light-vllm sizes the pool with CudaMemoryKVCachePlanner (paged_cache.py:
+    # 69-114): free device memory x a fraction, divided by the bytes of one
+    # block over all layers, in a PagedKVCacheConfig of its own class.  That
+    # config builds this package's cache unchanged (its fields are read, not
+    # its class), the pools hold exactly the planned bytes, and decode runs on
+    # a cache so sized.
+    _announce("cache from the capacity planner's config")
+    from dataclasses import dataclass
+
+    @dataclass(frozen=True)
+    class PlannerConfig:  # the reference config's fields, another class
+        num_blocks: int
+        block_size: int
+        dtype: torch.dtype
+        device: torch.device
+
+    layers = [(4, 128)] * 3
+    spec = lv.ModelKVCacheSpec(tuple(lv.AttentionLayerSpec(f"l{i}", 28, hkv, d) for i, (hkv, d) in enumerate(layers)))
+    free, _ = torch.cuda.mem_get_info(DEV)
+    fraction = min(0.004, (1 << 30) / free)  # a small slice of the free memory
+    num_blocks = O.planned_num_blocks(free, fraction, layers, block_size=16, element_size=2)
+    assert num_blocks > 0
+    config = PlannerConfig(num_blocks=num_blocks, block_size=16, dtype=torch.bfloat16, device=DEV)
+    cache = lv.PagedKVCache(spec, config)
+    pool_bytes = sum(cache.layer(f"l{i}").keys.nbytes + cache.layer(f"l{i}").values.nbytes for i in range(3))
+    per_block = O.kv_cache_bytes_per_block(layers, block_size=16, element_size=2)
+    assert pool_bytes == num_blocks * per_block <= int(free * fraction)
+    assert cache.config is config
+    computed = [100, 700]
+    need = [(c + 1 + 15) // 16 for c in computed]
+    tables = (tuple(range(need[0])), tuple(range(num_blocks - need[1], num_blocks)))
+    md = lv.PagedAttentionMetadata(block_tables=tables, num_computed_tokens=tuple(computed),
+                                   query_layouts=(lv.linear_query_layout(1), lv.linear_query_layout(1)))
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    q = torch.randn((2, 28, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    k = torch.randn((2, 4, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    layer = cache.layer("l0")
+    for pool in (layer.keys, layer.values):
+        pool.zero_()
+    out = lv.HipPagedAttentionBackend().create(cache, md).forward("l0", q, k, k, scale=0.1)
+    torch.cuda.synchronize()
+    # Zero history: each query sees its own key among zero keys, so the
+    # output is the softmax-weighted mean of zero rows and its own value.
+    scores = (q.float() * 0.1 * k.float().repeat_interleave(7, dim=1)).sum(-1)  # [2, 28]
+    weight = torch.exp(scores) / (torch.exp(scores) + torch.tensor(computed, device=DEV)[:, None])
+    expect = weight[..., None] * k.float().repeat_interleave(7, dim=1)
+    assert (out.float() - expect).abs().max().item() <= 2e-2

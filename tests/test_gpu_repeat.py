@@ -73,7 +73,16 @@ def _run(backend, step):
     return out.clone()
 
 
+def _short_decode_step(seed):
+    # Short contexts: the workgroup split (four waves per segment, LDS merge).
+    rng = np.random.default_rng(seed)
+    computed = [int(c) for c in rng.integers(0, 400, size=16)]
+    return make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=computed, layouts=[(-1,)] * 16,
+                     seed=seed)
+
+
 CASES = {
+    "short decode (workgroup split)": lambda: _short_decode_step(67),
     "decode bf16": lambda: _decode_step(torch.bfloat16, 61),
     "decode fp32": lambda: _decode_step(torch.float32, 62),
     "trees over a shared prefix": lambda: _tree_step(63),

@@ -414,3 +414,43 @@ def test_planted_rotary_mistakes_fail(name) -> None:
     bad = mutant(_as_bits(x), _as_bits(cos), _as_bits(sin), "bf16")
     np.testing.assert_array_equal(good, expected)
     assert (bad != expected).any()
+
+
+# ------------------------------------------------------ capacity planner arithmetic
+def test_bytes_per_block_known_answers() -> None:
+    # Qwen2.5-7B: 28 layers x K and V x 4 kv heads x 128 dims x 16 tokens x 2 bytes.
+    assert O.kv_cache_bytes_per_block([(4, 128)] * 28, block_size=16, element_size=2) == 917_504
+    # Qwen2.5-1.5B: 28 x 2 x 2 x 128 x 16 x 2; Qwen2.5-0.5B in fp32: 24 x 2 x 2 x 64 x 16 x 4.
+    assert O.kv_cache_bytes_per_block([(2, 128)] * 28, block_size=16, element_size=2) == 458_752
+    assert O.kv_cache_bytes_per_block([(2, 64)] * 24, block_size=16, element_size=4) == 393_216
+    # Layers of different kv shapes add up.
+    assert O.kv_cache_bytes_per_block([(4, 128), (2, 64)], block_size=1, element_size=2) == 2 * (512 + 128) * 2
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_planned_blocks_are_the_most_that_fit_the_budget(seed) -> None:
+    # Brute force: blocks added one by one until the next one would exceed
+    # int(free * fraction) bytes.
+    rng = np.random.default_rng(seed)
+    layers = [(int(rng.choice([1, 2, 4, 8])), int(rng.choice([64, 80, 128]))) for _ in range(int(rng.integers(1, 6)))]
+    bs, es = int(rng.choice([1, 16, 32])), int(rng.choice([2, 4]))
+    free = int(rng.integers(1 << 20, 1 << 28))
+    fraction = float(rng.uniform(0.05, 1.0))
+    per_block = O.kv_cache_bytes_per_block(layers, block_size=bs, element_size=es)
+    n = 0
+    while (n + 1) * per_block <= int(free * fraction):
+        n += 1
+    assert O.planned_num_blocks(free, fraction, layers, block_size=bs, element_size=es) == n
+    assert O.planned_num_blocks(per_block - 1, 1.0, layers, block_size=bs, element_size=es) == 0
+
+
+def test_package_bytes_per_block_follow_the_planner() -> None:
+    # The backend's own figure (PagedKVCache allocates exactly this per block)
+    # equals the planner's, so a planner budget maps to the same block count.
+    import light_vllm_amd as lv
+    import torch
+
+    spec = lv.ModelKVCacheSpec((lv.AttentionLayerSpec("a", 28, 4, 128), lv.AttentionLayerSpec("b", 12, 2, 64)))
+    for dtype, es in ((torch.bfloat16, 2), (torch.float32, 4)):
+        got = lv.paged_cache.kv_cache_bytes_per_block(spec, block_size=16, dtype=dtype)
+        assert got == O.kv_cache_bytes_per_block([(4, 128), (2, 64)], block_size=16, element_size=es)
