@@ -152,14 +152,16 @@ int lvamd_kv_append_rotary(const void* query, int64_t query_token_stride, int64_
  * to part_acc [slots][num_kv_heads][16 * col_tiles][head_size], and its fp32
  * (max, sum) to part_ml [slots][num_kv_heads][16 * col_tiles][2].
  *
- * Workgroup split: with group_waves 4 (col_tiles 1) the waves run in
- * workgroups of four, waves 4b .. 4b + 3 of a kv head in workgroup b, and each
- * workgroup holds the pieces of one segment, at most one per wave (a wave
- * without a piece idles).  A segment left whole in its workgroup's first
+ * Workgroup split: with group_waves W = lvamd_paged_decode_split_waves(...)
+ * (col_tiles 1) the waves run in workgroups of W, waves W*b .. W*b + W - 1 of
+ * a kv head in workgroup b, each workgroup holds one segment, and pieces
+ * holds exactly one record per wave (wave w's at index w; wave_first is not
+ * read): a piece of the segment, or an idle record with req -1 (idle waves
+ * follow the active ones).  A segment left whole in its workgroup's first
  * wave (partial_slot -1) is written by that wave; the pieces of a split one
  * (partial_slot >= 0) are combined in the workgroup's LDS and written by the
  * workgroup: no partials, no merge launch.  waves_per_head must then be a
- * multiple of 4.  group_waves 1 is the stream-K layout above.
+ * multiple of W.  group_waves 1 is the stream-K layout above.
  *
  * Append: when new_key / new_value are given ([tokens][num_kv_heads][D] with
  * the given strides), keys and values at positions >= computed are read from
@@ -193,10 +195,15 @@ int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_str
                        int32_t num_kv_heads, int32_t group, int32_t head_size, int32_t col_tiles,
                        int32_t group_waves, int32_t block_size, float scale, int32_t dtype, lvamd_stream_t stream);
 
-/* Workgroups of the workgroup-split decode kernel (group_waves 4, one column
- * tile) the current device holds at once for this dtype and head size: the
- * planner uses the split only when a step's segments fit them.  Needs a GPU. */
+/* Workgroups of the workgroup-split decode kernel (one column tile) the
+ * current device holds at once for this dtype and head size: the planner uses
+ * the split only when a step's segments fit them.  Needs a GPU. */
 int lvamd_paged_decode_split_groups(int32_t dtype, int32_t head_size);
+
+/* Waves per workgroup of the workgroup-split decode kernel for this dtype and
+ * head size (the group_waves it takes): 8, or 4 where eight would spill or
+ * exceed the LDS. */
+int lvamd_paged_decode_split_waves(int32_t dtype, int32_t head_size);
 
 /* How many decode waves (workgroups) the current device holds at once for this
  * dtype, head size and col_tiles: the planner's stream-K width.  Needs a GPU. */
@@ -282,7 +289,7 @@ typedef struct lvamd_attention_plan {
   const int32_t* jobs;
   int32_t num_jobs;
   int32_t merge_columns;
-  int32_t group_waves; /* 1: stream-K; 4: workgroup split */
+  int32_t group_waves; /* 1: stream-K; lvamd_paged_decode_split_waves: workgroup split */
   /* Prefill rows (num_units 0: none). */
   const int32_t* units;
   int32_t num_units;

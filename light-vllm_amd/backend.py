@@ -477,8 +477,9 @@ class HipPagedAttentionBackend:
         ``"grouped"`` always, ``"plain"`` never (heaviest first only);
         ``decode_workgroups=False`` keeps every decode step on stream-K
         shares (by default a latency-bound step, whose segments fit the
-        resident workgroups, runs one segment per workgroup of four waves
-        that combine their results in LDS, with no merge launch)."""
+        resident workgroups, runs one segment per workgroup of eight waves,
+        four for the widest rows, that combine their results in LDS, with no
+        merge launch)."""
 
         native.load()
         native.host()
@@ -534,6 +535,7 @@ class HipPagedAttentionBackend:
                 self._partition_tokens or 0, DECODE_MAX_COLUMNS, 4, PREFILL_MIN_TILES, int(self._shared_prefix),
                 native.xcd_count() if columns else 0, self._prefill_order,
                 native.decode_split_groups(code, d) if self._decode_workgroups else 0,
+                native.decode_split_waves(code, d),
             )
             self._facts[key] = found
         return found

@@ -150,26 +150,33 @@ struct LaneCol {
   const uint32_t* vrow;
 };
 
-// Waves per workgroup of the workgroup split.
-constexpr int kSplitWaves = 4;
-
-// Workgroup split (WG = 4): a latency-bound step (few short segments) is
-// spread over workgroups of four waves, one segment each: each wave runs one
+// Workgroup split (WG > 1): a latency-bound step (few short segments) is
+// spread over workgroups of WG waves, one segment each: each wave runs one
 // piece of its segment, the waves combine their results in LDS, and the
 // segment's output is written by the workgroup, with no partials in memory
 // and no merge launch.  WG = 1 is the stream-K kernel (one wave per
 // workgroup, split segments merged by lvamd_paged_attention_merge).
+//
+// WG is eight where eight waves fit a CU without spilling (two waves per
+// SIMD: at most 256 registers each) and their V buffers fit its LDS:
+// bf16/fp16 up to D = 128 and fp32 up to D = 96; four otherwise.  With one
+// piece per wave the kernel needs no next-piece prefetch registers.
+template <typename T, int D>
+constexpr int split_waves() {
+  return (sizeof(T) == 2 && D <= 128) || (sizeof(T) == 4 && D <= 96) ? 8 : 4;
+}
 // Wave i's result lives in its own LDS: (max, sum) of column c at ml + i *
 // ml_stride + 2c, the fp32 row at acc + i * acc_stride + c * D.
 template <typename T, int D, int CTW, int WG>
 __device__ __forceinline__ void merge_workgroup(const DecodeArgs& a, const float* ml, int ml_stride,
                                                 const float* acc, int acc_stride, int kvh, int cgroup, int q_start,
                                                 int q_len) {
-  // Thread t: column t % 16 of the segment's column tile (column group
-  // cgroup), dims [(t / 16) * D / 16, + D / 16); the waves' rows weigh
+  // Thread t < 256: column t % 16 of the segment's column tile (column
+  // group cgroup), dims [(t / 16) * D / 16, + D / 16); the waves' rows weigh
   // sum_i * 2^(max_i - max) (each row normalised by its own sum).
   constexpr int DPT = D / 16;
   const int t = threadIdx.x;
+  if (t >= 256) return;
   const int c = t & 15;
   const int d0 = (t >> 4) * DPT;
   const int col = cgroup * 16 + c;
@@ -215,18 +222,21 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
   static_assert(WG == 1 || CTW == 1, "the workgroup split runs one column tile per wave");
   // One column tile prefetches the next piece's Q; four load theirs at the
   // piece switch (their registers hold the extra accumulators instead).
-  constexpr bool kPrefetchQ = CTW == 1;
-  // Per wave: two V buffers and a table slice pair; in the workgroup split
-  // the first V buffers also take the waves' results at the end (fp32 rows).
-  __shared__ __attribute__((aligned(16))) uint4 vlds_a_all[WG * DT::VALLOC];
-  __shared__ __attribute__((aligned(16))) uint4 vlds_b_all[WG * DT::VALLOC];
+  // (In the workgroup split a wave has one piece: nothing to prefetch.)
+  constexpr bool kPrefetchQ = CTW == 1 && WG == 1;
+  // Per wave: two V buffers (contiguous) and a table slice pair; in the
+  // workgroup split the V buffers also take the wave's results at the end
+  // (fp32 rows), and they are not padded (the stream-K kernel's padding
+  // keeps it at one wave per SIMD).
+  constexpr int VAL = WG == 1 ? DT::VALLOC : DT::VSLOTS;
+  __shared__ __attribute__((aligned(16))) uint4 vlds_all[WG][2][VAL];
   __shared__ int32_t tab_all[WG][2][kTableSlice];
-  static_assert(WG == 1 || 16 * D * 4 <= DT::VALLOC * 16, "a wave's result rows must fit its V buffer");
+  static_assert(WG == 1 || 16 * D * 4 <= 2 * VAL * 16, "a wave's result rows must fit its V buffers");
 
   const int lane = threadIdx.x & 63;  // (the mask tells LLVM lane < 64)
   const int wid = WG == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  uint4* const vlds_a = vlds_a_all + wid * DT::VALLOC;
-  uint4* const vlds_b = vlds_b_all + wid * DT::VALLOC;
+  uint4* const vlds_a = &vlds_all[wid][0][0];
+  uint4* const vlds_b = &vlds_all[wid][1][0];
   int32_t(*const tab)[kTableSlice] = tab_all[wid];
   const int l16 = lane & 15;
   const int g = lane >> 4;
@@ -238,24 +248,26 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
   const int wg_per_head = waves_per_head / kWG;
   const int kvh = blockIdx.x / wg_per_head;
   const int w = (blockIdx.x - kvh * wg_per_head) * kWG + wid;
-  int p = wave_first[w];
-  const int p_end = wave_first[w + 1];
+  // The workgroup split holds one record per wave (wave w's at index w; an
+  // idle wave's has request -1), so no wave_first lookup delays it.
+  int p = WG == 1 ? wave_first[w] : w;
+  const int p_end = WG == 1 ? wave_first[w + 1] : (pieces[(int64_t)w * LVAMD_PIECE_FIELDS] >= 0 ? w + 1 : w);
   // Workgroup split: each wave's result rows (fp32, normalised) in its own
-  // first V buffer and its (max, sum) pairs in its own table slice, then the
+  // V buffers and its (max, sum) pairs in its own table slices, then the
   // segment's merge once every wave has written.
-  constexpr int kAccStride = DT::VALLOC * 4;   // floats per wave's V buffer
-  constexpr int kMlStride = 2 * kTableSlice;   // floats per wave's table slices
+  constexpr int kAccStride = 2 * VAL * 4;     // floats per wave's V buffers
+  constexpr int kMlStride = 2 * kTableSlice;  // floats per wave's table slices
   float* const wg_acc = reinterpret_cast<float*>(vlds_a);
   float* const wg_ml = reinterpret_cast<float*>(&tab[0][0]);
   auto finish_workgroup = [&]() {
     if constexpr (WG > 1) {
       __syncthreads();
-      const int32_t* lead = pieces + (int64_t)wave_first[w - wid] * LVAMD_PIECE_FIELDS;
+      const int32_t* lead = pieces + (int64_t)(w - wid) * LVAMD_PIECE_FIELDS;
       // A segment left whole in its first wave was written by that wave.
       if (lead[4] >= 0)
         merge_workgroup<T, D, CTW, WG>(a, reinterpret_cast<const float*>(&tab_all[0][0][0]), kMlStride,
-                                       reinterpret_cast<const float*>(vlds_a_all), kAccStride, kvh, lead[1],
-                                       lead[8], lead[7]);
+                                       reinterpret_cast<const float*>(&vlds_all[0][0][0]), kAccStride, kvh,
+                                       lead[1], lead[8], lead[7]);
     }
   };
   if (p >= p_end) {
@@ -428,7 +440,7 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
     issue_tile(cur, tb, cur.tok_begin, ka, vr0, fresh0);
   }
   load_q(cur, qf);
-  bool have_nxt = p + 1 < p_end;
+  bool have_nxt = WG == 1 && p + 1 < p_end;
   bool nxt_stored = false;  // the next piece's table slice is in tab[tb ^ 1]
   Piece nxt = cur;
   if (have_nxt) {
@@ -670,7 +682,7 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
           for (int r = 0; r < 4; ++r) orow[16 * n + 4 * g + r] = from_f32<T>(ax[ct][n][r] * inv);
       } else if constexpr (WG > 1) {
         // Workgroup split: this wave's fp32 rows and (max, sum) into LDS
-        // (the wave's own V buffer, free once its last tile is done).
+        // (the wave's own V buffers, free once its last tile is done).
         const float inv = sx[ct] > 0.f ? 1.f / sx[ct] : 0.f;
         float* racc = wg_acc + l16 * D;
 #pragma unroll
@@ -698,7 +710,7 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
   // in-flight tile loads, and reusing the accumulators would wait for them
   // (about 2 us per switch, measured).  Four column tiles and rows above 256
   // bytes have no registers to spare and write at once.
-  constexpr bool kDeferWrite = CTW == 1 && (int)sizeof(T) * D <= 256;
+  constexpr bool kDeferWrite = CTW == 1 && WG == 1 && (int)sizeof(T) * D <= 256;
   bool pend = false;
   Piece pend_piece = cur;
   LaneCol pend_lc[CTW];
@@ -754,7 +766,7 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
     }
     t0 = cur.tok_begin;
     ++p;
-    have_nxt = p + 1 < p_end;
+    have_nxt = WG == 1 && p + 1 < p_end;
     nxt_stored = false;
     if (have_nxt) {
       nxt = read_piece(pieces, p + 1);
@@ -982,7 +994,8 @@ extern "C" int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t
                                   lvamd_stream_t stream) {
   const int es = dtype_size(dtype);
   if (es == 0 || !head_size_supported(head_size) || !col_tiles_supported(col_tiles)) return LVAMD_ERR_UNSUPPORTED;
-  if (group_waves != 1 && !(group_waves == kSplitWaves && col_tiles == 1)) return LVAMD_ERR_UNSUPPORTED;
+  if (group_waves != 1 && (col_tiles != 1 || group_waves != lvamd_paged_decode_split_waves(dtype, head_size)))
+    return LVAMD_ERR_UNSUPPORTED;
   if (waves_per_head < 0 || num_kv_heads <= 0 || group <= 0 || block_size <= 0 || num_partial_slots < 0 ||
       waves_per_head % group_waves != 0)
     return LVAMD_ERR_INVALID_ARGUMENT;
@@ -1028,12 +1041,14 @@ extern "C" int lvamd_paged_decode(const void* q, int64_t q_token_stride, int64_t
   hipStream_t s = static_cast<hipStream_t>(stream);
   return dispatch_decode(dtype, head_size, col_tiles, [&]<typename T, int D, int CTW>() -> int {
     if constexpr (CTW == 1) {
-      if (group_waves == kSplitWaves) {
-        hipLaunchKernelGGL((paged_decode_kernel<T, D, CTW, kSplitWaves>), grid, dim3(64 * kSplitWaves), 0, s,
-                           wave_first, pieces, waves_per_head, a);
+      constexpr int WG = split_waves<T, D>();
+      if (group_waves == WG) {
+        hipLaunchKernelGGL((paged_decode_kernel<T, D, CTW, WG>), grid, dim3(64 * WG), 0, s, wave_first, pieces,
+                           waves_per_head, a);
         return launch_status();
       }
     }
+    if (group_waves != 1) return LVAMD_ERR_UNSUPPORTED;
     hipLaunchKernelGGL((paged_decode_kernel<T, D, CTW, 1>), grid, dim3(64), 0, s, wave_first, pieces,
                        waves_per_head, a);
     return launch_status();
@@ -1049,12 +1064,19 @@ extern "C" int lvamd_paged_decode_split_groups(int32_t dtype, int32_t head_size)
       if (hipGetDevice(&device) != hipSuccess) return LVAMD_ERR_LAUNCH;
       if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
         return LVAMD_ERR_LAUNCH;
+      constexpr int WG = split_waves<T, D>();
       if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-              &per_cu, reinterpret_cast<const void*>(&paged_decode_kernel<T, D, CTW, kSplitWaves>),
-              64 * kSplitWaves, 0) != hipSuccess)
+              &per_cu, reinterpret_cast<const void*>(&paged_decode_kernel<T, D, CTW, WG>), 64 * WG, 0) !=
+          hipSuccess)
         return LVAMD_ERR_LAUNCH;
       return per_cu * cus;
     }
+  });
+}
+
+extern "C" int lvamd_paged_decode_split_waves(int32_t dtype, int32_t head_size) {
+  return dispatch_decode(dtype, head_size, 1, []<typename T, int D, int CTW>() -> int {
+    return split_waves<T, D>();
   });
 }
 

@@ -948,15 +948,21 @@ struct DecodeLists {
 struct DecodeParams {
   int64_t group, col_tiles, max_cols, hkv, resident, bs, min_units, max_units, unit;
   int64_t split_groups = 0;  // resident workgroups of the workgroup-split kernel (0: not built)
+  int64_t split_waves = 0;   // its waves per workgroup
 };
 
-// Workgroup split of the decode kernel: workgroups of kSplitWaves waves, one
-// segment each, its pieces combined in LDS.  The planner takes it when the
-// step's segments fit the resident workgroups and its longest piece, in
-// tiles, is no longer than stream-K's largest share plus what the merge
-// launch it saves costs (kSplitMergeTiles tiles).
-constexpr int64_t kSplitWaves = 4;
+// Workgroup split of the decode kernel: workgroups of split_waves waves, one
+// segment each, its pieces combined in LDS.  The planner takes it for
+// latency-bound steps: the step's segments fit the resident workgroups, no
+// wave gets more than kSplitMaxTiles tiles (a CU then streams at most
+// split_waves * kSplitMaxTiles tiles, where its waves' load latency, not the
+// CU's share of HBM bandwidth, bounds it), and the longest piece is no longer
+// than stream-K's largest share plus what the merge launch it saves costs
+// (kSplitMergeTiles tiles).  (Without the cap C2's 64 contexts of 512-4096
+// tokens took one CU per segment: 84 us against 59 us on stream-K shares, the
+// longest segment's CU streaming alone at the end.)
 constexpr int64_t kSplitMergeTiles = 3;
+constexpr int64_t kSplitMaxTiles = 4;
 
 void build_decode(const Requests& q, const int32_t* ids, int64_t nflat, const DecodeParams& d, DecodeLists& out) {
   struct Seg {
@@ -1059,30 +1065,36 @@ void build_decode(const Requests& q, const int32_t* ids, int64_t nflat, const De
   }
   while (w <= waves) out.first[(size_t)w++] = (int32_t)recs.size();
 
-  // The workgroup split instead, when it is no slower (see kSplitWaves).
-  if (d.split_groups <= 0 || d.col_tiles != 1) return;
+  // The workgroup split instead, when it is no slower (see kSplitMergeTiles):
+  // one record per wave, an idle wave's with request -1.
+  const int64_t gw = d.split_waves;
+  if (d.split_groups <= 0 || gw <= 1 || d.col_tiles != 1) return;
   int64_t longest = 0;
   for (const Seg& sg : segs) longest = std::max(longest, sg.tiles);
-  const int64_t split_share = (longest + kSplitWaves - 1) / kSplitWaves;
+  const int64_t split_share = (longest + gw - 1) / gw;
   const int64_t nseg = (int64_t)segs.size();
-  if (nseg * d.hkv > d.split_groups || split_share > cap) return;
+  if (nseg * d.hkv > d.split_groups || split_share > cap || split_share > kSplitMaxTiles) return;
   if (split_share > per_wave + (out.jobs.empty() ? 0 : kSplitMergeTiles)) return;
   out.reset();
-  out.group_waves = kSplitWaves;
-  out.waves = kSplitWaves * nseg;
+  out.group_waves = gw;
+  out.waves = gw * nseg;
   out.per_wave = split_share;
-  out.first.assign((size_t)out.waves + 1, 0);
-  int32_t np = 0;
+  out.first.resize((size_t)out.waves + 1);
+  std::iota(out.first.begin(), out.first.end(), 0);
+  out.pieces.assign((size_t)(out.waves * kPieceFields), 0);
   for (int64_t s = 0; s < nseg; ++s) {
     const Seg& sg = segs[(size_t)s];
     const int32_t* m = q.row(sg.req);
-    const int64_t n = std::min(kSplitWaves, sg.tiles);
+    const int64_t n = std::min(gw, sg.tiles);
     const int64_t seq_end = q.computed(sg.req) + q.q_len(sg.req);
-    for (int64_t i = 0; i < kSplitWaves; ++i) {
-      out.first[(size_t)(kSplitWaves * s + i)] = np;
-      if (i >= n) continue;
+    for (int64_t i = 0; i < gw; ++i) {
+      int32_t* o = out.pieces.data() + (s * gw + i) * kPieceFields;
+      if (i >= n) {
+        o[0] = -1;  // an idle wave
+        o[4] = -1;
+        continue;
+      }
       const int64_t lo = i * sg.tiles / n, hi = (i + 1) * sg.tiles / n;
-      int32_t o[kPieceFields] = {};
       o[0] = sg.req;
       o[1] = sg.group;
       o[2] = (int32_t)(lo * d.unit);
@@ -1099,11 +1111,8 @@ void build_decode(const Requests& q, const int32_t* ids, int64_t nflat, const De
         const int64_t lb = lb0 + k, idx = m[0] + lb;
         o[11 + k] = (lb < m[1] && idx < nflat) ? ids[idx] : 0;
       }
-      out.pieces.insert(out.pieces.end(), o, o + kPieceFields);
-      ++np;
     }
   }
-  out.first[(size_t)out.waves] = np;
 }
 
 struct PrefillLists {
@@ -1531,22 +1540,22 @@ bool requests_of(const Buf& meta, Requests* q, const char* name) {
 
 // decode_work(req_meta i32[B*8], flat i32, group, col_tiles, decode_max_columns,
 //             num_kv_heads, resident_waves, block_size, min_units_per_wave,
-//             max_units_per_wave (0 = none), unit_tokens, split_groups)
+//             max_units_per_wave (0 = none), unit_tokens, split_groups, split_waves)
 //   -> (pieces i32 [n, 16], wave_first i32 [W + 1], jobs i32 [m, 8],
 //       W, largest share, partial slots, most columns of a merge job,
 //       waves per workgroup)
 // split_groups: resident workgroups of the workgroup-split kernel (0: never
-// split in workgroups).
+// split in workgroups) and split_waves its waves per workgroup.
 PyObject* decode_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
-  if (!want_args(nargs, 12, "decode_work")) return nullptr;
+  if (!want_args(nargs, 13, "decode_work")) return nullptr;
   Buf meta(args[0], false, 4, "req_meta"), flat(args[1], false, 4, "flat");
   if (!meta.ok() || !flat.ok()) return nullptr;
   Requests q;
   if (!requests_of(meta, &q, "decode_work")) return nullptr;
   DecodeParams d;
-  int64_t* fields[] = {&d.group, &d.col_tiles, &d.max_cols, &d.hkv,       &d.resident,
-                       &d.bs,    &d.min_units, &d.max_units, &d.unit, &d.split_groups};
-  for (int i = 0; i < 10; ++i)
+  int64_t* fields[] = {&d.group,     &d.col_tiles, &d.max_cols, &d.hkv,          &d.resident,   &d.bs,
+                       &d.min_units, &d.max_units, &d.unit,     &d.split_groups, &d.split_waves};
+  for (int i = 0; i < 11; ++i)
     if (!as_i64(args[2 + i], fields[i])) return nullptr;
   if (d.group <= 0 || d.col_tiles <= 0 || d.hkv <= 0 || d.bs <= 0 || d.unit <= 0 || d.min_units <= 0) {
     PyErr_SetString(PyExc_ValueError, "decode_work: inconsistent arguments");
@@ -1611,8 +1620,9 @@ PyObject* prefill_work(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
 //   19 prefill min tiles, 20 shared-prefix spans (0/1), 21 the device's XCDs
 //   (0: no per-XCD order of the prefill grid), 22 per-XCD order (0: grouped
 //   when its simulated packing is no slower, 1: grouped, 2: plain), 23
-//   resident workgroups of the workgroup-split decode kernel (0: never).
-constexpr int kKernelFacts = 24;
+//   resident workgroups of the workgroup-split decode kernel (0: never), 24
+//   its waves per workgroup.
+constexpr int kKernelFacts = 25;
 
 // One layer shape's plan: the choices and the lists of both kernels.
 struct LayerPlan {
@@ -1701,7 +1711,7 @@ const char* plan_layer(const Requests& q, const int32_t* ids, int64_t nflat, con
     const int64_t unit = ctw == 4 ? k[13] : k[11];
     const int64_t max_units = (k[16] > 0 && unit > 0) ? std::max<int64_t>(1, k[16] / unit) : 0;
     DecodeParams d{group, ctw, max_cols, hkv, ctw == 4 ? k[12] : k[10], bs, k[18] > 0 ? k[18] : 4, max_units, unit,
-                   k[23]};
+                   k[23], k[24]};
     if (d.unit <= 0 || d.resident <= 0) return "missing decode kernel facts";
     build_decode(q, ids, nflat, d, out.dec);
     out.has_dec = true;
@@ -1716,7 +1726,7 @@ const char* plan_layer(const Requests& q, const int32_t* ids, int64_t nflat, con
 // ---------------------------------------------------------------------------
 // plan_step(flat i32, counts i64, computed i64, reserved i64, readonly i64,
 //           q_lens i64, vis_off i64, vis_words i64, vis u32, num_blocks,
-//           block_size, kernel facts i64 [n][24], cost4, wide_max_tiles,
+//           block_size, kernel facts i64 [n][25], cost4, wide_max_tiles,
 //           out i32 (writable))
 //   -> rule (int 1..6): a block-table rule fails (validate's codes);
 //      (needed, None, None): ``out`` holds fewer than ``needed`` entries;

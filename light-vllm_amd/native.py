@@ -56,6 +56,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p],
     ),
     "lvamd_paged_decode_split_groups": (ctypes.c_int, [_i32, _i32]),
+    "lvamd_paged_decode_split_waves": (ctypes.c_int, [_i32, _i32]),
     "lvamd_paged_attention": (
         ctypes.c_int,
         [_p, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _f32, _p],
@@ -206,6 +207,15 @@ def decode_split_groups(dtype_code: int, head_size: int) -> int:
         found = int(load().lvamd_paged_decode_split_groups(dtype_code, head_size))
         check(min(found, 0), "lvamd_paged_decode_split_groups")
         _RESIDENT[key] = found
+    return found
+
+
+@functools.lru_cache(maxsize=None)
+def decode_split_waves(dtype_code: int, head_size: int) -> int:
+    """Waves per workgroup of the workgroup-split decode kernel."""
+
+    found = int(load().lvamd_paged_decode_split_waves(dtype_code, head_size))
+    check(min(found, 0), "lvamd_paged_decode_split_waves")
     return found
 
 

@@ -495,7 +495,7 @@ class StepPlan:
         self, group: int, num_kv_heads: int, resident_waves: int = 8 * NUM_CUS, prefill_columns: int = 0,
         unit_tokens: int = UNIT_TOKENS, col_tiles: int = 1, prefill_key_tokens: int = 64,
         prefill_resident: int = 0, prefill_waves: int = 4, shared_prefix: bool = False, xcds: int = 0,
-        prefill_order: int = 0, split_groups: int = 0,
+        prefill_order: int = 0, split_groups: int = 0, split_waves: int = 8,
     ) -> DecodeWork:
         """Work lists for layers of this (group, kv heads) shape.
 
@@ -512,13 +512,14 @@ class StepPlan:
         keeps each request's units on one XCD when the simulated packing is
         no slower, 1 always, 2 never; ``split_groups`` > 0 (the resident
         workgroups of the workgroup-split decode kernel) lets the planner
-        give each segment a workgroup of four waves when that is no slower
-        than stream-K with its merge launch.  The library reports the kernel
+        give each segment a workgroup of ``split_waves`` waves when that is
+        no slower than stream-K with its merge launch.  The library reports the kernel
         figures per dtype and head size.
         """
 
         key = (group, num_kv_heads, resident_waves, prefill_columns, unit_tokens, col_tiles, prefill_key_tokens,
-               prefill_resident, prefill_waves, bool(shared_prefix), int(xcds), int(prefill_order), int(split_groups))
+               prefill_resident, prefill_waves, bool(shared_prefix), int(xcds), int(prefill_order), int(split_groups),
+               int(split_waves))
         found = self._work.get(key)
         if found is None:
             found = self._build_work(*key)
@@ -558,7 +559,7 @@ class StepPlan:
     def _build_work(
         self, group: int, num_kv_heads: int, resident_waves: int, prefill_columns: int, unit_tokens: int,
         col_tiles: int, prefill_key_tokens: int, prefill_resident: int, prefill_waves: int, shared_prefix: bool,
-        xcds: int, prefill_order: int, split_groups: int,
+        xcds: int, prefill_order: int, split_groups: int, split_waves: int,
     ) -> DecodeWork:
         host = native.host()
         work = DecodeWork(col_tiles=col_tiles, prefill_waves=prefill_waves)
@@ -568,7 +569,8 @@ class StepPlan:
         if max_cols == 0 or bool(np.any(q_cols <= max_cols)):
             max_units = max(1, self.partition_tokens // unit_tokens) if self.partition_tokens else 0
             dec = host.decode_work(self._req_meta, self.facts.flat, group, col_tiles, max_cols, num_kv_heads,
-                                   resident_waves, self.block_size, 4, max_units, unit_tokens, split_groups)
+                                   resident_waves, self.block_size, 4, max_units, unit_tokens, split_groups,
+                                   split_waves)
         if max_cols and bool(np.any(q_cols > max_cols)):
             slots_per_head = prefill_resident // num_kv_heads if prefill_resident else 0
             pre = host.prefill_work(self._req_meta, self.facts.raw[0], group, prefill_columns, prefill_key_tokens,
@@ -585,6 +587,7 @@ KERNEL_FACTS = (
     "resident_waves_1", "tile_tokens_1", "resident_waves_4", "tile_tokens_4",
     "prefill_resident_4", "prefill_resident_8", "partition_tokens", "decode_max_columns",
     "min_units_per_wave", "prefill_min_tiles", "shared_prefix", "xcds", "prefill_order", "split_groups",
+    "split_waves",
 )
 
 

@@ -9,6 +9,7 @@ with plain torch indexing (test setup, independent of the kernels under test).
 from __future__ import annotations
 
 import math
+import sys
 from dataclasses import dataclass
 
 import numpy as np
@@ -139,6 +140,16 @@ def dense_oracle_attention(step: Step, layer_id: str) -> np.ndarray:
     q = step.query.float().cpu().numpy()
     parents = [l.parent_indices for l in step.metadata.query_layouts]
     return O.dense_attention(q, k, v, tables, step.metadata.num_computed_tokens, parents, scale=step.scale)
+
+
+def report_margin(config: str, err: np.ndarray, dtype: torch.dtype) -> None:
+    """Print a ``[margin]`` line: the errors against the tolerances, as a
+    share of each (the numerical margin table is built from these lines)."""
+
+    max_tol, mean_tol = tolerances(dtype)
+    mx, mean = float(err.max()), float(err.mean())
+    print(f"[margin] {config}: max-abs {mx:.3e} ({100 * mx / max_tol:.1f}% of {max_tol:g}), "
+          f"mean-abs {mean:.3e} ({100 * mean / mean_tol:.1f}% of {mean_tol:g})", file=sys.stderr, flush=True)
 
 
 def tolerances(dtype: torch.dtype) -> tuple[float, float]:

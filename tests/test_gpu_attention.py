@@ -16,7 +16,7 @@ import pytest
 import torch
 
 import light_vllm_amd as lv
-from paged_cases import DTYPES, make_step, oracle_attention, tolerances
+from paged_cases import DTYPES, make_step, oracle_attention, report_margin, tolerances
 
 pytestmark = pytest.mark.gpu
 if not torch.cuda.is_available():
@@ -29,7 +29,7 @@ def _announce(name: str) -> None:
     print(f"[gpu] {name}", file=sys.stderr, flush=True)
 
 
-def _run_and_check(step, *, backend=None, layer_index: int = 0):
+def _run_and_check(step, *, backend=None, layer_index: int = 0, margin: str | None = None):
     backend = backend or lv.HipPagedAttentionBackend()
     ctx = backend.create(step.cache, step.metadata)
     lid = step.layer_ids[layer_index]
@@ -47,6 +47,8 @@ def _run_and_check(step, *, backend=None, layer_index: int = 0):
     got = out.float().cpu().numpy()
     err = np.abs(got - expect)
     max_tol, mean_tol = tolerances(step.query.dtype)
+    if margin is not None:
+        report_margin(margin, err, step.query.dtype)
     assert np.isfinite(got).all()
     assert err.max() <= max_tol, f"max-abs {err.max():.3e} > {max_tol}"
     assert err.mean() <= mean_tol, f"mean-abs {err.mean():.3e} > {mean_tol}"
@@ -135,7 +137,7 @@ def test_c1_qwen05b_fp32_decode() -> None:
     _announce("C1 fp32 decode")
     step = make_step(hq=14, hkv=2, d=64, bs=16, dtype=torch.float32, computed=[37, 128, 200, 511],
                      layouts=_lin(1, 1, 1, 1), num_blocks=256, seed=1)
-    _run_and_check(step)
+    _run_and_check(step, margin="C1 (fp32, workgroup split)")
 
 
 def test_c2_qwen7b_bf16_decode_bs64() -> None:
@@ -144,9 +146,18 @@ def test_c2_qwen7b_bf16_decode_bs64() -> None:
     ctx = [int(c) for c in rng.integers(512, 4097, size=64)]
     step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=ctx,
                      layouts=_lin(*([1] * 64)), num_blocks=32768, seed=2)
-    _, ctx_obj = _run_and_check(step)
-    work = ctx_obj.plan.work(7, 4)
-    assert work.num_jobs > 0, "C2 must exercise the split-K merge"
+    _, ctx_obj = _run_and_check(step, margin="C2 (bf16, stream-K, bf16 partials)")
+    work = ctx_obj.work_of(step.cache.layer_spec(step.layer_ids[0]))
+    assert work.num_jobs > 0 and work.group_waves == 1, "C2 must exercise the split-K merge"
+
+
+def test_small_batch_reference_point_bf16() -> None:
+    # The reference's published operating point: B=16, context 256, Qwen2.5-7B.
+    _announce("small batch bf16 decode (B=16, ctx 256)")
+    step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[256] * 16,
+                     layouts=_lin(*([1] * 16)), num_blocks=1024, seed=16)
+    _, ctx_obj = _run_and_check(step, margin="small (bf16, workgroup split)")
+    assert ctx_obj.work_of(step.cache.layer_spec(step.layer_ids[0])).group_waves > 1
 
 
 @pytest.mark.parametrize("dtype", ("fp32", "fp16", "bf16"))
@@ -406,16 +417,17 @@ def test_one_metadata_on_caches_of_two_dtypes() -> None:
 @pytest.mark.parametrize("dtype", ("fp32", "fp16", "bf16"))
 @pytest.mark.parametrize("head_size", (32, 64, 80, 96, 128, 256))
 def test_workgroup_split_decode_matches_the_oracle(dtype, head_size) -> None:
-    # Short decode rows (one segment per workgroup of four waves, results
-    # combined in LDS): a 1-token context, segments of 1-3 tiles (idle
-    # waves) and of more than four, with the append fused.
+    # Short decode rows (one segment per workgroup of eight waves, four for
+    # the widest rows, results combined in LDS): a 1-token context, segments
+    # of fewer tiles than waves (idle waves) and of more, append fused.
     _announce(f"workgroup split d={head_size} {dtype}")
     hq, hkv = (28, 4) if head_size <= 128 else (16, 2)
     step = make_step(hq=hq, hkv=hkv, d=head_size, bs=16, dtype=DTYPES[dtype],
                      computed=[0, 31, 40, 250, 200, 130, 97, 5], layouts=_lin(*([1] * 8)), seed=400 + head_size)
     _, ctx = _run_and_check(step)
     work = ctx.work_of(step.cache.layer_spec(step.layer_ids[0]))
-    assert work.group_waves == 4 and work.num_jobs == 0
+    code = lv.paged_cache.dtype_code(DTYPES[dtype])
+    assert work.group_waves == lv.native.decode_split_waves(code, head_size) > 1 and work.num_jobs == 0
 
 
 @pytest.mark.parametrize("dtype", ("fp32", "bf16"))
@@ -428,7 +440,7 @@ def test_workgroup_split_of_multi_tile_rows_without_prefill_kernel(dtype) -> Non
                      layouts=_lin(40, 9, 17), seed=420)
     backend = lv.HipPagedAttentionBackend(use_prefill_kernel=False, decode_col_tiles=1)
     _, ctx = _run_and_check(step, backend=backend)
-    assert ctx.work_of(step.cache.layer_spec(step.layer_ids[0])).group_waves == 4
+    assert ctx.work_of(step.cache.layer_spec(step.layer_ids[0])).group_waves == 8
 
 
 @pytest.mark.parametrize("bs", (1, 3, 16))
@@ -440,7 +452,7 @@ def test_workgroup_split_block_sizes_and_groups(bs, hq, hkv) -> None:
     step = make_step(hq=hq, hkv=hkv, d=128, bs=bs, dtype=torch.bfloat16, computed=[250, 17, 260, 3, 129],
                      layouts=_lin(1, 1, 1, 1, 1), num_layers=2, seed=410 + bs + hq)
     out, ctx = _run_and_check(step)
-    assert ctx.work_of(step.cache.layer_spec(step.layer_ids[0])).group_waves == 4
+    assert ctx.work_of(step.cache.layer_spec(step.layer_ids[0])).group_waves == 8
     ref = lv.HipPagedAttentionBackend(decode_workgroups=False).create(step.cache, step.metadata)
     lid = step.layer_ids[1]
     # (layer1's pool holds this step's K/V only after the forward below)

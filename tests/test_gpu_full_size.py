@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 import torch
 
-from paged_cases import dense_oracle_attention, make_step, tolerances
+from paged_cases import dense_oracle_attention, make_step, report_margin, tolerances
 
 import light_vllm_amd as lv
 
@@ -35,7 +35,7 @@ def _lin(*lengths):
     return [tuple(range(-1, n - 1)) for n in lengths]
 
 
-def _run(step):
+def _run(step, margin: str):
     ctx = lv.HipPagedAttentionBackend().create(step.cache, step.metadata)
     lid = step.layer_ids[0]
     out = ctx.forward(lid, step.query, step.key, step.value, scale=step.scale)
@@ -49,6 +49,7 @@ def _run(step):
     got = out.float().cpu().numpy()
     err = np.abs(got - dense_oracle_attention(step, lid))
     max_tol, mean_tol = tolerances(step.query.dtype)
+    report_margin(margin, err, step.query.dtype)
     assert np.isfinite(got).all()
     assert err.max() <= max_tol, f"max-abs {err.max():.3e} > {max_tol}"
     assert err.mean() <= mean_tol, f"mean-abs {err.mean():.3e} > {mean_tol}"
@@ -61,7 +62,7 @@ def test_c3_full_mixed_batch() -> None:
     computed = [int(c) for c in rng.integers(0, 3073, size=8)] + [int(c) for c in rng.integers(256, 4097, size=56)]
     step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=computed,
                      layouts=_lin(*([512] * 8 + [1] * 56)), seed=3003)
-    ctx = _run(step)
+    ctx = _run(step, "C3 (bf16, prefill + decode rows)")
     work = ctx.work_of(step.cache.layer_spec(step.layer_ids[0]))
     assert work.num_prefill_units > 0 and work.waves_per_head > 0
 
@@ -70,7 +71,7 @@ def test_c4_full_one_layer_32k_contexts() -> None:
     _announce("C4 full: 16 x 32768, one layer")
     step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[32768] * 16,
                      layouts=_lin(*([1] * 16)), num_blocks=32800, seed=4004)
-    ctx = _run(step)
+    ctx = _run(step, "C4 (bf16, stream-K, 16 partials per row)")
     work = ctx.work_of(step.cache.layer_spec(step.layer_ids[0]))
     assert work.num_jobs == 16  # every 32K sequence is split across waves and merged
 
@@ -85,6 +86,6 @@ def test_c5_full_tree_verification_shared_prefix() -> None:
         computed.append(2048 + int(rng.integers(64, 513)))
     step = make_step(hq=12, hkv=2, d=128, bs=16, dtype=torch.bfloat16, computed=computed, layouts=layouts,
                      shared_prefix_blocks=128, seed=5005)
-    ctx = _run(step)
+    ctx = _run(step, "C5 (bf16, split-K prefill + spans)")
     work = ctx.work_of(step.cache.layer_spec(step.layer_ids[0]))
     assert work.num_prefill_partial_slots > 0  # split-K tree verification

@@ -22,7 +22,7 @@ import torch
 
 import light_vllm_amd as lv
 from oracle import paged_kv_oracle as O
-from paged_cases import Step, dense_oracle_attention, oracle_attention, tolerances
+from paged_cases import Step, dense_oracle_attention, oracle_attention, report_margin, tolerances
 
 pytestmark = pytest.mark.gpu
 if not torch.cuda.is_available():
@@ -97,6 +97,7 @@ def test_c4_whole_step_layer_matches_the_dense_oracle(c4_step, index) -> None:
     got = outs[index].float().cpu().numpy()
     err = np.abs(got - dense_oracle_attention(step, lid))
     max_tol, mean_tol = tolerances(torch.bfloat16)
+    report_margin(f"C4 whole step {lid}", err, torch.bfloat16)
     assert np.isfinite(got).all()
     assert err.max() <= max_tol and err.mean() <= mean_tol, (lid, err.max(), err.mean())
 
@@ -167,6 +168,7 @@ def test_c5_whole_step_copy_verify_compact() -> None:
         step = Step(cache, md, q, k, v, layer_ids, scale)
         _check_appended(step, lid, k, v)
         err = np.abs(out.float().cpu().numpy() - oracle_attention(step, lid))
+        report_margin(f"C5 whole step {lid}", err, torch.bfloat16)
         assert err.max() <= max_tol and err.mean() <= mean_tol, (lid, err.max(), err.mean())
     assert ctx.layer_ids == frozenset(layer_ids)
 

@@ -219,14 +219,16 @@ def test_stream_k_pieces_cover_every_segment_once(resident, bs, group, unit, ctw
     assert sorted(slots_seen) == list(range(work.num_partial_slots))
 
 
+@pytest.mark.parametrize("gw", (4, 8))
 @pytest.mark.parametrize("bs", (1, 16))
 @pytest.mark.parametrize("seed", range(6))
-def test_workgroup_split_gives_each_segment_one_workgroup(seed, bs) -> None:
+def test_workgroup_split_gives_each_segment_one_workgroup(seed, bs, gw) -> None:
     """A latency-bound decode step (short segments that fit the resident
-    workgroups) runs one segment per workgroup of four waves: the pieces of
-    workgroup b are the segment's near-equal contiguous parts, one per wave
-    from wave 4b on, no merge jobs or partial slots; a single-piece segment
-    is written by its piece (slot -1), the others name their wave (0..3)."""
+    workgroups) runs one segment per workgroup of ``gw`` waves, one record
+    per wave: workgroup b's records are the segment's near-equal contiguous
+    parts from wave gw*b on, then idle records (request -1); no merge jobs or
+    partial slots; a single-piece segment is written by its piece (slot -1),
+    the others name their wave."""
 
     rng = np.random.default_rng(900 + seed)
     batch = int(rng.integers(1, 20))
@@ -241,31 +243,33 @@ def test_workgroup_split_gives_each_segment_one_workgroup(seed, bs) -> None:
                                    query_layouts=tuple(lv.linear_query_layout(1) for _ in range(batch)))
     plan = StepPlan(md, block_size=bs, device=CPU)
     unit = 32
-    work = plan.work(7, 4, 1024, 0, unit, 1, split_groups=256)
+    work = plan.work(7, 4, 1024, 0, unit, 1, split_groups=256, split_waves=gw)
     seqs = np.asarray(computed) + 1
     tiles = -(-seqs // unit)
     stream_k = plan.work(7, 4, 1024, 0, unit, 1)
-    split = -(-int(tiles.max()) // 4)
+    split = -(-int(tiles.max()) // gw)
     cap = (254 * bs) // unit
-    use = batch * 4 <= 256 and split <= cap and split <= stream_k.units_per_wave + (3 if stream_k.num_jobs else 0)
+    use = batch * 4 <= 256 and split <= min(cap, 4) and split <= stream_k.units_per_wave + (
+        3 if stream_k.num_jobs else 0)
     if not use:
         assert work.group_waves == 1 and work.waves_per_head == stream_k.waves_per_head
         return
-    assert work.group_waves == 4 and work.waves_per_head == 4 * batch
+    assert work.group_waves == gw and work.waves_per_head == gw * batch
     assert work.num_jobs == 0 and work.num_partial_slots == 0 and work.units_per_wave == split
     pieces = work.pieces.numpy()
     first = work.wave_first.numpy()
+    assert pieces.shape[0] == gw * batch and first.tolist() == list(range(gw * batch + 1))
     for r in range(batch):
-        recs = [pieces[i] for w in range(4 * r, 4 * r + 4) for i in range(first[w], first[w + 1])]
-        assert all(first[w + 1] - first[w] <= 1 for w in range(4 * r, 4 * r + 4))
-        n = min(4, int(tiles[r]))
-        active = [first[w + 1] - first[w] for w in range(4 * r, 4 * r + 4)]
-        assert active == [1] * n + [0] * (4 - n)  # the first n waves, one piece each
+        block = pieces[gw * r : gw * (r + 1)]
+        n = min(gw, int(tiles[r]))
+        assert [int(x[0]) for x in block] == [r] * n + [-1] * (gw - n)  # the first n waves, then idle
+        recs = block[:n]
         assert recs[0][2] == 0 and recs[-1][3] == seqs[r]
         assert all(a[3] == b[2] for a, b in zip(recs, recs[1:]))
         assert [int(x[4]) for x in recs] == ([-1] if n == 1 else list(range(n)))
-        for i, x in enumerate(recs):
-            assert x[0] == r and x[2] % unit == 0
+        assert all(int(x[4]) == -1 for x in block[n:])
+        for x in recs:
+            assert x[2] % unit == 0
             assert -(-(int(x[3]) - int(x[2])) // unit) in (tiles[r] // n, -(-int(tiles[r]) // n))
             for j in range(5):
                 lb = x[2] // bs + j
@@ -283,12 +287,17 @@ def test_workgroup_split_is_not_used_where_stream_k_is_faster() -> None:
     md = lv.PagedAttentionMetadata(block_tables=tables, num_computed_tokens=computed,
                                    query_layouts=tuple(lv.linear_query_layout(1) for _ in range(64)))
     plan = StepPlan(md, block_size=16, device=CPU)
-    assert plan.work(7, 4, 1024, 0, 32, 1, split_groups=256).group_waves == 1
+    for gw in (4, 8):
+        assert plan.work(7, 4, 1024, 0, 32, 1, split_groups=256, split_waves=gw).group_waves == 1
+    # Long equal contexts: more than four tiles per wave stays on stream-K
+    # (the step is bandwidth-bound); short ones take the split.
     plan = StepPlan(_uniform_metadata(batch=64, computed=4000, q=1), block_size=16, device=CPU)
-    assert plan.work(7, 4, 1024, 0, 32, 1, split_groups=256).group_waves == 4
+    assert plan.work(7, 4, 1024, 0, 32, 1, split_groups=256, split_waves=8).group_waves == 1
+    plan = StepPlan(_uniform_metadata(batch=64, computed=1000, q=1), block_size=16, device=CPU)
+    assert plan.work(7, 4, 1024, 0, 32, 1, split_groups=256, split_waves=8).group_waves == 8
     plan = StepPlan(_uniform_metadata(batch=70, computed=100, q=1), block_size=16, device=CPU)
     assert plan.work(7, 4, 1024, 0, 32, 1, split_groups=256).group_waves == 1  # 280 workgroups > 256
-    assert plan.work(7, 4, 1024, 0, 32, 1, split_groups=512).group_waves == 4
+    assert plan.work(7, 4, 1024, 0, 32, 1, split_groups=512).group_waves == 8
     # Four column tiles per wave never split in workgroups.
     plan = StepPlan(_uniform_metadata(batch=4, computed=100, q=8), block_size=16, device=CPU)
     assert plan.work(7, 4, 1024, 0, 16, 4, split_groups=256).group_waves == 1
@@ -699,13 +708,15 @@ def test_library_loads_and_exports_every_header_function() -> None:
                                   None, None, 0, 4, 7, 128, 1, 1, 16, ctypes.c_float(0.1), 2, None) == -1
     assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 1, None, None,
                                   None, None, 0, 4, 7, 128, 2, 1, 16, ctypes.c_float(0.1), 2, None) == -2
-    # The workgroup split: four waves per workgroup, one column tile, whole workgroups.
+    # The workgroup split: one column tile, whole workgroups.
     assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 4, None, None,
                                   None, None, 0, 4, 7, 128, 4, 4, 16, ctypes.c_float(0.1), 2, None) == -2
     assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 4, None, None,
                                   None, None, 0, 4, 7, 128, 1, 2, 16, ctypes.c_float(0.1), 2, None) == -2
     assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 6, None, None,
-                                  None, None, 0, 4, 7, 128, 1, 4, 16, ctypes.c_float(0.1), 2, None) == -1
+                                  None, None, 0, 4, 7, 128, 1, 8, 16, ctypes.c_float(0.1), 2, None) == -1
+    assert lib.lvamd_paged_decode_split_waves(2, 128) == 8 and lib.lvamd_paged_decode_split_waves(2, 256) == 4
+    assert lib.lvamd_paged_decode_split_waves(0, 96) == 8 and lib.lvamd_paged_decode_split_waves(0, 128) == 4
     x = ctypes.c_void_p(16)  # (never dereferenced: the checks run first)
     # One layer's call: a null plan is refused; a plan without decode rows or
     # prefill units launches nothing.
@@ -843,8 +854,8 @@ def _layer_shapes(bs: int) -> LayerShapes:
     one-query-per-head shape without them."""
 
     return LayerShapes((
-        (7, 4, bs, 128, 64, 1, 0, 0, 4, 1, 2048, 32, 1024, 16, 512, 256, 0, 16, 4, 4, 1, 8, 0, 256),
-        (1, 8, bs, 256, 64, 0, 0, 0, 1, 0, 2048, 32, 0, 0, 512, 0, 0, 16, 4, 4, 0, 0, 0, 0),
+        (7, 4, bs, 128, 64, 1, 0, 0, 4, 1, 2048, 32, 1024, 16, 512, 256, 0, 16, 4, 4, 1, 8, 0, 256, 8),
+        (1, 8, bs, 256, 64, 0, 0, 0, 1, 0, 2048, 32, 0, 0, 512, 0, 0, 16, 4, 4, 0, 0, 0, 0, 4),
     ))
 
 
@@ -888,7 +899,7 @@ def test_one_call_step_plan_equals_the_per_shape_plan(seed, small_buffer, monkey
             if ptr is not None:
                 assert base <= ptr and ptr + 4 * rows.numel() <= end and (ptr - base) % 64 == 0
     # A layer shape asked for later is planned on its own, from the records.
-    late = (4, 2, bs, 128, 64, 1, 0, 0, 4, 1, 2048, 32, 1024, 16, 512, 256, 0, 16, 4, 4, 1, 8, 1, 128)
+    late = (4, 2, bs, 128, 64, 1, 0, 0, 4, 1, 2048, 32, 1024, 16, 512, 256, 0, 16, 4, 4, 1, 8, 1, 128, 4)
     assert one.layer_work(late).num_prefill_units == ref.layer_work(late).num_prefill_units
 
 
