@@ -369,6 +369,27 @@ int lvamd_kv_compact(const uint64_t* layer_key_ptrs, const uint64_t* layer_value
 int64_t lvamd_kv_compact_inline_pairs(void);
 
 /*
+ * lvamd_kv_compact in one HBM pass, in place, for pair lists whose order makes
+ * that safe (no workspace): the pairs come in num_groups groups, group g being
+ * pairs [group_starts[g], group_starts[g + 1]) (device int64 array).  The
+ * caller guarantees that (1) no pair's destination is the source of a later
+ * pair of its group, and (2) no destination of one group is a source or
+ * destination of another; destinations are unique.  Rows are then moved in
+ * order, so row dst_slots[i] receives what row src_slots[i] held before the
+ * call, as with lvamd_kv_compact.  A step's compacts qualify with one group
+ * per request whenever each request's retained indices are strictly
+ * increasing (speculative decoding's accepted root-to-leaf paths).
+ *
+ * Replaces: the gather / clone / scatter of PagedKVCache.compact
+ *   (src/light_vllm/runtime/execution/paged_cache.py:315-326), which moves
+ *   each row once per layer, for calls above lvamd_kv_compact_inline_pairs().
+ */
+int lvamd_kv_compact_ordered(const uint64_t* layer_key_ptrs, const uint64_t* layer_value_ptrs,
+                             int32_t num_layers, int64_t row_bytes,
+                             const int64_t* src_slots, const int64_t* dst_slots, const int64_t* group_starts,
+                             int64_t num_groups, lvamd_stream_t stream);
+
+/*
  * lvamd_kv_compact for at most lvamd_kv_compact_inline_pairs() pairs given
  * in HOST memory: the pairs travel in the kernel's arguments (one launch, no
  * device index buffer, no upload).  Same rules and result as

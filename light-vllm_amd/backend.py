@@ -177,29 +177,23 @@ class _LayerLaunch:
         self.plan_ptr = ctypes.addressof(p)
 
 
-class _BoundLayer:
-    """One layer's facts for the fast ``forward``: the shapes its tensors must
-    have, dtype and device, pool addresses, output strides and the bound
-    ``lvamd_attention_plan`` of its shape."""
+class _LayerStatic:
+    """What the fast ``forward`` needs of one layer that stays fixed for a
+    cache: its spec, shape key and place among the layers of that shape,
+    pool addresses, dtype and device.  Built once per (backend, cache)."""
 
-    __slots__ = ("q_shape", "kv_shape", "dtype", "device", "device_index", "element_size", "k_pool", "v_pool",
-                 "out_s0", "out_s1", "plan_ptr", "launch", "attend", "fn")
+    __slots__ = ("spec", "shape", "index", "k_pool", "v_pool", "dtype", "device", "device_index", "element_size")
 
-    def __init__(self, tokens: int, spec, config, device_index: int, launch: _LayerLaunch, layer) -> None:
-        self.q_shape = (tokens, spec.num_query_heads, spec.head_size)
-        self.kv_shape = (tokens, spec.num_kv_heads, spec.head_size)
+    def __init__(self, spec, index: int, layer, config, device_index: int) -> None:
+        self.spec = spec
+        self.shape = (spec.num_query_heads, spec.num_kv_heads, spec.head_size)
+        self.index = index
+        self.k_pool = layer.keys.data_ptr()
+        self.v_pool = layer.values.data_ptr()
         self.dtype = config.dtype
         self.device = config.device
         self.device_index = device_index
         self.element_size = config.dtype.itemsize
-        self.k_pool = layer.keys.data_ptr()
-        self.v_pool = layer.values.data_ptr()
-        self.out_s0 = spec.num_query_heads * spec.head_size
-        self.out_s1 = spec.head_size
-        self.launch = launch  # keeps the plan structure alive
-        self.plan_ptr = launch.plan_ptr
-        self.attend = native.host().attend
-        self.fn = native.attention_entry()
 
 
 _UNBOUND = object()
@@ -222,9 +216,11 @@ class HipPagedAttention:
         self._layer_ids: set[str] = set()
         self._plan = plan
         self._lib = native.load()
-        self._bound: dict[str, _BoundLayer | None] = {}
-        device = self._config.device
-        self._device_index = device.index if device.index is not None else torch.cuda.current_device()
+        self._bound: dict[str, tuple | None] = {}
+        self._outputs: dict[tuple, tuple] = {}
+        self._launches_held: list = []
+        self._attend = native.host().attend
+        self._attend_fn = native.attention_entry()
 
     @property
     def layer_ids(self) -> frozenset[str]:
@@ -257,11 +253,10 @@ class HipPagedAttention:
         if bound is _UNBOUND:
             bound = self._bind(layer_id)
         if bound is not None and rotary is None:
-            dt = bound.dtype
-            dev = bound.device
-            if (query.shape == bound.q_shape and key.shape == bound.kv_shape and value.shape == bound.kv_shape
-                    and query.dtype is dt and key.dtype is dt and value.dtype is dt and query.device == dev
-                    and key.device == dev and value.device == dev):
+            q_shape, kv_shape, dt, dev, es, plan_ptr, k_pool, v_pool, out, out_ptr, o0, o1, dev_index = bound
+            if (query.shape == q_shape and key.shape == kv_shape and value.shape == kv_shape and query.dtype is dt
+                    and key.dtype is dt and value.dtype is dt and query.device == dev and key.device == dev
+                    and value.device == dev):
                 qs = query.stride()
                 ks = key.stride()
                 vs = value.stride()
@@ -269,40 +264,45 @@ class HipPagedAttention:
                 kp = key.data_ptr()
                 vp = value.data_ptr()
                 if qs[2] == 1 and ks[2] == 1 and vs[2] == 1 and not (
-                    (qp | kp | vp | (qs[0] | qs[1] | ks[0] | ks[1] | vs[0] | vs[1]) * bound.element_size) & 15
+                    (qp | kp | vp | (qs[0] | qs[1] | ks[0] | ks[1] | vs[0] | vs[1]) * es) & 15
                 ):
-                    out = torch.empty(bound.q_shape, dtype=dt, device=dev)
-                    status = bound.attend(
-                        bound.fn, bound.plan_ptr, qp, qs[0], qs[1], kp, ks[0], ks[1], vp, vs[0], vs[1],
-                        bound.k_pool, bound.v_pool, out.data_ptr(), bound.out_s0, bound.out_s1, scale,
-                        _raw_stream(bound.device_index),
-                    )
+                    status = self._attend(self._attend_fn, plan_ptr, qp, qs[0], qs[1], kp, ks[0], ks[1], vp, vs[0],
+                                          vs[1], k_pool, v_pool, out_ptr, o0, o1, scale, _raw_stream(dev_index))
                     if status:
                         native.check(status, "lvamd_paged_attention")
                     return out
         return self._forward_general(layer_id, query, key, value, scale=scale, rotary=rotary)
 
-    def _bind(self, layer_id: str) -> "_BoundLayer | None":
-        """The fast path's facts for one layer (None when it must take the
-        general path: a cache off the GPU, an unknown layer, an unsupported
-        head size)."""
+    def _bind(self, layer_id: str) -> tuple | None:
+        """The fast path's facts for one layer in this step (None when it
+        must take the general path: a cache off the GPU, an unknown layer,
+        an unsupported head size): the tensor shapes, dtype and device it
+        accepts, its shape's bound plan, its pools and its output.
 
-        cache = self._cache
-        if _raw_stream is None or self._config.device.type != "cuda":
+        Outputs are views of one tensor per layer shape and step, made at the
+        first layer of that shape (one allocation for the step's layers in
+        place of one per layer); each layer's view is its own rows."""
+
+        found = self._backend.layer_statics(self._cache).get(layer_id) if self._config.device.type == "cuda" else None
+        if found is None or _raw_stream is None:
             self._bound[layer_id] = None
             return None
-        try:
-            spec = cache.layer_spec(layer_id)
-        except Exception:  # the general path raises the cache's own error
-            self._bound[layer_id] = None
-            return None
-        if spec.head_size not in SUPPORTED_HEAD_SIZES:
-            self._bound[layer_id] = None
-            return None
+        spec = found.spec
         launch = self._launch(spec)
-        layer = cache.layer(layer_id)
-        bound = self._bound[layer_id] = _BoundLayer(
-            self._plan.num_tokens, spec, self._config, self._device_index, launch, layer)
+        views = self._outputs.get(found.shape)
+        tokens = self._plan.num_tokens
+        if views is None:
+            count = self._backend.shape_counts(self._cache)[found.shape]
+            slab = torch.empty((count, tokens, spec.num_query_heads, spec.head_size), dtype=found.dtype,
+                               device=found.device)
+            views = self._outputs[found.shape] = slab.unbind(0)
+        out = views[found.index]
+        bound = self._bound[layer_id] = (
+            (tokens, spec.num_query_heads, spec.head_size), (tokens, spec.num_kv_heads, spec.head_size),
+            found.dtype, found.device, found.element_size, launch.plan_ptr, found.k_pool, found.v_pool, out,
+            out.data_ptr(), spec.num_query_heads * spec.head_size, spec.head_size, found.device_index,
+        )
+        self._launches_held.append(launch)  # the bound plan structure stays alive with the context
         return bound
 
     def _forward_general(self, layer_id: str, query: Tensor, key: Tensor, value: Tensor, *, scale: float,
@@ -505,6 +505,8 @@ class HipPagedAttentionBackend:
         # cache -> kernel facts of its layer shapes (dropped with the cache).
         self._shapes: "weakref.WeakKeyDictionary[object, LayerShapes]" = weakref.WeakKeyDictionary()
         self._head_sizes_ok: "weakref.WeakSet[object]" = weakref.WeakSet()
+        self._statics: "weakref.WeakKeyDictionary[object, dict]" = weakref.WeakKeyDictionary()
+        self._shape_counts: "weakref.WeakKeyDictionary[object, dict]" = weakref.WeakKeyDictionary()
         self._last: tuple[object, object, StepPlan] | None = None
 
     def prefill_columns(self, code: int, head_size: int) -> int:
@@ -539,6 +541,33 @@ class HipPagedAttentionBackend:
             )
             self._facts[key] = found
         return found
+
+    def layer_statics(self, cache) -> dict:
+        """Per layer id, the cache's fixed facts for the fast forward (built
+        once per cache); layers of unbuilt head sizes are left out."""
+
+        found = self._statics.get(cache)
+        if found is None:
+            config = cache.config
+            device = config.device
+            index = device.index if device.index is not None else torch.cuda.current_device()
+            seen: dict[tuple, int] = {}
+            found = {}
+            for spec in cache.model_spec.layers:
+                if spec.head_size not in SUPPORTED_HEAD_SIZES:
+                    continue
+                shape = (spec.num_query_heads, spec.num_kv_heads, spec.head_size)
+                position = seen.get(shape, 0)
+                seen[shape] = position + 1
+                found[spec.layer_id] = _LayerStatic(spec, position, cache.layer(spec.layer_id), config, index)
+            self._statics[cache] = found
+            self._shape_counts[cache] = seen
+        return found
+
+    def shape_counts(self, cache) -> dict:
+        """Layers of each shape in the cache (after ``layer_statics``)."""
+
+        return self._shape_counts[cache]
 
     def _check_head_sizes(self, cache) -> None:
         """A cache with a layer of an unbuilt head size is refused when the

@@ -953,16 +953,22 @@ struct DecodeParams {
 
 // Workgroup split of the decode kernel: workgroups of split_waves waves, one
 // segment each, its pieces combined in LDS.  The planner takes it for
-// latency-bound steps: the step's segments fit the resident workgroups, no
-// wave gets more than kSplitMaxTiles tiles (a CU then streams at most
-// split_waves * kSplitMaxTiles tiles, where its waves' load latency, not the
-// CU's share of HBM bandwidth, bounds it), and the longest piece is no longer
-// than stream-K's largest share plus what the merge launch it saves costs
-// (kSplitMergeTiles tiles).  (Without the cap C2's 64 contexts of 512-4096
-// tokens took one CU per segment: 84 us against 59 us on stream-K shares, the
-// longest segment's CU streaming alone at the end.)
+// latency-bound steps: the step's segments fit the resident workgroups and
+// the longest piece is no longer than stream-K's largest share plus what the
+// merge launch it saves costs (kSplitMergeTiles tiles).  A workgroup's time
+// grows by about one tile's load latency per tile of its longest wave, so
+// the split is taken at one tile per wave, and at two only where stream-K is
+// slower too: when the pieces average at most 1.5 tiles, or the step has
+// kSplitBusyGroups segments or more.  (Measured on 28 bf16 layers of 28 / 4
+// heads, D 128, per layer: one tile 4.3-12.6 us against stream-K's 4.9-18.3;
+// two tiles 13.4 vs 12.7 at 1 x 512 tokens, 15.6 vs 15.1 at 16 x 512, 13.6
+// vs 14.7 at 16 x 384, 16.6 vs 18.0 at 32 x 512, 19.8 vs 22.6 at 64 x 512;
+// three and four tiles lose, 19.3 vs 16.9 and 20.7 vs 13.7.  Without a cap
+// C2's 64 contexts of 512-4096 tokens took one CU per segment: 84 us against
+// 59 us on stream-K shares.)
 constexpr int64_t kSplitMergeTiles = 3;
-constexpr int64_t kSplitMaxTiles = 4;
+constexpr int64_t kSplitMaxTiles = 2;
+constexpr int64_t kSplitBusyGroups = 128;
 
 void build_decode(const Requests& q, const int32_t* ids, int64_t nflat, const DecodeParams& d, DecodeLists& out) {
   struct Seg {
@@ -1074,6 +1080,7 @@ void build_decode(const Requests& q, const int32_t* ids, int64_t nflat, const De
   const int64_t split_share = (longest + gw - 1) / gw;
   const int64_t nseg = (int64_t)segs.size();
   if (nseg * d.hkv > d.split_groups || split_share > cap || split_share > kSplitMaxTiles) return;
+  if (split_share == kSplitMaxTiles && 2 * longest > 3 * gw && nseg * d.hkv < kSplitBusyGroups) return;
   if (split_share > per_wave + (out.jobs.empty() ? 0 : kSplitMergeTiles)) return;
   out.reset();
   out.group_waves = gw;

@@ -286,6 +286,62 @@ __global__ __launch_bounds__(256) void kv_compact_phase_kernel(const CompactArgs
 }
 
 // ---------------------------------------------------------------------------
+// Ordered compact (lvamd_kv_compact_ordered): one HBM pass for pair lists
+// whose order makes moving in place safe.  The pairs come in groups (one per
+// request) that touch disjoint rows; inside a group no pair's destination is
+// the source of a later pair (the host proves both; a step's accepted tree
+// paths, retained indices strictly increasing, always qualify).  One thread
+// per (group, layer, K|V, column chunk) moves its group's rows in order,
+// kOrderedBatch pairs at a time: every source of a batch is read before its
+// destinations are written, and a later batch reads no row an earlier one
+// wrote.  Unlike the two-phase path, no row crosses HBM twice and no
+// workspace is needed.
+// ---------------------------------------------------------------------------
+constexpr int kOrderedBatch = 16;
+
+struct OrderedCompactArgs {
+  const uint64_t* kptrs;
+  const uint64_t* vptrs;
+  int32_t num_layers;
+  int64_t row_bytes;
+  const int64_t* src;
+  const int64_t* dst;
+  const int64_t* group_starts;  // [num_groups + 1]
+  int64_t num_groups;
+};
+
+template <typename V>
+__global__ __launch_bounds__(256) void kv_compact_ordered_kernel(const OrderedCompactArgs a) {
+  const int64_t cpr = a.row_bytes / (int64_t)sizeof(V);
+  const int64_t per_group = (int64_t)a.num_layers * 2 * cpr;
+  const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= a.num_groups * per_group) return;
+  const int64_t group = item / per_group;
+  const int64_t r = item - group * per_group;
+  const int64_t c = r % cpr;
+  const int64_t lk = r / cpr;  // layer * 2 + is_v
+  char* base = reinterpret_cast<char*>((lk & 1) ? a.vptrs[lk >> 1] : a.kptrs[lk >> 1]);
+  const int64_t p0 = a.group_starts[group], p1 = a.group_starts[group + 1];
+  for (int64_t b = p0; b < p1; b += kOrderedBatch) {
+    V tmp[kOrderedBatch];
+    // Every gather is issued (entries past the group re-read its last
+    // source) so the chunks stay in registers.
+#pragma unroll
+    for (int i = 0; i < kOrderedBatch; ++i) {
+      const int64_t p = b + i < p1 ? b + i : p1 - 1;
+      tmp[i] = reinterpret_cast<const V*>(base + a.src[p] * a.row_bytes)[c];
+    }
+    // Every gather of the batch has landed before its first scatter.
+    __threadfence_block();
+#pragma unroll
+    for (int i = 0; i < kOrderedBatch; ++i) {
+      if (b + i < p1) reinterpret_cast<V*>(base + a.dst[b + i] * a.row_bytes)[c] = tmp[i];
+    }
+    __threadfence_block();
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Allocation-free compact (lvamd_kv_compact_static): the two-phase kernels
 // stage their rows in this file-scope array instead of a caller workspace.
 // Each GPU holds its own copy for the life of the process; its device
@@ -584,6 +640,34 @@ int lvamd_kv_compact(const uint64_t* layer_key_ptrs, const uint64_t* layer_value
       hipLaunchKernelGGL((kv_compact_phase_kernel<uint8_t, false>), dim3((unsigned)blocks), dim3(256), 0, s, a);
       break;
   }
+  return launch_status();
+}
+
+int lvamd_kv_compact_ordered(const uint64_t* layer_key_ptrs, const uint64_t* layer_value_ptrs,
+                             int32_t num_layers, int64_t row_bytes,
+                             const int64_t* src_slots, const int64_t* dst_slots, const int64_t* group_starts,
+                             int64_t num_groups, lvamd_stream_t stream) {
+  if (num_groups < 0 || num_layers <= 0 || row_bytes <= 0) return LVAMD_ERR_INVALID_ARGUMENT;
+  if (num_groups == 0) return LVAMD_OK;
+  if (!layer_key_ptrs || !layer_value_ptrs || !src_slots || !dst_slots || !group_starts)
+    return LVAMD_ERR_INVALID_ARGUMENT;
+  OrderedCompactArgs a;
+  a.kptrs = layer_key_ptrs;
+  a.vptrs = layer_value_ptrs;
+  a.num_layers = num_layers;
+  a.row_bytes = row_bytes;
+  a.src = src_slots;
+  a.dst = dst_slots;
+  a.group_starts = group_starts;
+  a.num_groups = num_groups;
+  int width = common_vector_bytes({(uint64_t)row_bytes});
+  // Narrow the chunks (to 4 bytes at least) until about 64 workgroups share
+  // a latency-bound call.
+  while (width > 4 && num_groups * num_layers * 2 * (row_bytes / width) < 64 * 256) width /= 2;
+  const int64_t items = num_groups * num_layers * 2 * (row_bytes / width);
+  if ((items + 255) / 256 > 0x7fffffffLL) return LVAMD_ERR_INVALID_ARGUMENT;
+  LVAMD_LAUNCH_BY_WIDTH(kv_compact_ordered_kernel, width, dim3((unsigned)((items + 255) / 256)), dim3(256),
+                        static_cast<hipStream_t>(stream), a);
   return launch_status();
 }
 

@@ -84,6 +84,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_p, _p, _i32, _i64, _p, _p, _i64, _p],
     ),
+    "lvamd_kv_compact_ordered": (
+        ctypes.c_int,
+        [_p, _p, _i32, _i64, _p, _p, _p, _i64, _p],
+    ),
     "lvamd_kv_compact_small": (
         ctypes.c_int,
         [_p, _p, _i32, _i64, _p, _p, _i64, _p],

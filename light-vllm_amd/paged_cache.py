@@ -290,11 +290,49 @@ def hip_compact_many(cache, requests) -> tuple[int, ...]:
         requests = tuple(requests)
     moved, src, dst = _compact_plan(cache.config, requests)
     if src.size:
-        _launch_compact(cache, src, dst)
+        _launch_compact(cache, src, dst, moved)
     return tuple(moved.tolist())
 
 
-def _launch_compact(cache, src: np.ndarray, dst: np.ndarray) -> None:
+# The longest group the one-pass compact takes: one thread moves its group's
+# rows one batch of 16 after another, so a long group would serialise.
+ORDERED_MAX_PAIRS = 64
+
+
+def ordered_groups(moved: np.ndarray, src: np.ndarray, dst: np.ndarray) -> np.ndarray | None:
+    """Group boundaries (int64, one group per request that moves anything)
+    when the pairs may be moved in place in one pass, else None.
+
+    The pass moves each group's pairs in order while the groups run side by
+    side, so it is exact when every row that some pair writes is read only
+    by earlier pairs of the same group: a destination equal to a source
+    ``src[j]`` must be ``dst[i]`` with ``i > j`` in ``j``'s group.  Every
+    request whose retained indices are strictly increasing (an accepted
+    root-to-leaf path) meets this on its own rows: pair ``j`` reads position
+    ``computed + retained[j]`` and writes ``computed + j``, and
+    ``retained[j] >= j``.  Destinations are unique (compact's rules).
+    """
+
+    counts = moved[moved > 0]
+    if counts.size == 0 or int(counts.max()) > ORDERED_MAX_PAIRS:
+        return None
+    starts = np.zeros(counts.size + 1, dtype=np.int64)
+    np.cumsum(counts, out=starts[1:])
+    order = np.argsort(dst, kind="stable")
+    sorted_dst = dst[order]
+    k = np.searchsorted(sorted_dst, src)
+    k[k == sorted_dst.size] = 0
+    hit = sorted_dst[k] == src
+    if hit.any():
+        reader = np.flatnonzero(hit)
+        writer = order[k[hit]]
+        group = np.repeat(np.arange(counts.size), counts)
+        if np.any(writer <= reader) or np.any(group[writer] != group[reader]):
+            return None
+    return starts
+
+
+def _launch_compact(cache, src: np.ndarray, dst: np.ndarray, moved: np.ndarray | None = None) -> None:
     pointers = _layer_pointers(cache)
     device = cache.config.device
     n = int(src.size)
@@ -307,6 +345,21 @@ def _launch_compact(cache, src: np.ndarray, dst: np.ndarray) -> None:
         for row_bytes, num_layers, _, kptrs, vptrs in pointers.groups:
             native.check(lib.lvamd_kv_compact_small(kptrs, vptrs, num_layers, row_bytes, src.ctypes.data,
                                                     dst.ctypes.data, n, stream), "lvamd_kv_compact_small")
+        return
+    starts = ordered_groups(moved, src, dst) if moved is not None else None
+    if starts is not None:
+        # One pass, in place: [src | dst | group starts] in one upload.
+        g = int(starts.size) - 1
+        buf = pointers.staging.take(4 * n + 2 * (g + 1))
+        buf[: 2 * n] = src.view(np.int32)
+        buf[2 * n : 4 * n] = dst.view(np.int32)
+        buf[4 * n : 4 * n + 2 * (g + 1)] = starts.view(np.int32)
+        blob = pointers.staging.upload(buf[: 4 * n + 2 * (g + 1)])
+        src_ptr = blob.data_ptr()
+        for row_bytes, num_layers, _, kptrs, vptrs in pointers.groups:
+            native.check(lib.lvamd_kv_compact_ordered(kptrs, vptrs, num_layers, row_bytes, src_ptr,
+                                                      src_ptr + 8 * n, src_ptr + 16 * n, g, stream),
+                         "lvamd_kv_compact_ordered")
         return
     # [src | dst] as int64 pairs of int32 words, in one pinned buffer and copy.
     buf = pointers.staging.take(4 * n)

@@ -419,15 +419,18 @@ def test_one_metadata_on_caches_of_two_dtypes() -> None:
 def test_workgroup_split_decode_matches_the_oracle(dtype, head_size) -> None:
     # Short decode rows (one segment per workgroup of eight waves, four for
     # the widest rows, results combined in LDS): a 1-token context, segments
-    # of fewer tiles than waves (idle waves) and of more, append fused.
+    # of fewer tiles than waves (idle waves) and of more (up to the 1.5 tiles
+    # per wave the planner splits at), append fused.
     _announce(f"workgroup split d={head_size} {dtype}")
     hq, hkv = (28, 4) if head_size <= 128 else (16, 2)
-    step = make_step(hq=hq, hkv=hkv, d=head_size, bs=16, dtype=DTYPES[dtype],
-                     computed=[0, 31, 40, 250, 200, 130, 97, 5], layouts=_lin(*([1] * 8)), seed=400 + head_size)
+    code = lv.paged_cache.dtype_code(DTYPES[dtype])
+    unit, gw = lv.native.decode_tile_tokens(code, head_size), lv.native.decode_split_waves(code, head_size)
+    computed = [0, unit - 1, unit + 8, (3 * gw // 2) * unit - 1, gw * unit - 1, 2 * unit + 3, 3 * unit, 5]
+    step = make_step(hq=hq, hkv=hkv, d=head_size, bs=16, dtype=DTYPES[dtype], computed=computed,
+                     layouts=_lin(*([1] * 8)), seed=400 + head_size)
     _, ctx = _run_and_check(step)
     work = ctx.work_of(step.cache.layer_spec(step.layer_ids[0]))
-    code = lv.paged_cache.dtype_code(DTYPES[dtype])
-    assert work.group_waves == lv.native.decode_split_waves(code, head_size) > 1 and work.num_jobs == 0
+    assert work.group_waves == gw > 1 and work.num_jobs == 0 and work.units_per_wave == 2
 
 
 @pytest.mark.parametrize("dtype", ("fp32", "bf16"))

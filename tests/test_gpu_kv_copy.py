@@ -182,6 +182,118 @@ def test_compact_many_matches_per_request_oracle(n_requests, after_create) -> No
         np.testing.assert_array_equal(_bits(cache.layer(f"l{i}").values), vb)
 
 
+@pytest.mark.parametrize(
+    "dtype,bs,n_requests,max_q,mixed",
+    [
+        (torch.bfloat16, 16, 16, 12, False),   # C5-shaped: accepted paths of 16 requests
+        (torch.float16, 3, 5, 40, True),       # odd block size, layers of two row sizes
+        (torch.float32, 16, 2, 64, False),     # a group at the length cap (4 batches of 16)
+        (torch.bfloat16, 1, 40, 9, True),      # one-token blocks
+    ],
+)
+def test_ordered_compact_is_one_pass_and_matches_the_oracle(dtype, bs, n_requests, max_q, mixed) -> None:
+    # Strictly increasing retained indices over more pairs than ride in the
+    # kernel arguments: compact_many takes the one-pass in-place kernel
+    # (lvamd_kv_compact_ordered), and every byte of every layer equals the
+    # oracle's per-request compact.
+    from light_vllm_amd import native
+    from light_vllm_amd.paged_cache import _compact_plan, ordered_groups
+
+    _announce(f"ordered compact {dtype} bs={bs} x{n_requests} q<={max_q} mixed={mixed}")
+    rng = np.random.default_rng(300 + n_requests * bs)
+    shapes = [(2, 128), (4, 64), (1, 80)] if mixed else [(2, 128)] * 3
+    spec = lv.ModelKVCacheSpec(tuple(lv.AttentionLayerSpec(f"l{i}", 8, hkv, d) for i, (hkv, d) in enumerate(shapes)))
+    specs, num_blocks = [], 0
+    for r in range(n_requests):
+        computed, q = int(rng.integers(0, 50)), int(rng.integers(1, max_q + 1)) if r else max_q
+        retained = tuple(sorted(int(x) for x in rng.permutation(q)[: int(rng.integers(1, q + 1))]))
+        if r == 0:
+            retained = tuple(range(1, q)) if q > 1 else (0,)  # the longest group moves q - 1 rows
+        specs.append((computed, q, retained))
+        num_blocks += (computed + q + bs - 1) // bs
+    num_blocks += 3
+    cache = lv.PagedKVCache(spec, lv.PagedKVCacheConfig(num_blocks=num_blocks, block_size=bs, dtype=dtype,
+                                                        device=DEV))
+    gen = torch.Generator(device=DEV).manual_seed(num_blocks)
+    for i in range(len(shapes)):
+        for pool in (cache.layer(f"l{i}").keys, cache.layer(f"l{i}").values):
+            pool.copy_(torch.randn(pool.shape, generator=gen, device=DEV).to(dtype))
+    perm = [int(x) for x in rng.permutation(num_blocks)]
+    requests, off = [], 0
+    for computed, q, retained in specs:
+        need = (computed + q + bs - 1) // bs
+        requests.append(dict(block_ids=tuple(perm[off : off + need]), num_computed_tokens=computed,
+                             num_query_tokens=q, num_reserved_query_tokens=q, retained_query_indices=retained))
+        off += need
+    moved, src, dst = _compact_plan(cache.config, requests)
+    assert src.size > native.load().lvamd_kv_compact_inline_pairs()
+    assert ordered_groups(moved, src, dst) is not None, "this step must take the one-pass compact"
+    pools = [(_bits(cache.layer(f"l{i}").keys), _bits(cache.layer(f"l{i}").values)) for i in range(len(shapes))]
+    expect = []
+    for req in requests:
+        args = {k: v for k, v in req.items() if k != "block_ids"}
+        expect.append(O.compact(pools, req["block_ids"], num_blocks=num_blocks, block_size=bs, **args))
+    got_moved = cache.compact_many(requests)
+    torch.cuda.synchronize()
+    assert got_moved == tuple(expect)
+    for i, (kb, vb) in enumerate(pools):
+        np.testing.assert_array_equal(_bits(cache.layer(f"l{i}").keys), kb, err_msg=f"layer {i} keys")
+        np.testing.assert_array_equal(_bits(cache.layer(f"l{i}").values), vb, err_msg=f"layer {i} values")
+
+
+def test_ordered_compact_c_abi_matches_the_two_phase_compact() -> None:
+    # Through the C ABI on identical pools: lvamd_kv_compact_ordered and
+    # lvamd_kv_compact give the same bytes for a grouped, ordered pair list
+    # (groups of 1 to 40 pairs; each group reads rows at or after the ones it
+    # writes), and zero groups is a no-op.
+    from light_vllm_amd import native
+
+    _announce("ordered compact vs two-phase compact (C ABI)")
+    lib = native.load()
+    stream = torch.cuda.current_stream(DEV).cuda_stream
+    layers, slots, row = 5, 4096, 2 * 128 * 2
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    a = [torch.randn((slots, 2, 128), generator=gen, device=DEV).to(torch.bfloat16) for _ in range(2 * layers)]
+    b = [t.clone() for t in a]
+    rng = np.random.default_rng(4)
+    src, dst, starts, base = [], [], [0], 0
+    for size in rng.integers(1, 41, size=30):
+        keep = np.sort(rng.choice(np.arange(1, 2 * size), size=size, replace=False))
+        src += [base + int(k) for k in keep]
+        dst += [base + i for i in range(size)]
+        starts.append(starts[-1] + int(size))
+        base += 2 * int(size) + 5
+    src_t = torch.tensor(src, dtype=torch.int64, device=DEV)
+    dst_t = torch.tensor(dst, dtype=torch.int64, device=DEV)
+    starts_t = torch.tensor(starts, dtype=torch.int64, device=DEV)
+
+    def tables(pools):
+        k = torch.tensor([t.data_ptr() for t in pools[0::2]], dtype=torch.int64, device=DEV)
+        v = torch.tensor([t.data_ptr() for t in pools[1::2]], dtype=torch.int64, device=DEV)
+        return k, v
+
+    (ka, va), (kb, vb) = tables(a), tables(b)
+    before = [t.view(torch.int16).cpu().numpy().reshape(slots, -1) for t in a]
+    n = len(src)
+    ws_bytes = lib.lvamd_kv_compact_workspace_size(n, layers, row)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    native.check(lib.lvamd_kv_compact(ka.data_ptr(), va.data_ptr(), layers, row, src_t.data_ptr(), dst_t.data_ptr(),
+                                      n, ws.data_ptr(), ws_bytes, stream), "lvamd_kv_compact")
+    native.check(lib.lvamd_kv_compact_ordered(kb.data_ptr(), vb.data_ptr(), layers, row, src_t.data_ptr(),
+                                              dst_t.data_ptr(), starts_t.data_ptr(), len(starts) - 1, stream),
+                 "lvamd_kv_compact_ordered")
+    native.check(lib.lvamd_kv_compact_ordered(kb.data_ptr(), vb.data_ptr(), layers, row, src_t.data_ptr(),
+                                              dst_t.data_ptr(), starts_t.data_ptr(), 0, stream),
+                 "lvamd_kv_compact_ordered")
+    torch.cuda.synchronize()
+    for i, (x, y, rows) in enumerate(zip(a, b, before)):
+        expect = rows.copy()
+        expect[dst] = rows[src]  # every source read before any destination is written
+        np.testing.assert_array_equal(y.view(torch.int16).cpu().numpy().reshape(slots, -1), expect,
+                                      err_msg=f"pool {i} vs closed form")
+        assert torch.equal(x.view(torch.int16), y.view(torch.int16)), f"pool {i} vs two-phase compact"
+
+
 def test_compact_many_rejects_a_shared_destination() -> None:
     cache = _cache(hkv=2, d=64, bs=2, nb=8, dtype=torch.float32)
     req = dict(block_ids=(0, 1), num_computed_tokens=1, num_query_tokens=2, num_reserved_query_tokens=2,

@@ -249,8 +249,11 @@ def test_workgroup_split_gives_each_segment_one_workgroup(seed, bs, gw) -> None:
     stream_k = plan.work(7, 4, 1024, 0, unit, 1)
     split = -(-int(tiles.max()) // gw)
     cap = (254 * bs) // unit
-    use = batch * 4 <= 256 and split <= min(cap, 4) and split <= stream_k.units_per_wave + (
+    longest = int(tiles.max())
+    use = batch * 4 <= 256 and split <= min(cap, 2) and split <= stream_k.units_per_wave + (
         3 if stream_k.num_jobs else 0)
+    if split == 2 and 2 * longest > 3 * gw and batch * 4 < 128:
+        use = False
     if not use:
         assert work.group_waves == 1 and work.waves_per_head == stream_k.waves_per_head
         return
@@ -289,12 +292,14 @@ def test_workgroup_split_is_not_used_where_stream_k_is_faster() -> None:
     plan = StepPlan(md, block_size=16, device=CPU)
     for gw in (4, 8):
         assert plan.work(7, 4, 1024, 0, 32, 1, split_groups=256, split_waves=gw).group_waves == 1
-    # Long equal contexts: more than four tiles per wave stays on stream-K
-    # (the step is bandwidth-bound); short ones take the split.
-    plan = StepPlan(_uniform_metadata(batch=64, computed=4000, q=1), block_size=16, device=CPU)
-    assert plan.work(7, 4, 1024, 0, 32, 1, split_groups=256, split_waves=8).group_waves == 1
-    plan = StepPlan(_uniform_metadata(batch=64, computed=1000, q=1), block_size=16, device=CPU)
-    assert plan.work(7, 4, 1024, 0, 32, 1, split_groups=256, split_waves=8).group_waves == 8
+    # Equal contexts: more than two tiles per wave stays on stream-K; two
+    # take the split when the pieces average at most 1.5 tiles or the step
+    # has 128 segments or more; one always does.
+    for batch, computed, gw in ((64, 4000, 1), (64, 1000, 1), (8, 600, 1), (8, 500, 1), (32, 500, 8),
+                                (8, 380, 8), (8, 250, 8), (1, 0, 8)):
+        plan = StepPlan(_uniform_metadata(batch=batch, computed=computed, q=1), block_size=16, device=CPU)
+        got = plan.work(7, 4, 1024, 0, 32, 1, split_groups=256, split_waves=8).group_waves
+        assert got == gw, (batch, computed, got)
     plan = StepPlan(_uniform_metadata(batch=70, computed=100, q=1), block_size=16, device=CPU)
     assert plan.work(7, 4, 1024, 0, 32, 1, split_groups=256).group_waves == 1  # 280 workgroups > 256
     assert plan.work(7, 4, 1024, 0, 32, 1, split_groups=512).group_waves == 8
@@ -692,6 +697,10 @@ def test_library_loads_and_exports_every_header_function() -> None:
     assert lib.lvamd_kv_compact_workspace_size(33, 28, 1024) == 33 * 28 * 2 * 1024
     # The small compact takes at most the inline pair count (refused before any HIP call).
     assert lib.lvamd_kv_compact_small(None, None, 28, 1024, None, None, 33, None) == -1
+    # The one-pass compact checks its arguments before any HIP call.
+    assert lib.lvamd_kv_compact_ordered(None, None, 28, 1024, None, None, None, 0, None) == 0
+    assert lib.lvamd_kv_compact_ordered(None, None, 28, 1024, None, None, None, 2, None) == -1
+    assert lib.lvamd_kv_compact_ordered(None, None, 0, 1024, None, None, None, 2, None) == -1
     assert lib.lvamd_kv_block_copy_small_pairs() == 32
     assert lib.lvamd_kv_block_copy_small(None, None, 28, 8192, None, None, 33, None) == -1
     # The allocation-free compact refuses, before any HIP call, a call whose
@@ -1133,3 +1142,98 @@ def test_incremental_planner_paths_agree_with_a_fresh_check_every_step(seed) -> 
     proofs, checks, reused, _ = host.counts()
     assert proofs - proofs0 >= 20 and checks - checks0 >= 5, "both table paths must be exercised"
     assert reused - reused0 > 0, "the flatten must have reused the previous step's values"
+
+
+def _run_ordered(pool: np.ndarray, src, dst, starts, rng) -> None:
+    """The one-pass compact's schedule on the CPU: each group moves its pairs
+    in batches of 16 (every source of a batch read before its destinations
+    are written), batches of one group in order, groups interleaved in a
+    random order (the GPU runs them side by side at any relative speed)."""
+
+    nxt = [int(starts[g]) for g in range(starts.size - 1)]
+    live = [g for g in range(starts.size - 1) if nxt[g] < starts[g + 1]]
+    while live:
+        g = live[int(rng.integers(len(live)))]
+        b, end = nxt[g], min(nxt[g] + 16, int(starts[g + 1]))
+        rows = pool[src[b:end]].copy()
+        pool[dst[b:end]] = rows
+        nxt[g] = end
+        if end == starts[g + 1]:
+            live.remove(g)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_ordered_compact_schedule_reproduces_the_oracle(seed) -> None:
+    """Whenever ordered_groups accepts a step's compact pairs, every
+    interleaving of the one-pass kernel's per-group batches leaves the pool
+    as the oracle's compact (all sources read before any destination) does;
+    steps whose retained indices are strictly increasing are always
+    accepted."""
+
+    from types import SimpleNamespace
+
+    from light_vllm_amd.paged_cache import ORDERED_MAX_PAIRS, _compact_plan, ordered_groups
+
+    rng = np.random.default_rng(900 + seed)
+    bs = int(rng.choice([1, 3, 16]))
+    sorted_only = seed % 2 == 0
+    n_req = int(rng.integers(1, 9))
+    requests, tables, args_list = [], [], []
+    num_blocks = 0
+    specs = []
+    for _ in range(n_req):
+        computed, q = int(rng.integers(0, 40)), int(rng.integers(1, 70))
+        keep = int(rng.integers(1, q + 1))
+        retained = [int(x) for x in rng.permutation(q)[:keep]]
+        if sorted_only:
+            retained.sort()
+        specs.append((computed, q, tuple(retained)))
+        num_blocks += (computed + q + bs - 1) // bs
+    num_blocks += 4
+    perm = [int(x) for x in rng.permutation(num_blocks)]
+    off = 0
+    for computed, q, retained in specs:
+        need = (computed + q + bs - 1) // bs
+        table = tuple(perm[off : off + need])
+        off += need
+        args = dict(num_computed_tokens=computed, num_query_tokens=q, num_reserved_query_tokens=q,
+                    retained_query_indices=retained)
+        requests.append(dict(block_ids=table, **args))
+        tables.append(table)
+        args_list.append(args)
+    cfg = SimpleNamespace(block_size=bs, num_blocks=num_blocks)
+    moved, src, dst = _compact_plan(cfg, tuple(requests))
+    starts = ordered_groups(moved, src, dst)
+    if sorted_only and int(moved.max(initial=0)) <= ORDERED_MAX_PAIRS and src.size:
+        assert starts is not None, "strictly increasing retained indices must take the one-pass compact"
+    pool = rng.standard_normal((num_blocks, bs, 1, 1)).astype(np.float32)
+    expect = [(pool.copy(), pool.copy())]
+    for table, args in zip(tables, args_list):
+        O.compact(expect, table, num_blocks=num_blocks, block_size=bs, **args)
+    if starts is None:
+        return
+    assert starts[0] == 0 and starts[-1] == src.size and np.all(np.diff(starts) > 0)
+    for schedule in range(4):
+        got = pool.copy()
+        _run_ordered(got.reshape(-1), src, dst, starts, np.random.default_rng(schedule))
+        np.testing.assert_array_equal(got, expect[0][0])
+
+
+def test_ordered_groups_refuses_unsafe_orders() -> None:
+    """A destination read by a later pair of its group, a row one group
+    writes and another reads, and a group past the length cap all take the
+    two-phase compact."""
+
+    from light_vllm_amd.paged_cache import ORDERED_MAX_PAIRS, ordered_groups
+
+    i64 = lambda *v: np.array(v, dtype=np.int64)  # noqa: E731
+    # Pair 0 writes slot 10, which pair 1 reads afterwards.
+    assert ordered_groups(i64(2), i64(13, 10), i64(10, 12)) is None
+    # Pair 1 writes slot 13 after pair 0 read it: safe.
+    assert ordered_groups(i64(2), i64(13, 14), i64(12, 13)).tolist() == [0, 2]
+    # Request 0 writes slot 20, which request 1 reads.
+    assert ordered_groups(i64(1, 1), i64(21, 20), i64(20, 30)) is None
+    assert ordered_groups(i64(1, 0, 1), i64(21, 31), i64(20, 30)).tolist() == [0, 1, 2]
+    n = ORDERED_MAX_PAIRS + 1
+    assert ordered_groups(i64(n), np.arange(100, 100 + n), np.arange(n)) is None
+    assert ordered_groups(i64(n - 1), np.arange(100, 99 + n), np.arange(n - 1)) is not None

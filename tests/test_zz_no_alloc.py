@@ -5,8 +5,10 @@ Both run on identical copies of the same pools; every byte of every layer's
 K and V must agree, and the moved rows must equal the closed form (row
 dst[i] holds what row src[i] held before the call, every other row is
 unchanged).  Two calls in a row, the second with fewer pairs, so the second
-runs over the scratch the first left behind.  (The refusal of a call past the
-static size happens before any HIP call and is tested on the CPU.)
+runs over the scratch the first left behind.  The process's first call (the
+static array's address lookup) is checked on its own, and the device's free
+memory must not change across calls.  (The refusal of a call past the static
+size happens before any HIP call and is tested on the CPU.)
 """
 
 from __future__ import annotations
@@ -62,6 +64,47 @@ def _expected(before, src, dst):
             layer.append(flat.reshape(pool.shape))
         out.append(tuple(layer))
     return out
+
+
+def test_static_compact_allocates_nothing() -> None:
+    # The entry point's contract: no device allocation.  This file's first
+    # test, so its first call is the process's first (nothing else calls the
+    # static compact): the one that looks up the static array's device
+    # address, checked against the closed form on its own.  Then the
+    # device's free memory is read around two more calls (every tensor they
+    # use made beforehand) and must not change.
+    lib = native.load()
+    stream = torch.cuda.current_stream(DEV).cuda_stream
+    row_bytes = HKV * D * 2
+    rng = np.random.default_rng(12)
+    pools = _pools(6)
+    ptrs = _pointer_tables(pools)
+    calls = [_pairs(rng, n) for n in (300, 100, 33)]
+
+    def run(src, dst):
+        native.check(lib.lvamd_kv_compact_static(ptrs[0].data_ptr(), ptrs[1].data_ptr(), LAYERS, row_bytes,
+                                                 src.data_ptr(), dst.data_ptr(), src.numel(), stream),
+                     "lvamd_kv_compact_static")
+
+    print("[gpu] no-alloc compact: first call, then free memory around two calls", file=sys.stderr, flush=True)
+    before = _bits(pools)
+    run(*calls[0])
+    torch.cuda.synchronize()
+    for (gk, gv), (ek, ev) in zip(_bits(pools), _expected(before, *calls[0])):
+        np.testing.assert_array_equal(gk, ek)
+        np.testing.assert_array_equal(gv, ev)
+    before = _bits(pools)
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info(DEV)
+    run(*calls[1])
+    run(*calls[2])
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info(DEV)
+    assert free1 == free0, f"device free memory changed by {free0 - free1} bytes"
+    expect = _expected(_expected(before, *calls[1]), *calls[2])
+    for (gk, gv), (ek, ev) in zip(_bits(pools), expect):
+        np.testing.assert_array_equal(gk, ek)
+        np.testing.assert_array_equal(gv, ev)
 
 
 def test_static_compact_matches_the_workspace_compact_on_two_calls() -> None:
