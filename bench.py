@@ -14,7 +14,8 @@ head_size 128, block_size 16).
   256 MB Infinity Cache cannot serve a step from the previous one.
 * ``roofline``   the decode kernel alone: algorithmic bytes per launch / its
   mean launch time from HIP events on the launch stream (batches of
-  back-to-back launches), against 8 TB/s; ``traffic`` is the HBM bytes per
+  back-to-back launches; the kernel merges its split segments itself), against
+  8 TB/s; ``traffic`` is the HBM bytes per
   launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs.
 * ``serving``    the same shape served as light-vllm serves it: 28 layers,
   a new metadata object every step (so ``create()`` validates and stages a
@@ -336,8 +337,8 @@ def serving_steps(device: torch.device, steps: int, warmup: int) -> dict:
 
 
 def read_ceiling(device: torch.device, nbytes: int = 2 << 30) -> dict:
-    """Practical HBM read ceiling: the library's read probe (a plain stream of
-    16-byte loads, XOR-folded) over a buffer far larger than the 256 MB MALL,
+    """Practical HBM read ceiling: the library's read probe (a stream of
+    non-temporal 16-byte loads, XOR-folded) over a buffer far larger than the 256 MB MALL,
     at a few grid sizes; HIP events on the launch stream, best mean kept."""
 
     from light_vllm_amd import native
@@ -693,7 +694,6 @@ def run_c3(args, device, emit: bool = True):
 
     def decode(i):
         launches[i % len(launches)].decode()
-        launches[i % len(launches)].merge()
 
     decode_ms = _time_launches(decode, args.steps, args.warmup, device)
     comp = np.asarray(computed, dtype=np.int64)
@@ -1148,8 +1148,9 @@ def main() -> int:
     print(f"[bench] timed {args.steps} steps: {ms_per_step:.4f} ms/step "
           f"(host submit {submitted / args.steps * 1e3:.4f} ms/step)", file=sys.stderr, flush=True)
 
-    # Decode kernel alone: HIP events on the launch stream (torch's current
-    # stream) around batches of back-to-back launches, rotating pool sets.
+    # The decode kernel (its split segments merged in the kernel): HIP events
+    # on the launch stream (torch's current stream) around batches of
+    # back-to-back launches, rotating pool sets.
     stream = torch.cuda.current_stream(device)
     batch = 10
     rounds = max(1, args.steps // batch)
@@ -1233,7 +1234,7 @@ def main() -> int:
     ceiling = read_ceiling(device)
     record["hbm_read_ceiling"] = {
         **ceiling, "decode_kernel_frac": round(achieved / ceiling["GBps"], 4),
-        "note": "plain 16-byte load stream over 2 GiB on this GPU (lvamd_hbm_read_probe); peak stays 8 TB/s",
+        "note": "stream of non-temporal 16-byte loads over 2 GiB on this GPU (lvamd_hbm_read_probe); peak stays 8 TB/s",
     }
     traffic = measured_traffic()
     if traffic is not None:

@@ -117,7 +117,37 @@ struct DecodeTile {
   // (the older one wins arbitration), which left the younger waves of a
   // static split finishing last.
   static constexpr int VALLOC = VSLOTS < 1024 ? 1024 : VSLOTS;
+  // Line-order loads (one column tile, 16 chunks per head row: bf16/fp16 at
+  // D = 128, fp32 at D = 64): each load instruction covers four whole
+  // 256-byte row slices, i.e. whole 128-byte lines, instead of a 64-byte
+  // piece of sixteen rows, and the loads are non-temporal.  K then goes
+  // through LDS (into the MFMA operand layout) like V.  Gathering C2's blocks
+  // this way takes 48.7 us against 53.9 for the operand-order pattern, whose
+  // half-line accesses with non-temporal loads take 56.5 (probe kernels,
+  // one process).  The K tile sits in the V buffer's padding.
+  static constexpr int CPR = TileShape<T, D>::CPR;
+  static constexpr bool LINES_OK = CTW == 1 && CPR == 16 && TT == 32;
+  static constexpr int RPI = 64 / CPR;     // token rows per line-order load
+  static constexpr int LROWS = TT / RPI;   // line-order loads per lane per tensor
+  static constexpr int KSLOTS = TT * CPR;  // 16-byte LDS slots of a K tile
+  static_assert(!LINES_OK || (LROWS == SUB * TileShape<T, D>::NCH && VSLOTS + KSLOTS <= VALLOC),
+                "line-order tiles reuse the operand-order register arrays and the V padding");
 };
+
+// Line-order LDS slots of a tile (row r, 16-byte chunk c of its head slice,
+// CPR chunks per row): V rows XOR chunk bits 1-3 with row bits 0-2, so the
+// transpose reads of four rows x two chunk pairs hit distinct banks; K rows
+// XOR the chunk with row bits 0-3, so the 16 rows of an operand read hit
+// distinct banks.  The line-order writes (one row per 16 lanes) are a
+// permutation of one row's chunks either way.
+template <int CPR>
+__device__ __forceinline__ int vslot_lines(int r, int c) {
+  return r * CPR + (c ^ ((2 * r) & (CPR - 2)));
+}
+template <int CPR>
+__device__ __forceinline__ int kslot_lines(int r, int c) {
+  return r * CPR + (c ^ (r & (CPR - 1)));
+}
 
 // One piece of a wave's share: a contiguous token range of one
 // (request, column-tile group), with the request fields the kernel needs.
@@ -224,6 +254,18 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
   // piece switch (their registers hold the extra accumulators instead).
   // (In the workgroup split a wave has one piece: nothing to prefetch.)
   constexpr bool kPrefetchQ = CTW == 1 && WG == 1;
+  // Line-order loads in the stream-K kernel (the workgroup split's LDS has no
+  // room for K tiles): register array entry i = s * NCH + kk holds chunk
+  // lane % CPR of tile row RPI * i + lane / CPR.
+  constexpr bool LINES = DT::LINES_OK && WG == 1;
+  constexpr int FR = LINES ? DT::LROWS : SUB;  // rows per lane a tile may append
+  auto vs = [](int r, int c) -> int {
+    if constexpr (LINES) {
+      return vslot_lines<CPR>(r, c);
+    } else {
+      return vslot<NCH>(r, c);
+    }
+  };
   // Per wave: two V buffers (contiguous) and a table slice pair; in the
   // workgroup split the V buffers also take the wave's results at the end
   // (fp32 rows), and they are not padded (the stream-K kernel's padding
@@ -349,8 +391,37 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
   // offsets are read from LDS before any load is issued.  fresh[s] is the
   // pool offset of row group s's row when this tile must append it, else -1.
   auto issue_tile_ids = [&](const Piece& x, int t0, auto block_id, uint4 (&kdst)[SUB][NCH],
-                            uint4 (&vdst)[SUB][NCH], int64_t (&fresh)[SUB]) {
+                            uint4 (&vdst)[SUB][NCH], int64_t (&fresh)[FR]) {
     const int lb0 = logical_block(x.tok_begin);
+    if constexpr (LINES) {
+      // Line order: entry i is chunk lane % CPR of row RPI * i + lane / CPR.
+      constexpr int RPI = DT::RPI;
+      const int c = lane % CPR;
+      gptr<const T> kp[FR];
+      gptr<const T> vp[FR];
+#pragma unroll
+      for (int i = 0; i < FR; ++i) {
+        const int pos = t0 + RPI * i + lane / CPR;
+        const int pc = pos < x.tok_end ? pos : x.tok_end - 1;
+        const int lb = logical_block(pc);
+        const int64_t off = ((int64_t)block_id(lb - lb0) * a.block_size + (pc - lb * a.block_size)) * row_elems;
+        kp[i] = kbase + off;
+        vp[i] = vbase + off;
+        fresh[i] = -1;
+        if (knew != nullptr && pc >= x.computed) {
+          const int64_t t = x.q_start + (pc - x.computed);
+          kp[i] = knew + t * a.kn_tok_stride;
+          vp[i] = vnew + t * a.vn_tok_stride;
+          if (x.cgroup == 0 && pc == pos) fresh[i] = off;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < FR; ++i) {
+        kdst[i / NCH][i % NCH] = load16_stream(kp[i] + c * E16);
+        vdst[i / NCH][i % NCH] = load16_stream(vp[i] + c * E16);
+      }
+      return;
+    }
     gptr<const T> kp[SUB];
     gptr<const T> vp[SUB];
 #pragma unroll
@@ -384,11 +455,22 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
       }
   };
   auto issue_tile = [&](const Piece& x, int tb, int t0, uint4 (&kdst)[SUB][NCH], uint4 (&vdst)[SUB][NCH],
-                        int64_t (&fresh)[SUB]) {
+                        int64_t (&fresh)[FR]) {
     issue_tile_ids(x, t0, [&](int rel) { return tab[tb][rel]; }, kdst, vdst, fresh);
   };
   // Append the tile's fresh rows to the pool (bit-exact row copies).
-  auto store_fresh = [&](const uint4 (&kr)[SUB][NCH], const uint4 (&vr)[SUB][NCH], const int64_t (&fresh)[SUB]) {
+  auto store_fresh = [&](const uint4 (&kr)[SUB][NCH], const uint4 (&vr)[SUB][NCH], const int64_t (&fresh)[FR]) {
+    if constexpr (LINES) {
+      const int c = lane % CPR;
+#pragma unroll
+      for (int i = 0; i < FR; ++i) {
+        if (fresh[i] >= 0) {
+          store16(kbase + fresh[i] + c * E16, kr[i / NCH][i % NCH]);
+          store16(vbase + fresh[i] + c * E16, vr[i / NCH][i % NCH]);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int s = 0; s < SUB; ++s) {
       if (fresh[s] >= 0) {
@@ -403,12 +485,33 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
       }
     }
   };
-  // V tile into LDS: chunk (s, kk) of lane l at slot (s * NCH + kk) * 64 + l.
-  auto stage_v = [&](uint4* vdst, const uint4 (&vr)[SUB][NCH]) {
+  // Tile into LDS.  Operand order: V chunk (s, kk) of lane l at slot
+  // (s * NCH + kk) * 64 + l (K stays in registers).  Line order: V and K rows
+  // at their swizzled slots, K after the V tile.
+  auto stage_v = [&](uint4* vdst, const uint4 (&vr)[SUB][NCH], const uint4 (&kr)[SUB][NCH]) {
+    if constexpr (LINES) {
+      const int c = lane % CPR;
+#pragma unroll
+      for (int i = 0; i < FR; ++i) {
+        const int r = DT::RPI * i + lane / CPR;
+        vdst[vslot_lines<CPR>(r, c)] = vr[i / NCH][i % NCH];
+        vdst[DT::VSLOTS + kslot_lines<CPR>(r, c)] = kr[i / NCH][i % NCH];
+      }
+      return;
+    }
 #pragma unroll
     for (int s = 0; s < SUB; ++s)
 #pragma unroll
       for (int kk = 0; kk < NCH; ++kk) vdst[(s * NCH + kk) * 64 + lane] = vr[s][kk];
+  };
+  // Line order: this tile's K operands (A layout of S^T = K Q^T: lane
+  // (g, l16) holds chunk 4kk + g of row 16s + l16) from the LDS tile.
+  auto read_k = [&](const uint4* vsrc, uint4 (&kdst)[SUB][NCH]) {
+#pragma unroll
+    for (int s = 0; s < SUB; ++s)
+#pragma unroll
+      for (int kk = 0; kk < NCH; ++kk)
+        kdst[s][kk] = vsrc[DT::VSLOTS + kslot_lines<CPR>(16 * s + l16, kk * 4 + g)];
   };
 
   // Prologue.  The first tile is issued straight from the block ids the
@@ -422,7 +525,7 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
   int tn[TAB_PER_LANE];
   uint4 ka[SUB][NCH], kb[SUB][NCH];
   uint4 vr0[SUB][NCH];
-  int64_t fresh0[SUB];
+  int64_t fresh0[FR];
   int tc[TAB_PER_LANE];
   const int first_span = logical_block(min(cur.tok_begin + TT, cur.tok_end) - 1) - logical_block(cur.tok_begin);
   const bool direct = first_span < kPieceBlocks;
@@ -449,7 +552,7 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
     if constexpr (kPrefetchQ) load_q(nxt, qn);
   }
   if (direct) store_table(tb, tc);
-  stage_v(vlds_a, vr0);
+  stage_v(vlds_a, vr0, ka);
   store_fresh(ka, vr0, fresh0);
 
   LaneCol lc[CTW];
@@ -496,10 +599,15 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
       }
     }
 
+    // Line order: this tile's K operands come out of LDS (their reads
+    // overlap the next tile's address arithmetic).
+    uint4 kl[LINES ? SUB : 1][NCH];
+    if constexpr (LINES) read_k(vc, kl);
+
     const int nt0 = t0 + TT;
     const bool next_in_cur = nt0 < cur.tok_end;
     uint4 vr[SUB][NCH];
-    int64_t fresh[SUB];
+    int64_t fresh[FR];
     const bool issued = next_in_cur || have_nxt;
     if (next_in_cur) {
       issue_tile(cur, tb, nt0, kx, vr, fresh);
@@ -520,7 +628,8 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
       for (int ct = 0; ct < CTW; ++ct) {
         st[ct][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < NCH; ++kk) st[ct][s] = Mma<T>::qk(kc[s][kk], qf[ct][kk], st[ct][s]);
+        for (int kk = 0; kk < NCH; ++kk)
+          st[ct][s] = Mma<T>::qk(LINES ? kl[s][kk] : kc[s][kk], qf[ct][kk], st[ct][s]);
       }
 
     // Scale, mask and the online softmax of each column tile.
@@ -593,7 +702,7 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
         // The transpose hands lane (g, l16) dims 16n + l16 of rows 4g + 0..3:
         // the A operand of a 16x16x16 step whose k index is 4g + e.
         const int c = 2 * n + (q4 >> 1);
-        const int lo = vslot<NCH>(4 * g + (l16 >> 2), c) * 16 + (q4 & 1) * 8;
+        const int lo = vs(4 * g + (l16 >> 2), c) * 16 + (q4 & 1) * 8;
         const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vbytes + lo));
 #pragma unroll
         for (int ct = 0; ct < CTW; ++ct) {
@@ -622,8 +731,8 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
           // 16n + 4*(l16%4)..+3; the transpose hands it dims 16n + l16 of rows
           // 32h + 16j + 4g + 0..3.
           const int c = 2 * n + (q4 >> 1);
-          const int lo = vslot<NCH>(32 * h + 4 * g + (l16 >> 2), c) * 16 + (q4 & 1) * 8;
-          const int hi = vslot<NCH>(32 * h + 16 + 4 * g + (l16 >> 2), c) * 16 + (q4 & 1) * 8;
+          const int lo = vs(32 * h + 4 * g + (l16 >> 2), c) * 16 + (q4 & 1) * 8;
+          const int hi = vs(32 * h + 16 + 4 * g + (l16 >> 2), c) * 16 + (q4 & 1) * 8;
           const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vbytes + lo));
           const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vbytes + hi));
           const s16x4 both[2] = {v0, v1};
@@ -647,7 +756,7 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
         for (int s = 0; s < SUB; ++s)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float av = vfl[vslot<NCH>(16 * s + 4 * g + r, d >> 2) * 4 + (d & 3)];
+            const float av = vfl[vs(16 * s + 4 * g + r, d >> 2) * 4 + (d & 3)];
 #pragma unroll
             for (int ct = 0; ct < CTW; ++ct)
               acc[ct][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, p4[ct][s][r], acc[ct][n], 0, 0, 0);
@@ -658,7 +767,7 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
     // Next tile's V into the other LDS buffer (this waits for its loads),
     // and its fresh rows into the pool.
     if (issued) {
-      stage_v(vx, vr);
+      stage_v(vx, vr, kx);
       store_fresh(kx, vr, fresh);
     }
     if (next_in_cur) t0 = nt0;
@@ -721,16 +830,10 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
   // piece (its first tile is already staged) and start fetching the one
   // after.  Returns false after the wave's last piece.
   auto end_piece = [&]() -> bool {
+    if (!have_nxt) return false;
     float l_tot[CTW];
 #pragma unroll
     for (int ct = 0; ct < CTW; ++ct) l_tot[ct] = row_sum4(l_run[ct]);
-    if (!have_nxt) {
-      write_piece(cur, lc, acc, m_run, l_tot);
-      if constexpr (kDeferWrite) {
-        if (pend) write_piece(pend_piece, pend_lc, pend_acc, pend_m, pend_s);
-      }
-      return false;
-    }
     if constexpr (kDeferWrite) {
       if (pend) write_piece(pend_piece, pend_lc, pend_acc, pend_m, pend_s);
       pend = true;
@@ -781,6 +884,17 @@ __global__ __launch_bounds__(64 * WG) void paged_decode_kernel(
   while (true) {
     if (step(ka, kb, vlds_a, vlds_b) && !end_piece()) break;
     if (step(kb, ka, vlds_b, vlds_a) && !end_piece()) break;
+  }
+  // The wave's last piece, written once after the loop (its code is not
+  // duplicated into the two step copies).
+  {
+    float l_tot[CTW];
+#pragma unroll
+    for (int ct = 0; ct < CTW; ++ct) l_tot[ct] = row_sum4(l_run[ct]);
+    write_piece(cur, lc, acc, m_run, l_tot);
+    if constexpr (kDeferWrite) {
+      if (pend) write_piece(pend_piece, pend_lc, pend_acc, pend_m, pend_s);
+    }
   }
   finish_workgroup();
 }

@@ -465,7 +465,6 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W == 8 ?
       const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
 #pragma unroll
       for (int n = 0; n < NT; ++n) store_partial4<true, T>(pacc + 16 * n + 4 * g, acc[ct][n], inv);
-      typedef float f32x2 __attribute__((ext_vector_type(2)));
       if (g == 0) __builtin_nontemporal_store(f32x2{m_run[ct], l_tot}, reinterpret_cast<f32x2*>(a.part_ml + cs * 2));
       continue;
     }

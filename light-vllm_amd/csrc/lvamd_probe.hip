@@ -1,7 +1,8 @@
 // HBM read-bandwidth probe: the practical read ceiling that the paged decode
-// kernel's bandwidth is compared with.  A grid-stride stream of 16-byte
-// loads, kProbeUnroll in flight per lane, folded by XOR into one word per
-// lane so that no load can be dropped.  No counterpart in the reference.
+// kernel's bandwidth is compared with.  A grid-stride stream of streaming
+// (non-temporal) 16-byte loads, the form the decode kernel reads K/V with,
+// kProbeUnroll in flight per lane, folded by XOR into one word per lane so
+// that no load can be dropped.  No counterpart in the reference.
 
 #include "lvamd_common.h"
 
@@ -17,7 +18,7 @@ __global__ __launch_bounds__(64) void hbm_read_probe_kernel(gptr<const u32x4> p,
   for (; i + (kProbeUnroll - 1) * nthr < n16; i += kProbeUnroll * nthr) {
     u32x4 v[kProbeUnroll];
 #pragma unroll
-    for (int u = 0; u < kProbeUnroll; ++u) v[u] = p[i + u * nthr];
+    for (int u = 0; u < kProbeUnroll; ++u) v[u] = __builtin_nontemporal_load(p + i + u * nthr);
 #pragma unroll
     for (int u = 0; u < kProbeUnroll; ++u) acc ^= v[u];
   }
