@@ -117,8 +117,8 @@ struct DecodeTile {
   // (the older one wins arbitration), which left the younger waves of a
   // static split finishing last.
   static constexpr int VALLOC = VSLOTS < 1024 ? 1024 : VSLOTS;
-  // Line-order loads (one column tile, 16 chunks per head row: bf16/fp16 at
-  // D = 128, fp32 at D = 64): each load instruction covers four whole
+  // Line-order loads (one column tile, 16-bit pools with 16 chunks per head
+  // row, i.e. bf16/fp16 at D = 128): each load instruction covers four whole
   // 256-byte row slices, i.e. whole 128-byte lines, instead of a 64-byte
   // piece of sixteen rows, and the loads are non-temporal.  K then goes
   // through LDS (into the MFMA operand layout) like V.  Gathering C2's blocks
@@ -126,7 +126,9 @@ struct DecodeTile {
   // half-line accesses with non-temporal loads take 56.5 (probe kernels,
   // one process).  The K tile sits in the V buffer's padding.
   static constexpr int CPR = TileShape<T, D>::CPR;
-  static constexpr bool LINES_OK = CTW == 1 && CPR == 16 && TT == 32;
+  // (fp32 at D = 64 has 16 chunks per row too, but its latency-bound C1
+  // step ran 15.7 -> 19.9 us with them: the K round trip through LDS.)
+  static constexpr bool LINES_OK = sizeof(T) == 2 && CTW == 1 && CPR == 16 && TT == 32;
   static constexpr int RPI = 64 / CPR;     // token rows per line-order load
   static constexpr int LROWS = TT / RPI;   // line-order loads per lane per tensor
   static constexpr int KSLOTS = TT * CPR;  // 16-byte LDS slots of a K tile
