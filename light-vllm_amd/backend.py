@@ -34,7 +34,9 @@ from torch import Tensor
 from light_vllm_amd import errors, native
 from light_vllm_amd.metadata import PagedAttentionMetadata
 from light_vllm_amd.paged_cache import current_stream, dtype_code, hip_append_rotary
-from light_vllm_amd.plan import DECODE_MAX_COLUMNS, PREFILL_MIN_TILES, UNIT_TOKENS, LayerShapes, Staging, StepPlan
+from light_vllm_amd.plan import (
+    DECODE_MAX_COLUMNS, DECODE_MIN_UNITS_PER_WAVE, PREFILL_MIN_TILES, UNIT_TOKENS, LayerShapes, Staging, StepPlan,
+)
 
 SUPPORTED_HEAD_SIZES = (32, 64, 80, 96, 128, 256)
 
@@ -197,6 +199,7 @@ class _LayerStatic:
 
 
 _UNBOUND = object()
+_NOT_FAST = 1 << 30  # attend_tensors: a tensor rule of the fast path does not hold
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 _NO_APPEND = (None, 0, 0, None, 0, 0)
 # Per-XCD prefill order policies (the planner's kernel fact).
@@ -219,7 +222,7 @@ class HipPagedAttention:
         self._bound: dict[str, tuple | None] = {}
         self._outputs: dict[tuple, tuple] = {}
         self._launches_held: list = []
-        self._attend = native.host().attend
+        self._attend_tensors = native.host().attend_tensors
         self._attend_fn = native.attention_entry()
 
     @property
@@ -245,32 +248,21 @@ class HipPagedAttention:
         if layer_id in self._layer_ids:
             raise errors.KVCacheError(f"paged attention layer {layer_id!r} ran more than once")
         self._layer_ids.add(layer_id)
-        # The common case in one native call: every tensor rule holds (the
-        # layer's bound shapes, dtype and device), rows are 16-byte aligned
-        # and there is no rotary; anything else takes the general path,
-        # which raises the first broken rule's message.
+        # The common case in one native call (the host module's
+        # attend_tensors): it reads the tensors' dtype, device, shapes,
+        # strides and pointers, and launches when every rule holds (the
+        # layer's bound shapes, dtype and device, 16-byte rows); anything
+        # else, and rotary, takes the general path, which raises the first
+        # broken rule's message.
         bound = self._bound.get(layer_id, _UNBOUND)
         if bound is _UNBOUND:
             bound = self._bind(layer_id)
         if bound is not None and rotary is None:
-            q_shape, kv_shape, dt, dev, es, plan_ptr, k_pool, v_pool, out, out_ptr, o0, o1, dev_index = bound
-            if (query.shape == q_shape and key.shape == kv_shape and value.shape == kv_shape and query.dtype is dt
-                    and key.dtype is dt and value.dtype is dt and query.device == dev and key.device == dev
-                    and value.device == dev):
-                qs = query.stride()
-                ks = key.stride()
-                vs = value.stride()
-                qp = query.data_ptr()
-                kp = key.data_ptr()
-                vp = value.data_ptr()
-                if qs[2] == 1 and ks[2] == 1 and vs[2] == 1 and not (
-                    (qp | kp | vp | (qs[0] | qs[1] | ks[0] | ks[1] | vs[0] | vs[1]) * es) & 15
-                ):
-                    status = self._attend(self._attend_fn, plan_ptr, qp, qs[0], qs[1], kp, ks[0], ks[1], vp, vs[0],
-                                          vs[1], k_pool, v_pool, out_ptr, o0, o1, scale, _raw_stream(dev_index))
-                    if status:
-                        native.check(status, "lvamd_paged_attention")
-                    return out
+            status = self._attend_tensors(bound[0], query, key, value, scale)
+            if status == 0:
+                return bound[1]
+            if status != _NOT_FAST:
+                native.check(status, "lvamd_paged_attention")
         return self._forward_general(layer_id, query, key, value, scale=scale, rotary=rotary)
 
     def _bind(self, layer_id: str) -> tuple | None:
@@ -297,11 +289,12 @@ class HipPagedAttention:
                                device=found.device)
             views = self._outputs[found.shape] = slab.unbind(0)
         out = views[found.index]
-        bound = self._bound[layer_id] = (
-            (tokens, spec.num_query_heads, spec.head_size), (tokens, spec.num_kv_heads, spec.head_size),
-            found.dtype, found.device, found.element_size, launch.plan_ptr, found.k_pool, found.v_pool, out,
-            out.data_ptr(), spec.num_query_heads * spec.head_size, spec.head_size, found.device_index,
+        facts = (
+            self._attend_fn, launch.plan_ptr, found.k_pool, found.v_pool, out.data_ptr(),
+            spec.num_query_heads * spec.head_size, spec.head_size, found.dtype, found.device_index,
+            found.element_size, tokens, spec.num_query_heads, spec.num_kv_heads, spec.head_size, _raw_stream,
         )
+        bound = self._bound[layer_id] = (facts, out)
         self._launches_held.append(launch)  # the bound plan structure stays alive with the context
         return bound
 
@@ -534,7 +527,8 @@ class HipPagedAttentionBackend:
                 native.decode_tile_tokens(code, d, 4) if has4 else 0,
                 native.prefill_resident_units(code, d, 4) if columns else 0,
                 native.prefill_resident_units(code, d, 8) if wide else 0,
-                self._partition_tokens or 0, DECODE_MAX_COLUMNS, 4, PREFILL_MIN_TILES, int(self._shared_prefix),
+                self._partition_tokens or 0, DECODE_MAX_COLUMNS, DECODE_MIN_UNITS_PER_WAVE, PREFILL_MIN_TILES,
+                int(self._shared_prefix),
                 native.xcd_count() if columns else 0, self._prefill_order,
                 native.decode_split_groups(code, d) if self._decode_workgroups else 0,
                 native.decode_split_waves(code, d),

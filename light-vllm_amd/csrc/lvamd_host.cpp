@@ -2087,6 +2087,113 @@ PyObject* attend(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   return PyLong_FromLong(status);
 }
 
+// ---------------------------------------------------------------------------
+// attend_tensors(bound, q, k, v, scale) -> status, or kNotFast
+//
+// forward's common case in one call: reads each tensor's dtype, device,
+// shape, strides and data pointer itself and, when every rule of the fast
+// path holds (the layer's bound shapes, its dtype and device, contiguous
+// 16-byte rows), calls lvamd_paged_attention.  Any other tensor returns
+// kNotFast and the caller takes its general path, which raises the
+// reference's message for the first broken rule.  bound = (fn, plan,
+// key_pool, value_pool, out, out_s0, out_s1, dtype object, device index,
+// element size, tokens, query heads, kv heads, head size, raw-stream
+// getter), made once per layer and step.
+// ---------------------------------------------------------------------------
+constexpr long kNotFast = 1 << 30;
+PyObject* g_str_dtype = nullptr;
+PyObject* g_str_get_device = nullptr;
+PyObject* g_str_shape = nullptr;
+PyObject* g_str_stride = nullptr;
+PyObject* g_str_data_ptr = nullptr;
+
+// 1: the tensor fits (facts filled), 0: it does not, -1: a Python error.
+int tensor_facts(PyObject* t, PyObject* dtype, long device, int64_t n0, int64_t n1, int64_t n2, int64_t es,
+                 int64_t* ptr, int64_t* s0, int64_t* s1) {
+  PyObject* dt = PyObject_GetAttr(t, g_str_dtype);
+  if (dt == nullptr) return -1;
+  const bool same_dtype = dt == dtype;
+  Py_DECREF(dt);
+  if (!same_dtype) return 0;
+  PyObject* dev = PyObject_CallMethodNoArgs(t, g_str_get_device);
+  if (dev == nullptr) return -1;
+  const long d = PyLong_AsLong(dev);
+  Py_DECREF(dev);
+  if (d == -1 && PyErr_Occurred()) return -1;
+  if (d != device) return 0;
+  PyObject* shape = PyObject_GetAttr(t, g_str_shape);
+  if (shape == nullptr) return -1;
+  bool fits = PyTuple_Check(shape) && PyTuple_GET_SIZE(shape) == 3;
+  if (fits) {
+    const int64_t want[3] = {n0, n1, n2};
+    for (int i = 0; i < 3 && fits; ++i) fits = PyLong_AsLongLong(PyTuple_GET_ITEM(shape, i)) == want[i];
+  }
+  Py_DECREF(shape);
+  if (PyErr_Occurred()) return -1;
+  if (!fits) return 0;
+  PyObject* stride = PyObject_CallMethodNoArgs(t, g_str_stride);
+  if (stride == nullptr) return -1;
+  int64_t st[3] = {0, 0, 0};
+  fits = PyTuple_Check(stride) && PyTuple_GET_SIZE(stride) == 3;
+  for (int i = 0; i < 3 && fits; ++i) st[i] = PyLong_AsLongLong(PyTuple_GET_ITEM(stride, i));
+  Py_DECREF(stride);
+  if (PyErr_Occurred()) return -1;
+  if (!fits || st[2] != 1 || ((st[0] * es) & 15) || ((st[1] * es) & 15)) return 0;
+  PyObject* dp = PyObject_CallMethodNoArgs(t, g_str_data_ptr);
+  if (dp == nullptr) return -1;
+  const int64_t p = PyLong_AsLongLong(dp);
+  Py_DECREF(dp);
+  if (PyErr_Occurred()) return -1;
+  if (p & 15) return 0;
+  *ptr = p;
+  *s0 = st[0];
+  *s1 = st[1];
+  return 1;
+}
+
+PyObject* attend_tensors(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (!want_args(nargs, 5, "attend_tensors")) return nullptr;
+  PyObject* b = args[0];
+  if (!PyTuple_Check(b) || PyTuple_GET_SIZE(b) != 15) {
+    PyErr_SetString(PyExc_ValueError, "attend_tensors: bound facts must be a 15-tuple");
+    return nullptr;
+  }
+  int64_t f[15];
+  for (int i = 0; i < 15; ++i) {
+    if (i == 7 || i == 14) continue;
+    f[i] = (int64_t)PyLong_AsLongLong(PyTuple_GET_ITEM(b, i));
+  }
+  if (PyErr_Occurred()) return nullptr;
+  PyObject* dtype = PyTuple_GET_ITEM(b, 7);
+  const long device = (long)f[8];
+  const int64_t es = f[9], tokens = f[10], hq = f[11], hkv = f[12], d = f[13];
+  int64_t qp, qs0, qs1, kp, ks0, ks1, vp, vs0, vs1;
+  int r = tensor_facts(args[1], dtype, device, tokens, hq, d, es, &qp, &qs0, &qs1);
+  if (r == 1) r = tensor_facts(args[2], dtype, device, tokens, hkv, d, es, &kp, &ks0, &ks1);
+  if (r == 1) r = tensor_facts(args[3], dtype, device, tokens, hkv, d, es, &vp, &vs0, &vs1);
+  if (r < 0) return nullptr;
+  if (r == 0) return PyLong_FromLong(kNotFast);
+  const double scale = PyFloat_AsDouble(args[4]);
+  if (PyErr_Occurred()) return nullptr;
+  PyObject* dev = PyLong_FromLong(device);
+  if (dev == nullptr) return nullptr;
+  PyObject* stream = PyObject_CallOneArg(PyTuple_GET_ITEM(b, 14), dev);
+  Py_DECREF(dev);
+  if (stream == nullptr) return nullptr;
+  const int64_t sp = PyLong_AsLongLong(stream);
+  Py_DECREF(stream);
+  if (PyErr_Occurred()) return nullptr;
+  if (f[0] == 0 || f[1] == 0) {
+    PyErr_SetString(PyExc_ValueError, "attend_tensors: null function or plan");
+    return nullptr;
+  }
+  auto ptr = [](int64_t v) { return reinterpret_cast<void*>((intptr_t)v); };
+  const AttendFn fn = reinterpret_cast<AttendFn>((intptr_t)f[0]);
+  const int status = fn(ptr(f[1]), ptr(qp), qs0, qs1, ptr(kp), ks0, ks1, ptr(vp), vs0, vs1, ptr(f[2]), ptr(f[3]),
+                        ptr(f[4]), f[5], f[6], (float)scale, ptr(sp));
+  return PyLong_FromLong(status);
+}
+
 PyMethodDef kMethods[] = {
     {"flatten", (PyCFunction)(void (*)(void))flatten, METH_FASTCALL, "int sequences -> (flat, counts int64, status)"},
     {"validate", (PyCFunction)(void (*)(void))validate, METH_FASTCALL, "block-table rules -> (rule, request)"},
@@ -2100,6 +2207,8 @@ PyMethodDef kMethods[] = {
     {"counts", (PyCFunction)(void (*)(void))counts, METH_FASTCALL, "how the planner's calls were served"},
     {"compact_pairs", (PyCFunction)(void (*)(void))compact_pairs, METH_FASTCALL, "compact rules and moved slot pairs"},
     {"attend", (PyCFunction)(void (*)(void))attend, METH_FASTCALL, "one layer's lvamd_paged_attention call"},
+    {"attend_tensors", (PyCFunction)(void (*)(void))attend_tensors, METH_FASTCALL,
+     "forward's fast path: tensor rules and the lvamd_paged_attention call"},
     {nullptr, nullptr, 0, nullptr},
 };
 
@@ -2111,6 +2220,12 @@ PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_lvamd_host", "Native host-side s
 PyMODINIT_FUNC PyInit__lvamd_host(void) {
   g_parent_indices = PyUnicode_InternFromString("parent_indices");
   if (g_parent_indices == nullptr) return nullptr;
+  g_str_dtype = PyUnicode_InternFromString("dtype");
+  g_str_get_device = PyUnicode_InternFromString("get_device");
+  g_str_shape = PyUnicode_InternFromString("shape");
+  g_str_stride = PyUnicode_InternFromString("stride");
+  g_str_data_ptr = PyUnicode_InternFromString("data_ptr");
+  if (!g_str_dtype || !g_str_get_device || !g_str_shape || !g_str_stride || !g_str_data_ptr) return nullptr;
   static const char* kCompactKeys[6] = {"block_ids", "num_computed_tokens", "num_query_tokens",
                                         "num_reserved_query_tokens", "num_readonly_prefix_blocks",
                                         "retained_query_indices"};

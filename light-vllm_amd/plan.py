@@ -40,6 +40,11 @@ from light_vllm_amd.facts import TABLE_RULES, StepFacts, facts_of
 # prefill kernel when it covers the layer's shape, whose waves share each
 # K/V tile.
 DECODE_MAX_COLUMNS = 16
+# Fewest decode tiles per stream-K share: small steps are spread over more
+# waves down to this (C1, 4 sequences of 38-512 tokens in fp32: 15.5 us per
+# step at four tiles per share, 12.3 at two, 12.8 at one); steps that fill
+# the resident waves are not affected.
+DECODE_MIN_UNITS_PER_WAVE = 2
 # Smallest key range (in prefill key tiles) the planner gives one prefill
 # workgroup when it splits units to fill the GPU.
 PREFILL_MIN_TILES = 4
@@ -569,7 +574,8 @@ class StepPlan:
         if max_cols == 0 or bool(np.any(q_cols <= max_cols)):
             max_units = max(1, self.partition_tokens // unit_tokens) if self.partition_tokens else 0
             dec = host.decode_work(self._req_meta, self.facts.flat, group, col_tiles, max_cols, num_kv_heads,
-                                   resident_waves, self.block_size, 4, max_units, unit_tokens, split_groups,
+                                   resident_waves, self.block_size, DECODE_MIN_UNITS_PER_WAVE, max_units,
+                                   unit_tokens, split_groups,
                                    split_waves)
         if max_cols and bool(np.any(q_cols > max_cols)):
             slots_per_head = prefill_resident // num_kv_heads if prefill_resident else 0

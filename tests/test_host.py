@@ -1237,3 +1237,65 @@ def test_ordered_groups_refuses_unsafe_orders() -> None:
     n = ORDERED_MAX_PAIRS + 1
     assert ordered_groups(i64(n), np.arange(100, 100 + n), np.arange(n)) is None
     assert ordered_groups(i64(n - 1), np.arange(100, 99 + n), np.arange(n - 1)) is not None
+
+
+_ATTEND_FN = ctypes.CFUNCTYPE(
+    ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+    ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+    ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p,
+)
+
+
+def test_attend_tensors_passes_the_tensors_and_refuses_what_the_fast_path_cannot_take() -> None:
+    """forward's native fast path (the host module's attend_tensors), with a
+    recording stand-in for lvamd_paged_attention: every pointer, stride,
+    scale and stream arrives as given; each broken rule returns the
+    not-fast code without calling it, and a library status comes back."""
+
+    calls = []
+
+    def record(*args):
+        calls.append(args)
+        return -7 if len(calls) == 3 else 0
+
+    fn = _ATTEND_FN(record)
+    fn_addr = ctypes.cast(fn, ctypes.c_void_p).value
+    host = native.host()
+    not_fast = 1 << 30
+    tokens, hq, hkv, d = 5, 8, 2, 64
+    dt = torch.bfloat16
+    q = torch.zeros((tokens, hq, d), dtype=dt)
+    k = torch.zeros((tokens, hkv, d), dtype=dt)
+    v = torch.zeros((tokens, hkv, d), dtype=dt)
+    bound = (fn_addr, 0x1000, 0x2000, 0x3000, 0x4000, hq * d, d, dt, -1, 2, tokens, hq, hkv, d, lambda dev: 0x5000 + dev)
+    assert host.attend_tensors(bound, q, k, v, 0.125) == 0
+    got = calls[-1]
+    assert got[0] == 0x1000 and got[1] == q.data_ptr() and got[2:4] == (hq * d, d)
+    assert got[4] == k.data_ptr() and got[5:7] == (hkv * d, d) and got[7] == v.data_ptr() and got[8:10] == (hkv * d, d)
+    assert got[10:13] == (0x2000, 0x3000, 0x4000) and got[13:15] == (hq * d, d)
+    assert got[15] == pytest.approx(0.125) and got[16] == 0x5000 - 1
+    # Strided rows (a view of a wider buffer) are taken as they are.
+    wide = torch.zeros((tokens, hq + 8, d), dtype=dt)[:, 4 : 4 + hq]
+    assert host.attend_tensors(bound, wide, k, v, 0.5) == 0 and calls[-1][1] == wide.data_ptr()
+    assert calls[-1][2:4] == ((hq + 8) * d, d)
+    # A library status comes back unchanged.
+    assert host.attend_tensors(bound, q, k, v, 0.5) == -7
+    n = len(calls)
+    refused = [
+        (q.float(), k, v),                                     # dtype
+        (q[:, :, :32], k, v),                                  # shape
+        (q, k[:4], v),                                         # tokens
+        (q.transpose(1, 2).contiguous().transpose(1, 2), k, v),  # last dim not contiguous
+        (torch.zeros(tokens * hq * d + 1, dtype=dt)[1:].view(tokens, hq, d), k, v),  # 2-byte offset: unaligned
+    ]
+    padded = (q, k, torch.zeros((tokens, hkv, d + 8), dtype=dt)[:, :, :d])  # 144-byte rows: still 16-byte aligned
+    for args in refused:
+        assert host.attend_tensors(bound, *args, 0.5) == not_fast
+    assert len(calls) == n
+    assert host.attend_tensors(bound, *padded, 0.5) == 0
+    odd = torch.zeros((tokens, hkv, d + 1), dtype=dt)[:, :, :d]  # 130-byte rows: not 16-byte aligned
+    assert host.attend_tensors(bound, q, k, odd, 0.5) == not_fast
+    other_device = bound[:8] + (0,) + bound[9:]
+    assert host.attend_tensors(other_device, q, k, v, 0.5) == not_fast
+    with pytest.raises(ValueError):
+        host.attend_tensors(bound[:14], q, k, v, 0.5)
