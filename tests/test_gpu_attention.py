@@ -478,3 +478,27 @@ def test_unbuilt_head_sizes_are_refused_when_the_step_starts(head_size) -> None:
                                    query_layouts=(lv.linear_query_layout(1),))
     with pytest.raises(lv.KVCacheError, match=f"not {head_size}"):
         lv.HipPagedAttentionBackend().create(cache, md)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ("bf16", "fp16"))
+@pytest.mark.parametrize("bs", (1, 3, 12, 16, 32))
+@pytest.mark.parametrize("partition", (None, 32))
+def test_line_order_decode_tiles_at_every_row_offset(dtype, bs, partition) -> None:
+    """The stream-K decode kernel's line-order tiles (16-bit pools, head size
+    128): contexts that end at every row of a 32-token tile (a piece's last
+    rows repeat its last key, masked), a fresh token landing on each row of
+    its tile (the fused append writes it from the line-order registers), and
+    one-tile shares (partition 32) so that pieces start and end inside
+    segments.  Outputs against the oracle, pool slots bit for bit."""
+
+    _announce(f"line-order decode {dtype} bs {bs} partition {partition}")
+    computed = [0, 1, 2, 3, 4, 5, 15, 16, 17, 30, 31, 32, 33, 63, 64, 65, 100, 255, 300]
+    step = make_step(hq=28, hkv=4, d=128, bs=bs, dtype=DTYPES[dtype], computed=computed,
+                     layouts=_lin(*([1] * len(computed))), seed=4100 + bs)
+    backend = lv.HipPagedAttentionBackend(partition_tokens=partition, decode_workgroups=False)
+    _, ctx = _run_and_check(step, backend=backend)
+    work = ctx.work_of(step.cache.layer_spec(step.layer_ids[0]))
+    assert work.group_waves == 1 and work.col_tiles == 1  # the stream-K kernel, one column tile
+    if partition:
+        assert work.units_per_wave == 1
