@@ -198,7 +198,6 @@ class _LayerStatic:
         self.element_size = config.dtype.itemsize
 
 
-_UNBOUND = object()
 _NOT_FAST = 1 << 30  # attend_tensors: a tensor rule of the fast path does not hold
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 _NO_APPEND = (None, 0, 0, None, 0, 0)
@@ -219,9 +218,11 @@ class HipPagedAttention:
         self._layer_ids: set[str] = set()
         self._plan = plan
         self._lib = native.load()
-        self._bound: dict[str, tuple | None] = {}
-        self._outputs: dict[tuple, tuple] = {}
-        self._launches_held: list = []
+        # The fast forward's facts: per layer the cache's fixed ones (pools,
+        # shape, place among the layers of its shape), per layer shape this
+        # step's (bound plan, output slab), bound at the shape's first layer.
+        self._statics = backend.layer_statics(cache) if _raw_stream is not None else {}
+        self._shape_bound: dict[tuple, tuple] = {}
         self._attend_tensors = native.host().attend_tensors
         self._attend_fn = native.attention_entry()
 
@@ -251,51 +252,47 @@ class HipPagedAttention:
         # The common case in one native call (the host module's
         # attend_tensors): it reads the tensors' dtype, device, shapes,
         # strides and pointers, and launches when every rule holds (the
-        # layer's bound shapes, dtype and device, 16-byte rows); anything
-        # else, and rotary, takes the general path, which raises the first
-        # broken rule's message.
-        bound = self._bound.get(layer_id, _UNBOUND)
-        if bound is _UNBOUND:
-            bound = self._bind(layer_id)
-        if bound is not None and rotary is None:
-            status = self._attend_tensors(bound[0], query, key, value, scale)
+        # layer's shapes, dtype and device, 16-byte rows); anything else, and
+        # rotary, takes the general path, which raises the first broken
+        # rule's message.
+        static = self._statics.get(layer_id)
+        if static is not None and rotary is None:
+            bound = self._shape_bound.get(static.shape)
+            if bound is None:
+                bound = self._bind_shape(static)
+            index = static.index
+            status = self._attend_tensors(bound[0], static.k_pool, static.v_pool, bound[1] + index * bound[2],
+                                          query, key, value, scale)
             if status == 0:
-                return bound[1]
+                return bound[3][index]
             if status != _NOT_FAST:
                 native.check(status, "lvamd_paged_attention")
         return self._forward_general(layer_id, query, key, value, scale=scale, rotary=rotary)
 
-    def _bind(self, layer_id: str) -> tuple | None:
-        """The fast path's facts for one layer in this step (None when it
-        must take the general path: a cache off the GPU, an unknown layer,
-        an unsupported head size): the tensor shapes, dtype and device it
-        accepts, its shape's bound plan, its pools and its output.
+    def _bind_shape(self, static) -> tuple:
+        """The fast path's facts for the layers of one shape in this step:
+        (the shape's facts for attend_tensors, the output slab's address,
+        its bytes per layer, the per-layer output views).
 
         Outputs are views of one tensor per layer shape and step, made at the
         first layer of that shape (one allocation for the step's layers in
-        place of one per layer); each layer's view is its own rows."""
+        place of one per layer); each layer's view is its own rows.  The
+        bound launch stays alive with the context."""
 
-        found = self._backend.layer_statics(self._cache).get(layer_id) if self._config.device.type == "cuda" else None
-        if found is None or _raw_stream is None:
-            self._bound[layer_id] = None
-            return None
-        spec = found.spec
+        spec = static.spec
         launch = self._launch(spec)
-        views = self._outputs.get(found.shape)
         tokens = self._plan.num_tokens
-        if views is None:
-            count = self._backend.shape_counts(self._cache)[found.shape]
-            slab = torch.empty((count, tokens, spec.num_query_heads, spec.head_size), dtype=found.dtype,
-                               device=found.device)
-            views = self._outputs[found.shape] = slab.unbind(0)
-        out = views[found.index]
+        count = self._backend.shape_counts(self._cache)[static.shape]
+        slab = torch.empty((count, tokens, spec.num_query_heads, spec.head_size), dtype=static.dtype,
+                           device=static.device)
         facts = (
-            self._attend_fn, launch.plan_ptr, found.k_pool, found.v_pool, out.data_ptr(),
-            spec.num_query_heads * spec.head_size, spec.head_size, found.dtype, found.device_index,
-            found.element_size, tokens, spec.num_query_heads, spec.num_kv_heads, spec.head_size, _raw_stream,
+            self._attend_fn, launch.plan_ptr, spec.num_query_heads * spec.head_size, spec.head_size, static.dtype,
+            static.device_index, static.element_size, tokens, spec.num_query_heads, spec.num_kv_heads,
+            spec.head_size, _raw_stream,
         )
-        bound = self._bound[layer_id] = (facts, out)
-        self._launches_held.append(launch)  # the bound plan structure stays alive with the context
+        bound = (facts, slab.data_ptr(), tokens * spec.num_query_heads * spec.head_size * static.element_size,
+                 slab.unbind(0), launch)
+        self._shape_bound[static.shape] = bound
         return bound
 
     def _forward_general(self, layer_id: str, query: Tensor, key: Tensor, value: Tensor, *, scale: float,

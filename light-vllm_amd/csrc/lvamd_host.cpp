@@ -2088,17 +2088,18 @@ PyObject* attend(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
 }
 
 // ---------------------------------------------------------------------------
-// attend_tensors(bound, q, k, v, scale) -> status, or kNotFast
+// attend_tensors(shape, key_pool, value_pool, out, q, k, v, scale) -> status,
+// or kNotFast
 //
 // forward's common case in one call: reads each tensor's dtype, device,
 // shape, strides and data pointer itself and, when every rule of the fast
-// path holds (the layer's bound shapes, its dtype and device, contiguous
-// 16-byte rows), calls lvamd_paged_attention.  Any other tensor returns
-// kNotFast and the caller takes its general path, which raises the
-// reference's message for the first broken rule.  bound = (fn, plan,
-// key_pool, value_pool, out, out_s0, out_s1, dtype object, device index,
-// element size, tokens, query heads, kv heads, head size, raw-stream
-// getter), made once per layer and step.
+// path holds (the layer's shapes, its dtype and device, contiguous 16-byte
+// rows), calls lvamd_paged_attention.  Any other tensor returns kNotFast and
+// the caller takes its general path, which raises the reference's message
+// for the first broken rule.  shape = (fn, plan, out_s0, out_s1, dtype
+// object, device index, element size, tokens, query heads, kv heads, head
+// size, raw-stream getter), made once per layer shape and step; the pools
+// are the layer's (fixed for a cache) and out its output rows.
 // ---------------------------------------------------------------------------
 constexpr long kNotFast = 1 << 30;
 PyObject* g_str_dtype = nullptr;
@@ -2152,32 +2153,35 @@ int tensor_facts(PyObject* t, PyObject* dtype, long device, int64_t n0, int64_t 
 }
 
 PyObject* attend_tensors(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
-  if (!want_args(nargs, 5, "attend_tensors")) return nullptr;
+  if (!want_args(nargs, 8, "attend_tensors")) return nullptr;
   PyObject* b = args[0];
-  if (!PyTuple_Check(b) || PyTuple_GET_SIZE(b) != 15) {
-    PyErr_SetString(PyExc_ValueError, "attend_tensors: bound facts must be a 15-tuple");
+  if (!PyTuple_Check(b) || PyTuple_GET_SIZE(b) != 12) {
+    PyErr_SetString(PyExc_ValueError, "attend_tensors: shape facts must be a 12-tuple");
     return nullptr;
   }
-  int64_t f[15];
-  for (int i = 0; i < 15; ++i) {
-    if (i == 7 || i == 14) continue;
+  int64_t f[12];
+  for (int i = 0; i < 12; ++i) {
+    if (i == 4 || i == 11) continue;
     f[i] = (int64_t)PyLong_AsLongLong(PyTuple_GET_ITEM(b, i));
   }
+  const int64_t k_pool = (int64_t)PyLong_AsLongLong(args[1]);
+  const int64_t v_pool = (int64_t)PyLong_AsLongLong(args[2]);
+  const int64_t out = (int64_t)PyLong_AsLongLong(args[3]);
   if (PyErr_Occurred()) return nullptr;
-  PyObject* dtype = PyTuple_GET_ITEM(b, 7);
-  const long device = (long)f[8];
-  const int64_t es = f[9], tokens = f[10], hq = f[11], hkv = f[12], d = f[13];
+  PyObject* dtype = PyTuple_GET_ITEM(b, 4);
+  const long device = (long)f[5];
+  const int64_t es = f[6], tokens = f[7], hq = f[8], hkv = f[9], d = f[10];
   int64_t qp, qs0, qs1, kp, ks0, ks1, vp, vs0, vs1;
-  int r = tensor_facts(args[1], dtype, device, tokens, hq, d, es, &qp, &qs0, &qs1);
-  if (r == 1) r = tensor_facts(args[2], dtype, device, tokens, hkv, d, es, &kp, &ks0, &ks1);
-  if (r == 1) r = tensor_facts(args[3], dtype, device, tokens, hkv, d, es, &vp, &vs0, &vs1);
+  int r = tensor_facts(args[4], dtype, device, tokens, hq, d, es, &qp, &qs0, &qs1);
+  if (r == 1) r = tensor_facts(args[5], dtype, device, tokens, hkv, d, es, &kp, &ks0, &ks1);
+  if (r == 1) r = tensor_facts(args[6], dtype, device, tokens, hkv, d, es, &vp, &vs0, &vs1);
   if (r < 0) return nullptr;
   if (r == 0) return PyLong_FromLong(kNotFast);
-  const double scale = PyFloat_AsDouble(args[4]);
+  const double scale = PyFloat_AsDouble(args[7]);
   if (PyErr_Occurred()) return nullptr;
   PyObject* dev = PyLong_FromLong(device);
   if (dev == nullptr) return nullptr;
-  PyObject* stream = PyObject_CallOneArg(PyTuple_GET_ITEM(b, 14), dev);
+  PyObject* stream = PyObject_CallOneArg(PyTuple_GET_ITEM(b, 11), dev);
   Py_DECREF(dev);
   if (stream == nullptr) return nullptr;
   const int64_t sp = PyLong_AsLongLong(stream);
@@ -2189,8 +2193,8 @@ PyObject* attend_tensors(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   }
   auto ptr = [](int64_t v) { return reinterpret_cast<void*>((intptr_t)v); };
   const AttendFn fn = reinterpret_cast<AttendFn>((intptr_t)f[0]);
-  const int status = fn(ptr(f[1]), ptr(qp), qs0, qs1, ptr(kp), ks0, ks1, ptr(vp), vs0, vs1, ptr(f[2]), ptr(f[3]),
-                        ptr(f[4]), f[5], f[6], (float)scale, ptr(sp));
+  const int status = fn(ptr(f[1]), ptr(qp), qs0, qs1, ptr(kp), ks0, ks1, ptr(vp), vs0, vs1, ptr(k_pool), ptr(v_pool),
+                        ptr(out), f[2], f[3], (float)scale, ptr(sp));
   return PyLong_FromLong(status);
 }
 

@@ -128,7 +128,7 @@ def test_backend_sites_raise_the_host_class(host_classes) -> None:
     cache = SimpleNamespace(config=lv.PagedKVCacheConfig(num_blocks=4, block_size=2),
                             layer_spec=lambda layer_id: spec)
     ctx = HipPagedAttention.__new__(HipPagedAttention)
-    ctx._cache, ctx._config, ctx._layer_ids, ctx._bound = cache, cache.config, set(), {}
+    ctx._cache, ctx._config, ctx._layer_ids, ctx._statics = cache, cache.config, set(), {}
     ctx._plan = SimpleNamespace(num_query_tokens=1)
     q, kv = torch.zeros(1, 4, 64), torch.zeros(1, 2, 64)
     with pytest.raises(HostKVCacheError, match="three dimensions"):

@@ -1249,8 +1249,9 @@ _ATTEND_FN = ctypes.CFUNCTYPE(
 def test_attend_tensors_passes_the_tensors_and_refuses_what_the_fast_path_cannot_take() -> None:
     """forward's native fast path (the host module's attend_tensors), with a
     recording stand-in for lvamd_paged_attention: every pointer, stride,
-    scale and stream arrives as given; each broken rule returns the
-    not-fast code without calling it, and a library status comes back."""
+    scale and stream arrives as given (the layer's pools and output rows
+    apart from the shape's facts); each broken rule returns the not-fast
+    code without calling it, and a library status comes back."""
 
     calls = []
 
@@ -1267,19 +1268,22 @@ def test_attend_tensors_passes_the_tensors_and_refuses_what_the_fast_path_cannot
     q = torch.zeros((tokens, hq, d), dtype=dt)
     k = torch.zeros((tokens, hkv, d), dtype=dt)
     v = torch.zeros((tokens, hkv, d), dtype=dt)
-    bound = (fn_addr, 0x1000, 0x2000, 0x3000, 0x4000, hq * d, d, dt, -1, 2, tokens, hq, hkv, d, lambda dev: 0x5000 + dev)
-    assert host.attend_tensors(bound, q, k, v, 0.125) == 0
+    shape = (fn_addr, 0x1000, hq * d, d, dt, -1, 2, tokens, hq, hkv, d, lambda dev: 0x5000 + dev)
+    pools = (0x2000, 0x3000)
+    assert host.attend_tensors(shape, *pools, 0x4000, q, k, v, 0.125) == 0
     got = calls[-1]
     assert got[0] == 0x1000 and got[1] == q.data_ptr() and got[2:4] == (hq * d, d)
     assert got[4] == k.data_ptr() and got[5:7] == (hkv * d, d) and got[7] == v.data_ptr() and got[8:10] == (hkv * d, d)
     assert got[10:13] == (0x2000, 0x3000, 0x4000) and got[13:15] == (hq * d, d)
     assert got[15] == pytest.approx(0.125) and got[16] == 0x5000 - 1
+    # Another layer of the shape: its own pools and output rows.
+    assert host.attend_tensors(shape, 0x6000, 0x7000, 0x8000, q, k, v, 0.125) == 0
+    assert calls[-1][10:13] == (0x6000, 0x7000, 0x8000) and calls[-1][0] == 0x1000
     # Strided rows (a view of a wider buffer) are taken as they are.
     wide = torch.zeros((tokens, hq + 8, d), dtype=dt)[:, 4 : 4 + hq]
-    assert host.attend_tensors(bound, wide, k, v, 0.5) == 0 and calls[-1][1] == wide.data_ptr()
+    # A library status comes back unchanged (the third call returns -7).
+    assert host.attend_tensors(shape, *pools, 0x4000, wide, k, v, 0.5) == -7 and calls[-1][1] == wide.data_ptr()
     assert calls[-1][2:4] == ((hq + 8) * d, d)
-    # A library status comes back unchanged.
-    assert host.attend_tensors(bound, q, k, v, 0.5) == -7
     n = len(calls)
     refused = [
         (q.float(), k, v),                                     # dtype
@@ -1290,12 +1294,12 @@ def test_attend_tensors_passes_the_tensors_and_refuses_what_the_fast_path_cannot
     ]
     padded = (q, k, torch.zeros((tokens, hkv, d + 8), dtype=dt)[:, :, :d])  # 144-byte rows: still 16-byte aligned
     for args in refused:
-        assert host.attend_tensors(bound, *args, 0.5) == not_fast
+        assert host.attend_tensors(shape, *pools, 0x4000, *args, 0.5) == not_fast
     assert len(calls) == n
-    assert host.attend_tensors(bound, *padded, 0.5) == 0
+    assert host.attend_tensors(shape, *pools, 0x4000, *padded, 0.5) == 0
     odd = torch.zeros((tokens, hkv, d + 1), dtype=dt)[:, :, :d]  # 130-byte rows: not 16-byte aligned
-    assert host.attend_tensors(bound, q, k, odd, 0.5) == not_fast
-    other_device = bound[:8] + (0,) + bound[9:]
-    assert host.attend_tensors(other_device, q, k, v, 0.5) == not_fast
+    assert host.attend_tensors(shape, *pools, 0x4000, q, k, odd, 0.5) == not_fast
+    other_device = shape[:5] + (0,) + shape[6:]
+    assert host.attend_tensors(other_device, *pools, 0x4000, q, k, v, 0.5) == not_fast
     with pytest.raises(ValueError):
-        host.attend_tensors(bound[:14], q, k, v, 0.5)
+        host.attend_tensors(shape[:11], *pools, 0x4000, q, k, v, 0.5)
