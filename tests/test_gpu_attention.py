@@ -413,6 +413,66 @@ def test_one_metadata_on_caches_of_two_dtypes() -> None:
         assert mx <= max_tol and mean <= mean_tol, (s.query.dtype, mx, mean)
 
 
+def test_layers_of_two_shapes_alternating_in_one_cache() -> None:
+    # forward binds the fast path once per layer shape and step (plan and
+    # output slab) and passes each layer's pools and output rows on their
+    # own: layers of two shapes, interleaved, each match the oracle; the
+    # outputs are distinct rows, later layers leave earlier outputs alone,
+    # and a second step on the same metadata (the plan reused, new slabs)
+    # leaves the first step's outputs alone too.
+    _announce("two layer shapes, alternating")
+    base = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[700, 40, 1500, 0],
+                     layouts=_lin(1, 9, 1, 33), seed=401)
+    config = base.cache.config
+    shapes = {"a0": (28, 4, 128), "b0": (12, 2, 64), "a1": (28, 4, 128), "b1": (12, 2, 64)}
+    spec = lv.ModelKVCacheSpec(tuple(lv.AttentionLayerSpec(lid, *shape) for lid, shape in shapes.items()))
+    cache = lv.PagedKVCache(spec, lv.PagedKVCacheConfig(num_blocks=config.num_blocks, block_size=config.block_size,
+                                                        dtype=config.dtype, device=DEV))
+    gen = torch.Generator(device=DEV).manual_seed(402)
+    for lid in shapes:
+        layer = cache.layer(lid)
+        layer.keys.copy_(torch.randn(layer.keys.shape, generator=gen, device=DEV).to(config.dtype))
+        layer.values.copy_(torch.randn(layer.values.shape, generator=gen, device=DEV).to(config.dtype))
+    t = base.query.shape[0]
+
+    def inputs(lid):
+        hq, hkv, d = shapes[lid]
+        q = torch.randn((t, hq, d), generator=gen, device=DEV).to(config.dtype)
+        k = torch.randn((t, hkv, d), generator=gen, device=DEV).to(config.dtype)
+        v = torch.randn((t, hkv, d), generator=gen, device=DEV).to(config.dtype)
+        return q, k, v, 1.0 / float(np.sqrt(d))
+
+    step_inputs = {lid: inputs(lid) for lid in shapes}
+    backend = lv.HipPagedAttentionBackend()
+    ctx = backend.create(cache, base.metadata)
+    outs = {lid: ctx.forward(lid, *step_inputs[lid][:3], scale=step_inputs[lid][3]) for lid in shapes}
+    torch.cuda.synchronize()
+    assert len({o.data_ptr() for o in outs.values()}) == len(outs)
+    max_tol, mean_tol = tolerances(config.dtype)
+    first = {}
+    for lid, out in outs.items():
+        q, k, v, scale = step_inputs[lid]
+        assert out.shape == q.shape and out.dtype == q.dtype
+        check = type(base)(cache, base.metadata, q, k, v, (lid,), scale)
+        mx, mean = _forward_error(check, lid, out)
+        assert mx <= max_tol and mean <= mean_tol, (lid, mx, mean)
+        first[lid] = out.clone()
+    # The same step again (same K/V, new queries): new outputs, old ones kept.
+    ctx2 = backend.create(cache, base.metadata)
+    again = {}
+    for lid in shapes:
+        q, k, v, scale = step_inputs[lid]
+        again[lid] = ctx2.forward(lid, -q, k, v, scale=scale)
+    torch.cuda.synchronize()
+    for lid in shapes:
+        assert torch.equal(outs[lid], first[lid]), lid
+        assert again[lid].data_ptr() != outs[lid].data_ptr()
+        q, k, v, scale = step_inputs[lid]
+        check = type(base)(cache, base.metadata, -q, k, v, (lid,), scale)
+        mx, mean = _forward_error(check, lid, again[lid])
+        assert mx <= max_tol and mean <= mean_tol, (lid, mx, mean)
+
+
 # ------------------------------------------------------ workgroup split (latency-bound decode)
 @pytest.mark.parametrize("dtype", ("fp32", "fp16", "bf16"))
 @pytest.mark.parametrize("head_size", (32, 64, 80, 96, 128, 256))
