@@ -387,13 +387,13 @@ def kv_move_sweep(args, device: torch.device) -> int:
     # workspace already on the GPU, so the sweep times the kernels and not
     # the host-side validation and list conversion of the Python entry points.
     lib = native.load()
-    _, num_layers, ptrs = _layer_pointers(cache).groups[0]
+    _, num_layers, _, kptrs, vptrs = _layer_pointers(cache).groups[0]
     for n in (32, 256, 2048, 8192):
         blocks = torch.from_numpy(rng.permutation(nb)[: 2 * n].astype(np.int64)).to(device)
 
         def block_copy(i: int) -> None:
             native.check(lib.lvamd_kv_block_copy(
-                ptrs[0].data_ptr(), ptrs[1].data_ptr(), num_layers, row * bs, blocks[:n].data_ptr(),
+                kptrs, vptrs, num_layers, row * bs, blocks[:n].data_ptr(),
                 blocks[n:].data_ptr(), n, current_stream(device)), "lvamd_kv_block_copy")
 
         ms = _time_launches(block_copy, 20, 3, device, batch=5)
@@ -406,13 +406,30 @@ def kv_move_sweep(args, device: torch.device) -> int:
 
         def compact(i: int) -> None:
             native.check(lib.lvamd_kv_compact(
-                ptrs[0].data_ptr(), ptrs[1].data_ptr(), num_layers, row, slots[:n].data_ptr(),
+                kptrs, vptrs, num_layers, row, slots[:n].data_ptr(),
                 slots[n:].data_ptr(), n, ws.data_ptr() if ws_bytes else None, ws_bytes,
                 current_stream(device)), "lvamd_kv_compact")
 
         ms = _time_launches(compact, 20, 3, device, batch=5)
         moved = 2 * n * layers * 2 * row
         out["compact"].append({"rows": n, "us": round(ms * 1e3, 2), "GBps": round(moved / (ms * 1e-3) / 1e9, 1)})
+    # The one-pass compact for ordered pair lists (groups of eight pairs, as a
+    # step's accepted tree paths give; distinct slots satisfy its rules).
+    out["compact_ordered"] = []
+    for n in (128, 1024, 8192):
+        slots = torch.from_numpy(rng.permutation(nb * bs)[: 2 * n].astype(np.int64)).to(device)
+        starts = torch.arange(0, n + 1, 8, dtype=torch.int64, device=device)
+
+        def compact_ordered(i: int) -> None:
+            native.check(lib.lvamd_kv_compact_ordered(
+                kptrs, vptrs, num_layers, row, slots[:n].data_ptr(),
+                slots[n:].data_ptr(), starts.data_ptr(), starts.numel() - 1, current_stream(device)),
+                "lvamd_kv_compact_ordered")
+
+        ms = _time_launches(compact_ordered, 20, 3, device, batch=5)
+        moved = 2 * n * layers * 2 * row
+        out["compact_ordered"].append({"rows": n, "us": round(ms * 1e3, 2),
+                                       "GBps": round(moved / (ms * 1e-3) / 1e9, 1)})
     # Append: one C2-shaped layer (4 KV heads, D 128, bf16, 1 GiB per pool),
     # T tokens to random distinct slots; bytes = 4 * T * Hkv * D * 2.
     out["append"] = []

@@ -310,8 +310,16 @@ struct OrderedCompactArgs {
   int64_t num_groups;
 };
 
+// V is the chunk type: the native 4 x u32 vector for 16-byte chunks (an
+// array of HIP's uint4 struct stayed in scratch memory, 272 bytes per lane,
+// and the scratch traffic made this one-pass kernel slower than the
+// two-phase one).  Eight 16-byte chunks per batch (sixteen narrower ones)
+// keep the batch in registers.  Every gather of a batch is issued (entries
+// past the group re-read its last source): conditional gathers into the
+// array also leave it in scratch.
 template <typename V>
 __global__ __launch_bounds__(256) void kv_compact_ordered_kernel(const OrderedCompactArgs a) {
+  constexpr int kBatch = sizeof(V) >= 16 ? kOrderedBatch / 2 : kOrderedBatch;
   const int64_t cpr = a.row_bytes / (int64_t)sizeof(V);
   const int64_t per_group = (int64_t)a.num_layers * 2 * cpr;
   const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -322,19 +330,17 @@ __global__ __launch_bounds__(256) void kv_compact_ordered_kernel(const OrderedCo
   const int64_t lk = r / cpr;  // layer * 2 + is_v
   char* base = reinterpret_cast<char*>((lk & 1) ? a.vptrs[lk >> 1] : a.kptrs[lk >> 1]);
   const int64_t p0 = a.group_starts[group], p1 = a.group_starts[group + 1];
-  for (int64_t b = p0; b < p1; b += kOrderedBatch) {
-    V tmp[kOrderedBatch];
-    // Every gather is issued (entries past the group re-read its last
-    // source) so the chunks stay in registers.
+  for (int64_t b = p0; b < p1; b += kBatch) {
+    V tmp[kBatch];
 #pragma unroll
-    for (int i = 0; i < kOrderedBatch; ++i) {
+    for (int i = 0; i < kBatch; ++i) {
       const int64_t p = b + i < p1 ? b + i : p1 - 1;
       tmp[i] = reinterpret_cast<const V*>(base + a.src[p] * a.row_bytes)[c];
     }
     // Every gather of the batch has landed before its first scatter.
     __threadfence_block();
 #pragma unroll
-    for (int i = 0; i < kOrderedBatch; ++i) {
+    for (int i = 0; i < kBatch; ++i) {
       if (b + i < p1) reinterpret_cast<V*>(base + a.dst[b + i] * a.row_bytes)[c] = tmp[i];
     }
     __threadfence_block();
@@ -666,8 +672,15 @@ int lvamd_kv_compact_ordered(const uint64_t* layer_key_ptrs, const uint64_t* lay
   while (width > 4 && num_groups * num_layers * 2 * (row_bytes / width) < 64 * 256) width /= 2;
   const int64_t items = num_groups * num_layers * 2 * (row_bytes / width);
   if ((items + 255) / 256 > 0x7fffffffLL) return LVAMD_ERR_INVALID_ARGUMENT;
-  LVAMD_LAUNCH_BY_WIDTH(kv_compact_ordered_kernel, width, dim3((unsigned)((items + 255) / 256)), dim3(256),
-                        static_cast<hipStream_t>(stream), a);
+  const dim3 grid((unsigned)((items + 255) / 256));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (width) {
+    case 16: hipLaunchKernelGGL(kv_compact_ordered_kernel<u32x4>, grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL(kv_compact_ordered_kernel<uint2>, grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(kv_compact_ordered_kernel<uint32_t>, grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(kv_compact_ordered_kernel<uint16_t>, grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(kv_compact_ordered_kernel<uint8_t>, grid, dim3(256), 0, s, a); break;
+  }
   return launch_status();
 }
 
