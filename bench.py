@@ -455,6 +455,69 @@ def kv_move_sweep(args, device: torch.device) -> int:
     return 0
 
 
+def head_size_sweep(args, device: torch.device) -> int:
+    """Decode bandwidth and prefill throughput per head size and dtype, one
+    layer of 28 Q / 4 KV heads, block 16, through the backend's forward (plan
+    reused, HIP events over 50 and 30 steps): decode at C2's batch shape (64
+    sequences, contexts U[512, 4096]), prefill as 4 causal chunks of 512
+    queries after 1024 tokens of history.  Pools hold N(0, 1) rows."""
+
+    def build(dtype, d, computed, q_lens, seed):
+        rng = np.random.default_rng(seed)
+        bs = 16
+        need = [(c + q + bs - 1) // bs for c, q in zip(computed, q_lens)]
+        nb = sum(need) + 16
+        perm = rng.permutation(nb)
+        tables, off = [], 0
+        for n in need:
+            tables.append(tuple(int(x) for x in perm[off : off + n]))
+            off += n
+        md = lv.PagedAttentionMetadata(block_tables=tuple(tables), num_computed_tokens=tuple(computed),
+                                       query_layouts=tuple(_linear(q) for q in q_lens))
+        spec = lv.ModelKVCacheSpec((lv.AttentionLayerSpec("l0", 28, 4, d),))
+        cache = lv.PagedKVCache(spec, lv.PagedKVCacheConfig(num_blocks=nb, block_size=bs, dtype=dtype, device=device))
+        gen = torch.Generator(device=device).manual_seed(seed)
+        for pool in (cache.layer("l0").keys, cache.layer("l0").values):
+            pool.copy_(torch.randn(pool.shape, generator=gen, device=device).to(dtype))
+        t = sum(q_lens)
+        qkv = [torch.randn((t, h, d), generator=gen, device=device).to(dtype) for h in (28, 4, 4)]
+        return cache, md, qkv
+
+    def step_us(cache, md, qkv, d, n):
+        backend = lv.HipPagedAttentionBackend()
+
+        def step(i: int) -> None:
+            backend.create(cache, md).forward("l0", *qkv, scale=1.0 / math.sqrt(d))
+
+        return _time_launches(step, n, 10, device, batch=n) * 1e3
+
+    out = {"mode": "head-sweep", "decode": [], "prefill": []}
+    ctx = [int(x) for x in np.random.default_rng(7).integers(512, 4097, size=64)]
+    for dtype, sizes in ((torch.bfloat16, (32, 64, 80, 96, 128, 256)), (torch.float16, (64, 128, 256)),
+                         (torch.float32, (32, 64, 128))):
+        for d in sizes:
+            cache, md, qkv = build(dtype, d, ctx, [1] * len(ctx), 11)
+            us = step_us(cache, md, qkv, d, 50)
+            nbytes = sum(c + 1 for c in ctx) * 2 * 4 * d * dtype.itemsize
+            out["decode"].append({"dtype": str(dtype).split(".")[-1], "head_size": d, "us": round(us, 2),
+                                  "pct_of_hbm_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1)})
+            del cache
+            torch.cuda.empty_cache()
+    for dtype, sizes in ((torch.bfloat16, (64, 80, 96, 128, 256)), (torch.float16, (128,))):
+        for d in sizes:
+            computed, q_lens = [1024] * 4, [512] * 4
+            cache, md, qkv = build(dtype, d, computed, q_lens, 12)
+            us = step_us(cache, md, qkv, d, 30)
+            pairs = sum(sum(c + j + 1 for j in range(q)) for c, q in zip(computed, q_lens))
+            tflops = 4 * 28 * d * pairs / (us * 1e-6) / 1e12
+            out["prefill"].append({"dtype": str(dtype).split(".")[-1], "head_size": d, "us": round(us, 2),
+                                   "pct_of_bf16_peak": round(100 * tflops / MFMA_BF16_PEAK_TFLOPS, 1)})
+            del cache
+            torch.cuda.empty_cache()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def copy_calibration(args, device: torch.device) -> int:
     """A plain device-to-device copy of 1 GiB: counter calibration and practical ceiling."""
 
@@ -1110,10 +1173,11 @@ def main() -> int:
                         help="skip the RoPE-fused step timing (keeps a kernel trace to the attention step)")
     parser.add_argument("--no-serving", action="store_true",
                         help="skip the serving-shaped 28-layer steps (keeps a kernel trace to the headline step)")
-    parser.add_argument("--mode", choices=("full", "decode", "copy", "kv-sweep"), default="full",
+    parser.add_argument("--mode", choices=("full", "decode", "copy", "kv-sweep", "head-sweep"), default="full",
                         help="decode: only the decode kernel (counter runs); copy: a plain 1 GiB device "
                              "copy of known size (counter calibration and the practical HBM ceiling); kv-sweep: "
-                             "block copy and compact bandwidth over sizes")
+                             "block copy and compact bandwidth over sizes; head-sweep: decode bandwidth and "
+                             "prefill throughput per head size and dtype")
     parser.add_argument("--partition", type=int, default=None,
                         help="cap on the tokens one decode wave handles (default: spread over all resident waves)")
     parser.add_argument("--col-tiles", type=int, choices=(1, 4), default=None,
@@ -1137,6 +1201,8 @@ def main() -> int:
         return copy_calibration(args, device)
     if args.mode == "kv-sweep":
         return kv_move_sweep(args, device)
+    if args.mode == "head-sweep":
+        return head_size_sweep(args, device)
     if args.config != "c2":
         return {"c1": run_c1, "c3": run_c3, "c4": run_c4, "c5": run_c5, "small": run_small}[args.config](args, device)
     print(f"[bench] building C2 workload, {args.sets} pool sets", file=sys.stderr, flush=True)
