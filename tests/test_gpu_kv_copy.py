@@ -241,23 +241,29 @@ def test_ordered_compact_is_one_pass_and_matches_the_oracle(dtype, bs, n_request
         np.testing.assert_array_equal(_bits(cache.layer(f"l{i}").values), vb, err_msg=f"layer {i} values")
 
 
-def test_ordered_compact_c_abi_matches_the_two_phase_compact() -> None:
+@pytest.mark.parametrize("layers,groups", [(5, 30), (8, 64)])
+def test_ordered_compact_c_abi_matches_the_two_phase_compact(layers, groups) -> None:
     # Through the C ABI on identical pools: lvamd_kv_compact_ordered and
     # lvamd_kv_compact give the same bytes for a grouped, ordered pair list
     # (groups of 1 to 40 pairs; each group reads rows at or after the ones it
-    # writes), and zero groups is a no-op.
+    # writes), and zero groups is a no-op.  Chunk widths: 5 layers x 30
+    # groups is narrowed to 8-byte chunks (fewer than 64 workgroups of 16-byte
+    # items); 8 layers x 64 groups (32,768 items of 16 bytes) keeps 16-byte
+    # chunks, whose batches hold 8 pairs, so longer groups take several.
     from light_vllm_amd import native
 
-    _announce("ordered compact vs two-phase compact (C ABI)")
+    _announce(f"ordered compact vs two-phase compact (C ABI), {layers} layers x {groups} groups")
     lib = native.load()
     stream = torch.cuda.current_stream(DEV).cuda_stream
-    layers, slots, row = 5, 4096, 2 * 128 * 2
+    slots, row = 8192, 2 * 128 * 2
     gen = torch.Generator(device=DEV).manual_seed(3)
     a = [torch.randn((slots, 2, 128), generator=gen, device=DEV).to(torch.bfloat16) for _ in range(2 * layers)]
     b = [t.clone() for t in a]
     rng = np.random.default_rng(4)
     src, dst, starts, base = [], [], [0], 0
-    for size in rng.integers(1, 41, size=30):
+    sizes = rng.integers(1, 41, size=groups)
+    assert (sizes > 8).any() and (sizes <= 8).any()
+    for size in sizes:
         keep = np.sort(rng.choice(np.arange(1, 2 * size), size=size, replace=False))
         src += [base + int(k) for k in keep]
         dst += [base + i for i in range(size)]
