@@ -7,7 +7,11 @@ Compact: row dst[i] of every layer's K and V must hold what row src[i] held
 before the call (sources may repeat and may be destinations: every source is
 read before any destination is written); every other row is unchanged.
 Block copy: block dst[i] becomes block src[i] (disjoint sets).  Row sizes
-cover each access width the kernels pick (16, 8, 4 and 2 bytes).
+and layer counts cover each access width the kernels pick (16, 8, 4 and 2
+bytes): the compact narrows its chunks until about 32 workgroups share the
+call, so 16- and 8-byte chunks need many layers of wide rows (32 layers of
+2048-byte rows, 16 layers of 2056-byte rows); three layers of 512-, 72- and
+36-byte rows run 4-byte chunks, 18-byte rows 2-byte chunks.
 """
 
 from __future__ import annotations
@@ -28,11 +32,11 @@ DEV = torch.device("cuda:0")
 LAYERS, SLOTS = 3, 512
 
 
-def _pools(seed: int, row: int):
+def _pools(seed: int, row: int, layers: int = LAYERS):
     gen = torch.Generator(device=DEV).manual_seed(seed)
     return [(torch.randint(-30000, 30000, (SLOTS, row), generator=gen, device=DEV, dtype=torch.int16),
              torch.randint(-30000, 30000, (SLOTS, row), generator=gen, device=DEV, dtype=torch.int16))
-            for _ in range(LAYERS)]
+            for _ in range(layers)]
 
 
 def _tables(pools):
@@ -41,23 +45,23 @@ def _tables(pools):
     return keys, values
 
 
-@pytest.mark.parametrize("row", (256, 36, 18, 9))  # int16 elements: 512, 72, 36, 18 bytes
+@pytest.mark.parametrize("layers,row", [(3, 256), (3, 36), (3, 18), (3, 9), (32, 1024), (16, 1028)])  # int16 elements
 @pytest.mark.parametrize("n", (1, 7, 8, 9, 16, 17, 32))  # the kernel's 8 / 16 / 32-pair buckets
-def test_small_compact_matches_the_closed_form_and_the_device_pair_compact(n, row) -> None:
-    print(f"[gpu] small compact n={n} row={2 * row} bytes", file=sys.stderr, flush=True)
+def test_small_compact_matches_the_closed_form_and_the_device_pair_compact(n, layers, row) -> None:
+    print(f"[gpu] small compact n={n} layers={layers} row={2 * row} bytes", file=sys.stderr, flush=True)
     lib = native.load()
     stream = torch.cuda.current_stream(DEV).cuda_stream
     rng = np.random.default_rng(n * 1000 + row)
     dst = rng.permutation(SLOTS)[:n].astype(np.int64)
     src = rng.integers(0, SLOTS, size=n).astype(np.int64)
-    small, device_pairs = _pools(row, row), _pools(row, row)
+    small, device_pairs = _pools(row, row, layers), _pools(row, row, layers)
     before = [(k.cpu().numpy(), v.cpu().numpy()) for k, v in small]
     sk, sv = _tables(small)
     dk, dv = _tables(device_pairs)
-    native.check(lib.lvamd_kv_compact_small(sk.data_ptr(), sv.data_ptr(), LAYERS, 2 * row, src.ctypes.data,
+    native.check(lib.lvamd_kv_compact_small(sk.data_ptr(), sv.data_ptr(), layers, 2 * row, src.ctypes.data,
                                             dst.ctypes.data, n, stream), "lvamd_kv_compact_small")
     src_d, dst_d = torch.tensor(src, device=DEV), torch.tensor(dst, device=DEV)
-    native.check(lib.lvamd_kv_compact(dk.data_ptr(), dv.data_ptr(), LAYERS, 2 * row, src_d.data_ptr(),
+    native.check(lib.lvamd_kv_compact(dk.data_ptr(), dv.data_ptr(), layers, 2 * row, src_d.data_ptr(),
                                       dst_d.data_ptr(), n, None, 0, stream), "lvamd_kv_compact")
     torch.cuda.synchronize()
     for layer, ((gk, gv), (rk, rv), (bk, bv)) in enumerate(zip(small, device_pairs, before)):
