@@ -180,3 +180,60 @@ def test_rotary_shape_errors() -> None:
     ctx = lv.HipPagedAttentionBackend().create(step.cache, step.metadata)
     with pytest.raises(lv.KVCacheError, match="rotary sines dtype"):
         ctx.forward("layer0", step.query, step.key, step.value, scale=step.scale, rotary=(cos, sin.float()))
+
+
+def _from_bits(bits: np.ndarray, dtype: torch.dtype) -> torch.Tensor:
+    if dtype == torch.float32:
+        return torch.from_numpy(bits).to(DEV)
+    return torch.from_numpy(bits.view(np.int16)).view(dtype).to(DEV)
+
+
+# Decode steps at the model's shape (the rotary append, then attention over
+# the pool), against the fused-append attention step over rows rotated
+# beforehand: the outputs and the pools must agree bit for bit.
+ROTATED_CASES = {
+    "c2_shape_bf16": dict(dtype=torch.bfloat16, seqs=64, lo=512, hi=4096, layout=(-1,), seed=5),
+    "chain2_f16": dict(dtype=torch.float16, seqs=48, lo=200, hi=3000, layout=(-1, 0), seed=6),
+    "short_bf16": dict(dtype=torch.bfloat16, seqs=96, lo=1, hi=300, layout=(-1,), seed=7),
+}
+
+
+@pytest.mark.parametrize("name", sorted(ROTATED_CASES))
+def test_forward_with_rotary_bit_equals_attention_over_rotated_rows(name) -> None:
+    """forward(..., rotary) must give the outputs and pool rows of forward over
+    queries and keys rotated beforehand (the oracle's rotary_half, pinned bit
+    for bit by the tests above), and leave every other pool byte unchanged."""
+
+    _announce(f"rotary vs rotated rows {name}")
+    c = ROTATED_CASES[name]
+    dtype = c["dtype"]
+    rng = np.random.default_rng(c["seed"])
+    computed = rng.integers(c["lo"], c["hi"] + 1, size=c["seqs"]).tolist()
+    case = dict(hq=28, hkv=4, d=128, bs=16, dtype=dtype, computed=computed, layouts=[c["layout"]] * c["seqs"])
+    rotary = make_step(seed=c["seed"], **case)
+    rotated = make_step(seed=c["seed"], **case)
+    lid = rotary.layer_ids[0]
+    cos, sin = rope_rows(_positions(rotary.metadata), 128, dtype)
+    q_rot = _from_bits(O.rotary_half(_bits(rotary.query), _bits(cos), _bits(sin), NAMES[dtype]), dtype)
+    k_rot = _from_bits(O.rotary_half(_bits(rotary.key), _bits(cos), _bits(sin), NAMES[dtype]), dtype)
+    rl, dl = rotary.cache.layer(lid), rotated.cache.layer(lid)
+    before_k, before_v = _bits(rl.keys), _bits(rl.values)
+    ctx = lv.HipPagedAttentionBackend().create(rotary.cache, rotary.metadata)
+    out_rotary = ctx.forward(lid, rotary.query, rotary.key, rotary.value, scale=rotary.scale, rotary=(cos, sin))
+    ctx = lv.HipPagedAttentionBackend().create(rotated.cache, rotated.metadata)
+    out_rotated = ctx.forward(lid, q_rot, k_rot, rotated.value, scale=rotated.scale)
+    torch.cuda.synchronize()
+    assert np.isfinite(out_rotary.float().cpu().numpy()).all()
+    np.testing.assert_array_equal(_bits(out_rotary), _bits(out_rotated))
+    # This step's slots hold the same rows in both caches; every other pool
+    # byte is unchanged (the caches' unwritten rows differ between the two
+    # allocations, so only the slots are compared across them).
+    cfg = rotary.cache.config
+    slots = rotary.metadata.slot_mapping(block_size=cfg.block_size, device=DEV)
+    n = cfg.num_blocks * cfg.block_size
+    for pool_r, pool_d, before in ((rl.keys, dl.keys, before_k), (rl.values, dl.values, before_v)):
+        np.testing.assert_array_equal(_bits(pool_r.view(n, 4, 128).index_select(0, slots)),
+                                      _bits(pool_d.view(n, 4, 128).index_select(0, slots)))
+        keep = np.ones(n, dtype=bool)
+        keep[slots.cpu().numpy()] = False
+        np.testing.assert_array_equal(_bits(pool_r).reshape(n, -1)[keep], before.reshape(n, -1)[keep])
