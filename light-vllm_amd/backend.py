@@ -217,14 +217,14 @@ class HipPagedAttention:
         self._config = cache.config
         self._layer_ids: set[str] = set()
         self._plan = plan
-        self._lib = native.load()
+        self._lib = backend._lib
         # The fast forward's facts: per layer the cache's fixed ones (pools,
         # shape, place among the layers of its shape), per layer shape this
         # step's (bound plan, output slab), bound at the shape's first layer.
         self._statics = backend.layer_statics(cache) if _raw_stream is not None else {}
         self._shape_bound: dict[tuple, tuple] = {}
-        self._attend_tensors = native.host().attend_tensors
-        self._attend_fn = native.attention_entry()
+        self._attend_tensors = backend._attend_tensors
+        self._attend_fn = backend._attend_fn
 
     @property
     def layer_ids(self) -> frozenset[str]:
@@ -283,15 +283,22 @@ class HipPagedAttention:
         launch = self._launch(spec)
         tokens = self._plan.num_tokens
         count = self._backend.shape_counts(self._cache)[static.shape]
-        slab = torch.empty((count, tokens, spec.num_query_heads, spec.head_size), dtype=static.dtype,
-                           device=static.device)
+        if count == 1:
+            # One layer of this shape: its output is the slab (no views).
+            slab = torch.empty((tokens, spec.num_query_heads, spec.head_size), dtype=static.dtype,
+                               device=static.device)
+            views = (slab,)
+        else:
+            slab = torch.empty((count, tokens, spec.num_query_heads, spec.head_size), dtype=static.dtype,
+                               device=static.device)
+            views = slab.unbind(0)
         facts = (
             self._attend_fn, launch.plan_ptr, spec.num_query_heads * spec.head_size, spec.head_size, static.dtype,
             static.device_index, static.element_size, tokens, spec.num_query_heads, spec.num_kv_heads,
             spec.head_size, _raw_stream,
         )
         bound = (facts, slab.data_ptr(), tokens * spec.num_query_heads * spec.head_size * static.element_size,
-                 slab.unbind(0), launch)
+                 views, launch)
         self._shape_bound[static.shape] = bound
         return bound
 
@@ -497,7 +504,13 @@ class HipPagedAttentionBackend:
         self._head_sizes_ok: "weakref.WeakSet[object]" = weakref.WeakSet()
         self._statics: "weakref.WeakKeyDictionary[object, dict]" = weakref.WeakKeyDictionary()
         self._shape_counts: "weakref.WeakKeyDictionary[object, dict]" = weakref.WeakKeyDictionary()
-        self._last: tuple[object, object, StepPlan] | None = None
+        # (geometry, metadata key, plan, weak reference to the cache) of the
+        # most recent create().
+        self._last: tuple[object, object, StepPlan, weakref.ref] | None = None
+        # What every context's fast forward calls, looked up once.
+        self._lib = native.load()
+        self._attend_tensors = native.host().attend_tensors
+        self._attend_fn = native.attention_entry()
 
     def prefill_columns(self, code: int, head_size: int) -> int:
         return native.prefill_unit_columns(code, head_size) if self._use_prefill else 0
@@ -592,6 +605,15 @@ class HipPagedAttentionBackend:
         return found
 
     def create(self, cache, metadata) -> HipPagedAttention:
+        # This package's metadata is recognised by its facts object, which the
+        # plan holds anyway: the metadata itself (a step's worth of tuples) is
+        # not kept alive, so the caller frees it, not the next create().  The
+        # same metadata on the same cache object takes the last plan with no
+        # rule to re-check (the cache's configuration does not change).
+        key = metadata.facts if isinstance(metadata, PagedAttentionMetadata) else metadata
+        last = self._last
+        if last is not None and last[1] is key and last[3]() is cache:
+            return HipPagedAttention(self, cache, last[2])
         config = cache.config
         if config.device.type != "cuda":
             raise errors.KVCacheError("HIP paged attention requires a GPU KV cache")
@@ -601,12 +623,8 @@ class HipPagedAttentionBackend:
         # layer shapes: its work lists were built from the kernel facts of
         # those shapes in that dtype.
         geometry = (config.num_blocks, config.block_size, config.device, config.dtype, shapes.keys)
-        # This package's metadata is recognised by its facts object, which the
-        # plan holds anyway: the metadata itself (a step's worth of tuples) is
-        # not kept alive, so the caller frees it, not the next create().
-        key = metadata.facts if isinstance(metadata, PagedAttentionMetadata) else metadata
-        last = self._last
         if last is not None and last[1] is key and last[0] == geometry:
+            self._last = (geometry, key, last[2], weakref.ref(cache))
             return HipPagedAttention(self, cache, last[2])
         staging = self._staging.get(config.device)
         if staging is None:
@@ -615,5 +633,5 @@ class HipPagedAttentionBackend:
         # stages it all; one copy uploads it.
         plan = StepPlan(metadata, block_size=config.block_size, device=config.device, num_blocks=config.num_blocks,
                         partition_tokens=self._partition_tokens, staging=staging, shapes=shapes)
-        self._last = (geometry, key, plan)
+        self._last = (geometry, key, plan, weakref.ref(cache))
         return HipPagedAttention(self, cache, plan)
