@@ -41,10 +41,11 @@ from light_vllm_amd.facts import TABLE_RULES, StepFacts, facts_of
 # K/V tile.
 DECODE_MAX_COLUMNS = 16
 # Fewest decode tiles per stream-K share: small steps are spread over more
-# waves down to this (C1, 4 sequences of 38-512 tokens in fp32: 15.5 us per
-# step at four tiles per share, 12.3 at two, 12.8 at one); steps that fill
-# the resident waves are not affected.
-DECODE_MIN_UNITS_PER_WAVE = 2
+# waves down to this (C1, 4 sequences of 38-512 tokens in fp32: 10.6-10.8 us
+# per step at one tile per share against 11.5 at two, once the host path no
+# longer set the step's pace); steps that fill the resident waves are not
+# affected.
+DECODE_MIN_UNITS_PER_WAVE = 1
 # Smallest key range (in prefill key tiles) the planner gives one prefill
 # workgroup when it splits units to fill the GPU.
 PREFILL_MIN_TILES = 4
