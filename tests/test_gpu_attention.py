@@ -388,7 +388,9 @@ def test_fused_qkv_views_take_either_path() -> None:
 def test_one_metadata_on_caches_of_two_dtypes() -> None:
     # A plan is reused only by a cache of the same geometry, dtype and layer
     # shapes: the same metadata object sent to a bf16 cache and then to an
-    # fp16 cache of equal geometry must run each cache's own kernels.
+    # fp16 cache of equal geometry must run each cache's own kernels; back on
+    # the bf16 cache it is planned again, and a second create() on that same
+    # cache takes the plan by identity.
     _announce("one metadata, two dtypes")
     step = make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=[1500, 33, 700],
                      layouts=_lin(1, 9, 1), seed=321)
@@ -403,7 +405,7 @@ def test_one_metadata_on_caches_of_two_dtypes() -> None:
     step16 = type(step)(cache16, step.metadata, step.query.to(torch.float16), step.key.to(torch.float16),
                         step.value.to(torch.float16), step.layer_ids, step.scale)
     backend = lv.HipPagedAttentionBackend()
-    for s in (step, step16):
+    for s in (step, step16, step, step):
         ctx = backend.create(s.cache, s.metadata)
         out = ctx.forward(lid, s.query, s.key, s.value, scale=s.scale)
         torch.cuda.synchronize()
