@@ -958,16 +958,14 @@ struct DecodeParams {
 // merge launch it saves costs (kSplitMergeTiles tiles).  A workgroup's time
 // grows by about one tile's load latency per tile of its longest wave, so
 // the split is taken at one tile per wave, and at two only where stream-K is
-// slower too: when the step has kSplitBusyGroups workgroups or more.
-// (Measured on 8 bf16 layers of 28 / 4 heads, D 128, one HIP graph, per
-// layer, against stream-K at one tile per share: one tile 6.5-9.1 us
-// against 9.5-15.0 for 1-64 sequences of 64-128 tokens; two tiles at 256
-// tokens 10.8 vs 9.9 (1 sequence), 10.9 vs 10.0 (4), 11.3 vs 11.4 (16;
-// 28 layers of the small config: 327 vs 314 us per step), 11.5 vs 14.5 (32),
-// 13.4 vs 18.0 (64), at 384 tokens 12.5 vs 16.0 (32) and 16.5 vs 21.7 (64).
-// Earlier, three and four tiles lost, 19.3 vs 16.9 and 20.7 vs 13.7, and
-// without a cap C2's 64 contexts of 512-4096 tokens took one CU per segment:
-// 84 us against 59 us on stream-K shares.)
+// slower too: when the pieces average at most 1.5 tiles, or the step has
+// kSplitBusyGroups segments or more.  (Measured on 28 bf16 layers of 28 / 4
+// heads, D 128, per layer: one tile 4.3-12.6 us against stream-K's 4.9-18.3;
+// two tiles 13.4 vs 12.7 at 1 x 512 tokens, 15.6 vs 15.1 at 16 x 512, 13.6
+// vs 14.7 at 16 x 384, 16.6 vs 18.0 at 32 x 512, 19.8 vs 22.6 at 64 x 512;
+// three and four tiles lose, 19.3 vs 16.9 and 20.7 vs 13.7.  Without a cap
+// C2's 64 contexts of 512-4096 tokens took one CU per segment: 84 us against
+// 59 us on stream-K shares.)
 constexpr int64_t kSplitMergeTiles = 3;
 constexpr int64_t kSplitMaxTiles = 2;
 constexpr int64_t kSplitBusyGroups = 128;
@@ -1082,7 +1080,7 @@ void build_decode(const Requests& q, const int32_t* ids, int64_t nflat, const De
   const int64_t split_share = (longest + gw - 1) / gw;
   const int64_t nseg = (int64_t)segs.size();
   if (nseg * d.hkv > d.split_groups || split_share > cap || split_share > kSplitMaxTiles) return;
-  if (split_share == kSplitMaxTiles && nseg * d.hkv < kSplitBusyGroups) return;
+  if (split_share == kSplitMaxTiles && 2 * longest > 3 * gw && nseg * d.hkv < kSplitBusyGroups) return;
   if (split_share > per_wave + (out.jobs.empty() ? 0 : kSplitMergeTiles)) return;
   out.reset();
   out.group_waves = gw;

@@ -74,10 +74,9 @@ def _run(backend, step):
 
 
 def _short_decode_step(seed):
-    # Short contexts: the workgroup split (eight waves per segment of at most
-    # eight tiles, LDS merge).
+    # Short contexts: the workgroup split (eight waves per segment, LDS merge).
     rng = np.random.default_rng(seed)
-    computed = [int(c) for c in rng.integers(0, 250, size=16)]
+    computed = [int(c) for c in rng.integers(0, 370, size=16)]
     return make_step(hq=28, hkv=4, d=128, bs=16, dtype=torch.bfloat16, computed=computed, layouts=[(-1,)] * 16,
                      seed=seed)
 
