@@ -965,7 +965,14 @@ struct DecodeParams {
 // vs 14.7 at 16 x 384, 16.6 vs 18.0 at 32 x 512, 19.8 vs 22.6 at 64 x 512;
 // three and four tiles lose, 19.3 vs 16.9 and 20.7 vs 13.7.  Without a cap
 // C2's 64 contexts of 512-4096 tokens took one CU per segment: 84 us against
-// 59 us on stream-K shares.)
+// 59 us on stream-K shares.  Against stream-K at one tile per share, in a HIP
+// graph of 8 layers: one tile 6.5-9.1 us against 9.5-15.0; two tiles at 256
+// tokens 10.8 vs 9.9 (1 sequence), 10.9 vs 10.0 (4), 11.3 vs 11.4 (16),
+// 11.5 vs 14.5 (32), 13.4 vs 18.0 (64).  The two-tile split is kept where
+// stream-K's GPU time is lower by up to a tenth: it is one launch per layer
+// where stream-K makes two, and the host submits about 4 us more per layer
+// for the second (the 28-layer small config: 325 us of GPU time and 5.3 us of
+// host time per layer on the split, 313 us and 9.3 us on stream-K).)
 constexpr int64_t kSplitMergeTiles = 3;
 constexpr int64_t kSplitMaxTiles = 2;
 constexpr int64_t kSplitBusyGroups = 128;

@@ -137,7 +137,7 @@ def test_c1_qwen05b_fp32_decode() -> None:
     _announce("C1 fp32 decode")
     step = make_step(hq=14, hkv=2, d=64, bs=16, dtype=torch.float32, computed=[37, 128, 200, 511],
                      layouts=_lin(1, 1, 1, 1), num_blocks=256, seed=1)
-    _run_and_check(step, margin="C1 (fp32, workgroup split)")
+    _run_and_check(step, margin="C1 (fp32, stream-K)")
 
 
 def test_c2_qwen7b_bf16_decode_bs64() -> None:
