@@ -219,6 +219,21 @@ def test_stream_k_pieces_cover_every_segment_once(resident, bs, group, unit, ctw
     assert sorted(slots_seen) == list(range(work.num_partial_slots))
 
 
+@pytest.mark.parametrize("computed, waves", ((1024, 33), (2048, 33), (4096, 43), (300, 10)))
+def test_stream_k_cuts_no_segment_into_more_than_48_pieces(computed, waves) -> None:
+    """One sequence on stream-K shares: one tile per share while that cuts it
+    into at most 48 pieces (the merge reads 16 partials per round trip),
+    longer shares past that (65 tiles: 33 shares of two; 129: 43 of three)."""
+
+    md = lv.PagedAttentionMetadata(block_tables=(tuple(range(-(-(computed + 1) // 16))),),
+                                   num_computed_tokens=(computed,),
+                                   query_layouts=(lv.linear_query_layout(1),))
+    plan = StepPlan(md, block_size=16, device=CPU)
+    work = plan.work(7, 4, 1024, 0, 32, 1)
+    assert work.waves_per_head == waves and work.group_waves == 1
+    assert work.num_jobs == 1 and int(work.jobs.numpy()[0][3]) == waves <= 48
+
+
 @pytest.mark.parametrize("gw", (4, 8))
 @pytest.mark.parametrize("bs", (1, 16))
 @pytest.mark.parametrize("seed", range(6))
