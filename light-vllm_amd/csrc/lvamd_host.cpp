@@ -999,12 +999,14 @@ void build_decode(const Requests& q, const int32_t* ids, int64_t nflat, const De
   int64_t cap = std::max<int64_t>(1, ((kTableSlice - 2) * d.bs) / d.unit);
   if (d.max_units > 0) cap = std::max<int64_t>(1, std::min(cap, d.max_units));
   // Shares of at least min_units tiles, and long enough that no segment is
-  // cut into more than kMergePiecesMax pieces (the merge reads 16 partials
+  // cut into more than kMergePiecesMax pieces (a segment of T tiles over
+  // shares of P takes at most ceil(T / P) + 1; the merge reads 16 partials
   // per round trip: one sequence of 2048 tokens in 65 one-tile pieces took
   // 15.7 us per layer against 14.9 in 33).
   int64_t longest_seg = 0;
   for (const Seg& sg : segs) longest_seg = std::max(longest_seg, sg.tiles);
-  const int64_t min_units = std::max<int64_t>(d.min_units, (longest_seg + kMergePiecesMax - 1) / kMergePiecesMax);
+  const int64_t min_units =
+      std::max<int64_t>(d.min_units, (longest_seg + kMergePiecesMax - 2) / (kMergePiecesMax - 1));
   int64_t waves = std::max<int64_t>(
       1, std::min(std::max<int64_t>(1, d.resident / d.hkv), (total + min_units - 1) / min_units));
   waves = std::max(waves, (total + cap - 1) / cap);

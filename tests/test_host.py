@@ -204,6 +204,7 @@ def test_stream_k_pieces_cover_every_segment_once(resident, bs, group, unit, ctw
     jobs = {(int(j[0]), int(j[1])): (int(j[2]), int(j[3])) for j in job_rows}
     for j in job_rows:  # the merge kernel reads q_start and q_len from the job
         assert j[4] == md.query_start_loc[j[0]] and j[5] == md.query_lengths[j[0]]
+        assert j[3] <= 48  # pieces per segment (the planner's cap)
     slots_seen = []
     for r, q in enumerate(md.query_lengths):
         for ct in range(ngroups[r]):
