@@ -235,8 +235,8 @@ int lvamd_paged_attention_merge(const void* part_acc, const float* part_ml,
 
 /*
  * Chunked-prefill paged attention for query runs of more than one column
- * tile (prompt chunks, tree verification; bf16 / fp16, head sizes 64, 80, 96,
- * 128, 256): one workgroup per (unit, kv head); a unit
+ * tile (prompt chunks, tree verification; bf16 / fp16, head sizes that are
+ * multiples of 16 from 32 to 256): one workgroup per (unit, kv head); a unit
  * (units [num_units][LVAMD_PREFILL_FIELDS]) is a run of MFMA columns of one
  * request over a key range, a column being a (query, head-in-group) pair,
  * column c = query (c / group), head (c % group).  K/V tiles (64 tokens up to

@@ -38,7 +38,8 @@ from light_vllm_amd.plan import (
     DECODE_MAX_COLUMNS, DECODE_MIN_UNITS_PER_WAVE, PREFILL_MIN_TILES, UNIT_TOKENS, LayerShapes, Staging, StepPlan,
 )
 
-SUPPORTED_HEAD_SIZES = (32, 64, 80, 96, 128, 256)
+# Head sizes the kernels are built for: multiples of 16 from 32 to 256.
+SUPPORTED_HEAD_SIZES = tuple(range(32, 257, 16))
 
 
 def validate_paged_attention_tensors(cache, metadata, layer_id: str, query: Tensor, key: Tensor, value: Tensor):

@@ -1023,9 +1023,8 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_merge_kernel(
 // ---------------------------------------------------------------------------
 // Launch tables: (dtype, head size, column tiles per wave) -> kernel.
 // ---------------------------------------------------------------------------
-static bool head_size_supported(int d) {
-  return d == 32 || d == 64 || d == 80 || d == 96 || d == 128 || d == 256;
-}
+// Head sizes: multiples of 16 from 32 to 256.
+static bool head_size_supported(int d) { return d >= 32 && d <= 256 && d % 16 == 0; }
 static bool col_tiles_supported(int ctw) { return ctw == 1 || ctw == 4; }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -1050,10 +1049,19 @@ template <typename T, int CTW, typename F>
 static int with_head_size(int head_size, F& f) {
   switch (head_size) {
     case 32: return with_kernel<T, 32, CTW>(f);
+    case 48: return with_kernel<T, 48, CTW>(f);
     case 64: return with_kernel<T, 64, CTW>(f);
     case 80: return with_kernel<T, 80, CTW>(f);
     case 96: return with_kernel<T, 96, CTW>(f);
+    case 112: return with_kernel<T, 112, CTW>(f);
     case 128: return with_kernel<T, 128, CTW>(f);
+    case 144: return with_kernel<T, 144, CTW>(f);
+    case 160: return with_kernel<T, 160, CTW>(f);
+    case 176: return with_kernel<T, 176, CTW>(f);
+    case 192: return with_kernel<T, 192, CTW>(f);
+    case 208: return with_kernel<T, 208, CTW>(f);
+    case 224: return with_kernel<T, 224, CTW>(f);
+    case 240: return with_kernel<T, 240, CTW>(f);
     case 256: return with_kernel<T, 256, CTW>(f);
     default: return LVAMD_ERR_UNSUPPORTED;
   }
@@ -1082,10 +1090,19 @@ static int launch_merge_t(int head_size, dim3 grid, hipStream_t s, const int32_t
   const dim3 block(64 * kMergeWaves);
   switch (head_size) {
     case 32: hipLaunchKernelGGL((paged_merge_kernel<T, 32>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
+    case 48: hipLaunchKernelGGL((paged_merge_kernel<T, 48>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
     case 64: hipLaunchKernelGGL((paged_merge_kernel<T, 64>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
     case 80: hipLaunchKernelGGL((paged_merge_kernel<T, 80>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
     case 96: hipLaunchKernelGGL((paged_merge_kernel<T, 96>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
+    case 112: hipLaunchKernelGGL((paged_merge_kernel<T, 112>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
     case 128: hipLaunchKernelGGL((paged_merge_kernel<T, 128>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
+    case 144: hipLaunchKernelGGL((paged_merge_kernel<T, 144>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
+    case 160: hipLaunchKernelGGL((paged_merge_kernel<T, 160>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
+    case 176: hipLaunchKernelGGL((paged_merge_kernel<T, 176>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
+    case 192: hipLaunchKernelGGL((paged_merge_kernel<T, 192>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
+    case 208: hipLaunchKernelGGL((paged_merge_kernel<T, 208>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
+    case 224: hipLaunchKernelGGL((paged_merge_kernel<T, 224>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
+    case 240: hipLaunchKernelGGL((paged_merge_kernel<T, 240>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
     case 256: hipLaunchKernelGGL((paged_merge_kernel<T, 256>), grid, block, 0, s, jobs, quads, num_kv_heads, group, col_tiles, a); break;
     default: return LVAMD_ERR_UNSUPPORTED;
   }

@@ -509,10 +509,20 @@ template <typename T>
 static int launch_prefill_t(int head_size, int waves, dim3 grid, hipStream_t s, const int32_t* units,
                             int32_t num_kv_heads, const PrefillArgs& a) {
   switch (head_size) {
+    case 32: return launch_prefill_d<T, 32>(waves, grid, s, units, num_kv_heads, a);
+    case 48: return launch_prefill_d<T, 48>(waves, grid, s, units, num_kv_heads, a);
     case 64: return launch_prefill_d<T, 64>(waves, grid, s, units, num_kv_heads, a);
     case 80: return launch_prefill_d<T, 80>(waves, grid, s, units, num_kv_heads, a);
     case 96: return launch_prefill_d<T, 96>(waves, grid, s, units, num_kv_heads, a);
+    case 112: return launch_prefill_d<T, 112>(waves, grid, s, units, num_kv_heads, a);
     case 128: return launch_prefill_d<T, 128>(waves, grid, s, units, num_kv_heads, a);
+    case 144: return launch_prefill_d<T, 144>(waves, grid, s, units, num_kv_heads, a);
+    case 160: return launch_prefill_d<T, 160>(waves, grid, s, units, num_kv_heads, a);
+    case 176: return launch_prefill_d<T, 176>(waves, grid, s, units, num_kv_heads, a);
+    case 192: return launch_prefill_d<T, 192>(waves, grid, s, units, num_kv_heads, a);
+    case 208: return launch_prefill_d<T, 208>(waves, grid, s, units, num_kv_heads, a);
+    case 224: return launch_prefill_d<T, 224>(waves, grid, s, units, num_kv_heads, a);
+    case 240: return launch_prefill_d<T, 240>(waves, grid, s, units, num_kv_heads, a);
     case 256: return launch_prefill_d<T, 256>(waves, grid, s, units, num_kv_heads, a);
     default: return LVAMD_ERR_UNSUPPORTED;
   }
@@ -530,18 +540,28 @@ static const void* prefill_fn(int waves) {
 template <typename T>
 static const void* prefill_fn_t(int head_size, int waves) {
   switch (head_size) {
+    case 32: return prefill_fn<T, 32>(waves);
+    case 48: return prefill_fn<T, 48>(waves);
     case 64: return prefill_fn<T, 64>(waves);
     case 80: return prefill_fn<T, 80>(waves);
     case 96: return prefill_fn<T, 96>(waves);
+    case 112: return prefill_fn<T, 112>(waves);
     case 128: return prefill_fn<T, 128>(waves);
+    case 144: return prefill_fn<T, 144>(waves);
+    case 160: return prefill_fn<T, 160>(waves);
+    case 176: return prefill_fn<T, 176>(waves);
+    case 192: return prefill_fn<T, 192>(waves);
+    case 208: return prefill_fn<T, 208>(waves);
+    case 224: return prefill_fn<T, 224>(waves);
+    case 240: return prefill_fn<T, 240>(waves);
     case 256: return prefill_fn<T, 256>(waves);
     default: return nullptr;
   }
 }
 
+// 16-bit pools, head sizes that are multiples of 16 from 32 to 256.
 static bool prefill_supported(int dtype, int head_size) {
-  return (dtype == LVAMD_BF16 || dtype == LVAMD_F16) &&
-         (head_size == 64 || head_size == 80 || head_size == 96 || head_size == 128 || head_size == 256);
+  return (dtype == LVAMD_BF16 || dtype == LVAMD_F16) && head_size >= 32 && head_size <= 256 && head_size % 16 == 0;
 }
 
 }  // namespace lvamd

@@ -161,7 +161,7 @@ def test_small_batch_reference_point_bf16() -> None:
 
 
 @pytest.mark.parametrize("dtype", ("fp32", "fp16", "bf16"))
-@pytest.mark.parametrize("head_size", (32, 64, 80, 96, 128, 256))
+@pytest.mark.parametrize("head_size", range(32, 257, 16))
 def test_head_sizes_and_dtypes_decode_with_split_k(dtype, head_size) -> None:
     _announce(f"decode d={head_size} {dtype}")
     step = make_step(hq=8, hkv=2, d=head_size, bs=16, dtype=DTYPES[dtype], computed=[700, 3, 1500, 64],
@@ -295,7 +295,7 @@ def test_split_k_partials_hold_values_near_the_fp16_limit(prefill) -> None:
 
 # ------------------------------------------------------ four column tiles per decode wave
 @pytest.mark.parametrize("dtype", ("fp32", "fp16", "bf16"))
-@pytest.mark.parametrize("head_size", (32, 64, 80, 96, 128))
+@pytest.mark.parametrize("head_size", (32, 48, 64, 80, 96, 112, 128))
 def test_four_column_tiles_across_dtypes_and_head_sizes(dtype, head_size) -> None:
     # Eight queries x group 4 = 32 columns: two column tiles of a four-tile group.
     _announce(f"col_tiles=4 d={head_size} {dtype}")
@@ -477,7 +477,7 @@ def test_layers_of_two_shapes_alternating_in_one_cache() -> None:
 
 # ------------------------------------------------------ workgroup split (latency-bound decode)
 @pytest.mark.parametrize("dtype", ("fp32", "fp16", "bf16"))
-@pytest.mark.parametrize("head_size", (32, 64, 80, 96, 128, 256))
+@pytest.mark.parametrize("head_size", range(32, 257, 16))
 def test_workgroup_split_decode_matches_the_oracle(dtype, head_size) -> None:
     # Short decode rows (one segment per workgroup of eight waves, four for
     # the widest rows, results combined in LDS): a 1-token context, segments
@@ -529,11 +529,11 @@ def test_workgroup_split_block_sizes_and_groups(bs, hq, hkv) -> None:
     assert (out1.float() - out2.float()).abs().max().item() <= max_tol
 
 
-@pytest.mark.parametrize("head_size", (48, 112, 160, 192))
+@pytest.mark.parametrize("head_size", (16, 40, 72, 264))
 def test_unbuilt_head_sizes_are_refused_when_the_step_starts(head_size) -> None:
-    # The kernels are built for head sizes 32, 64, 80, 96, 128 and 256; a
-    # cache with another layer shape fails at create() with the reference's
-    # error class, before any layer's forward.
+    # The kernels are built for head sizes that are multiples of 16 from 32
+    # to 256; a cache with another layer shape fails at create() with the
+    # reference's error class, before any layer's forward.
     spec = lv.ModelKVCacheSpec((lv.AttentionLayerSpec("a", 8, 2, 128), lv.AttentionLayerSpec("b", 8, 2, head_size)))
     cache = lv.PagedKVCache(spec, lv.PagedKVCacheConfig(num_blocks=8, block_size=16, dtype=torch.bfloat16, device=DEV))
     md = lv.PagedAttentionMetadata(block_tables=((0,),), num_computed_tokens=(3,),

@@ -66,7 +66,7 @@ def _check(step, *, backend=None, dense=False, expect_prefill=True, waves=None):
 
 @pytest.mark.parametrize("waves", WAVES)
 @pytest.mark.parametrize("dtype", ("bf16", "fp16"))
-@pytest.mark.parametrize("head_size", (64, 80, 96, 128, 256))
+@pytest.mark.parametrize("head_size", range(32, 257, 16))
 def test_prefill_head_sizes_and_dtypes(dtype, head_size, waves) -> None:
     _announce(f"prefill d={head_size} {dtype} waves={waves}")
     step = make_step(hq=8, hkv=2, d=head_size, bs=16, dtype=DTYPES[dtype], computed=[0, 37, 300, 90],
@@ -182,7 +182,7 @@ def _split_work(step, waves=None):
 
 @pytest.mark.parametrize("waves", WAVES)
 @pytest.mark.parametrize("dtype", ("bf16", "fp16"))
-@pytest.mark.parametrize("head_size", (64, 80, 96, 128, 256))
+@pytest.mark.parametrize("head_size", range(32, 257, 16))
 def test_split_k_tree_verification_head_sizes(dtype, head_size, waves) -> None:
     _announce(f"split-K prefill tree d={head_size} {dtype} waves={waves}")
     rng = np.random.default_rng(head_size)

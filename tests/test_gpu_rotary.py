@@ -93,7 +93,7 @@ def _expected(q, k, v, cos, sin, kpool, vpool, slots, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("d", [64, 80, 96, 128, 256])
+@pytest.mark.parametrize("d", [48, 64, 80, 96, 112, 128, 160, 192, 240, 256])
 def test_rotary_append_matches_oracle_bit_for_bit(dtype, d) -> None:
     _announce(f"rotary append {dtype} D={d}")
     q, k, v, cos, sin, kpool, vpool, slots = _case(dtype, d, seed=d)
