@@ -493,7 +493,7 @@ def head_size_sweep(args, device: torch.device) -> int:
 
     out = {"mode": "head-sweep", "decode": [], "prefill": []}
     ctx = [int(x) for x in np.random.default_rng(7).integers(512, 4097, size=64)]
-    for dtype, sizes in ((torch.bfloat16, (32, 64, 80, 96, 128, 256)), (torch.float16, (64, 128, 256)),
+    for dtype, sizes in ((torch.bfloat16, tuple(range(32, 257, 16))), (torch.float16, (64, 128, 256)),
                          (torch.float32, (32, 64, 128))):
         for d in sizes:
             cache, md, qkv = build(dtype, d, ctx, [1] * len(ctx), 11)
@@ -503,7 +503,7 @@ def head_size_sweep(args, device: torch.device) -> int:
                                   "pct_of_hbm_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1)})
             del cache
             torch.cuda.empty_cache()
-    for dtype, sizes in ((torch.bfloat16, (64, 80, 96, 128, 256)), (torch.float16, (128,))):
+    for dtype, sizes in ((torch.bfloat16, tuple(range(32, 257, 16))), (torch.float16, (128,))):
         for d in sizes:
             computed, q_lens = [1024] * 4, [512] * 4
             cache, md, qkv = build(dtype, d, computed, q_lens, 12)
