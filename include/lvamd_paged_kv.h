@@ -173,7 +173,9 @@ int lvamd_kv_append_rotary(const void* query, int64_t query_token_stride, int64_
  * tile.  bf16/fp16 QK^T and PV on MFMA (fp32 on 16x16x4), fp32 online softmax;
  * K/V gathered through the block table (tables: flat int32 block ids); vis
  * holds uint32 ancestor bit rows for requests with vis_off >= 0.  scale is the
- * caller's softmax scale.
+ * caller's softmax scale.  head_size: a multiple of 16 from 32 to 256 (the
+ * merge and prefill entry points take the same set); any other returns
+ * LVAMD_ERR_UNSUPPORTED.
  *
  * Together with lvamd_paged_attention_merge and lvamd_paged_prefill this
  * replaces TorchPagedAttention.forward / _attend_query_token
