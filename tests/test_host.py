@@ -729,6 +729,17 @@ def test_library_loads_and_exports_every_header_function() -> None:
     no_append = (None, 0, 0, None, 0, 0)
     assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 1, None, None,
                                   None, None, 0, 4, 7, 72, 1, 1, 16, ctypes.c_float(0.1), 2, None) == -2
+    # Head sizes: multiples of 16 from 32 to 256 pass the shape check (and
+    # stop at the null pointers), others are not built.
+    for d, want in ((48, -1), (112, -1), (240, -1), (16, -2), (40, -2), (264, -2), (272, -2)):
+        for dtype in (0, 1, 2):
+            assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 1, None, None,
+                                          None, None, 0, 4, 7, d, 1, 1, 16, ctypes.c_float(0.1), dtype,
+                                          None) == want, (d, dtype)
+        assert lib.lvamd_paged_attention_merge(None, None, None, 0, 0, None, 1, 4, 7, d, 1, 16, 2, None) == want
+        assert (lib.lvamd_paged_prefill_waves_built(2, d, 4) == 1) == (want == -1)
+        assert lib.lvamd_paged_prefill_key_tokens(2, d) == (-2 if want == -2 else 64 if d <= 128 else 32)
+    assert lib.lvamd_paged_prefill_waves_built(1, 112, 8) == 1 and lib.lvamd_paged_prefill_waves_built(1, 144, 8) == 0
     assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 1, None, None,
                                   None, None, 0, 4, 7, 128, 1, 1, 16, ctypes.c_float(0.1), 2, None) == -1
     assert lib.lvamd_paged_decode(None, 0, 0, *no_append, None, None, None, 0, 0, None, None, 1, None, None,
