@@ -30,7 +30,7 @@ if not torch.cuda.is_available():
 DEV = torch.device("cuda:0")
 NAMES = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
 GEOMETRIES = [(28, 4, 128), (12, 2, 128), (14, 2, 64), (8, 8, 64), (16, 2, 80), (16, 4, 96), (8, 2, 256),
-              (32, 4, 32)]
+              (32, 4, 32), (12, 4, 48), (16, 2, 112), (8, 2, 160), (16, 4, 192), (4, 2, 240)]
 
 
 def _bits(t: torch.Tensor) -> np.ndarray:
